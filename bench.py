@@ -1,0 +1,248 @@
+"""Benchmark of the quantized-projection path on one MI355X.
+
+Headline (`value`): GGUF Q4_K matvec, 4096 -> 14336, M = 1, in GB/s of algorithmic
+bytes (raw weight blocks + activations read + outputs written) with the inputs
+resident in HBM.  A step is one call of the hot path on one weight copy; the
+copies rotate through a pool of more than 1 GiB so that no timed call is served
+from the 256 MB Infinity Cache.  Kernel time is taken with HIP events recorded on
+the stream the kernels run on.
+
+Also reported under "extra": the Q8_0 4096x4096 M=1 matvec, the fused
+SiLU(gate)*up + Q4_K 14336 -> 4096 down projection, and the M = 16 block-verify
+products (Q4_K 4096 -> 14336 with bf16 and f32 activations, Q8_0 4096 -> 4096
+with f32 activations).
+
+`cpu_baseline`: the same Q4_K matvec computed by the oracle (a C restatement of
+kernels/proj_q4k.comp's per-element decode and f32 accumulation) on the host
+cores, over a bounded sample of output rows.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "laguna-raw-halo-strix_amd"))
+
+import laguna_hip as lh  # noqa: E402
+import synth  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "Q4_K/Q8_0 matvec HBM GB/s (% of peak) M=1; 6-layer draft block fwd µs"
+POOL_BYTES = 1 << 30
+
+
+class HipEvents:
+    """hipEvent timing through the HIP runtime the library itself uses."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def new(self):
+        e = ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e, stream):
+        assert self.hip.hipEventRecord(e, stream) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+
+class Workload:
+    name = ""
+    bytes_per_call = 0
+
+    def setup(self, ctx):
+        raise NotImplementedError
+
+    def step(self, ctx, i):
+        raise NotImplementedError
+
+
+class MatvecM1(Workload):
+    def __init__(self, dtype, k, n, seed, fused=False):
+        self.dtype, self.k, self.n, self.seed, self.fused = dtype, k, n, seed, fused
+        wbytes = synth.weight_bytes(dtype, k, n)
+        xbytes = 4 * k * (2 if fused else 1)
+        self.bytes_per_call = wbytes + xbytes + 4 * n
+        tag = {lh.Q4_K: "Q4_K", lh.Q8_0: "Q8_0"}[dtype]
+        self.name = (f"fused SiLU(gate)*up + {tag} matvec {k}->{n} M=1" if fused else f"{tag} matvec {k}->{n} M=1")
+
+    def setup(self, ctx):
+        k, n = self.k, self.n
+        raw = synth.q4k_weight(self.seed, k, n) if self.dtype == lh.Q4_K else synth.q8_0_weight(self.seed, k, n)
+        copies = max(2, -(-POOL_BYTES // raw.nbytes))
+        self.pool = []
+        for _ in range(copies):
+            b = lh.GpuBuffer(ctx, raw.nbytes)
+            b.upload(raw)
+            self.pool.append(b)
+        self.pool_bytes = copies * raw.nbytes
+        self.x = lh.upload_f32(ctx, synth.normal(self.seed + 1, k))
+        self.up = lh.upload_f32(ctx, synth.normal(self.seed + 2, k)) if self.fused else None
+        self.c = lh.GpuBuffer(ctx, 4 * n)
+
+    def step(self, ctx, i):
+        w = self.pool[i % len(self.pool)]
+        if self.fused:
+            lh.dispatch_silu_mul_proj_quant(ctx, self.x, self.up, w, self.c, self.k, self.n, self.dtype)
+        else:
+            lh.dispatch_proj_quant(ctx, self.x, w, self.c, self.k, self.n, self.dtype)
+
+
+class BatchM16(Workload):
+    def __init__(self, dtype, k, n, x_dtype, seed, m=16):
+        self.dtype, self.k, self.n, self.x_dtype, self.seed, self.m = dtype, k, n, x_dtype, seed, m
+        xb = 2 if x_dtype == lh.BF16 else 4
+        self.bytes_per_call = synth.weight_bytes(dtype, k, n) + m * k * xb + 4 * m * n
+        tag = {lh.Q4_K: "Q4_K", lh.Q8_0: "Q8_0"}[dtype]
+        self.name = f"{tag} block-verify {k}->{n} M={m} x={'bf16' if x_dtype == lh.BF16 else 'f32'}"
+
+    def setup(self, ctx):
+        k, n, m = self.k, self.n, self.m
+        raw = synth.q4k_weight(self.seed, k, n) if self.dtype == lh.Q4_K else synth.q8_0_weight(self.seed, k, n)
+        copies = max(2, -(-POOL_BYTES // raw.nbytes))
+        self.pool = []
+        for _ in range(copies):
+            b = lh.GpuBuffer(ctx, raw.nbytes)
+            b.upload(raw)
+            self.pool.append(b)
+        self.pool_bytes = copies * raw.nbytes
+        x = synth.normal(self.seed + 0x100, m * k)
+        if self.x_dtype == lh.BF16:
+            u = x.view(np.uint32).astype(np.uint64)
+            x = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        self.x = lh.upload_bytes(ctx, x.view(np.uint8))
+        self.c = lh.GpuBuffer(ctx, 4 * m * n)
+
+    def step(self, ctx, i):
+        w = self.pool[i % len(self.pool)]
+        lh.dispatch_proj_quant_batch(ctx, self.x, self.x_dtype, w, self.c, self.k, self.n, self.m, self.dtype)
+
+
+WORKLOADS = {
+    "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003),
+    "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001),
+    "q4k_down_silu": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, fused=True),
+    "q4k_m16_bf16": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008),
+    "q4k_m16_f32": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008),
+    "q8_0_m16_f32": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009),
+}
+
+
+def time_workload(ctx, ev, wl, steps, warmup):
+    wl.setup(ctx)
+    for i in range(warmup):
+        wl.step(ctx, i)
+    ctx.sync()
+    a, b = ev.new(), ev.new()
+    t0 = time.perf_counter()
+    ev.record(a, ctx.stream)
+    for i in range(steps):
+        wl.step(ctx, warmup + i)
+    ev.record(b, ctx.stream)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ms = ev.elapsed_ms(a, b)
+    us = 1000.0 * ms / steps
+    gbs = wl.bytes_per_call / (us * 1e-6) / 1e9
+    for p in wl.pool:
+        p.free()
+    wl.pool = []
+    return {"workload": wl.name, "us_per_call": round(us, 3), "GBps": round(gbs, 1),
+            "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_call": wl.bytes_per_call,
+            "pool_MB": round(wl.pool_bytes / 2 ** 20, 1), "host_wall_s": round(wall, 4)}
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle's proj_q4k.comp-order matvec on host threads, over a bounded
+    sample of output rows of the same 4096 -> 14336 Q4_K workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+
+    k, n = 4096, 14336
+    threads = max(1, min(16, os.cpu_count() or 1))
+    raw = synth.q4k_weight(0x5EED0003, k, n)
+    x = synth.normal(0x5EED0004, k)
+    rows_done, t_used = 0, 0.0
+    chunk = 256 * threads
+    while t_used < budget_s and rows_done < n:
+        r = min(chunk, n - rows_done)
+        sub = raw[rows_done * (k // 256) * 144:(rows_done + r) * (k // 256) * 144]
+        t0 = time.perf_counter()
+        orc.proj_q4k(x, sub, k, r, threads=threads)
+        t_used += time.perf_counter() - t0
+        rows_done += r
+    bytes_per_row = (k // 256) * 144 + 4
+    gbs = (rows_done * bytes_per_row + 4 * k) / t_used / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{rows_done} of {n} output rows of Q4_K 4096->14336 M=1 "
+                      f"(oracle restatement of kernels/proj_q4k.comp, f32 per-element decode), "
+                      f"{t_used:.1f} s on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="q4k_m1", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the projection path would shard by output rows; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = lh.VulkanContext(0)
+    ev = HipEvents()
+    head = time_workload(ctx, ev, WORKLOADS[args.workload](), args.steps, args.warmup)
+    extra = {}
+    if not args.no_extra:
+        for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32"]:
+            if name != args.workload:
+                extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(50, args.steps // 4), 20)
+    line = {
+        "metric": METRIC,
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] / 1000.0, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded SplitMix64: random valid Q4_K blocks, ggml-quantized Q8_0, N(0,1) activations)",
+        "config": {"workload": head["workload"], "k": 4096, "n": 14336, "m": 1, "weight_pool_MB": head["pool_MB"],
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": None,
+                     "us_per_call": head["us_per_call"], "algorithmic_bytes": head["bytes_per_call"]},
+        "extra": extra,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

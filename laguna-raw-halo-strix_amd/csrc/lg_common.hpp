@@ -1,0 +1,106 @@
+// Shared host/device helpers of the gfx950 projection library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "laguna_hip.h"
+
+namespace lg {
+
+// ---- error state (thread-local text, status codes; nothing crosses the ABI as an exception)
+int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Extent check: if p lies inside an allocation made by lg_buf_alloc, the
+// range [p, p+bytes) must lie inside it too.  Unknown pointers pass.
+bool extent_ok(const void *p, uint64_t bytes);
+bool blocking();
+
+#define LG_HIP_TRY(expr)                                                                  \
+    do {                                                                                  \
+        hipError_t e_ = (expr);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return ::lg::fail(LG_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));     \
+    } while (0)
+
+// Check a launch and honour blocking mode.
+int after_launch(const char *what, hipStream_t s);
+
+#define LG_REQUIRE(cond, ...)                                                             \
+    do {                                                                                  \
+        if (!(cond)) return ::lg::fail(LG_EINVAL, __VA_ARGS__);                           \
+    } while (0)
+
+#define LG_EXTENT(ptr, bytes, name)                                                       \
+    LG_REQUIRE(::lg::extent_ok((ptr), (bytes)),                                           \
+               "%s: %llu bytes at %p run past the end of its lg_buf_alloc allocation",     \
+               name, (unsigned long long)(bytes), (const void *)(ptr))
+
+// ---- GGUF block geometry (src/gguf.rs:97,101,134,136)
+constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;
+constexpr uint32_t QK8_0 = 32, Q80_BYTES = 34;
+
+inline uint64_t tensor_bytes(int dtype, uint64_t elems) {
+    switch (dtype) {
+    case LG_Q4_K: return (elems + QK_K - 1) / QK_K * Q4K_BYTES;
+    case LG_Q8_0: return (elems + QK8_0 - 1) / QK8_0 * Q80_BYTES;
+    case LG_F32: return elems * 4;
+    case LG_F16:
+    case LG_BF16: return elems * 2;
+    default: return 0;
+    }
+}
+
+}  // namespace lg
+
+// ---- device helpers ------------------------------------------------------------------
+
+// The reference's binary16 decoder (src/dflash.rs:314-329, kernels/proj_q4k.comp:28-44):
+// IEEE for normals, zeros, inf and NaN (payload kept), but exponent-0 codes with a
+// non-zero mantissa decode as 2^-14 * (1 + m/1024) instead of 2^-24 * m.
+// Written as one add on the shifted code: bias = 112, 113 (quirk) or 224 (inf/NaN).
+__device__ __forceinline__ float ref_half(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 31u;
+    const uint32_t t = (h & 0x7FFFu) << 13;
+    uint32_t bias = 112u << 23;
+    if (e == 0u) bias = (h & 0x3FFu) ? (113u << 23) : 0u;
+    if (e == 31u) bias = 224u << 23;
+    return __uint_as_float((t + bias) | sign);
+}
+
+// ggml get_scale_min_k4 (kernels/proj_q4k.comp:46-58) on the 12 scale bytes held in
+// three little-endian dwords s0 = bytes 0-3, s1 = bytes 4-7, s2 = bytes 8-11.
+__device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t &sc, uint32_t &mn) {
+    if (j < 4u) {
+        sc = (s0 >> (8u * j)) & 63u;
+        mn = (s1 >> (8u * j)) & 63u;
+    } else {
+        const uint32_t sh = 8u * (j - 4u);
+        const uint32_t bp = (s2 >> sh) & 0xFFu;
+        sc = (bp & 15u) | (((s0 >> sh) >> 6 & 3u) << 4);
+        mn = (bp >> 4) | (((s1 >> sh) >> 6 & 3u) << 4);
+    }
+}
+
+// Byte I of u as float (selected into v_cvt_f32_ubyteI).
+template <int I>
+__device__ __forceinline__ float ubyte_f(uint32_t u) { return (float)((u >> (8 * I)) & 0xFFu); }
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+// Lanes 0-15 of each row combine with DPP (xor 1, xor 2 via quad_perm, then
+// row_ror 4 and 8), the four rows with two cross-row swizzles.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)); // row_ror 4
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)); // row_ror 8
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}

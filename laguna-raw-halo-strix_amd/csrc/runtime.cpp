@@ -1,0 +1,165 @@
+// Runtime half of the C ABI: errors, devices, buffers, streams.
+// Replaces the reference's VulkanContext / GpuBuffer (src/vulkan.rs:16-452):
+// device-local HBM instead of host-visible coherent memory, explicit frees,
+// asynchronous streams instead of one fence wait per dispatch.
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "lg_common.hpp"
+
+namespace lg {
+
+static thread_local std::string g_err;
+static bool g_blocking = false;
+
+int fail(int status, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return status;
+}
+
+void clear_error() { g_err.clear(); }
+
+// Registry of live lg_buf_alloc allocations: base -> size.
+static std::mutex g_mu;
+static std::map<uintptr_t, uint64_t> g_allocs;
+
+bool extent_ok(const void *p, uint64_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_allocs.upper_bound(a);
+    if (it == g_allocs.begin()) return true;  // below every known allocation
+    --it;
+    const uintptr_t base = it->first;
+    const uint64_t size = it->second;
+    if (a >= base + size) return true;  // not inside a known allocation
+    return (a - base) + bytes <= size;
+}
+
+bool blocking() { return g_blocking; }
+
+int after_launch(const char *what, hipStream_t s) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(LG_EHIP, "%s launch failed: %s", what, hipGetErrorString(e));
+    if (g_blocking) {
+        e = hipStreamSynchronize(s);
+        if (e != hipSuccess) return fail(LG_EHIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    return LG_OK;
+}
+
+}  // namespace lg
+
+using namespace lg;
+
+extern "C" {
+
+const char *lg_last_error(void) { return g_err.c_str(); }
+
+const char *lg_version(void) { return "laguna-hip 0.1 (gfx950)"; }
+
+int lg_device_count(int *count) {
+    LG_REQUIRE(count, "lg_device_count: null count");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    (void)hipGetLastError();
+    *count = n;
+    return LG_OK;
+}
+
+int lg_init(int device) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+        (void)hipGetLastError();
+        return fail(LG_ENODEV, "lg_init: no HIP device");
+    }
+    LG_REQUIRE(device >= 0 && device < n, "lg_init: device %d out of range (%d devices)", device, n);
+    LG_HIP_TRY(hipSetDevice(device));
+    LG_HIP_TRY(hipFree(nullptr));  // create the context now, not inside the first timed call
+    clear_error();
+    return LG_OK;
+}
+
+int lg_set_blocking(int b) {
+    g_blocking = b != 0;
+    return LG_OK;
+}
+
+int lg_buf_alloc(void **dptr, uint64_t bytes) {
+    LG_REQUIRE(dptr, "lg_buf_alloc: null dptr");
+    LG_REQUIRE(bytes > 0, "lg_buf_alloc: zero bytes");
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(LG_ENOMEM, "lg_buf_alloc(%llu): %s", (unsigned long long)bytes, hipGetErrorString(e));
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_allocs[reinterpret_cast<uintptr_t>(p)] = bytes;
+    }
+    *dptr = p;
+    return LG_OK;
+}
+
+int lg_buf_free(void *dptr) {
+    if (!dptr) return LG_OK;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_allocs.erase(reinterpret_cast<uintptr_t>(dptr));
+    }
+    LG_HIP_TRY(hipFree(dptr));
+    return LG_OK;
+}
+
+int lg_buf_upload(void *dst, const void *src, uint64_t bytes, void *stream) {
+    if (bytes == 0) return LG_OK;
+    LG_REQUIRE(dst && src, "lg_buf_upload: null pointer");
+    LG_EXTENT(dst, bytes, "lg_buf_upload dst");
+    LG_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    LG_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return LG_OK;
+}
+
+int lg_buf_download(void *dst, const void *src, uint64_t bytes, void *stream) {
+    if (bytes == 0) return LG_OK;
+    LG_REQUIRE(dst && src, "lg_buf_download: null pointer");
+    LG_EXTENT(src, bytes, "lg_buf_download src");
+    LG_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    LG_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return LG_OK;
+}
+
+int lg_buf_memset(void *dst, int value, uint64_t bytes, void *stream) {
+    if (bytes == 0) return LG_OK;
+    LG_REQUIRE(dst, "lg_buf_memset: null pointer");
+    LG_EXTENT(dst, bytes, "lg_buf_memset dst");
+    LG_HIP_TRY(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+    return after_launch("lg_buf_memset", (hipStream_t)stream);
+}
+
+int lg_stream_create(void **stream) {
+    LG_REQUIRE(stream, "lg_stream_create: null");
+    hipStream_t s = nullptr;
+    LG_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return LG_OK;
+}
+
+int lg_stream_destroy(void *stream) {
+    if (!stream) return LG_OK;
+    LG_HIP_TRY(hipStreamDestroy((hipStream_t)stream));
+    return LG_OK;
+}
+
+int lg_sync(void *stream) {
+    LG_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    return LG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+"""Seeded synthetic inputs for the quantized-projection workloads.
+
+Everything is derived from SplitMix64 streams so a workload is fully named by
+its seed and shape:
+
+* uniform doubles: the top 53 bits of each SplitMix64 output;
+* normals: Box-Muller on pairs of uniforms, in float64, rounded to float32;
+* Q8_0 weights: float32 N(0, sigma) quantized by the ggml Q8_0 rule (32-element
+  blocks, d = max|x|/127 stored as IEEE f16 with round-to-nearest-even,
+  q = roundf(x * (1/d)) with the float32 1/d taken before d is stored);
+* Q4_K weights: random valid super-blocks of 144 bytes, d and dmin =
+  f16(U[1e-4, 4e-3]), 12 uniform random scale/min bytes (every byte pattern
+  decodes to 6-bit scales and mins in [0, 63]) and 128 uniform random bytes of
+  4-bit quants.
+
+Byte layouts are GGUF's (src/gguf.rs:97,101): Q8_0 block = f16 d + 32 int8,
+Q4_K super-block = f16 d, f16 dmin, 12 scale bytes, 128 quant bytes.
+"""
+import numpy as np
+
+GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+QK8_0, Q8_0_BYTES = 32, 34
+QK_K, Q4_K_BYTES = 256, 144
+
+
+def splitmix64(seed, count):
+    """count consecutive SplitMix64 outputs for the given seed (vectorised)."""
+    with np.errstate(over="ignore"):
+        s = np.uint64(seed) + GOLDEN * np.arange(1, count + 1, dtype=np.uint64)
+        z = s
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def uniform(seed, count):
+    """Doubles in [0, 1)."""
+    return (splitmix64(seed, count) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+def normal(seed, count, sigma=1.0):
+    """float32 N(0, sigma^2) via Box-Muller in float64."""
+    pairs = (count + 1) // 2
+    u = uniform(seed, 2 * pairs)
+    u1 = 1.0 - u[0::2]  # (0, 1]: log is finite
+    u2 = u[1::2]
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.empty(2 * pairs, np.float64)
+    z[0::2] = r * np.cos(2.0 * np.pi * u2)
+    z[1::2] = r * np.sin(2.0 * np.pi * u2)
+    return (z[:count] * sigma).astype(np.float32)
+
+
+def random_bytes(seed, count):
+    words = splitmix64(seed, (count + 7) // 8)
+    return words.view(np.uint8)[:count].copy()
+
+
+def _roundf(v):
+    """C roundf: halves away from zero (numpy's round is half-to-even)."""
+    return np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))
+
+
+def quantize_q8_0(x):
+    """ggml Q8_0 of a float32 tensor whose size is a multiple of 32 -> raw bytes."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, QK8_0)
+    amax = np.max(np.abs(x), axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    q = _roundf((x * idv[:, None]).astype(np.float32))
+    q = np.clip(q, -127, 127).astype(np.int8)
+    out = np.empty((x.shape[0], Q8_0_BYTES), np.uint8)
+    out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q.view(np.uint8)
+    return out.ravel()
+
+
+def random_q4k(seed, n_blocks, dlo=1e-4, dhi=4e-3):
+    """n_blocks random valid Q4_K super-blocks -> raw bytes (144 per block)."""
+    out = random_bytes(seed, n_blocks * Q4_K_BYTES).reshape(n_blocks, Q4_K_BYTES)
+    u = uniform(seed ^ 0xD1B54A32D192ED03, 2 * n_blocks).reshape(n_blocks, 2)
+    dd = (dlo + (dhi - dlo) * u).astype(np.float16)
+    out[:, 0:4] = dd.view(np.uint8).reshape(n_blocks, 4)
+    return out.ravel()
+
+
+def q8_0_weight(seed, k, n, sigma=0.02):
+    """[n rows][k] weight, GGUF layout (k contiguous per output row), as Q8_0 bytes."""
+    return quantize_q8_0(normal(seed, k * n, sigma))
+
+
+def q4k_weight(seed, k, n):
+    assert (k * n) % QK_K == 0
+    return random_q4k(seed, k * n // QK_K)
+
+
+def weight_bytes(dtype, k, n):
+    from laguna_hip import Q4_K, Q8_0, F32
+    if dtype == Q4_K:
+        return k * n // QK_K * Q4_K_BYTES
+    if dtype == Q8_0:
+        return k * n // QK8_0 * Q8_0_BYTES
+    if dtype == F32:
+        return k * n * 4
+    raise ValueError(dtype)

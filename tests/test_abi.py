@@ -1,0 +1,101 @@
+"""CPU checks of the C ABI: the library loads, exports every function that
+include/laguna_hip.h declares, and rejects bad arguments with status codes
+(no exception or abort crosses the ABI).  No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import laguna_hip as lh
+import synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "laguna_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    declared = header_functions()
+    assert declared, "no declarations found"
+    assert set(declared) == set(lh.SIGNATURES), set(declared) ^ set(lh.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = lh.lib()
+    for name in header_functions():
+        assert hasattr(L, name), name
+
+
+def test_version_and_device_count_without_gpu():
+    assert b"gfx950" in lh.lib().lg_version()
+    assert lh.device_count() >= 0
+
+
+def _status(fn, *args):
+    return getattr(lh.lib(), fn)(*args)
+
+
+def test_null_pointers_are_einval():
+    assert _status("lg_dispatch_proj_quant", None, None, None, 256, 4, lh.Q4_K, None) == lh.EINVAL
+    assert b"null" in lh.lib().lg_last_error()
+    assert _status("lg_dispatch_proj_quant_batch", None, lh.F32, None, None, 256, 4, 2, lh.Q4_K, None) == lh.EINVAL
+    assert _status("lg_dispatch_activation", None, None, None, 4, None) == lh.EINVAL
+    assert _status("lg_dequant_to_f32", None, 0, lh.Q8_0, 32, None, None) == lh.EINVAL
+
+
+def test_bad_dtypes_are_einval():
+    x = np.zeros(256, np.float32)
+    c = np.zeros(4, np.float32)
+    # host pointers are fine for argument validation: the call fails before any launch
+    assert _status("lg_dispatch_proj_quant", x.ctypes.data, x.ctypes.data, c.ctypes.data, 256, 4, 13, None) == lh.EINVAL
+    assert _status("lg_dispatch_proj_quant_batch", x.ctypes.data, lh.Q8_0, x.ctypes.data, c.ctypes.data, 256, 4, 1,
+                   lh.Q4_K, None) == lh.EINVAL
+    assert _status("lg_dispatch_proj_quant_batch", x.ctypes.data, lh.F32, x.ctypes.data, c.ctypes.data, 256, 4, 65,
+                   lh.Q4_K, None) == lh.EINVAL
+
+
+def test_zero_rows_is_a_no_op():
+    # the reference dispatches ceil(0/256) = 0 workgroups
+    assert _status("lg_dispatch_proj_quant", None, None, None, 256, 0, lh.Q4_K, None) == lh.OK
+    assert _status("lg_dispatch_proj_quant_batch", None, lh.F32, None, None, 256, 0, 4, lh.Q4_K, None) == lh.OK
+
+
+def test_buffer_calls_without_device_fail_cleanly():
+    if lh.device_count() > 0:
+        pytest.skip("host has a GPU")
+    p = ctypes.c_void_p()
+    st = lh.lib().lg_buf_alloc(ctypes.byref(p), 1024)
+    assert st in (lh.ENOMEM, lh.EHIP, lh.ENODEV)
+    assert lh.lib().lg_init(0) == lh.ENODEV
+
+
+def test_synth_q8_0_quantizer_rule():
+    x = synth.normal(1, 32 * 64, 0.02)
+    raw = synth.quantize_q8_0(x).reshape(-1, 34)
+    d = raw[:, 0:2].copy().view(np.float16)[:, 0].astype(np.float32)
+    q = raw[:, 2:].view(np.int8).astype(np.float32)
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    assert np.array_equal(d, (amax / np.float32(127)).astype(np.float16).astype(np.float32))
+    assert np.abs(q).max() <= 127 and np.abs(q).max(axis=1).min() == 127  # the max element maps to +-127
+    # reconstruction error bounded by half a step of the unrounded scale
+    assert np.all(np.abs(q * d[:, None] - xb) <= 0.5 * d[:, None] * 1.01 + 1e-3 * amax[:, None])
+
+
+def test_synth_q4k_blocks():
+    raw = synth.random_q4k(5, 1000).reshape(-1, 144)
+    d = raw[:, 0:4].copy().view(np.float16).astype(np.float32)
+    assert np.all((d >= 9.99e-5) & (d <= 4.01e-3))
+    assert np.array_equal(synth.random_q4k(5, 1000), synth.random_q4k(5, 1000).copy())
+    assert not np.array_equal(synth.random_q4k(5, 10), synth.random_q4k(6, 10))
+
+
+def test_synth_normal_moments():
+    z = synth.normal(0x5EED0002, 1 << 18).astype(np.float64)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01

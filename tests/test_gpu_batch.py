@@ -1,0 +1,100 @@
+"""GPU: small-M (block verify) products against the oracle's f64 accumulation."""
+import numpy as np
+import pytest
+
+import laguna_hip as lh
+import oracle as orc
+import synth
+from conftest import parity
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def bf16_bits(x):
+    """Round float32 to bf16 (nearest-even) and return the raw 16-bit codes."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def run_batch(ctx, x, x_dtype, raw, w_dtype, k, n, m):
+    xb = lh.upload_bytes(ctx, np.ascontiguousarray(x).view(np.uint8).ravel())
+    wb = lh.upload_bytes(ctx, np.ascontiguousarray(raw).view(np.uint8).ravel())
+    cb = lh.GpuBuffer(ctx, 4 * m * n)
+    lh.dispatch_proj_quant_batch(ctx, xb, x_dtype, wb, cb, k, n, m, w_dtype)
+    return cb.read_f32(m * n).reshape(m, n)
+
+
+@pytest.mark.parametrize("w_dtype,k,n,x_dtype,seed", [
+    (lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008),
+    (lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008),
+    (lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009),
+    (lh.Q8_0, 4096, 4096, lh.BF16, 0x5EED0009),
+])
+def test_block_verify_configs(ctx, w_dtype, k, n, x_dtype, seed):
+    m = 16
+    print(f"batch m=16 w={w_dtype} x={x_dtype} k={k} n={n} seed={seed:#x}", flush=True)
+    raw = synth.q4k_weight(seed, k, n) if w_dtype == lh.Q4_K else synth.q8_0_weight(seed, k, n)
+    x32 = synth.normal(seed + 0x100, m * k).reshape(m, k)
+    if x_dtype == lh.BF16:
+        xin = bf16_bits(x32)
+        xref = (xin.astype(np.uint32) << 16).view(np.float32)
+    else:
+        xin, xref = x32, x32
+    c = run_batch(ctx, xin, x_dtype, raw, w_dtype, k, n, m)
+    y64, a = orc.proj_quant_f64(xref, raw, w_dtype, k, n)
+    parity(c, y64, a, TOL)
+
+
+@pytest.mark.parametrize("m", [1, 2, 5, 15, 16, 17, 31, 33, 48, 64])
+@pytest.mark.parametrize("w_dtype", [lh.Q4_K, lh.Q8_0])
+def test_token_counts(ctx, m, w_dtype):
+    k, n = 1024, 100
+    print(f"batch m={m} w={w_dtype}", flush=True)
+    raw = synth.q4k_weight(200 + m, k, n) if w_dtype == lh.Q4_K else synth.q8_0_weight(200 + m, k, n)
+    x = synth.normal(300 + m, m * k).reshape(m, k)
+    c = run_batch(ctx, x, lh.F32, raw, w_dtype, k, n, m)
+    y64, a = orc.proj_quant_f64(x, raw, w_dtype, k, n)
+    parity(c, y64, a, TOL)
+
+
+def test_m1_matches_matvec(ctx):
+    k, n = 4096, 512
+    raw = synth.q4k_weight(400, k, n)
+    x = synth.normal(401, k)
+    print("batch m=1 vs matvec", flush=True)
+    c = run_batch(ctx, x[None, :], lh.F32, raw, lh.Q4_K, k, n, 1)[0]
+    xb, wb, cb = lh.upload_f32(ctx, x), lh.upload_bytes(ctx, raw), lh.GpuBuffer(ctx, 4 * n)
+    lh.dispatch_proj_quant(ctx, xb, wb, cb, k, n, lh.Q4_K)
+    y = cb.read_f32(n)
+    y64, a = orc.proj_quant_f64(x, raw, orc.Q4_K, k, n)
+    parity(c, y64, a, TOL)
+    parity(y, y64, a, TOL)
+
+
+@pytest.mark.parametrize("w_dtype,k,n,m", [(lh.F32, 512, 40, 7), (lh.Q4_K, 96, 8, 3), (lh.Q8_0, 4128, 9, 20)])
+def test_generic_path(ctx, w_dtype, k, n, m):
+    print(f"batch generic w={w_dtype} k={k} n={n} m={m}", flush=True)
+    if w_dtype == lh.F32:
+        raw = synth.normal(500, k * n, 0.02)
+    elif w_dtype == lh.Q4_K:
+        raw = synth.random_q4k(501, -(-(k * n) // 256))
+    else:
+        raw = synth.q8_0_weight(502, 32, -(-(k * n) // 32))
+    x = synth.normal(503, m * k).reshape(m, k)
+    c = run_batch(ctx, x, lh.F32, raw, w_dtype, k, n, m)
+    y64, a = orc.proj_quant_f64(x, raw, w_dtype, k, n)
+    parity(c, y64, a, TOL)
+
+
+def test_workspace_reuse_across_shapes(ctx):
+    # the activation workspace grows and is reused: results must not depend on history
+    k, n = 2048, 64
+    raw = synth.q4k_weight(600, k, n)
+    x = synth.normal(601, 40 * k).reshape(40, k)
+    print("batch workspace reuse", flush=True)
+    big = run_batch(ctx, x, lh.F32, raw, lh.Q4_K, k, n, 40)
+    small = run_batch(ctx, x[:3], lh.F32, raw, lh.Q4_K, k, n, 3)
+    assert np.array_equal(big[:3], small)
