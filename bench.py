@@ -171,8 +171,10 @@ def time_workload(ctx, ev, wl, steps, warmup):
 
 
 def cpu_baseline(budget_s=12.0):
-    """The oracle's proj_q4k.comp-order matvec on host threads, over a bounded
-    sample of output rows of the same 4096 -> 14336 Q4_K workload."""
+    """The oracle's proj_q4k.comp-order matvec (per-element decode, f32 accumulation)
+    on the host cores, on the same 4096 -> 14336 Q4_K workload: the whole matvec
+    repeated on `threads` OpenMP threads for about budget_s/2 seconds, and a
+    bounded sample of output rows on one thread for the other half."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
 
@@ -180,21 +182,63 @@ def cpu_baseline(budget_s=12.0):
     threads = max(1, min(16, os.cpu_count() or 1))
     raw = synth.q4k_weight(0x5EED0003, k, n)
     x = synth.normal(0x5EED0004, k)
-    rows_done, t_used = 0, 0.0
-    chunk = 256 * threads
-    while t_used < budget_s and rows_done < n:
-        r = min(chunk, n - rows_done)
-        sub = raw[rows_done * (k // 256) * 144:(rows_done + r) * (k // 256) * 144]
-        t0 = time.perf_counter()
-        orc.proj_q4k(x, sub, k, r, threads=threads)
-        t_used += time.perf_counter() - t0
-        rows_done += r
     bytes_per_row = (k // 256) * 144 + 4
-    gbs = (rows_done * bytes_per_row + 4 * k) / t_used / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{rows_done} of {n} output rows of Q4_K 4096->14336 M=1 "
-                      f"(oracle restatement of kernels/proj_q4k.comp, f32 per-element decode), "
-                      f"{t_used:.1f} s on {threads} threads"}
+    # multi-threaded: whole matvecs
+    reps, t_mt = 0, 0.0
+    while t_mt < budget_s / 2 or reps < 2:
+        t0 = time.perf_counter()
+        orc.proj_q4k(x, raw, k, n, threads=threads)
+        t_mt += time.perf_counter() - t0
+        reps += 1
+    gbs_mt = reps * (n * bytes_per_row + 4 * k) / t_mt / 1e9
+    # single thread: consecutive 512-row blocks (wrapping) until the budget is spent
+    rows, t_st = 0, 0.0
+    while t_st < budget_s / 2:
+        r0 = rows % n
+        r = min(512, n - r0)
+        sub = raw[r0 * (k // 256) * 144:(r0 + r) * (k // 256) * 144]
+        t0 = time.perf_counter()
+        orc.proj_q4k(x, sub, k, r, threads=1)
+        t_st += time.perf_counter() - t0
+        rows += r
+    gbs_st = (rows * bytes_per_row + 4 * k) / t_st / 1e9
+    return {"value": round(gbs_mt, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "single_thread_GBps": round(gbs_st, 4),
+            "sample": f"oracle restatement of kernels/proj_q4k.comp (f32 per-element decode) on Q4_K "
+                      f"4096->14336 M=1: {reps} full matvecs on {threads} threads in {t_mt:.1f} s; "
+                      f"single thread {rows} rows in {t_st:.1f} s"}
+
+
+CAL_BYTES = 64 << 20  # lg_buf_copy size that hardware traffic counters are calibrated against
+
+
+def traffic_from_profile(workload):
+    """HBM bytes per launch of the workload's kernel, from the committed summary of
+    two rocprofv3 --pmc runs of `bench.py --pmc` (FETCH_SIZE, then WRITE_SIZE, each
+    scaled by what the counter reads for lg_buf_copy of CAL_BYTES); None if absent."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def pmc_run(ctx, wl, steps):
+    """For counter collection: three lg_buf_copy calls of CAL_BYTES (the calibration
+    kernel) followed by `steps` calls of the workload, each on its own weight copy."""
+    a, b = lh.GpuBuffer(ctx, CAL_BYTES), lh.GpuBuffer(ctx, CAL_BYTES)
+    for _ in range(3):
+        b.copy_from(a, CAL_BYTES)
+    ctx.sync()
+    a.free()
+    b.free()
+    wl.setup(ctx)
+    for i in range(steps):
+        wl.step(ctx, i)
+    ctx.sync()
+    print(json.dumps({"pmc_run": wl.name, "steps": steps, "calibration_copy_bytes": CAL_BYTES}), flush=True)
 
 
 def main():
@@ -205,6 +249,8 @@ def main():
     ap.add_argument("--workload", default="q4k_m1", choices=sorted(WORKLOADS))
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--pmc", action="store_true",
+                    help="counter-collection mode: calibration copies, then --steps calls of --workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -212,8 +258,12 @@ def main():
         sys.exit(2)
 
     ctx = lh.VulkanContext(0)
+    if args.pmc:
+        pmc_run(ctx, WORKLOADS[args.workload](), args.steps)
+        return
     ev = HipEvents()
-    head = time_workload(ctx, ev, WORKLOADS[args.workload](), args.steps, args.warmup)
+    wl = WORKLOADS[args.workload]()
+    head = time_workload(ctx, ev, wl, args.steps, args.warmup)
     extra = {}
     if not args.no_extra:
         for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32"]:
@@ -232,10 +282,10 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded SplitMix64: random valid Q4_K blocks, ggml-quantized Q8_0, N(0,1) activations)",
-        "config": {"workload": head["workload"], "k": 4096, "n": 14336, "m": 1, "weight_pool_MB": head["pool_MB"],
-                   "parallelism": "single GPU"},
+        "config": {"workload": head["workload"], "k": wl.k, "n": wl.n, "m": getattr(wl, "m", 1),
+                   "weight_pool_MB": head["pool_MB"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": None,
+                     "frac": head["frac_of_peak"], "traffic": traffic_from_profile(args.workload),
                      "us_per_call": head["us_per_call"], "algorithmic_bytes": head["bytes_per_call"]},
         "extra": extra,
     }

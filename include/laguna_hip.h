@@ -78,6 +78,9 @@ int lg_buf_free(void *dptr);
 int lg_buf_upload(void *dst, const void *src, uint64_t bytes, void *stream);
 int lg_buf_download(void *dst, const void *src, uint64_t bytes, void *stream);
 int lg_buf_memset(void *dst, int value, uint64_t bytes, void *stream);
+/* Device-to-device copy (no counterpart in the reference, whose buffers are
+ * host-visible and copied through the host); asynchronous on `stream`. */
+int lg_buf_copy(void *dst, const void *src, uint64_t bytes, void *stream);
 int lg_stream_create(void **stream);
 int lg_stream_destroy(void *stream);
 int lg_sync(void *stream);

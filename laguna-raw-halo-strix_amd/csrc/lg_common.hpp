@@ -88,6 +88,13 @@ __device__ __forceinline__ void scale_min_k4(uint32_t j, uint32_t s0, uint32_t s
     }
 }
 
+// 16-byte load with the nontemporal (streaming) hint, for data read exactly once.
+typedef uint32_t lg_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream16(const void *p) {
+    const lg_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const lg_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Byte I of u as float (selected into v_cvt_f32_ubyteI).
 template <int I>
 __device__ __forceinline__ float ubyte_f(uint32_t u) { return (float)((u >> (8 * I)) & 0xFFu); }

@@ -2,30 +2,42 @@
 //
 // Replaces kernels/proj_q4k.comp, proj_q8_0.comp, proj.comp and activation.comp
 // (one invocation per output row, per-element byte decode, uncoalesced) with
-// wavefront-cooperative gfx950 kernels:
+// wavefront-cooperative gfx950 kernels.
 //
-// Q4_K (k % 256 == 0, 16-byte aligned tensor): lane p of a row team owns the
-// 64-element group p of the row (super-block p/4, group p%4).  Per row it loads
-// the 16-byte block header and the 32 quant bytes of its group with three
-// 16-byte loads; the team's loads together cover the row's bytes exactly once.
-// The lane keeps its 64 activations in registers for every row it visits.
-// Nibbles are turned into f16 values 1 + q/16 with one shift and one and-or per
-// pair and accumulated with v_fma_mix_f32 against the f32 activations:
-//     S = sum x (1 + q/16)  =>  sum x q = 16 (S - X),  X = sum x (per lane, once)
-// and the block's scale and min enter once per 32-element sub-block:
-//     sum_j x_j ((d sc) q_j - dmin m) = 16 d sc (S - X) - dmin m X.
-// Partial sums meet in a DPP/swizzle wavefront reduction (and LDS across the
-// waves of a team when k > 4096).
+// Work split.  A "team" of TW = ceil(k/4096) waves covers one row: lane p of the
+// team owns the 64-element group p of the row (k/64 groups) and keeps the 64
+// activations of that group in registers; the team's partial sums meet in a
+// DPP/swizzle wavefront reduction (plus LDS across the TW waves).  A workgroup
+// holds TEAMS teams (8 waves) and normally there is one workgroup per CU: each
+// team owns a contiguous block of RPW rows (RPW <= 8, chosen so that the grid
+// covers the CUs once), and issues the loads of all RPW rows before anything else.
+// A matvec of this size is over in a few microseconds, so the whole share of a CU
+// (about 130 KB for Q4_K 4096 -> 14336) is in flight at once and each row is
+// computed as its bytes arrive.  The activations are read once per workgroup:
+// their global loads go out first, the row loads next, and only then is the
+// vector staged through LDS into registers.
 //
-// Q8_0: the same lane ownership (64 elements = two 34-byte blocks, 68 bytes,
-// dword aligned).  Rows are staged through LDS with coalesced 16-byte loads and
-// each lane reads its 17 dwords back (stride 17 dwords: no bank conflicts).
-// Bytes are biased to unsigned (q + 128), converted with v_cvt_f32_ubyte and
-// corrected by 128 X per block.
+// Q4_K (k % 256 == 0, 16-byte aligned tensor): per row the lane loads the 16-byte
+// super-block header and the 32 quant bytes of its group with three 16-byte loads;
+// the team's loads cover the row's bytes exactly once.  A nibble masked in place
+// is an f16 subnormal (q * 2^-24, or q * 2^-20 for a high nibble), so one AND gives
+// two operands of v_fma_mix_f32 against the f32 activations, and the block's scale
+// and min enter once per 32-element sub-block:
+//     sum_j x_j ((d sc) q_j - dmin m) = d sc 2^24 S - dmin m X,
+//     S = sum x q 2^-24,  X = sum x (per lane, once).
+//
+// Q8_0: the same lane ownership (64 elements = two 34-byte blocks, 68 bytes, dword
+// aligned).  Each wave loads its 64-group share of a row with coalesced 16-byte
+// loads, writes it to its own LDS stage and each lane reads its 17 dwords back
+// (stride 17 dwords: no bank conflicts).  Bytes are biased to unsigned (q + 128),
+// converted with v_cvt_f32_ubyte and corrected by 128 X per block.
 //
 // Inputs outside these fast paths (k not a multiple of 256, unaligned pointers,
 // element offsets that are not block aligned) go to a per-element kernel that
 // follows the reference's linear addressing exactly (lin = offset + i*k + j).
+#include <map>
+#include <mutex>
+
 #include "lg_common.hpp"
 
 namespace {
@@ -35,93 +47,99 @@ using namespace lg;
 uint32_t g_grid_cap = 0;  // 0 = automatic
 
 constexpr uint32_t M1_MAX_K = 16384;  // 4 waves x 64 lanes x 64 elements
+constexpr int M1_RPW_MAX = 8;         // rows per team whose loads are in flight together
 
 // ------------------------------------------------------------------------------------------
-// activation staging
+// activations
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
     // kernels/activation.comp:21-28: silu(g) * up, silu(x) = x * (1 / (1 + exp(-x)))
     return g * (1.0f / (1.0f + __expf(-g))) * u;
 }
 
-// Load this lane's 64 activations (elements 64p .. 64p+63) into registers, either
-// straight from global memory or from an LDS copy of the whole vector (padded by
-// 4 floats per 64 so that 16-byte LDS reads by consecutive lanes spread over banks).
-template <int TEAMS, bool FUSE>
-__device__ __forceinline__ void load_x(const float *__restrict__ x, const float *__restrict__ up,
-                                       uint32_t k, uint32_t p, bool active, float *lds,
-                                       float (&xr)[64]) {
-    if constexpr (TEAMS > 1) {
-        const float4 *x4 = reinterpret_cast<const float4 *>(x);
-        const float4 *u4 = reinterpret_cast<const float4 *>(up);
-        for (uint32_t e4 = threadIdx.x; e4 < k / 4; e4 += blockDim.x) {
-            float4 v = x4[e4];
+// The workgroup's copy of the activations, in two halves so that the row loads
+// can be issued in between:
+//   x_fetch: this thread's float4s of x (and up) into registers;
+//   x_share: (with FUSE: silu(x) * up) into LDS, one barrier, and lane p of wave wt
+//            takes elements 64p .. 64p+63 of the team's k range into registers.
+// LDS rows are padded to 68 floats (64 + 4) so that the lanes' 16-byte reads
+// spread over the banks.  `xs` holds TW * 64 * 68 floats.
+template <int XPT, bool FUSE>
+struct XFetch {
+    float4 x[XPT];
+    float4 u[FUSE ? XPT : 1];
+};
+
+template <int XPT, bool FUSE>
+__device__ __forceinline__ void x_fetch(XFetch<XPT, FUSE> &f, const float *__restrict__ x,
+                                        const float *__restrict__ up, uint32_t k) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *u4 = reinterpret_cast<const float4 *>(up);
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const uint32_t e4 = threadIdx.x + i * blockDim.x;
+        if (e4 < k / 4) {
+            f.x[i] = x4[e4];
+            if constexpr (FUSE) f.u[i] = u4[e4];
+        }
+    }
+}
+
+template <int XPT, bool FUSE>
+__device__ __forceinline__ void x_share(const XFetch<XPT, FUSE> &f, uint32_t k, uint32_t wt, uint32_t lane,
+                                        float *xs, float (&xr)[64]) {
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const uint32_t e4 = threadIdx.x + i * blockDim.x;
+        if (e4 < k / 4) {
+            float4 v = f.x[i];
             if constexpr (FUSE) {
-                const float4 u = u4[e4];
+                const float4 u = f.u[i];
                 v = make_float4(silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w));
             }
             const uint32_t e = 4 * e4;
-            *reinterpret_cast<float4 *>(lds + e + 4 * (e >> 6)) = v;
-        }
-        __syncthreads();
-        if (active) {
-            const float4 *s4 = reinterpret_cast<const float4 *>(lds + 68 * p);
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float4 v = s4[i];
-                xr[4 * i] = v.x, xr[4 * i + 1] = v.y, xr[4 * i + 2] = v.z, xr[4 * i + 3] = v.w;
-            }
-        }
-    } else {
-        if (active) {
-            const float4 *x4 = reinterpret_cast<const float4 *>(x + 64 * p);
-            const float4 *u4 = reinterpret_cast<const float4 *>(up + 64 * p);
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float4 v = x4[i];
-                if constexpr (FUSE) {
-                    const float4 u = u4[i];
-                    v = make_float4(silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w));
-                }
-                xr[4 * i] = v.x, xr[4 * i + 1] = v.y, xr[4 * i + 2] = v.z, xr[4 * i + 3] = v.w;
-            }
+            *reinterpret_cast<float4 *>(xs + e + 4 * (e >> 6)) = v;
         }
     }
-    if (!active) {
+    __syncthreads();
+    const float4 *s4 = reinterpret_cast<const float4 *>(xs + 68 * (wt * 64 + lane));
 #pragma unroll
-        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
+    for (int i = 0; i < 16; i++) {
+        const float4 v = s4[i];
+        xr[4 * i] = v.x, xr[4 * i + 1] = v.y, xr[4 * i + 2] = v.z, xr[4 * i + 3] = v.w;
     }
 }
 
 __device__ __forceinline__ float h_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
 __device__ __forceinline__ float h_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 
-// Team-wide sum of R row partials: DPP/swizzle inside each wave, LDS across the TW
-// waves of a team.  The caller guarantees uniform control flow for the barriers.
-template <int TW, int R>
-__device__ __forceinline__ void team_store(float (&acc)[R], uint32_t row0, uint32_t n, float *__restrict__ y,
-                                           float *red, uint32_t lane, uint32_t wt) {
+// Team sums of the RPW row partials and their stores.  TW == 1: DPP/swizzle only.
+// TW > 1: every wave's wavefront sums go to LDS, one barrier, wave 0 of the team
+// adds the TW partials of each row.  Every wave of the workgroup calls this once.
+template <int TW, int TEAMS, int RPW>
+__device__ __forceinline__ void team_store(float (&acc)[RPW], uint32_t row0, uint32_t n, float *__restrict__ y,
+                                           float *red, uint32_t team, uint32_t lane, uint32_t wt) {
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < RPW; r++) acc[r] = wave_sum(acc[r]);
     if constexpr (TW == 1) {
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < R; r++)
+            for (int r = 0; r < RPW; r++)
                 if (row0 + r < n) y[row0 + r] = acc[r];
         }
     } else {
+        float *buf = red + team * (RPW * TW);
         if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < R; r++) red[r * TW + wt] = acc[r];
+            for (int r = 0; r < RPW; r++) buf[r * TW + wt] = acc[r];
         }
         __syncthreads();
-        if (wt == 0 && lane < (uint32_t)R && row0 + lane < n) {
+        if (wt == 0 && lane < (uint32_t)RPW && row0 + lane < n) {
             float s = 0.0f;
 #pragma unroll
-            for (int t = 0; t < TW; t++) s += red[lane * TW + t];
+            for (int t = 0; t < TW; t++) s += buf[lane * TW + t];
             y[row0 + lane] = s;
         }
-        __syncthreads();
     }
 }
 
@@ -129,7 +147,7 @@ __device__ __forceinline__ void team_store(float (&acc)[R], uint32_t row0, uint3
 // Q4_K
 
 struct Q4Lane {
-    uint32_t g;          // group within the super-block (0..3): sub-blocks 2g, 2g+1
+    uint32_t g;                           // group within the super-block (0..3): sub-blocks 2g, 2g+1
     uint32_t sa[2], sb[2], ma[2], mb[2];  // bit offsets of the 4 + 2 scale/min bits
 };
 
@@ -150,25 +168,26 @@ __device__ __forceinline__ Q4Lane q4_lane(uint32_t g) {
 
 // One lane's contribution to one row: 64 weights of super-block header `hd`
 // (d, dmin, scales) and quant bytes qa (bytes 0-15 of the group) and qb (16-31).
+// A nibble masked in place is read as an f16 subnormal: low nibbles as q * 2^-24,
+// high nibbles as 16 q * 2^-24 = q * 2^-20 (exact; v_fma_mix_f32 keeps f16
+// denormals), so one AND yields two operands and no bias has to be removed:
+//     S0 = sum x q 2^-24 (sub-block 2g),  S1 = sum x q 2^-20 (sub-block 2g+1)
+//     sum_j x_j ((d sc) q_j - dmin m) = d sc 2^24 S0 - dmin m X0   (and 2^20 S1, X1).
 __device__ __forceinline__ float q4_dot(const uint4 &hd, const uint4 &qa, const uint4 &qb, const float (&xr)[64],
                                         float X0, float X1, const Q4Lane &L) {
-    // Mask and bias live in VGPRs so that each pair is one shift + one v_and_or_b32
-    // (a GFX9 VOP3 instruction cannot encode two literal constants).
-    uint32_t M = 0x03C003C0u, C = 0x3C003C00u;
-    asm volatile("" : "+v"(M), "+v"(C));
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     float s0a = 0.f, s0b = 0.f, s1a = 0.f, s1b = 0.f;
 #pragma unroll
     for (int t = 0; t < 8; t++) {
-        const uint32_t v = q[t];
-        const uint32_t p02 = ((v << 6) & M) | C;  // low nibbles of bytes 4t, 4t+2  -> sub-block 2g
-        const uint32_t p13 = ((v >> 2) & M) | C;  // low nibbles of bytes 4t+1, 4t+3
-        const uint32_t h02 = ((v << 2) & M) | C;  // high nibbles of bytes 4t, 4t+2 -> sub-block 2g+1
-        const uint32_t h13 = ((v >> 6) & M) | C;  // high nibbles of bytes 4t+1, 4t+3
-        s0a = __builtin_fmaf(xr[4 * t + 0], h_lo(p02), s0a);
-        s0b = __builtin_fmaf(xr[4 * t + 1], h_lo(p13), s0b);
-        s0a = __builtin_fmaf(xr[4 * t + 2], h_hi(p02), s0a);
-        s0b = __builtin_fmaf(xr[4 * t + 3], h_hi(p13), s0b);
+        const uint32_t v = q[t], v8 = q[t] >> 8;
+        const uint32_t l02 = v & 0x000F000Fu;   // low nibbles of bytes 4t, 4t+2  -> sub-block 2g
+        const uint32_t l13 = v8 & 0x000F000Fu;  // low nibbles of bytes 4t+1, 4t+3
+        const uint32_t h02 = v & 0x00F000F0u;   // high nibbles of bytes 4t, 4t+2 -> sub-block 2g+1
+        const uint32_t h13 = v8 & 0x00F000F0u;  // high nibbles of bytes 4t+1, 4t+3
+        s0a = __builtin_fmaf(xr[4 * t + 0], h_lo(l02), s0a);
+        s0b = __builtin_fmaf(xr[4 * t + 1], h_lo(l13), s0b);
+        s0a = __builtin_fmaf(xr[4 * t + 2], h_hi(l02), s0a);
+        s0b = __builtin_fmaf(xr[4 * t + 3], h_hi(l13), s0b);
         s1a = __builtin_fmaf(xr[32 + 4 * t + 0], h_lo(h02), s1a);
         s1b = __builtin_fmaf(xr[32 + 4 * t + 1], h_lo(h13), s1b);
         s1a = __builtin_fmaf(xr[32 + 4 * t + 2], h_hi(h02), s1a);
@@ -179,129 +198,224 @@ __device__ __forceinline__ float q4_dot(const uint4 &hd, const uint4 &qa, const 
     const bool lo = L.g < 2;
     const uint32_t srcA = lo ? hd.y : hd.w, srcM = lo ? hd.z : hd.w;
     const float d = ref_half(hd.x & 0xFFFFu), dmin = ref_half(hd.x >> 16);
-    const float d16 = d * 16.0f;
     float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const uint32_t sc = __builtin_amdgcn_ubfe(srcA, L.sa[u], 4) | (__builtin_amdgcn_ubfe(hd.y, L.sb[u], 2) << 4);
         const uint32_t mn = __builtin_amdgcn_ubfe(srcM, L.ma[u], 4) | (__builtin_amdgcn_ubfe(hd.z, L.mb[u], 2) << 4);
-        const float a = d16 * (float)sc;                     // 16 d sc
-        const float c = __builtin_fmaf(dmin, (float)mn, a);  // 16 d sc + dmin m
+        const float a = d * (float)sc * (u ? 1048576.0f : 16777216.0f);  // d sc 2^24 (low), 2^20 (high)
         const float S = u ? S1 : S0, X = u ? X1 : X0;
         acc = __builtin_fmaf(a, S, acc);
-        acc = __builtin_fmaf(-c, X, acc);
+        acc = __builtin_fmaf(-(dmin * (float)mn), X, acc);
     }
     return acc;
 }
 
-template <int TW, int TEAMS, int R, bool FUSE>
+// Rows row0 .. row0+RPW-1 of the team, loaded all at once (rows past n clamp to n-1
+// and are not stored).  Then the activations, then one row at a time as it lands.
+template <int TW, int TEAMS, int RPW, bool FUSE>
 __global__ __launch_bounds__(TW *TEAMS * 64) void k_q4k_m1(const float *__restrict__ x, const float *__restrict__ up,
                                                             const uint8_t *__restrict__ w, float *__restrict__ y,
                                                             uint32_t k, uint32_t n, uint64_t row_bytes) {
-    __shared__ __attribute__((aligned(16))) float xs[TEAMS > 1 ? 4096 + 256 : 4];
-    __shared__ float red[TW > 1 ? R * TW : 1];
+    constexpr int XPT = (16 * TW + TEAMS * TW - 1) / (TEAMS * TW);
+    __shared__ __attribute__((aligned(16))) float xs[TW * 64 * 68];
+    __shared__ float red[TW > 1 ? TEAMS * RPW * TW : 1];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t team = wave / TW, wt = wave % TW;
     const uint32_t P = k >> 6;
-    const uint32_t p = wt * 64 + lane;
-    const bool active = p < P;
+    const uint32_t p0 = wt * 64 + lane;
+    const bool active = p0 < P;
+    const uint32_t p = active ? p0 : 0;  // idle lanes read group 0 and contribute 0
+    const Q4Lane L = q4_lane(p & 3u);
+    const uint64_t lane_off = (uint64_t)(p >> 2) * Q4K_BYTES;
+    const uint32_t qoff = 16 + 32 * L.g;
+    const uint32_t row0 = (blockIdx.x * TEAMS + team) * RPW;
+
+    XFetch<XPT, FUSE> xf;
+    x_fetch<XPT, FUSE>(xf, x, up, k);
+    uint4 hd[RPW], qa[RPW], qb[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const uint32_t row = row0 + r < n ? row0 + r : n - 1;
+        const uint8_t *blk = w + (uint64_t)row * row_bytes + lane_off;
+        hd[r] = *reinterpret_cast<const uint4 *>(blk);
+        qa[r] = *reinterpret_cast<const uint4 *>(blk + qoff);
+        qb[r] = *reinterpret_cast<const uint4 *>(blk + qoff + 16);
+    }
     float xr[64];
-    load_x<TEAMS, FUSE>(x, up, k, p, active, xs, xr);
+    x_share<XPT, FUSE>(xf, k, wt, lane, xs, xr);
+    if (!active) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
+    }
+    float X0 = 0.f, X1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
+
+    // Idle lanes contribute an explicit 0, not 0 * (a scale that may be inf or NaN).
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const float v = q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L);
+        acc[r] = active ? v : 0.0f;
+    }
+    team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
+}
+
+// Q4_K with k <= 4096, not fused: one wave per row, x staged once per workgroup
+// in LDS, grid-stride rows, R per team per iteration.  Written so that the
+// compiler re-reads the activations from LDS instead of holding all 64 in
+// registers: at about 60 VGPRs all 16 waves of a CU stay resident, which hides
+// the latency of the small per-row loads better than a register-resident vector.
+template <int TEAMS, int R>
+__global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_rows(const float *__restrict__ x, const uint8_t *__restrict__ w,
+                                                             float *__restrict__ y, uint32_t k, uint32_t n,
+                                                             uint64_t row_bytes) {
+    __shared__ __attribute__((aligned(16))) float xs[64 * 68];
+    const uint32_t lane = threadIdx.x & 63u, team = threadIdx.x >> 6;
+    const uint32_t P = k >> 6;
+    const uint32_t p = lane;
+    const bool active = p < P;
+    for (uint32_t e4 = threadIdx.x; e4 < k / 4; e4 += blockDim.x) {
+        const uint32_t e = 4 * e4;
+        *reinterpret_cast<float4 *>(xs + e + 4 * (e >> 6)) = reinterpret_cast<const float4 *>(x)[e4];
+    }
+    __syncthreads();
+    float xr[64];
+    if (active) {
+        const float4 *s4 = reinterpret_cast<const float4 *>(xs + 68 * p);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 v = s4[i];
+            xr[4 * i] = v.x, xr[4 * i + 1] = v.y, xr[4 * i + 2] = v.z, xr[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
+    }
     float X0 = 0.f, X1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
     const Q4Lane L = q4_lane(p & 3u);
     const uint64_t lane_off = (uint64_t)(p >> 2) * Q4K_BYTES;
-    const uint32_t step = TEAMS * R;
-    for (uint32_t r0 = blockIdx.x * step; r0 < n; r0 += gridDim.x * step) {
-        const uint32_t rb = r0 + team * R;
+    for (uint32_t r0 = (blockIdx.x * TEAMS + team) * R; r0 < n; r0 += gridDim.x * TEAMS * R) {
         uint4 hd[R], qa[R], qb[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            if (active && rb + r < n) {
-                const uint8_t *blk = w + (uint64_t)(rb + r) * row_bytes + lane_off;
+            if (active && r0 + r < n) {
+                const uint8_t *blk = w + (uint64_t)(r0 + r) * row_bytes + lane_off;
                 hd[r] = *reinterpret_cast<const uint4 *>(blk);
                 qa[r] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * L.g);
                 qb[r] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * L.g);
             } else {
-                hd[r] = qa[r] = qb[r] = make_uint4(0, 0, 0, 0);
+                hd[r] = qa[r] = qb[r] = make_uint4(0, 0, 0, 0);  // idle lanes: zero scales, zero sums
             }
         }
-        float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; r++) acc[r] = q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L);
-        team_store<TW, R>(acc, rb, n, y, red, lane, wt);
+        for (int r = 0; r < R; r++) {
+            const float v = wave_sum(q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L));
+            if (lane == 0 && r0 + r < n) y[r0 + r] = v;
+        }
     }
 }
 
 // ------------------------------------------------------------------------------------------
 // Q8_0
 
-template <int TW, int TEAMS, int R>
+constexpr uint32_t Q8_SEG = 64 * 68;                  // bytes of one wave's 64-group share of a row
+constexpr uint32_t Q8_CHUNKS = Q8_SEG / 16;           // 272 16-byte chunks
+constexpr uint32_t Q8_LOADS = (Q8_CHUNKS + 63) / 64;  // 5 per lane
+
+__device__ __forceinline__ float q8_dot(const uint32_t *__restrict__ D, const float (&xr)[64], float X0, float X1) {
+    uint32_t v[17];
+#pragma unroll
+    for (int i = 0; i < 17; i++) v[i] = D[i];
+    const float d0 = ref_half(v[0] & 0xFFFFu), d1 = ref_half(v[8] >> 16);
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        // block 0 quants start 2 bytes into the lane's 68 bytes: realign
+        const uint32_t a = __builtin_amdgcn_alignbit(v[t + 1], v[t], 16) ^ 0x80808080u;
+        const uint32_t b = v[9 + t] ^ 0x80808080u;
+        s0 = __builtin_fmaf(xr[4 * t + 0], ubyte_f<0>(a), s0);
+        s0 = __builtin_fmaf(xr[4 * t + 1], ubyte_f<1>(a), s0);
+        s0 = __builtin_fmaf(xr[4 * t + 2], ubyte_f<2>(a), s0);
+        s0 = __builtin_fmaf(xr[4 * t + 3], ubyte_f<3>(a), s0);
+        s1 = __builtin_fmaf(xr[32 + 4 * t + 0], ubyte_f<0>(b), s1);
+        s1 = __builtin_fmaf(xr[32 + 4 * t + 1], ubyte_f<1>(b), s1);
+        s1 = __builtin_fmaf(xr[32 + 4 * t + 2], ubyte_f<2>(b), s1);
+        s1 = __builtin_fmaf(xr[32 + 4 * t + 3], ubyte_f<3>(b), s1);
+    }
+    // sum x q = S - 128 X  (q + 128 was accumulated)
+    return d0 * __builtin_fmaf(-128.0f, X0, s0) + d1 * __builtin_fmaf(-128.0f, X1, s1);
+}
+
+// Each wave stages its share of one row at a time in its own LDS region and reads
+// it back; the region is only touched by that wave, whose LDS operations execute
+// in order, so no barrier is needed between the write and the reads.  Every lane
+// stores all of its Q8_LOADS chunks (unconditional stores keep the row registers
+// out of divergent code); chunks past the share land in the stage's tail, which no
+// lane reads.
+template <int TW, int TEAMS, int RPW>
 __global__ __launch_bounds__(TW *TEAMS * 64) void k_q80_m1(const float *__restrict__ x, const uint8_t *__restrict__ w,
                                                             float *__restrict__ y, uint32_t k, uint32_t n,
                                                             uint64_t row_bytes) {
-    constexpr uint32_t SEG = 64 * 68;  // bytes of one wave's share of a row
-    __shared__ __attribute__((aligned(16))) float xs[TEAMS > 1 ? 4096 + 256 : 4];
-    __shared__ __attribute__((aligned(16))) uint32_t stage[TW * TEAMS][R][SEG / 4];
-    __shared__ float red[TW > 1 ? R * TW : 1];
+    constexpr int XPT = (16 * TW + TEAMS * TW - 1) / (TEAMS * TW);
+    __shared__ __attribute__((aligned(16))) float xs[TW * 64 * 68];
+    __shared__ __attribute__((aligned(16))) lg_u32x4 stage_all[TW * TEAMS][64 * Q8_LOADS];
+    __shared__ float red[TW > 1 ? TEAMS * RPW * TW : 1];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t team = wave / TW, wt = wave % TW;
     const uint32_t P = k >> 6;
-    const uint32_t p = wt * 64 + lane;
-    const bool active = p < P;
+    const uint32_t p0 = wt * 64 + lane;
+    const bool active = p0 < P;
+    // this wave's share of a row: groups wt*64 .. min(P, wt*64+64), a multiple of 4 groups
+    const uint32_t groups = P > wt * 64 ? (P - wt * 64 < 64 ? P - wt * 64 : 64) : 0;
+    const uint32_t seg16 = groups * 68 / 16;
+    lg_u32x4 *stage = stage_all[wave];
+    const uint32_t row0 = (blockIdx.x * TEAMS + team) * RPW;
+
+    XFetch<XPT, false> xf;
+    x_fetch<XPT, false>(xf, x, nullptr, k);
+    constexpr int NL = (int)Q8_LOADS;
+    lg_u32x4 c[RPW * NL];  // native vectors: plain loads and stores, kept in registers
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const uint32_t row = row0 + r < n ? row0 + r : n - 1;
+        const lg_u32x4 *src =
+            reinterpret_cast<const lg_u32x4 *>(w + (uint64_t)row * row_bytes + (uint64_t)wt * Q8_SEG);
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const uint32_t ch = lane + 64 * i;
+            c[r * NL + i] = src[ch < seg16 ? ch : 0];  // chunks past the share re-read chunk 0
+        }
+    }
     float xr[64];
-    load_x<TEAMS, false>(x, nullptr, k, p, active, xs, xr);
+    x_share<XPT, false>(xf, k, wt, lane, xs, xr);
+    if (!active) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
+    }
     float X0 = 0.f, X1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
-    // this wave's byte range of a row: groups wt*64 .. min(P, wt*64+64)
-    const uint32_t groups = P > wt * 64 ? (P - wt * 64 < 64 ? P - wt * 64 : 64) : 0;
-    const uint32_t seg16 = groups * 68 / 16;  // groups is a multiple of 4 -> whole 16-byte units
-    const uint32_t step = TEAMS * R;
-    for (uint32_t r0 = blockIdx.x * step; r0 < n; r0 += gridDim.x * step) {
-        const uint32_t rb = r0 + team * R;
+
+    // Idle lanes read stage words nobody wrote: their partials are replaced by 0.
+    float acc[RPW];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (rb + r < n) {
-                const uint4 *src = reinterpret_cast<const uint4 *>(w + (uint64_t)(rb + r) * row_bytes + (uint64_t)wt * SEG);
-                uint4 *dst = reinterpret_cast<uint4 *>(stage[wave][r]);
-                for (uint32_t c = lane; c < seg16; c += 64) dst[c] = src[c];
-            }
-        }
-        __syncthreads();
-        float acc[R];
+    for (int r = 0; r < RPW; r++) {
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            acc[r] = 0.0f;
-            if (active && rb + r < n) {
-                const uint32_t *D = stage[wave][r] + 17 * lane;
-                uint32_t v[17];
-#pragma unroll
-                for (int i = 0; i < 17; i++) v[i] = D[i];
-                const float d0 = ref_half(v[0] & 0xFFFFu), d1 = ref_half(v[8] >> 16);
-                float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    // block 0 quants start 2 bytes into the lane's 68 bytes: realign
-                    const uint32_t a = __builtin_amdgcn_alignbit(v[t + 1], v[t], 16) ^ 0x80808080u;
-                    const uint32_t b = v[9 + t] ^ 0x80808080u;
-                    s0 = __builtin_fmaf(xr[4 * t + 0], ubyte_f<0>(a), s0);
-                    s0 = __builtin_fmaf(xr[4 * t + 1], ubyte_f<1>(a), s0);
-                    s0 = __builtin_fmaf(xr[4 * t + 2], ubyte_f<2>(a), s0);
-                    s0 = __builtin_fmaf(xr[4 * t + 3], ubyte_f<3>(a), s0);
-                    s1 = __builtin_fmaf(xr[32 + 4 * t + 0], ubyte_f<0>(b), s1);
-                    s1 = __builtin_fmaf(xr[32 + 4 * t + 1], ubyte_f<1>(b), s1);
-                    s1 = __builtin_fmaf(xr[32 + 4 * t + 2], ubyte_f<2>(b), s1);
-                    s1 = __builtin_fmaf(xr[32 + 4 * t + 3], ubyte_f<3>(b), s1);
-                }
-                // sum x q = S - 128 X  (q + 128 was accumulated)
-                acc[r] = d0 * __builtin_fmaf(-128.0f, X0, s0) + d1 * __builtin_fmaf(-128.0f, X1, s1);
-            }
-        }
-        team_store<TW, R>(acc, rb, n, y, red, lane, wt);
-        if constexpr (TW == 1) __syncthreads();  // stage[] is rewritten by the next iteration
+        for (int i = 0; i < NL; i++) stage[lane + 64 * i] = c[r * NL + i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float v = q8_dot(reinterpret_cast<const uint32_t *>(stage) + 17 * lane, xr, X0, X1);
+        acc[r] = active ? v : 0.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
+    team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -400,48 +514,103 @@ __global__ __launch_bounds__(256) void k_activation(const float *__restrict__ g,
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-uint32_t grid_for(uint32_t n, uint32_t rows_per_wg, uint32_t cap_default) {
-    uint32_t g = (n + rows_per_wg - 1) / rows_per_wg;
-    const uint32_t cap = g_grid_cap ? g_grid_cap : cap_default;
-    return g < cap ? g : cap;
+std::mutex g_cu_mu;
+
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lk(g_cu_mu);
+    if (!cus[dev]) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
 }
 
-constexpr int R_Q4 = 2, R_Q8 = 2;
+// Rows per team: enough that the grid covers the CUs once (or the tuning cap on
+// workgroups), at most M1_RPW_MAX; larger n simply launches more workgroups.
+uint32_t rows_per_team(uint32_t n, uint32_t teams) {
+    uint64_t wgs = (uint64_t)device_cus();
+    if (g_grid_cap && g_grid_cap < wgs) wgs = g_grid_cap;
+    uint64_t rpw = (n + wgs * teams - 1) / (wgs * teams);
+    if (rpw < 1) rpw = 1;
+    if (rpw > (uint64_t)M1_RPW_MAX) rpw = M1_RPW_MAX;
+    return (uint32_t)rpw;
+}
+
+template <int TW, int TEAMS, int RPW, bool FUSE>
+void launch_q4k_r(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n,
+                  hipStream_t s) {
+    const uint32_t grid = (n + TEAMS * RPW - 1) / (TEAMS * RPW);
+    const uint64_t rb = (uint64_t)k / QK_K * Q4K_BYTES;
+    hipLaunchKernelGGL((k_q4k_m1<TW, TEAMS, RPW, FUSE>), dim3(grid), dim3(TW * TEAMS * 64), 0, s, x, up, w, y, k,
+                       n, rb);
+}
+
+template <int TW, int TEAMS, bool FUSE>
+int launch_q4k_t(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n,
+                 hipStream_t s) {
+    switch (rows_per_team(n, TEAMS)) {
+    case 1: launch_q4k_r<TW, TEAMS, 1, FUSE>(x, up, w, y, k, n, s); break;
+    case 2: launch_q4k_r<TW, TEAMS, 2, FUSE>(x, up, w, y, k, n, s); break;
+    case 3: launch_q4k_r<TW, TEAMS, 3, FUSE>(x, up, w, y, k, n, s); break;
+    case 4: launch_q4k_r<TW, TEAMS, 4, FUSE>(x, up, w, y, k, n, s); break;
+    case 5: launch_q4k_r<TW, TEAMS, 5, FUSE>(x, up, w, y, k, n, s); break;
+    case 6: launch_q4k_r<TW, TEAMS, 6, FUSE>(x, up, w, y, k, n, s); break;
+    case 7: launch_q4k_r<TW, TEAMS, 7, FUSE>(x, up, w, y, k, n, s); break;
+    default: launch_q4k_r<TW, TEAMS, 8, FUSE>(x, up, w, y, k, n, s); break;
+    }
+    return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
+}
 
 template <bool FUSE>
 int launch_q4k(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
-    const uint64_t rb = (uint64_t)k / QK_K * Q4K_BYTES;
     const uint32_t P = k / 64;
-    if (P <= 64) {
-        hipLaunchKernelGGL((k_q4k_m1<1, 4, R_Q4, FUSE>), dim3(grid_for(n, 4 * R_Q4, 1024)), dim3(256), 0, s, x, up, w,
-                           y, k, n, rb);
-    } else if (P <= 128) {
-        hipLaunchKernelGGL((k_q4k_m1<2, 1, R_Q4, FUSE>), dim3(grid_for(n, R_Q4, 2048)), dim3(128), 0, s, x, up, w, y,
-                           k, n, rb);
-    } else if (P <= 192) {
-        hipLaunchKernelGGL((k_q4k_m1<3, 1, R_Q4, FUSE>), dim3(grid_for(n, R_Q4, 2048)), dim3(192), 0, s, x, up, w, y,
-                           k, n, rb);
-    } else {
-        hipLaunchKernelGGL((k_q4k_m1<4, 1, R_Q4, FUSE>), dim3(grid_for(n, R_Q4, 2048)), dim3(256), 0, s, x, up, w, y,
-                           k, n, rb);
+    if (P <= 64 && !FUSE) {
+        constexpr int TEAMS = 4, R = 2;
+        uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
+        const uint32_t cap = g_grid_cap ? g_grid_cap : 1024;
+        grid = grid < cap ? grid : cap;
+        hipLaunchKernelGGL((k_q4k_m1_rows<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
+                           (uint64_t)k / QK_K * Q4K_BYTES);
+        return after_launch("proj_q4k_m1", s);
     }
-    return after_launch("proj_q4k_m1", s);
+    if (P <= 64) return launch_q4k_t<1, 8, FUSE>(x, up, w, y, k, n, s);
+    if (P <= 128) return launch_q4k_t<2, 4, FUSE>(x, up, w, y, k, n, s);
+    if (P <= 192) return launch_q4k_t<3, 2, FUSE>(x, up, w, y, k, n, s);
+    return launch_q4k_t<4, 2, FUSE>(x, up, w, y, k, n, s);
+}
+
+template <int TW, int TEAMS, int RPW>
+void launch_q80_r(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
+    const uint32_t grid = (n + TEAMS * RPW - 1) / (TEAMS * RPW);
+    const uint64_t rb = (uint64_t)k / QK8_0 * Q80_BYTES;
+    hipLaunchKernelGGL((k_q80_m1<TW, TEAMS, RPW>), dim3(grid), dim3(TW * TEAMS * 64), 0, s, x, w, y, k, n, rb);
+}
+
+template <int TW, int TEAMS>
+int launch_q80_t(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
+    switch (rows_per_team(n, TEAMS)) {
+    case 1: launch_q80_r<TW, TEAMS, 1>(x, w, y, k, n, s); break;
+    case 2: launch_q80_r<TW, TEAMS, 2>(x, w, y, k, n, s); break;
+    case 3: launch_q80_r<TW, TEAMS, 3>(x, w, y, k, n, s); break;
+    case 4: launch_q80_r<TW, TEAMS, 4>(x, w, y, k, n, s); break;
+    case 5: launch_q80_r<TW, TEAMS, 5>(x, w, y, k, n, s); break;
+    case 6: launch_q80_r<TW, TEAMS, 6>(x, w, y, k, n, s); break;
+    case 7: launch_q80_r<TW, TEAMS, 7>(x, w, y, k, n, s); break;
+    default: launch_q80_r<TW, TEAMS, 8>(x, w, y, k, n, s); break;
+    }
+    return after_launch("proj_q8_0_m1", s);
 }
 
 int launch_q80(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
-    const uint64_t rb = (uint64_t)k / QK8_0 * Q80_BYTES;
     const uint32_t P = k / 64;
-    if (P <= 64) {
-        hipLaunchKernelGGL((k_q80_m1<1, 4, R_Q8>), dim3(grid_for(n, 4 * R_Q8, 1024)), dim3(256), 0, s, x, w, y, k, n,
-                           rb);
-    } else if (P <= 128) {
-        hipLaunchKernelGGL((k_q80_m1<2, 1, R_Q8>), dim3(grid_for(n, R_Q8, 2048)), dim3(128), 0, s, x, w, y, k, n, rb);
-    } else if (P <= 192) {
-        hipLaunchKernelGGL((k_q80_m1<3, 1, R_Q8>), dim3(grid_for(n, R_Q8, 2048)), dim3(192), 0, s, x, w, y, k, n, rb);
-    } else {
-        hipLaunchKernelGGL((k_q80_m1<4, 1, R_Q8>), dim3(grid_for(n, R_Q8, 2048)), dim3(256), 0, s, x, w, y, k, n, rb);
-    }
-    return after_launch("proj_q8_0_m1", s);
+    if (P <= 64) return launch_q80_t<1, 8>(x, w, y, k, n, s);
+    if (P <= 128) return launch_q80_t<2, 4>(x, w, y, k, n, s);
+    if (P <= 192) return launch_q80_t<3, 2>(x, w, y, k, n, s);
+    return launch_q80_t<4, 2>(x, w, y, k, n, s);
 }
 
 // Shared front end of every quantized M=1 entry point.

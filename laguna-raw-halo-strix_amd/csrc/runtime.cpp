@@ -53,6 +53,12 @@ int after_launch(const char *what, hipStream_t s) {
     return LG_OK;
 }
 
+// Plain 16-byte copy (lg_buf_copy).  It is also the known-size kernel that hardware
+// traffic counters are calibrated against (bytes read = bytes written = size).
+__global__ __launch_bounds__(256) void k_copy16(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint64_t n16) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * 256) dst[i] = src[i];
+}
+
 }  // namespace lg
 
 using namespace lg;
@@ -141,6 +147,26 @@ int lg_buf_memset(void *dst, int value, uint64_t bytes, void *stream) {
     LG_EXTENT(dst, bytes, "lg_buf_memset dst");
     LG_HIP_TRY(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
     return after_launch("lg_buf_memset", (hipStream_t)stream);
+}
+
+int lg_buf_copy(void *dst, const void *src, uint64_t bytes, void *stream) {
+    if (bytes == 0) return LG_OK;
+    LG_REQUIRE(dst && src, "lg_buf_copy: null pointer");
+    LG_EXTENT(dst, bytes, "lg_buf_copy dst");
+    LG_EXTENT(src, bytes, "lg_buf_copy src");
+    hipStream_t s = (hipStream_t)stream;
+    const bool vec = bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(src) & 15u) == 0;
+    if (!vec) {
+        LG_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s));
+        return after_launch("lg_buf_copy", s);
+    }
+    const uint64_t n16 = bytes / 16;
+    uint64_t grid = (n16 + 255) / 256;
+    grid = grid < 4096 ? grid : 4096;
+    hipLaunchKernelGGL(k_copy16, dim3((unsigned)grid), dim3(256), 0, s, static_cast<const uint4 *>(src),
+                       static_cast<uint4 *>(dst), n16);
+    return after_launch("lg_buf_copy", s);
 }
 
 int lg_stream_create(void **stream) {

@@ -42,6 +42,7 @@ SIGNATURES = {
     "lg_buf_upload": (_i, [_vp, _vp, _u64, _vp]),
     "lg_buf_download": (_i, [_vp, _vp, _u64, _vp]),
     "lg_buf_memset": (_i, [_vp, _i, _u64, _vp]),
+    "lg_buf_copy": (_i, [_vp, _vp, _u64, _vp]),
     "lg_stream_create": (_i, [ctypes.POINTER(_vp)]),
     "lg_stream_destroy": (_i, [_vp]),
     "lg_sync": (_i, [_vp]),
@@ -152,6 +153,10 @@ class GpuBuffer:
 
     def read_f32(self, n, offset=0):
         return self.download(4 * n, offset).view(np.float32)
+
+    def copy_from(self, other, nbytes=None):
+        nbytes = min(self.size, other.size) if nbytes is None else nbytes
+        check(lib().lg_buf_copy(self.ptr, other.ptr, nbytes, self.ctx.stream))
 
     def fill(self, value=0):
         check(lib().lg_buf_memset(self.ptr, value, self.size, self.ctx.stream))
