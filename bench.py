@@ -8,9 +8,12 @@ from the 256 MB Infinity Cache.  Kernel time is taken with HIP events recorded o
 the stream the kernels run on.
 
 Also reported under "extra": the Q8_0 4096x4096 M=1 matvec, the fused
-SiLU(gate)*up + Q4_K 14336 -> 4096 down projection, and the M = 16 block-verify
+SiLU(gate)*up + Q4_K 14336 -> 4096 down projection, the M = 16 block-verify
 products (Q4_K 4096 -> 14336 with bf16 and f32 activations, Q8_0 4096 -> 4096
-with f32 activations).
+with f32 activations), and the 6-layer draft decoder's 16-token block forward
+over a 2048-position context (HIP graph replay and eager), in us per block, draft
+tokens/s and GB/s of algorithmic bytes (every weight, the context K/V, inputs
+and outputs once per block).
 
 `cpu_baseline`: the same Q4_K matvec computed by the oracle (a C restatement of
 kernels/proj_q4k.comp's per-element decode and f32 accumulation) on the host
@@ -136,6 +139,51 @@ class BatchM16(Workload):
         lh.dispatch_proj_quant_batch(ctx, self.x, self.x_dtype, w, self.c, self.k, self.n, self.m, self.dtype)
 
 
+class DFlashBlock(Workload):
+    """The 6-layer draft decoder's block forward: 16 tokens over a 2048-position f32
+    K/V context, random-init weights (Q4_K except Q8_0 attn_output), replayed as a
+    captured HIP graph.  One forward reads every weight once (917 MB > the 256 MB
+    Infinity Cache), so a single model copy needs no rotation."""
+
+    def __init__(self, m=16, ctx_len=2048, seed=0x5EED000A, graph=True):
+        self.m, self.ctx_len, self.seed, self.graph_mode = m, ctx_len, seed, graph
+        self.cfg = lh.DFlashConfig()
+        self.k, self.n = self.cfg.n_embd, self.cfg.n_embd
+        self.name = (f"DFlash 6-layer block forward, {m} tokens over {ctx_len}-position f32 KV "
+                     f"({'HIP graph' if graph else 'eager'})")
+
+    def setup(self, ctx):
+        cfg, m = self.cfg, self.m
+        W, layers = synth.dflash_model(self.seed, cfg, cfg.n_layers)
+        feat, tok, kc, vc = synth.dflash_inputs(self.seed + 1, cfg, cfg.n_layers, m, self.ctx_len)
+        nbytes = lambda a: np.asarray(a).nbytes
+        wbytes = sum(nbytes(W[n]) for n in ("enc_aux_norm", "fc", "enc_output_norm", "output_norm"))
+        wbytes += sum(nbytes(L[n]) for L in layers for n in lh.DFLASH_NORMS + lh.DFLASH_PROJ)
+        kvbytes = sum(nbytes(a) for a in kc + vc)
+        self.bytes_per_call = wbytes + kvbytes + feat.nbytes + tok.nbytes + 4 * m * cfg.n_embd
+        self.model = lh.DFlashModel(ctx, cfg, W, layers)
+        self.model.set_context(kc, vc)
+        del W, layers, kc, vc
+        self.fb, self.tb = lh.upload_f32(ctx, feat), lh.upload_f32(ctx, tok)
+        self.ob = lh.GpuBuffer(ctx, 4 * m * cfg.n_embd)
+        self.stream = lh.Stream()
+        self.g = self.model.capture(self.fb, self.tb, m, self.ob, self.stream) if self.graph_mode else None
+        self.pool = [self.fb, self.tb, self.ob]
+        self.pool_bytes = self.bytes_per_call
+
+    def step(self, ctx, i):
+        if self.g is not None:
+            self.g.launch()
+        else:
+            self.model.forward_block_device(self.fb, self.tb, self.m, self.ob, stream=self.stream)
+
+    def teardown(self):
+        if self.g is not None:
+            self.g.destroy()
+        self.model.free()
+        self.stream.sync()
+
+
 WORKLOADS = {
     "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003),
     "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001),
@@ -143,21 +191,25 @@ WORKLOADS = {
     "q4k_m16_bf16": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008),
     "q4k_m16_f32": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008),
     "q8_0_m16_f32": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009),
+    "dflash_block": lambda: DFlashBlock(),
+    "dflash_block_eager": lambda: DFlashBlock(graph=False),
 }
 
 
 def time_workload(ctx, ev, wl, steps, warmup):
     wl.setup(ctx)
+    stream = wl.stream.ptr if getattr(wl, "stream", None) is not None else ctx.stream
+    sync = wl.stream.sync if getattr(wl, "stream", None) is not None else ctx.sync
     for i in range(warmup):
         wl.step(ctx, i)
-    ctx.sync()
+    sync()
     a, b = ev.new(), ev.new()
     t0 = time.perf_counter()
-    ev.record(a, ctx.stream)
+    ev.record(a, stream)
     for i in range(steps):
         wl.step(ctx, warmup + i)
-    ev.record(b, ctx.stream)
-    ctx.sync()
+    ev.record(b, stream)
+    sync()
     wall = time.perf_counter() - t0
     ms = ev.elapsed_ms(a, b)
     us = 1000.0 * ms / steps
@@ -165,9 +217,14 @@ def time_workload(ctx, ev, wl, steps, warmup):
     for p in wl.pool:
         p.free()
     wl.pool = []
-    return {"workload": wl.name, "us_per_call": round(us, 3), "GBps": round(gbs, 1),
-            "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_call": wl.bytes_per_call,
-            "pool_MB": round(wl.pool_bytes / 2 ** 20, 1), "host_wall_s": round(wall, 4)}
+    if hasattr(wl, "teardown"):
+        wl.teardown()
+    r = {"workload": wl.name, "us_per_call": round(us, 3), "GBps": round(gbs, 1),
+         "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_call": wl.bytes_per_call,
+         "pool_MB": round(wl.pool_bytes / 2 ** 20, 1), "host_wall_s": round(wall, 4)}
+    if isinstance(wl, DFlashBlock):
+        r["draft_tokens_per_s"] = round(wl.m / (us * 1e-6), 1)
+    return r
 
 
 def cpu_baseline(budget_s=12.0):
@@ -269,6 +326,9 @@ def main():
         for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32"]:
             if name != args.workload:
                 extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(50, args.steps // 4), 20)
+        for name in ["dflash_block", "dflash_block_eager"]:
+            if name != args.workload:
+                extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(10, args.steps // 40), 3)
     line = {
         "metric": METRIC,
         "value": head["GBps"],

@@ -154,6 +154,107 @@ int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, floa
                                  uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                  void *stream);
 
+/* ---- DFlash draft glue (src/dflash.rs dispatch_* helpers, rows >= 1) ---- */
+
+/* dispatch_rmsnorm (src/dflash.rs:978-1007), kernels/rmsnorm.comp: for each of
+ * `rows` rows of n floats, out = x * w * (mean(x^2) + eps)^-1/2.  The reference
+ * passes eps = 1e-5 and one row. */
+int lg_dispatch_rmsnorm(const float *w, const float *x, float *out, uint32_t n, uint32_t rows, float eps,
+                        void *stream);
+
+/* dispatch_enc_aux_norm (src/dflash.rs:1196-1236), kernels/enc_aux_norm.comp: RMSNorm
+ * of each n_feat chunk of the n_aux*n_feat features of each of n_tokens rows,
+ * times aux_norm_w[aux*n_feat + feat]. */
+int lg_dispatch_enc_aux_norm(const float *x, const float *aux_norm_w, float *out, uint32_t n_feat,
+                             uint32_t n_aux, uint32_t n_tokens, float eps, void *stream);
+
+/* dispatch_qk_norm_rope (src/dflash.rs:1092-1128), kernels/qk_norm_rope.comp:
+ * per-head RMSNorm times norm_w[dim], then GPT-NeoX rotation of dims < rope_dim
+ * with angle freq[dim % (rope_dim/2)] * pos.  Row r (of `rows`, each
+ * n_heads*head_dim floats) is at position pos + r.  head_dim <= 256 and even;
+ * rope_dim is head_dim or 0 (for a smaller rope_dim the shader's partner index of
+ * the second rotary half, i - head_dim/2, leaves the head).  The reference passes
+ * eps = 1e-6. */
+int lg_dispatch_qk_norm_rope(const float *x, const float *norm_w, const float *freq, float *out,
+                             uint32_t n_heads, uint32_t head_dim, uint32_t rope_dim, uint32_t pos,
+                             uint32_t rows, float eps, void *stream);
+
+/* dispatch_mha_attn_seq (src/dflash.rs:1158-1194), kernels/mha_attn.comp:
+ * out[r][h] = softmax_p(q[r][h] . k_seq[p][kv(h)] / sqrt(head_dim)) v_seq[p][kv(h)]
+ * over p < seq_len (and p <= q_pos + r when causal), kv(h) = h * n_kv / n_q.
+ * q: [rows][n_q*head_dim], k_seq, v_seq: [seq_len][n_kv*head_dim]. */
+int lg_dispatch_mha_attn(const float *q, const float *k_seq, const float *v_seq, float *out, uint32_t n_q_heads,
+                         uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len, uint32_t q_pos,
+                         uint32_t rows, int causal, void *stream);
+
+/* dispatch_gate_mul (src/dflash.rs:1238-1270), kernels/gate_mul.comp:
+ * out[r][i] = v[r][i] * gate[r][i / head_dim]. */
+int lg_dispatch_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
+                         uint32_t rows, void *stream);
+
+/* The attention gate of src/dflash.rs:956-959 on the device: the reference
+ * applies softplus on the host (g > 20 ? g : ln(1 + e^g)) and then gate_mul. */
+int lg_dispatch_softplus_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads,
+                                  uint32_t head_dim, uint32_t rows, void *stream);
+
+/* dispatch_add (src/dflash.rs:1284-1303), kernels/add.comp: out = a + b. */
+int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream);
+
+/* ---- DFlash draft model (src/dflash.rs DFlashModel) ---- */
+
+typedef struct {
+    uint32_t n_embd, n_heads, n_kv_heads, head_dim, rope_dim, n_ff, n_aux, n_layers;
+    float rope_base;  /* rope_freq_base (src/dflash.rs:898-904; default 500000) */
+    float rms_eps;    /* 1e-5 (src/dflash.rs:987) */
+    float qk_eps;     /* 1e-6 (src/dflash.rs:1105) */
+} lg_dflash_hparams;
+
+/* One decoder layer: device pointers to the tensors of src/dflash.rs:68-79
+ * (raw GGUF blocks for the projections, f32 for the norms), their GGUF types,
+ * and the layer's cached context keys (normed and roped) and values, each
+ * [ctx_len][n_kv_heads*head_dim] f32. */
+typedef struct {
+    const float *attn_norm, *attn_q_norm, *attn_k_norm, *ffn_norm;
+    const void *attn_q, *attn_k, *attn_v, *attn_gate, *attn_output, *ffn_gate, *ffn_up, *ffn_down;
+    int attn_q_type, attn_k_type, attn_v_type, attn_gate_type, attn_output_type, ffn_gate_type, ffn_up_type,
+        ffn_down_type;
+    const float *k_ctx, *v_ctx;
+} lg_dflash_layer;
+
+typedef struct {
+    lg_dflash_hparams hp;
+    const float *enc_aux_norm;    /* [n_aux*n_embd] */
+    const void *fc;               /* [n_aux*n_embd -> n_embd] */
+    int fc_type;
+    const float *enc_output_norm; /* [n_embd] */
+    const float *output_norm;     /* [n_embd] or NULL */
+    const lg_dflash_layer *layers;
+} lg_dflash_model;
+
+/* DFlashModel::encode (src/dflash.rs:157-234) for m feature rows:
+ * enc_aux_norm, fc, rmsnorm(enc_output_norm).  features: [m][n_aux*n_embd],
+ * out: [m][n_embd]. */
+int lg_dflash_encode(const lg_dflash_model *model, const float *features, uint32_t m, float *out, void *stream);
+
+/* DFlashModel::forward_injected_decode_hidden (src/dflash.rs:877-976) for a block
+ * of m tokens over ctx_len cached positions.  Per layer the queries attend
+ * causally to [context (0..ctx_len-1)] ++ [the m injected encoder keys/values at
+ * positions ctx_len..ctx_len+m-1] ++ [the m token keys/values at ctx_len+m..];
+ * token t is at ctx_len+m+t.  With m = 1 and ctx_len = 0 this is the
+ * reference's sequence exactly.  features: [m][n_aux*n_embd], tokens:
+ * [m][n_embd] (token inputs), out: [m][n_embd] final hidden (after output_norm
+ * when present).  1 <= m <= 32; head_dim 128 uses the matrix-core attention. */
+int lg_dflash_forward_block(const lg_dflash_model *model, const float *features, const float *tokens,
+                            uint32_t m, uint32_t ctx_len, float *out, void *stream);
+
+/* The same forward captured once into a HIP graph on `stream` (the eager call is
+ * made first to size the workspaces) and replayed by lg_dflash_graph_launch.
+ * Inputs and outputs are read and written at the captured addresses. */
+int lg_dflash_graph_create(const lg_dflash_model *model, const float *features, const float *tokens, uint32_t m,
+                           uint32_t ctx_len, float *out, void *stream, void **graph);
+int lg_dflash_graph_launch(void *graph, void *stream);
+int lg_dflash_graph_destroy(void *graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,917 @@
+// DFlash draft model glue and block forward on gfx950.
+//
+// The reference runs the draft one token at a time through per-op Vulkan
+// dispatches with host round trips (K/V sequence rebuilt on the host,
+// src/dflash.rs:945-952; softplus on the host, :956-958).  Here a block of m
+// tokens goes through the layers on one stream, every intermediate stays in HBM,
+// and the projections read the raw GGUF blocks (lg_dispatch_proj_quant_batch).
+//
+//   rmsnorm / enc_aux_norm      one workgroup per row (or row chunk)
+//   qk_norm_rope                one wavefront per (row, head)
+//   attention (head_dim 128)    flash-decoding: one workgroup per (kv head, 64
+//                               positions); the 64 queries of a kv head (m tokens x
+//                               n_q/n_kv heads) against the chunk's keys and values
+//                               with v_mfma_f32_16x16x32_bf16, every f32 operand split
+//                               exactly into three bf16 parts and the six significant
+//                               part products accumulated (f32-grade); per-chunk
+//                               maxima, sums and partial outputs merged by a second
+//                               kernel
+//   attention (other head_dim)  one wavefront per (row, head), online softmax
+//   softplus gate, add          elementwise
+#include <cmath>
+#include <mutex>
+#include <vector>
+
+#include "lg_common.hpp"
+
+namespace {
+
+using namespace lg;
+
+#define LG_TRY(expr)                                                                                                   \
+    do {                                                                                                               \
+        const int st_ = (expr);                                                                                        \
+        if (st_ != LG_OK) return st_;                                                                                  \
+    } while (0)
+
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7F800000u) == 0x7F800000u) return (u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u);  // inf / NaN
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_f(uint32_t b) { return __uint_as_float(b << 16); }
+
+// Sum over the threads of a workgroup of THREADS; every thread receives it.
+template <int THREADS>
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < THREADS / 64; w++) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+// ------------------------------------------------------------------------------------------
+// RMSNorm (kernels/rmsnorm.comp:23-34, kernels/enc_aux_norm.comp:21-43)
+
+// Row `blockIdx.x` of `x` (n floats, row stride ldx): out = x * w * (mean(x^2)+eps)^-1/2.
+// blockIdx.y selects a chunk of n floats inside the row (enc_aux_norm: chunk aux of a
+// token's n_aux * n_feat features, weights w + aux * n).
+__global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *__restrict__ w, float *out, uint32_t n,
+                                                 uint32_t ldx, float eps) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * ldx + (uint64_t)blockIdx.y * n;
+    const float *xr = x + base;
+    const float *wr = w + (uint64_t)blockIdx.y * n;
+    float s = 0.0f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) s = __builtin_fmaf(xr[i], xr[i], s);
+    const float ms = block_sum<256>(s, red) / (float)n;
+    const float rms = 1.0f / sqrtf(ms + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += 256) out[base + i] = xr[i] * wr[i] * rms;
+}
+
+// ------------------------------------------------------------------------------------------
+// QK-norm + NeoX RoPE (kernels/qk_norm_rope.comp:23-67): one wavefront per (row, head).
+
+// In place (out == x) is allowed: a wavefront reads its head before writing it.
+__global__ __launch_bounds__(256) void k_qk_norm_rope(const float *x, const float *__restrict__ w,
+                                                      const float *__restrict__ freq, float *out,
+                                                      uint32_t n_heads, uint32_t hd, uint32_t rope_dim, uint32_t pos0,
+                                                      uint32_t units, float eps) {
+    __shared__ float nrm[4][256];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t unit = blockIdx.x * 4 + wave;  // (row, head)
+    const bool live = unit < units;
+    const uint32_t row = live ? unit / n_heads : 0, head = live ? unit % n_heads : 0;
+    const float *xh = x + (uint64_t)row * n_heads * hd + (uint64_t)head * hd;
+    float v[4];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t d = lane + 64 * j;
+        v[j] = (live && d < hd) ? xh[d] : 0.0f;
+        s = __builtin_fmaf(v[j], v[j], s);
+    }
+    const float ms = wave_sum(s) / (float)hd;
+    const float rms = 1.0f / sqrtf(ms + eps);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t d = lane + 64 * j;
+        if (d < hd) nrm[wave][d] = v[j] * w[d] * rms;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (!live) return;
+    const uint32_t half = rope_dim / 2, hd2 = hd / 2;
+    const float fpos = (float)(pos0 + row);
+    float *oh = out + (uint64_t)row * n_heads * hd + (uint64_t)head * hd;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t d = lane + 64 * j;
+        if (d >= hd) continue;
+        const float n = nrm[wave][d];
+        if (d >= rope_dim) {
+            oh[d] = n;
+            continue;
+        }
+        const float ang = freq[d % half] * fpos;
+        const float c = cosf(ang), sn = sinf(ang);
+        oh[d] = d < half ? n * c - nrm[wave][d + hd2] * sn : n * c + nrm[wave][d - hd2] * sn;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Attention, head_dim 128, matrix cores.
+//
+// Sequence: positions p < n0 come from (k0, v0) row p, positions n0 <= p < S from
+// (k1, v1) row p - n0 (the reference's K/V sequence without the host copy).  Query qi
+// of kv head h is (row t = qi / G, q head h*G + qi % G), at position qpos0 + t.
+
+constexpr uint32_t AHD = 128;       // head dim of the matrix-core path
+constexpr uint32_t ACH = 64;        // positions per chunk (workgroup)
+constexpr uint32_t AQ = 64;         // queries per kv head handled by one workgroup
+constexpr uint32_t KSTR = AHD + 8;  // bf16 row stride of the K tile (padding against bank conflicts)
+constexpr uint32_t VSTR = ACH + 8;  // bf16 row stride of the transposed V tile
+constexpr uint32_t PSTR = ACH + 8;  // bf16 row stride of P
+constexpr int NP = 3;               // bf16 parts per f32 operand
+
+// f32 operands enter the matrix cores as three bf16 parts x = x0 + x1 + x2, each the
+// nearest bf16 of what the previous parts leave: together all 24 significant bits.
+struct __attribute__((aligned(16))) AttnLds {
+    uint16_t k[NP][ACH * KSTR];
+    uint16_t v[NP][AHD * VSTR];  // transposed: [dim][position]
+    uint16_t p[NP][AQ * PSTR];
+};
+
+__device__ __forceinline__ void split3(float x, uint32_t &a, uint32_t &b, uint32_t &c) {
+    a = bf16_rne(x);
+    float r = x - bf16_f(a);  // exact
+    b = bf16_rne(r);
+    r -= bf16_f(b);           // exact
+    c = bf16_rne(r);
+}
+
+__device__ __forceinline__ bf16x8 ld_frag(const uint16_t *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(p));
+}
+
+__device__ __forceinline__ bf16x8 pack8(const uint32_t *h) {
+    return __builtin_bit_cast(bf16x8, make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16,
+                                                 h[6] | h[7] << 16));
+}
+
+// D += A B over the six part products that reach f32 precision (|a_i b_j| <= 2^-9(i+j)
+// |a b|; the three dropped ones are below 2^-26), smallest first.
+__device__ __forceinline__ f32x4 mfma6(const bf16x8 *a, const bf16x8 *b, f32x4 d) {
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], d, 0, 0, 0);
+    return d;
+}
+
+// Partials per (kv head, chunk, query): O (unnormalised, AHD floats), max, sum.
+// Wavefront w owns queries 16w..16w+15 (A operands in registers), all 64 positions
+// of the chunk (K tile in LDS) and all 128 output dims (V tile in LDS).
+__global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q, const float *__restrict__ k0,
+                                                    const float *__restrict__ v0, uint32_t n0,
+                                                    const float *__restrict__ k1, const float *__restrict__ v1,
+                                                    uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv,
+                                                    uint32_t qpos0, int causal, float scale, uint32_t nch,
+                                                    float *__restrict__ part_o, float *__restrict__ part_ml) {
+    __shared__ AttnLds L;
+    const uint32_t h = blockIdx.y, c = blockIdx.x;
+    const uint32_t G = n_q / n_kv, nq = rows * G;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t l16 = lane & 15u, kg = lane >> 4;
+    const uint32_t kvld = n_kv * AHD, qld = n_q * AHD;
+
+    // K and V of the chunk's 64 positions, 4 floats per step, as bf16 parts
+    for (uint32_t e = tid; e < ACH * AHD / 4; e += 256) {
+        const uint32_t pi = e / (AHD / 4), d = 4 * (e % (AHD / 4));
+        const uint32_t p = c * ACH + pi;
+        float4 kv = make_float4(0, 0, 0, 0), vv = kv;
+        if (p < S) {
+            const bool s0 = p < n0;
+            const uint64_t off = (uint64_t)(s0 ? p : p - n0) * kvld + h * AHD + d;
+            kv = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + off);
+            vv = *reinterpret_cast<const float4 *>((s0 ? v0 : v1) + off);
+        }
+        const float fk[4] = {kv.x, kv.y, kv.z, kv.w}, fv[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t a, b, cc;
+            split3(fk[i], a, b, cc);
+            L.k[0][pi * KSTR + d + i] = (uint16_t)a;
+            L.k[1][pi * KSTR + d + i] = (uint16_t)b;
+            L.k[2][pi * KSTR + d + i] = (uint16_t)cc;
+            split3(fv[i], a, b, cc);
+            L.v[0][(d + i) * VSTR + pi] = (uint16_t)a;
+            L.v[1][(d + i) * VSTR + pi] = (uint16_t)b;
+            L.v[2][(d + i) * VSTR + pi] = (uint16_t)cc;
+        }
+    }
+    // this lane's query row: A operand fragments for the 4 k-steps, straight from HBM
+    const uint32_t qr = 16 * wave + l16;
+    bf16x8 qa[AHD / 32][NP];
+    {
+        const bool live = qr < nq;
+        const uint32_t t = live ? qr / G : 0, hq = live ? h * G + qr % G : 0;
+        const float *qp = q + (uint64_t)t * qld + hq * AHD + 8 * kg;
+#pragma unroll
+        for (int ks = 0; ks < (int)(AHD / 32); ks++) {
+            float4 x0 = make_float4(0, 0, 0, 0), x1 = x0;
+            if (live) {
+                x0 = *reinterpret_cast<const float4 *>(qp + 32 * ks);
+                x1 = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
+            }
+            const float f[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            uint32_t hp[NP][8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) split3(f[i], hp[0][i], hp[1][i], hp[2][i]);
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) qa[ks][pp] = pack8(hp[pp]);
+        }
+    }
+    __syncthreads();
+
+    // S = Q K^T for query rows 16*wave .. +15 and the 4 position tiles
+    f32x4 Sd[4];
+#pragma unroll
+    for (int pt = 0; pt < 4; pt++) Sd[pt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < (int)(AHD / 32); ks++) {
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) {
+            const uint32_t ko = (16 * pt + l16) * KSTR + 32 * ks + 8 * kg;
+            const bf16x8 kb[NP] = {ld_frag(L.k[0] + ko), ld_frag(L.k[1] + ko), ld_frag(L.k[2] + ko)};
+            Sd[pt] = mfma6(qa[ks], kb, Sd[pt]);
+        }
+    }
+    // scale, mask, row max / sum; lane holds rows 16w + 4kg + r, columns 16pt + l16
+    float mrow[4], lrow[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t qi = 16 * wave + 4 * kg + r;
+        const uint32_t qpos = qi < nq ? qpos0 + qi / G : 0;
+        float m = -INFINITY;
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) {
+            const uint32_t p = c * ACH + 16 * pt + l16;
+            const bool ok = qi < nq && p < S && (!causal || p <= qpos);
+            const float sv = ok ? Sd[pt][r] * scale : -INFINITY;
+            Sd[pt][r] = sv;
+            m = fmaxf(m, sv);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float mu = m == -INFINITY ? 0.0f : m;  // a fully masked row has P = 0
+        float l = 0.0f;
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) {
+            const float pv = expf(Sd[pt][r] - mu);
+            Sd[pt][r] = pv;
+            l += pv;
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
+        mrow[r] = m, lrow[r] = l;
+    }
+    // P to LDS (rows of this wave only) as bf16 parts in A-operand order
+#pragma unroll
+    for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t idx = (16 * wave + 4 * kg + r) * PSTR + 16 * pt + l16;
+            uint32_t a, b, cc;
+            split3(Sd[pt][r], a, b, cc);
+            L.p[0][idx] = (uint16_t)a;
+            L.p[1][idx] = (uint16_t)b;
+            L.p[2][idx] = (uint16_t)cc;
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // O = P V for this wave's 16 query rows and the 8 dimension tiles
+    f32x4 Od[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) Od[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < (int)(ACH / 32); ks++) {
+        const uint32_t po = (16 * wave + l16) * PSTR + 32 * ks + 8 * kg;
+        const bf16x8 pa[NP] = {ld_frag(L.p[0] + po), ld_frag(L.p[1] + po), ld_frag(L.p[2] + po)};
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const uint32_t vo = (16 * dt + l16) * VSTR + 32 * ks + 8 * kg;
+            const bf16x8 vb[NP] = {ld_frag(L.v[0] + vo), ld_frag(L.v[1] + vo), ld_frag(L.v[2] + vo)};
+            Od[dt] = mfma6(pa, vb, Od[dt]);
+        }
+    }
+    // partials: O[q][d], (m, l)[q]
+    const uint64_t pbase = ((uint64_t)h * nch + c) * AQ;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t qi = 16 * wave + 4 * kg + r;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) part_o[(pbase + qi) * AHD + 16 * dt + l16] = Od[dt][r];
+        if (l16 == 0) {
+            part_ml[2 * (pbase + qi)] = mrow[r];
+            part_ml[2 * (pbase + qi) + 1] = lrow[r];
+        }
+    }
+}
+
+// out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c; one wavefront per query.
+__global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
+                                                      const float *__restrict__ part_ml, float *__restrict__ out,
+                                                      uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t gq = blockIdx.x * 4 + (threadIdx.x >> 6);  // over n_kv * AQ
+    const uint32_t G = n_q / n_kv;
+    const uint32_t h = gq / AQ, qi = gq % AQ;
+    if (h >= n_kv || qi >= rows * G) return;
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < nch; c++) M = fmaxf(M, part_ml[2 * (((uint64_t)h * nch + c) * AQ + qi)]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint64_t pq = ((uint64_t)h * nch + c) * AQ + qi;
+        const float mc = part_ml[2 * pq];
+        const float wgt = mc == -INFINITY ? 0.0f : expf(mc - M);
+        L = __builtin_fmaf(wgt, part_ml[2 * pq + 1], L);
+        o0 = __builtin_fmaf(wgt, part_o[pq * AHD + lane], o0);
+        o1 = __builtin_fmaf(wgt, part_o[pq * AHD + 64 + lane], o1);
+    }
+    const uint32_t t = qi / G, hq = h * G + qi % G;
+    float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    o[lane] = o0 * inv;
+    o[64 + lane] = o1 * inv;
+}
+
+// Any head_dim <= 256: one wavefront per (row, q head), online softmax as mha_attn.comp.
+__global__ __launch_bounds__(256) void k_attn_simple(const float *__restrict__ q, const float *__restrict__ k0,
+                                                     const float *__restrict__ v0, uint32_t n0,
+                                                     const float *__restrict__ k1, const float *__restrict__ v1,
+                                                     uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv,
+                                                     uint32_t hd, uint32_t qpos0, int causal, float scale,
+                                                     float *__restrict__ out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t unit = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (unit >= rows * n_q) return;
+    const uint32_t r = unit / n_q, hq = unit % n_q, kh = hq * n_kv / n_q;
+    const float *qh = q + (uint64_t)r * n_q * hd + hq * hd;
+    float qv[4], acc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; j++) qv[j] = lane + 64 * j < hd ? qh[lane + 64 * j] : 0.0f;
+    const uint32_t end = causal ? (qpos0 + r + 1 < S ? qpos0 + r + 1 : S) : S;
+    float m = -INFINITY, l = 0.0f;
+    for (uint32_t p = 0; p < end; p++) {
+        const bool s0 = p < n0;
+        const uint64_t off = (uint64_t)(s0 ? p : p - n0) * n_kv * hd + kh * hd;
+        const float *kp = (s0 ? k0 : k1) + off, *vp = (s0 ? v0 : v1) + off;
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j < hd) d = __builtin_fmaf(qv[j], kp[lane + 64 * j], d);
+        const float s = wave_sum(d) * scale;
+        const float mn = fmaxf(m, s);
+        const float corr = expf(m - mn), wgt = expf(s - mn);
+        l = l * corr + wgt;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (lane + 64 * j < hd) acc[j] = acc[j] * corr + wgt * vp[lane + 64 * j];
+        m = mn;
+    }
+    float *oh = out + (uint64_t)r * n_q * hd + hq * hd;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        if (lane + 64 * j < hd) oh[lane + 64 * j] = l > 0.0f ? acc[j] / l : 0.0f;
+}
+
+// ------------------------------------------------------------------------------------------
+// elementwise
+
+__global__ __launch_bounds__(256) void k_gate_mul(const float *v, const float *__restrict__ gate, float *out, uint32_t n_heads, uint32_t hd,
+                                                  uint64_t total, int softplus) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const uint64_t row = i / ((uint64_t)n_heads * hd);
+    const uint32_t head = (uint32_t)(i % ((uint64_t)n_heads * hd)) / hd;
+    float g = gate[row * n_heads + head];
+    if (softplus) g = g > 20.0f ? g : logf(1.0f + expf(g));  // src/dflash.rs:957
+    out[i] = v[i] * g;
+}
+
+__global__ __launch_bounds__(256) void k_add(const float *a, const float *b, float *out, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void k_copy(const float *__restrict__ src, float *__restrict__ dst, uint64_t n) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+inline unsigned blocks_for(uint64_t n) { return (unsigned)((n + 255) / 256); }
+
+// ------------------------------------------------------------------------------------------
+// launchers shared by the C entry points and the forward
+
+int run_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, uint32_t chunks, uint32_t ldx,
+                float eps, hipStream_t s) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows, chunks), dim3(256), 0, s, x, w, out, n, ldx, eps);
+    return after_launch("rmsnorm", s);
+}
+
+int run_qk_norm_rope(const float *x, const float *w, const float *freq, float *out, uint32_t n_heads, uint32_t hd,
+                     uint32_t rope_dim, uint32_t pos, uint32_t rows, float eps, hipStream_t s) {
+    const uint32_t units = rows * n_heads;
+    hipLaunchKernelGGL(k_qk_norm_rope, dim3((units + 3) / 4), dim3(256), 0, s, x, w, freq, out, n_heads, hd, rope_dim,
+                       pos, units, eps);
+    return after_launch("qk_norm_rope", s);
+}
+
+size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
+    const uint32_t nch = (S + ACH - 1) / ACH;
+    return (size_t)n_kv * nch * AQ * (AHD + 2);
+}
+
+// `part` holds attn_partial_floats(S, n_kv) floats when the matrix-core path applies.
+int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0, const float *k1, const float *v1,
+                  uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t qpos0, int causal,
+                  float *out, float *part, hipStream_t s) {
+    const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
+    const uint32_t G = n_q / n_kv;
+    if (part && hd == AHD && rows * G <= AQ) {
+        const uint32_t nch = (S + ACH - 1) / ACH;
+        float *part_ml = part + (size_t)n_kv * nch * AQ * AHD;
+        hipLaunchKernelGGL(k_attn_chunk, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S,
+                           rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
+        int st = after_launch("attn_chunk", s);
+        if (st != LG_OK) return st;
+        hipLaunchKernelGGL(k_attn_combine, dim3((n_kv * AQ + 3) / 4), dim3(256), 0, s, part, part_ml, out, rows, n_q,
+                           n_kv, nch);
+        return after_launch("attn_combine", s);
+    }
+    hipLaunchKernelGGL(k_attn_simple, dim3((rows * n_q + 3) / 4), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S, rows,
+                       n_q, n_kv, hd, qpos0, causal, scale, out);
+    return after_launch("attn_simple", s);
+}
+
+// Per-device scratch for lg_dispatch_mha_attn's partials (grown on demand).
+struct Scratch {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+std::vector<Scratch> g_attn_scratch;
+std::mutex g_scratch_mu;
+
+int scratch(std::vector<Scratch> &v, size_t need, void **out) {
+    int dev = 0;
+    LG_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((size_t)dev >= v.size()) v.resize(dev + 1);
+    Scratch &sc = v[dev];
+    if (sc.bytes < need) {
+        if (sc.ptr) {
+            LG_HIP_TRY(hipDeviceSynchronize());  // earlier launches may still use it
+            LG_HIP_TRY(hipFree(sc.ptr));
+        }
+        sc.ptr = nullptr;
+        sc.bytes = 0;
+        const size_t sz = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+        if (hipMalloc(&sc.ptr, sz) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(LG_ENOMEM, "scratch (%zu bytes)", sz);
+        }
+        sc.bytes = sz;
+    }
+    *out = sc.ptr;
+    return LG_OK;
+}
+
+// ------------------------------------------------------------------------------------------
+// forward
+
+constexpr uint64_t FREQ_BYTES = 1024;  // rope_dim <= head_dim <= 256: at most 128 frequencies
+
+// Device workspace of one block forward: every intermediate, the RoPE table, the
+// attention partials and the small-M product workspace.  The eager entry points
+// share one per device (grown on demand); a graph owns its own, since a captured
+// graph keeps the addresses it was recorded with.
+struct FwdLayout {
+    float *xe, *nxe, *kk, *vv, *q, *att, *gate, *o, *h, *g, *u, *feat_n, *part, *freq;
+    void *pws;
+    uint64_t pws_bytes, total;
+};
+
+uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8_t *base, FwdLayout &L) {
+    const uint64_t E = hp.n_embd, QD = (uint64_t)hp.n_heads * hp.head_dim, KVD = (uint64_t)hp.n_kv_heads * hp.head_dim;
+    const uint64_t FF = hp.n_ff, A = (uint64_t)hp.n_aux * hp.n_embd;
+    const uint32_t S = ctx_len + 2 * m;
+    const uint64_t floats[] = {2 * m * E, 2 * m * E, 2 * m * KVD, 2 * m * KVD,  m * QD, m * QD,
+                               (uint64_t)m * hp.n_heads,          m * E,        m * E,  m * FF, m * FF, m * A,
+                               attn_partial_floats(S, hp.n_kv_heads)};
+    float **dst[] = {&L.xe, &L.nxe, &L.kk, &L.vv, &L.q, &L.att, &L.gate, &L.o, &L.h, &L.g, &L.u, &L.feat_n, &L.part};
+    // the RoPE table sits at offset 0 whatever (m, ctx_len) are, so an uploaded
+    // table stays valid across calls that lay the same workspace out differently
+    L.freq = reinterpret_cast<float *>(base);
+    uint64_t off = FREQ_BYTES;
+    for (size_t i = 0; i < sizeof(floats) / sizeof(floats[0]); i++) {
+        *dst[i] = reinterpret_cast<float *>(base + off);
+        off += (floats[i] * 4 + 255) & ~(uint64_t)255;
+    }
+    uint64_t pw = 0;
+    const uint64_t cand[] = {proj_batch_ws_bytes(hp.n_embd, 2 * m, LG_F32), proj_batch_ws_bytes(hp.n_embd, m, LG_F32),
+                             proj_batch_ws_bytes(hp.n_heads * hp.head_dim, m, LG_F32),
+                             proj_batch_ws_bytes(hp.n_ff, m, LG_F32),
+                             proj_batch_ws_bytes(hp.n_aux * hp.n_embd, m, LG_F32)};
+    for (uint64_t c : cand) pw = c > pw ? c : pw;
+    L.pws = base + off;
+    L.pws_bytes = pw;
+    L.total = off + ((pw + 255) & ~(uint64_t)255);
+    return L.total;
+}
+
+// f32 RoPE frequency table exactly as the reference computes it on the host
+// (src/dflash.rs:898-904: 1.0 / base.powf((2.0 * i as f32) / rope_dim as f32)).
+std::vector<float> rope_table(const lg_dflash_hparams &hp) {
+    std::vector<float> f(hp.rope_dim / 2 + 1, 0.0f);
+    const float base = hp.rope_base > 0.0f ? hp.rope_base : 500000.0f;
+    for (uint32_t i = 0; i < hp.rope_dim / 2; i++)
+        f[i] = 1.0f / std::pow(base, (2.0f * (float)i) / (float)hp.rope_dim);
+    return f;
+}
+
+// A workspace with its table uploaded for (rope_dim, rope_base).
+struct Ws {
+    uint8_t *base = nullptr;
+    uint64_t bytes = 0;
+    uint32_t rope_dim = 0xFFFFFFFFu;
+    float rope_base = 0.0f;
+};
+
+int ws_alloc(Ws &w, uint64_t need) {
+    if (w.bytes >= need) return LG_OK;
+    if (w.base) {
+        LG_HIP_TRY(hipDeviceSynchronize());  // earlier launches may still use it
+        LG_HIP_TRY(hipFree(w.base));
+    }
+    w = Ws();
+    const uint64_t sz = (need + (1u << 20) - 1) & ~(uint64_t)((1u << 20) - 1);
+    void *p = nullptr;
+    if (hipMalloc(&p, sz) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(LG_ENOMEM, "draft forward workspace (%llu bytes)", (unsigned long long)sz);
+    }
+    w.base = static_cast<uint8_t *>(p);
+    w.bytes = sz;
+    return LG_OK;
+}
+
+int ws_table(Ws &w, const lg_dflash_hparams &hp, const FwdLayout &L, hipStream_t s) {
+    if (w.rope_dim == hp.rope_dim && w.rope_base == hp.rope_base) return LG_OK;
+    const std::vector<float> f = rope_table(hp);
+    LG_HIP_TRY(hipMemcpyAsync(L.freq, f.data(), f.size() * 4, hipMemcpyHostToDevice, s));
+    LG_HIP_TRY(hipStreamSynchronize(s));  // f is released on return
+    w.rope_dim = hp.rope_dim;
+    w.rope_base = hp.rope_base;
+    return LG_OK;
+}
+
+std::vector<Ws> g_ws;  // eager calls, per device (guarded by g_scratch_mu)
+
+// The per-device eager workspace laid out for (hp, m, ctx_len), table uploaded.
+int eager_ws(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, FwdLayout &L, hipStream_t s) {
+    int dev = 0;
+    LG_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
+    Ws &w = g_ws[dev];
+    LG_TRY(ws_alloc(w, layout(hp, m, ctx_len, nullptr, L)));
+    layout(hp, m, ctx_len, w.base, L);
+    return ws_table(w, hp, L, s);
+}
+
+// with_layers = false checks what the encoder needs only.
+int check_model(const lg_dflash_model *md, uint32_t m, const char *name, bool with_layers = true) {
+    LG_REQUIRE(md, "%s: null model", name);
+    const lg_dflash_hparams &hp = md->hp;
+    LG_REQUIRE(m >= 1 && m <= 32, "%s: m = %u (1..32)", name, m);
+    LG_REQUIRE(hp.n_embd && hp.n_aux, "%s: zero n_embd or n_aux", name);
+    LG_REQUIRE(md->enc_aux_norm && md->fc && md->enc_output_norm, "%s: missing encoder tensor", name);
+    if (!with_layers) return LG_OK;
+    LG_REQUIRE(md->layers && hp.n_layers, "%s: no layers", name);
+    LG_REQUIRE(hp.n_heads && hp.n_kv_heads && hp.head_dim && hp.n_ff, "%s: zero hyperparameter", name);
+    LG_REQUIRE(hp.n_heads % hp.n_kv_heads == 0, "%s: n_heads %u not a multiple of n_kv_heads %u", name, hp.n_heads,
+               hp.n_kv_heads);
+    LG_REQUIRE(hp.head_dim <= 256 && hp.head_dim % 2 == 0 && (hp.rope_dim == 0 || hp.rope_dim == hp.head_dim),
+               "%s: head_dim %u / rope_dim %u unsupported (rope_dim must be 0 or head_dim)", name, hp.head_dim,
+               hp.rope_dim);
+    for (uint32_t l = 0; l < hp.n_layers; l++) {
+        const lg_dflash_layer &L = md->layers[l];
+        LG_REQUIRE(L.attn_norm && L.attn_q_norm && L.attn_k_norm && L.ffn_norm && L.attn_q && L.attn_k && L.attn_v &&
+                       L.attn_gate && L.attn_output && L.ffn_gate && L.ffn_up && L.ffn_down,
+                   "%s: layer %u is missing a tensor", name, l);
+    }
+    return LG_OK;
+}
+
+int proj(const FwdLayout &W, const float *x, const void *w, int type, float *c, uint32_t k, uint32_t n, uint32_t m,
+         hipStream_t s) {
+    return proj_batch(x, LG_F32, w, c, k, n, m, type, W.pws, W.pws_bytes, s);
+}
+
+// DFlashModel::encode (src/dflash.rs:157-234) on m feature rows.
+int encode(const lg_dflash_model *md, const FwdLayout &W, const float *features, uint32_t m, float *out,
+           hipStream_t s) {
+    const lg_dflash_hparams &hp = md->hp;
+    const uint32_t E = hp.n_embd, A = hp.n_aux * hp.n_embd;
+    LG_TRY(run_rmsnorm(features, md->enc_aux_norm, W.feat_n, E, m, hp.n_aux, A, hp.rms_eps, s));
+    LG_TRY(proj(W, W.feat_n, md->fc, md->fc_type, W.o, A, E, m, s));
+    return run_rmsnorm(W.o, md->enc_output_norm, out, E, m, 1, E, hp.rms_eps, s);
+}
+
+// Block generalisation of DFlashModel::forward_injected_decode_hidden
+// (src/dflash.rs:877-976): m tokens over ctx_len cached positions.
+int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features, const float *tokens, uint32_t m,
+            uint32_t ctx_len, float *out, hipStream_t s) {
+    const lg_dflash_hparams &hp = md->hp;
+    const uint32_t E = hp.n_embd, H = hp.n_heads, KV = hp.n_kv_heads, HD = hp.head_dim, FF = hp.n_ff;
+    const uint32_t QD = H * HD, KVD = KV * HD;
+    const uint64_t mE = (uint64_t)m * E;
+    // rows 0..m-1 of xe: encoder output (fixed over the layers), rows m..2m-1: the hidden x
+    LG_TRY(encode(md, W, features, m, W.xe, s));
+    float *x = W.xe + mE;
+    hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, tokens, x, mE);
+    LG_TRY(after_launch("copy tokens", s));
+    for (uint32_t li = 0; li < hp.n_layers; li++) {
+        const lg_dflash_layer &L = md->layers[li];
+        const float *nx = W.nxe + mE;
+        // attn_norm of the injected rows and the tokens in one launch (src/dflash.rs:917-923, :927)
+        LG_TRY(run_rmsnorm(W.xe, L.attn_norm, W.nxe, E, 2 * m, 1, E, hp.rms_eps, s));
+        // K, V of [injected; tokens] at positions ctx_len .. ctx_len + 2m - 1 (src/dflash.rs:924-941)
+        LG_TRY(proj(W, W.nxe, L.attn_k, L.attn_k_type, W.kk, E, KVD, 2 * m, s));
+        LG_TRY(proj(W, W.nxe, L.attn_v, L.attn_v_type, W.vv, E, KVD, 2 * m, s));
+        LG_TRY(proj(W, nx, L.attn_q, L.attn_q_type, W.q, E, QD, m, s));
+        LG_TRY(proj(W, nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, m, s));
+        LG_TRY(run_qk_norm_rope(W.kk, L.attn_k_norm, W.freq, W.kk, KV, HD, hp.rope_dim, ctx_len, 2 * m, hp.qk_eps, s));
+        LG_TRY(run_qk_norm_rope(W.q, L.attn_q_norm, W.freq, W.q, H, HD, hp.rope_dim, ctx_len + m, m, hp.qk_eps, s));
+        // causal attention over [context; injected; tokens] (src/dflash.rs:945-954)
+        LG_TRY(run_attention(W.q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
+                             W.att, W.part, s));
+        hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for((uint64_t)m * QD)), dim3(256), 0, s, W.att, W.gate, W.att, H,
+                           HD, (uint64_t)m * QD, 1);
+        LG_TRY(after_launch("softplus_gate_mul", s));
+        LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, W.o, QD, E, m, s));
+        hipLaunchKernelGGL(k_add, dim3(blocks_for(mE)), dim3(256), 0, s, x, W.o, x, mE);
+        LG_TRY(after_launch("residual", s));
+        // SwiGLU FFN (src/dflash.rs:962-968)
+        LG_TRY(run_rmsnorm(x, L.ffn_norm, W.h, E, m, 1, E, hp.rms_eps, s));
+        LG_TRY(proj(W, W.h, L.ffn_gate, L.ffn_gate_type, W.g, E, FF, m, s));
+        LG_TRY(proj(W, W.h, L.ffn_up, L.ffn_up_type, W.u, E, FF, m, s));
+        LG_TRY(lg_dispatch_activation(W.g, W.u, W.g, m * FF, s));
+        LG_TRY(proj(W, W.g, L.ffn_down, L.ffn_down_type, W.o, FF, E, m, s));
+        hipLaunchKernelGGL(k_add, dim3(blocks_for(mE)), dim3(256), 0, s, x, W.o, x, mE);
+        LG_TRY(after_launch("residual", s));
+    }
+    if (md->output_norm) return run_rmsnorm(x, md->output_norm, out, E, m, 1, E, hp.rms_eps, s);
+    hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, x, out, mE);
+    return after_launch("copy hidden", s);
+}
+
+struct Graph {
+    hipGraph_t g = nullptr;
+    hipGraphExec_t exec = nullptr;
+    Ws ws;
+};
+
+void graph_free(Graph *G) {
+    if (G->exec) (void)hipGraphExecDestroy(G->exec);
+    if (G->g) (void)hipGraphDestroy(G->g);
+    if (G->ws.base) (void)hipFree(G->ws.base);
+    delete G;
+}
+
+int check_forward(const lg_dflash_model *md, const float *features, const float *tokens, uint32_t m,
+                  uint32_t ctx_len, float *out, const char *name) {
+    LG_TRY(check_model(md, m, name));
+    LG_REQUIRE(features && tokens && out, "%s: null input or output", name);
+    if (ctx_len)
+        for (uint32_t l = 0; l < md->hp.n_layers; l++)
+            LG_REQUIRE(md->layers[l].k_ctx && md->layers[l].v_ctx, "%s: layer %u has no context cache", name, l);
+    return LG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lg_dispatch_rmsnorm(const float *w, const float *x, float *out, uint32_t n, uint32_t rows, float eps,
+                        void *stream) {
+    clear_error();
+    if (n == 0 || rows == 0) return LG_OK;
+    LG_REQUIRE(w && x && out, "lg_dispatch_rmsnorm: null pointer");
+    LG_EXTENT(x, (uint64_t)n * rows * 4, "lg_dispatch_rmsnorm x");
+    LG_EXTENT(out, (uint64_t)n * rows * 4, "lg_dispatch_rmsnorm out");
+    LG_EXTENT(w, (uint64_t)n * 4, "lg_dispatch_rmsnorm w");
+    return run_rmsnorm(x, w, out, n, rows, 1, n, eps, (hipStream_t)stream);
+}
+
+int lg_dispatch_enc_aux_norm(const float *x, const float *aux_norm_w, float *out, uint32_t n_feat, uint32_t n_aux,
+                             uint32_t n_tokens, float eps, void *stream) {
+    clear_error();
+    if (n_feat == 0 || n_aux == 0 || n_tokens == 0) return LG_OK;
+    LG_REQUIRE(x && aux_norm_w && out, "lg_dispatch_enc_aux_norm: null pointer");
+    const uint64_t tot = (uint64_t)n_feat * n_aux * n_tokens * 4;
+    LG_EXTENT(x, tot, "lg_dispatch_enc_aux_norm x");
+    LG_EXTENT(out, tot, "lg_dispatch_enc_aux_norm out");
+    LG_EXTENT(aux_norm_w, (uint64_t)n_feat * n_aux * 4, "lg_dispatch_enc_aux_norm w");
+    return run_rmsnorm(x, aux_norm_w, out, n_feat, n_tokens, n_aux, n_feat * n_aux, eps, (hipStream_t)stream);
+}
+
+int lg_dispatch_qk_norm_rope(const float *x, const float *norm_w, const float *freq, float *out, uint32_t n_heads,
+                             uint32_t head_dim, uint32_t rope_dim, uint32_t pos, uint32_t rows, float eps,
+                             void *stream) {
+    clear_error();
+    if (n_heads == 0 || rows == 0 || head_dim == 0) return LG_OK;
+    LG_REQUIRE(x && norm_w && out && (freq || rope_dim == 0), "lg_dispatch_qk_norm_rope: null pointer");
+    LG_REQUIRE(head_dim <= 256 && head_dim % 2 == 0 && (rope_dim == 0 || rope_dim == head_dim),
+               "lg_dispatch_qk_norm_rope: head_dim %u / rope_dim %u unsupported (rope_dim must be 0 or head_dim)",
+               head_dim, rope_dim);
+    const uint64_t tot = (uint64_t)rows * n_heads * head_dim * 4;
+    LG_EXTENT(x, tot, "lg_dispatch_qk_norm_rope x");
+    LG_EXTENT(out, tot, "lg_dispatch_qk_norm_rope out");
+    LG_EXTENT(norm_w, (uint64_t)head_dim * 4, "lg_dispatch_qk_norm_rope norm_w");
+    return run_qk_norm_rope(x, norm_w, freq, out, n_heads, head_dim, rope_dim, pos, rows, eps, (hipStream_t)stream);
+}
+
+int lg_dispatch_mha_attn(const float *q, const float *k_seq, const float *v_seq, float *out, uint32_t n_q_heads,
+                         uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len, uint32_t q_pos, uint32_t rows,
+                         int causal, void *stream) {
+    clear_error();
+    const char *name = "lg_dispatch_mha_attn";
+    if (rows == 0 || n_q_heads == 0) return LG_OK;
+    LG_REQUIRE(q && out && (seq_len == 0 || (k_seq && v_seq)), "%s: null pointer", name);
+    LG_REQUIRE(n_kv_heads && n_q_heads % n_kv_heads == 0, "%s: n_q %u, n_kv %u", name, n_q_heads, n_kv_heads);
+    LG_REQUIRE(head_dim && head_dim <= 256, "%s: head_dim %u unsupported", name, head_dim);
+    LG_EXTENT(q, (uint64_t)rows * n_q_heads * head_dim * 4, name);
+    LG_EXTENT(out, (uint64_t)rows * n_q_heads * head_dim * 4, name);
+    if (seq_len) {
+        LG_EXTENT(k_seq, (uint64_t)seq_len * n_kv_heads * head_dim * 4, name);
+        LG_EXTENT(v_seq, (uint64_t)seq_len * n_kv_heads * head_dim * 4, name);
+    }
+    hipStream_t s = (hipStream_t)stream;
+    float *part = nullptr;
+    const uint32_t G = n_q_heads / n_kv_heads;
+    if (head_dim == AHD && rows * G <= AQ && seq_len) {
+        void *p = nullptr;
+        LG_TRY(scratch(g_attn_scratch, attn_partial_floats(seq_len, n_kv_heads) * 4, &p));
+        part = static_cast<float *>(p);
+    }
+    return run_attention(q, k_seq, v_seq, seq_len, nullptr, nullptr, seq_len, rows, n_q_heads, n_kv_heads, head_dim,
+                         q_pos, causal, out, part, s);
+}
+
+int lg_dispatch_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
+                         uint32_t rows, void *stream) {
+    clear_error();
+    const uint64_t total = (uint64_t)rows * n_heads * head_dim;
+    if (total == 0) return LG_OK;
+    LG_REQUIRE(v && gate && out, "lg_dispatch_gate_mul: null pointer");
+    LG_EXTENT(v, total * 4, "lg_dispatch_gate_mul v");
+    LG_EXTENT(out, total * 4, "lg_dispatch_gate_mul out");
+    LG_EXTENT(gate, (uint64_t)rows * n_heads * 4, "lg_dispatch_gate_mul gate");
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, v, gate, out, n_heads, head_dim, total, 0);
+    return after_launch("lg_dispatch_gate_mul", s);
+}
+
+int lg_dispatch_softplus_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
+                                  uint32_t rows, void *stream) {
+    clear_error();
+    const uint64_t total = (uint64_t)rows * n_heads * head_dim;
+    if (total == 0) return LG_OK;
+    LG_REQUIRE(v && gate && out, "lg_dispatch_softplus_gate_mul: null pointer");
+    LG_EXTENT(v, total * 4, "lg_dispatch_softplus_gate_mul v");
+    LG_EXTENT(out, total * 4, "lg_dispatch_softplus_gate_mul out");
+    LG_EXTENT(gate, (uint64_t)rows * n_heads * 4, "lg_dispatch_softplus_gate_mul gate");
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, v, gate, out, n_heads, head_dim, total, 1);
+    return after_launch("lg_dispatch_softplus_gate_mul", s);
+}
+
+int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream) {
+    clear_error();
+    if (n == 0) return LG_OK;
+    LG_REQUIRE(a && b && out, "lg_dispatch_add: null pointer");
+    LG_EXTENT(a, (uint64_t)n * 4, "lg_dispatch_add a");
+    LG_EXTENT(b, (uint64_t)n * 4, "lg_dispatch_add b");
+    LG_EXTENT(out, (uint64_t)n * 4, "lg_dispatch_add out");
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_add, dim3(blocks_for(n)), dim3(256), 0, s, a, b, out, (uint64_t)n);
+    return after_launch("lg_dispatch_add", s);
+}
+
+int lg_dflash_encode(const lg_dflash_model *model, const float *features, uint32_t m, float *out, void *stream) {
+    clear_error();
+    LG_TRY(check_model(model, m, "lg_dflash_encode", false));
+    LG_REQUIRE(features && out, "lg_dflash_encode: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    FwdLayout W;
+    LG_TRY(eager_ws(model->hp, m, 0, W, s));
+    int st;
+    {
+        DeferSync d;
+        st = encode(model, W, features, m, out, s);
+    }
+    return st != LG_OK ? st : after_launch("lg_dflash_encode", s);
+}
+
+int lg_dflash_forward_block(const lg_dflash_model *model, const float *features, const float *tokens, uint32_t m,
+                            uint32_t ctx_len, float *out, void *stream) {
+    clear_error();
+    LG_TRY(check_forward(model, features, tokens, m, ctx_len, out, "lg_dflash_forward_block"));
+    hipStream_t s = (hipStream_t)stream;
+    FwdLayout W;
+    LG_TRY(eager_ws(model->hp, m, ctx_len, W, s));
+    int st;
+    {
+        DeferSync d;
+        st = forward(model, W, features, tokens, m, ctx_len, out, s);
+    }
+    return st != LG_OK ? st : after_launch("lg_dflash_forward_block", s);
+}
+
+int lg_dflash_graph_create(const lg_dflash_model *model, const float *features, const float *tokens, uint32_t m,
+                           uint32_t ctx_len, float *out, void *stream, void **graph) {
+    clear_error();
+    const char *name = "lg_dflash_graph_create";
+    LG_REQUIRE(graph, "%s: null graph", name);
+    LG_REQUIRE(stream, "%s: capture needs a created stream (not the null stream)", name);
+    LG_TRY(check_forward(model, features, tokens, m, ctx_len, out, name));
+    hipStream_t s = (hipStream_t)stream;
+    Graph *G = new Graph();
+    FwdLayout W;
+    int st = ws_alloc(G->ws, layout(model->hp, m, ctx_len, nullptr, W));
+    if (st == LG_OK) {
+        layout(model->hp, m, ctx_len, G->ws.base, W);
+        st = ws_table(G->ws, model->hp, W, s);
+    }
+    if (st == LG_OK) {  // one eager pass: every lazy set-up happens before capture
+        DeferSync d;
+        st = forward(model, W, features, tokens, m, ctx_len, out, s);
+    }
+    if (st == LG_OK && hipStreamSynchronize(s) != hipSuccess) st = fail(LG_EHIP, "%s: warm-up run failed", name);
+    if (st != LG_OK) {
+        graph_free(G);
+        return st;
+    }
+    hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        graph_free(G);
+        return fail(LG_EHIP, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    }
+    st = forward(model, W, features, tokens, m, ctx_len, out, s);
+    e = hipStreamEndCapture(s, &G->g);
+    if (st != LG_OK || e != hipSuccess) {
+        graph_free(G);
+        if (st != LG_OK) return st;
+        return fail(LG_EHIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    }
+    e = hipGraphInstantiate(&G->exec, G->g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        graph_free(G);
+        return fail(LG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    *graph = G;
+    return LG_OK;
+}
+
+int lg_dflash_graph_launch(void *graph, void *stream) {
+    clear_error();
+    LG_REQUIRE(graph, "lg_dflash_graph_launch: null graph");
+    hipStream_t s = (hipStream_t)stream;
+    LG_HIP_TRY(hipGraphLaunch(static_cast<Graph *>(graph)->exec, s));
+    return after_launch("lg_dflash_graph_launch", s);
+}
+
+int lg_dflash_graph_destroy(void *graph) {
+    clear_error();
+    if (!graph) return LG_OK;
+    graph_free(static_cast<Graph *>(graph));
+    return LG_OK;
+}
+
+}  // extern "C"

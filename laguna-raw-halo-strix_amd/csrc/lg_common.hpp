@@ -27,8 +27,15 @@ bool blocking();
             return ::lg::fail(LG_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));     \
     } while (0)
 
-// Check a launch and honour blocking mode.
+// Check a launch and honour blocking mode (no wait while the stream is being captured).
 int after_launch(const char *what, hipStream_t s);
+
+// While one lives, after_launch on this thread does not wait in blocking mode: a
+// multi-launch entry point waits once, at its end.
+struct DeferSync {
+    DeferSync();
+    ~DeferSync();
+};
 
 #define LG_REQUIRE(cond, ...)                                                             \
     do {                                                                                  \
@@ -39,6 +46,13 @@ int after_launch(const char *what, hipStream_t s);
     LG_REQUIRE(::lg::extent_ok((ptr), (bytes)),                                           \
                "%s: %llu bytes at %p run past the end of its lg_buf_alloc allocation",     \
                name, (unsigned long long)(bytes), (const void *)(ptr))
+
+// Small-M product behind lg_dispatch_proj_quant_batch.  ws == nullptr uses the
+// per-device workspace; otherwise ws holds at least proj_batch_ws_bytes(k, m,
+// x_dtype) bytes owned by the caller (graphs capture it, so it must outlive them).
+uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t m, int x_dtype);
+int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
+               void *ws, uint64_t ws_bytes, hipStream_t s);
 
 // ---- GGUF block geometry (src/gguf.rs:97,101,134,136)
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;

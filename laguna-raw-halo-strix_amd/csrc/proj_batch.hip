@@ -3,8 +3,9 @@
 // tiles on gfx950 (v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16]).
 //
 //   A = activations: 16 rows (tokens) x 32 k (one 32-element sub-block).  f32
-//       activations are split exactly into bf16 hi + bf16 lo (16 significant bits
-//       together); bf16 activations use one part.  A prep kernel writes them once
+//       activations are split exactly into three bf16 parts hi + mid + lo (each the
+//       nearest bf16 of what the previous parts leave: together all 24 significant
+//       bits, so the products are f32-grade); bf16 activations use one part.  A prep kernel writes them once
 //       per call in MFMA operand order, with the per-sub-block sums X of the
 //       represented values, into a device workspace.
 //   B = weight codes of 16 output rows x the same 32 k, built in registers from
@@ -42,38 +43,40 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_floa
 // Workspace layout, per 16-row tile tt and sub-block j (nsb = k/32 sub-blocks):
 //   frag[((tt*nsb + j)*parts + part)*64 + lane] : 8 bf16 (16 bytes)
 //   xsum[(tt*nsb + j)*16 + token]              : f32
-template <bool BF16_IN>
+template <int PARTS>
 __global__ __launch_bounds__(64) void k_prep_x(const void *__restrict__ xv, uint32_t m, uint32_t k,
                                                uint4 *__restrict__ frag, float *__restrict__ xsum) {
-    constexpr int parts = BF16_IN ? 1 : 2;
     const uint32_t nsb = k / 32;
     const uint32_t j = blockIdx.x, tt = blockIdx.y, l = threadIdx.x;
     const uint32_t tok = tt * 16 + (l & 15u), kg = l >> 4;
-    uint32_t hi[8], lo[8];
+    uint32_t pc[PARTS][8];
     float part = 0.0f;
 #pragma unroll
     for (int v = 0; v < 8; v++) {
         const uint32_t e = j * 32 + 8 * kg + PERM[v];
+#pragma unroll
+        for (int p = 0; p < PARTS; p++) pc[p][v] = 0;
         if (tok < m) {
-            if constexpr (BF16_IN) {
-                hi[v] = static_cast<const uint16_t *>(xv)[(uint64_t)tok * k + e];
-                lo[v] = 0;
-                part += bf16_to_f32(hi[v]);
+            if constexpr (PARTS == 1) {
+                pc[0][v] = static_cast<const uint16_t *>(xv)[(uint64_t)tok * k + e];
+                part += bf16_to_f32(pc[0][v]);
             } else {
                 const float x = static_cast<const float *>(xv)[(uint64_t)tok * k + e];
-                hi[v] = f32_to_bf16_rne(x);
-                const float r = x - bf16_to_f32(hi[v]);  // exact
-                lo[v] = f32_to_bf16_rne(r);
-                part += bf16_to_f32(hi[v]) + bf16_to_f32(lo[v]);
+                float r = x;
+#pragma unroll
+                for (int p = 0; p < PARTS; p++) {
+                    pc[p][v] = f32_to_bf16_rne(r);
+                    r -= bf16_to_f32(pc[p][v]);  // exact: r stays a multiple of x's last place
+                }
+                part += x;  // the parts sum to x exactly
             }
-        } else {
-            hi[v] = lo[v] = 0;
         }
     }
-    const uint64_t base = ((uint64_t)tt * nsb + j) * parts;
-    frag[base * 64 + l] = make_uint4(hi[0] | hi[1] << 16, hi[2] | hi[3] << 16, hi[4] | hi[5] << 16, hi[6] | hi[7] << 16);
-    if constexpr (!BF16_IN)
-        frag[(base + 1) * 64 + l] = make_uint4(lo[0] | lo[1] << 16, lo[2] | lo[3] << 16, lo[4] | lo[5] << 16, lo[6] | lo[7] << 16);
+    const uint64_t base = ((uint64_t)tt * nsb + j) * PARTS;
+#pragma unroll
+    for (int p = 0; p < PARTS; p++)
+        frag[(base + p) * 64 + l] = make_uint4(pc[p][0] | pc[p][1] << 16, pc[p][2] | pc[p][3] << 16,
+                                               pc[p][4] | pc[p][5] << 16, pc[p][6] | pc[p][7] << 16);
     part += __shfl_xor(part, 16);
     part += __shfl_xor(part, 32);
     if (l < 16) xsum[((uint64_t)tt * nsb + j) * 16 + l] = part;
@@ -150,9 +153,10 @@ __global__ __launch_bounds__(256) void k_q4k_batch(const uint4 *__restrict__ fra
                     f32x4 D = {0.f, 0.f, 0.f, 0.f};
                     const bf16x8 a0 = __builtin_bit_cast(bf16x8, frag[fb * 64 + l]);
                     D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, u ? bhi : blo, D, 0, 0, 0);
-                    if constexpr (PARTS == 2) {
-                        const bf16x8 a1 = __builtin_bit_cast(bf16x8, frag[(fb + 1) * 64 + l]);
-                        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, u ? bhi : blo, D, 0, 0, 0);
+#pragma unroll
+                    for (int p = 1; p < PARTS; p++) {
+                        const bf16x8 ap = __builtin_bit_cast(bf16x8, frag[(fb + p) * 64 + l]);
+                        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, u ? bhi : blo, D, 0, 0, 0);
                     }
                     const float4 X = *reinterpret_cast<const float4 *>(xsum + ((uint64_t)t * nsb + sb) * 16 + 4 * kg);
                     acc[t][0] = __builtin_fmaf(a, D[0], __builtin_fmaf(-cc, X.x, acc[t][0]));
@@ -208,8 +212,9 @@ __global__ __launch_bounds__(256) void k_q80_batch(const uint4 *__restrict__ fra
             const uint64_t fb = ((uint64_t)t * nsb + sb) * PARTS;
             f32x4 D = {0.f, 0.f, 0.f, 0.f};
             D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, frag[fb * 64 + l]), B, D, 0, 0, 0);
-            if constexpr (PARTS == 2)
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, frag[(fb + 1) * 64 + l]), B, D,
+#pragma unroll
+            for (int p = 1; p < PARTS; p++)
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, frag[(fb + p) * 64 + l]), B, D,
                                                             0, 0, 0);
             const float4 X = *reinterpret_cast<const float4 *>(xsum + ((uint64_t)t * nsb + sb) * 16 + 4 * kg);
             acc[t][0] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X.x, D[0]), acc[t][0]);
@@ -337,16 +342,22 @@ int launch_main(int dtype, const uint4 *frag, const float *xs, const uint8_t *w,
 
 }  // namespace
 
-extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k,
-                                            uint32_t n, uint32_t m, int w_dtype, void *stream) {
-    clear_error();
+namespace lg {
+
+uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t m, int x_dtype) {
+    const uint64_t tiles = (m + 15) / 16, nsb = k / 32;
+    const int parts = x_dtype == LG_BF16 ? 1 : 3;
+    return tiles * nsb * parts * 64 * 16 + tiles * nsb * 16 * 4;
+}
+
+int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
+               void *ws_given, uint64_t ws_bytes, hipStream_t s) {
     const char *name = "lg_dispatch_proj_quant_batch";
     if (n == 0 || m == 0) return LG_OK;
     LG_REQUIRE(m <= 64, "%s: m=%u exceeds 64", name, m);
     LG_REQUIRE(x && w && c, "%s: null pointer", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
     LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32, "%s: weight dtype %d", name, w_dtype);
-    hipStream_t s = (hipStream_t)stream;
     const uint64_t xbytes = (uint64_t)m * k * (x_dtype == LG_F32 ? 4 : 2);
     LG_EXTENT(c, (uint64_t)m * n * 4, name);
     if (k == 0) {
@@ -365,21 +376,34 @@ extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const vo
         return after_launch(name, s);
     }
     const uint32_t tiles = (m + 15) / 16, nsb = k / 32;
-    const int parts = x_dtype == LG_BF16 ? 1 : 2;
+    const int parts = x_dtype == LG_BF16 ? 1 : 3;
     const uint64_t frag_bytes = (uint64_t)tiles * nsb * parts * 64 * 16;
-    const uint64_t xs_bytes = (uint64_t)tiles * nsb * 16 * 4;
-    void *ws = nullptr;
-    int st = workspace(frag_bytes + xs_bytes, &ws);
-    if (st != LG_OK) return st;
+    void *ws = ws_given;
+    int st = LG_OK;
+    if (ws) {
+        LG_REQUIRE(ws_bytes >= proj_batch_ws_bytes(k, m, x_dtype), "%s: workspace of %llu bytes too small", name,
+                   (unsigned long long)ws_bytes);
+    } else {
+        st = workspace(proj_batch_ws_bytes(k, m, x_dtype), &ws);
+        if (st != LG_OK) return st;
+    }
     uint4 *frag = static_cast<uint4 *>(ws);
     float *xs = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + frag_bytes);
     if (parts == 1)
-        hipLaunchKernelGGL(k_prep_x<true>, dim3(nsb, tiles), dim3(64), 0, s, x, m, k, frag, xs);
+        hipLaunchKernelGGL(k_prep_x<1>, dim3(nsb, tiles), dim3(64), 0, s, x, m, k, frag, xs);
     else
-        hipLaunchKernelGGL(k_prep_x<false>, dim3(nsb, tiles), dim3(64), 0, s, x, m, k, frag, xs);
+        hipLaunchKernelGGL(k_prep_x<3>, dim3(nsb, tiles), dim3(64), 0, s, x, m, k, frag, xs);
     st = after_launch("prep_x", s);
     if (st != LG_OK) return st;
     const uint8_t *wb = static_cast<const uint8_t *>(w);
     return parts == 1 ? launch_main<1>(w_dtype, frag, xs, wb, c, m, k, n, s)
-                      : launch_main<2>(w_dtype, frag, xs, wb, c, m, k, n, s);
+                      : launch_main<3>(w_dtype, frag, xs, wb, c, m, k, n, s);
+}
+
+}  // namespace lg
+
+extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k,
+                                            uint32_t n, uint32_t m, int w_dtype, void *stream) {
+    clear_error();
+    return lg::proj_batch(x, x_dtype, w, c, k, n, m, w_dtype, nullptr, 0, (hipStream_t)stream);
 }

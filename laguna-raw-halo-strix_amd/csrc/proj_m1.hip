@@ -54,7 +54,7 @@ constexpr int M1_RPW_MAX = 8;         // rows per team whose loads are in flight
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
     // kernels/activation.comp:21-28: silu(g) * up, silu(x) = x * (1 / (1 + exp(-x)))
-    return g * (1.0f / (1.0f + __expf(-g))) * u;
+    return g * (1.0f / (1.0f + expf(-g))) * u;
 }
 
 // The workgroup's copy of the activations, in two halves so that the row loads

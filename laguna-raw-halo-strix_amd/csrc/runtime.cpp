@@ -41,12 +41,19 @@ bool extent_ok(const void *p, uint64_t bytes) {
     return (a - base) + bytes <= size;
 }
 
-bool blocking() { return g_blocking; }
+static thread_local int t_deferred = 0;
+bool blocking() { return g_blocking && t_deferred == 0; }
+DeferSync::DeferSync() { t_deferred++; }
+DeferSync::~DeferSync() { t_deferred--; }
 
 int after_launch(const char *what, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(LG_EHIP, "%s launch failed: %s", what, hipGetErrorString(e));
-    if (g_blocking) {
+    if (blocking()) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(s, &cs);
+        if (e != hipSuccess) return fail(LG_EHIP, "%s: %s", what, hipGetErrorString(e));
+        if (cs != hipStreamCaptureStatusNone) return LG_OK;  // a capturing stream cannot be synchronised
         e = hipStreamSynchronize(s);
         if (e != hipSuccess) return fail(LG_EHIP, "%s: %s", what, hipGetErrorString(e));
     }

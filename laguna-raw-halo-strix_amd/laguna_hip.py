@@ -30,7 +30,7 @@ F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
 OK, EINVAL, EHIP, ENOMEM, EUNSUPPORTED, EIO, ENODEV = range(7)
 
 # C-ABI symbols declared in include/laguna_hip.h, with ctypes signatures.
-_vp, _u32, _u64, _i = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int
+_vp, _u32, _u64, _i, _f = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
 SIGNATURES = {
     "lg_last_error": (ctypes.c_char_p, []),
     "lg_version": (ctypes.c_char_p, []),
@@ -55,6 +55,18 @@ SIGNATURES = {
     "lg_dispatch_activation": (_i, [_vp, _vp, _vp, _u32, _vp]),
     "lg_dispatch_silu_mul_proj_quant": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _i, _vp]),
     "lg_dispatch_proj_quant_batch": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
+    "lg_dispatch_rmsnorm": (_i, [_vp, _vp, _vp, _u32, _u32, _f, _vp]),
+    "lg_dispatch_enc_aux_norm": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _f, _vp]),
+    "lg_dispatch_qk_norm_rope": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f, _vp]),
+    "lg_dispatch_mha_attn": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _i, _vp]),
+    "lg_dispatch_gate_mul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "lg_dispatch_softplus_gate_mul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "lg_dispatch_add": (_i, [_vp, _vp, _vp, _u32, _vp]),
+    "lg_dflash_encode": (_i, [_vp, _vp, _u32, _vp, _vp]),
+    "lg_dflash_forward_block": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
+    "lg_dflash_graph_create": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, ctypes.POINTER(_vp)]),
+    "lg_dflash_graph_launch": (_i, [_vp, _vp]),
+    "lg_dflash_graph_destroy": (_i, [_vp]),
 }
 # Tuning hooks exported beside the ABI (not part of the drop-in surface).
 EXTRA = {
@@ -239,3 +251,267 @@ def dequant_to_f32(ctx, data, dtype, n_elements):
     src.free()
     out.free()
     return r
+
+
+# ---- streams ------------------------------------------------------------------------
+
+
+class Stream:
+    """A created (non-null) HIP stream: HIP graph capture needs one."""
+
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib().lg_stream_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def sync(self):
+        check(lib().lg_sync(self.ptr))
+
+    def destroy(self):
+        if self.ptr:
+            lib().lg_stream_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def _stream(ctx, stream):
+    return stream.ptr if isinstance(stream, Stream) else (ctx.stream if stream is None else stream)
+
+
+# ---- DFlash glue (src/dflash.rs dispatch_* helpers; one row each, as the reference) ----
+
+RMS_EPS = 1e-5   # src/dflash.rs:987
+QK_EPS = 1e-6    # src/dflash.rs:1105
+
+
+def dispatch_rmsnorm(ctx, w, x, out, n, rows=1, eps=RMS_EPS):
+    """dispatch_rmsnorm(ctx, shader, w, x, out, n) (src/dflash.rs:979-1007)."""
+    check(lib().lg_dispatch_rmsnorm(_ptr(w), _ptr(x), _ptr(out), n, rows, eps, ctx.stream))
+
+
+def dispatch_enc_aux_norm(ctx, x, aux_norm_w, out, n_feat, n_aux, n_total, eps=RMS_EPS):
+    """dispatch_enc_aux_norm (src/dflash.rs:1201-1234); n_total = n_aux * n_feat per token."""
+    n_tokens = n_total // (n_aux * n_feat) if n_aux * n_feat else 0
+    check(lib().lg_dispatch_enc_aux_norm(_ptr(x), _ptr(aux_norm_w), _ptr(out), n_feat, n_aux, n_tokens, eps,
+                                         ctx.stream))
+
+
+def dispatch_qk_norm_rope(ctx, x, norm_w, freq, out, n_heads, head_dim, rope_dim, pos, rows=1, eps=QK_EPS):
+    """dispatch_qk_norm_rope (src/dflash.rs:1093-1129)."""
+    check(lib().lg_dispatch_qk_norm_rope(_ptr(x), _ptr(norm_w), _ptr(freq), _ptr(out), n_heads, head_dim, rope_dim,
+                                         pos, rows, eps, ctx.stream))
+
+
+def dispatch_mha_attn_seq(ctx, q_normed, k_seq, v_seq, out, n_q_heads, n_kv_heads, head_dim, seq_len, q_pos,
+                          rows=1, causal=1):
+    """dispatch_mha_attn_seq (src/dflash.rs:1160-1199); the reference always passes causal = 1."""
+    check(lib().lg_dispatch_mha_attn(_ptr(q_normed), _ptr(k_seq), _ptr(v_seq), _ptr(out), n_q_heads, n_kv_heads,
+                                     head_dim, seq_len, q_pos, rows, causal, ctx.stream))
+
+
+def dispatch_gate_mul(ctx, attn_out, v_rep, gate, n_hd, n_heads, head_dim):
+    """dispatch_gate_mul(ctx, shader, attn_out, v_rep, gate, ...) (src/dflash.rs:1236-1266):
+    attn_out[i] = v_rep[i] * gate[i / head_dim] over n_hd = rows * n_heads * head_dim."""
+    rows = n_hd // (n_heads * head_dim) if n_heads * head_dim else 0
+    check(lib().lg_dispatch_gate_mul(_ptr(v_rep), _ptr(gate), _ptr(attn_out), n_heads, head_dim, rows, ctx.stream))
+
+
+def dispatch_softplus_gate_mul(ctx, attn_out, v_rep, gate, n_hd, n_heads, head_dim):
+    """src/dflash.rs:956-959 on the device: gate -> softplus (threshold 20), then gate_mul."""
+    rows = n_hd // (n_heads * head_dim) if n_heads * head_dim else 0
+    check(lib().lg_dispatch_softplus_gate_mul(_ptr(v_rep), _ptr(gate), _ptr(attn_out), n_heads, head_dim, rows,
+                                              ctx.stream))
+
+
+def dispatch_add(ctx, a, b, out, n):
+    """dispatch_add (src/dflash.rs:1281-1303)."""
+    check(lib().lg_dispatch_add(_ptr(a), _ptr(b), _ptr(out), n, ctx.stream))
+
+
+def rope_freq(rope_dim, base=500000.0):
+    """The f32 table of src/dflash.rs:898-904: 1 / base^(2i / rope_dim)."""
+    i = np.arange(rope_dim // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(base), (np.float32(2.0) * i) / np.float32(rope_dim))).astype(
+        np.float32)
+
+
+# ---- DFlash draft model ----------------------------------------------------------------
+
+
+class DFlashConfig:
+    """Hyperparameters of DFlashModel (src/dflash.rs:121-155 accessors).  Defaults are
+    the 6-layer draft: hidden 4096, 32 Q / 8 KV heads of 128, FFN 14336, 3 aux layers."""
+
+    def __init__(self, n_embd=4096, n_heads=32, n_kv=8, head_dim=128, rope_dim=128, n_ff=14336, n_aux=3,
+                 n_layers=6, rope_base=500000.0, rms_eps=RMS_EPS, qk_eps=QK_EPS):
+        self.n_embd, self.n_heads, self.n_kv, self.head_dim = n_embd, n_heads, n_kv, head_dim
+        self.rope_dim, self.n_ff, self.n_aux, self.n_layers = rope_dim, n_ff, n_aux, n_layers
+        self.rope_base, self.rms_eps, self.qk_eps = rope_base, rms_eps, qk_eps
+
+
+class _Hparams(ctypes.Structure):
+    _fields_ = [(n, _u32) for n in ("n_embd", "n_heads", "n_kv_heads", "head_dim", "rope_dim", "n_ff", "n_aux",
+                                    "n_layers")] + [("rope_base", _f), ("rms_eps", _f), ("qk_eps", _f)]
+
+
+DFLASH_NORMS = ("attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm")
+DFLASH_PROJ = ("attn_q", "attn_k", "attn_v", "attn_gate", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = ([(n, _vp) for n in DFLASH_NORMS] + [(n, _vp) for n in DFLASH_PROJ]
+                + [(n + "_type", _i) for n in DFLASH_PROJ] + [("k_ctx", _vp), ("v_ctx", _vp)])
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [("hp", _Hparams), ("enc_aux_norm", _vp), ("fc", _vp), ("fc_type", _i), ("enc_output_norm", _vp),
+                ("output_norm", _vp), ("layers", ctypes.POINTER(_Layer))]
+
+
+class DFlashModel:
+    """DFlashModel (src/dflash.rs:22-31) over device tensors.
+
+    `enc` holds enc_aux_norm, fc (+ fc_dtype), enc_output_norm and optionally
+    output_norm; `layers` one dict per decoder layer with the f32 norms of
+    DFLASH_NORMS and, for each projection p of DFLASH_PROJ, the raw GGUF bytes
+    p and their type p + "_dtype" (tensor names of src/dflash.rs:68-79).  The
+    bytes are uploaded unchanged (Model::upload_tensor_quantized)."""
+
+    def __init__(self, ctx, cfg, enc, layers):
+        self.ctx, self.cfg = ctx, cfg
+        self._bufs = []
+        self.layers = []
+        up = self._up
+        self._enc = {"enc_aux_norm": up(enc["enc_aux_norm"], np.float32), "fc": up(enc["fc"]),
+                     "enc_output_norm": up(enc["enc_output_norm"], np.float32),
+                     "output_norm": up(enc["output_norm"], np.float32) if enc.get("output_norm") is not None else None}
+        self._layer_desc = (_Layer * len(layers))()
+        for i, L in enumerate(layers):
+            d = self._layer_desc[i]
+            for n in DFLASH_NORMS:
+                setattr(d, n, up(L[n], np.float32).ptr)
+            for n in DFLASH_PROJ:
+                setattr(d, n, up(L[n]).ptr)
+                setattr(d, n + "_type", int(L[n + "_dtype"]))
+        self._desc = _Model()
+        h = self._desc.hp
+        h.n_embd, h.n_heads, h.n_kv_heads, h.head_dim = cfg.n_embd, cfg.n_heads, cfg.n_kv, cfg.head_dim
+        h.rope_dim, h.n_ff, h.n_aux, h.n_layers = cfg.rope_dim, cfg.n_ff, cfg.n_aux, len(layers)
+        h.rope_base, h.rms_eps, h.qk_eps = cfg.rope_base, cfg.rms_eps, cfg.qk_eps
+        self._desc.enc_aux_norm = self._enc["enc_aux_norm"].ptr
+        self._desc.fc = self._enc["fc"].ptr
+        self._desc.fc_type = int(enc["fc_dtype"])
+        self._desc.enc_output_norm = self._enc["enc_output_norm"].ptr
+        self._desc.output_norm = self._enc["output_norm"].ptr if self._enc["output_norm"] else None
+        self._desc.layers = self._layer_desc
+        self.ctx_len = 0
+
+    def _up(self, a, dtype=None):
+        a = np.ascontiguousarray(a if dtype is None else np.asarray(a, dtype))
+        b = upload_bytes(self.ctx, a.view(np.uint8).ravel())
+        self._bufs.append(b)
+        return b
+
+    # accessors of src/dflash.rs:121-155
+    def layer_count(self):
+        return self._desc.hp.n_layers
+
+    def embedding_length(self):
+        return self.cfg.n_embd
+
+    def ffn_length(self):
+        return self.cfg.n_ff
+
+    def head_count(self):
+        return self.cfg.n_heads
+
+    def head_count_kv(self):
+        return self.cfg.n_kv
+
+    def rope_dim(self):
+        return self.cfg.rope_dim
+
+    def head_dim(self):
+        return self.cfg.head_dim
+
+    def n_embd_inp(self):
+        return self.cfg.n_aux * self.cfg.n_embd
+
+    def set_context(self, k_ctx, v_ctx):
+        """Per-layer cached context keys (normed, roped) and values, [ctx_len][n_kv*head_dim] f32."""
+        assert len(k_ctx) == len(v_ctx) == self.layer_count()
+        n = np.asarray(k_ctx[0]).shape[0]
+        for i in range(self.layer_count()):
+            assert np.asarray(k_ctx[i]).shape[0] == np.asarray(v_ctx[i]).shape[0] == n
+            self._layer_desc[i].k_ctx = self._up(k_ctx[i], np.float32).ptr if n else None
+            self._layer_desc[i].v_ctx = self._up(v_ctx[i], np.float32).ptr if n else None
+        self.ctx_len = n
+
+    @property
+    def desc(self):
+        return ctypes.byref(self._desc)
+
+    def encode(self, target_features):
+        """DFlashModel::encode (src/dflash.rs:157-234) for one or more feature rows."""
+        f = np.ascontiguousarray(target_features, np.float32).reshape(-1, self.n_embd_inp())
+        m = f.shape[0]
+        fb = upload_f32(self.ctx, f)
+        ob = GpuBuffer(self.ctx, 4 * m * self.cfg.n_embd)
+        check(lib().lg_dflash_encode(self.desc, fb.ptr, m, ob.ptr, self.ctx.stream))
+        return ob.read_f32(m * self.cfg.n_embd).reshape(m, -1)
+
+    def forward_block_device(self, feat, tok, m, out, ctx_len=None, stream=None):
+        ctx_len = self.ctx_len if ctx_len is None else ctx_len
+        check(lib().lg_dflash_forward_block(self.desc, _ptr(feat), _ptr(tok), m, ctx_len, _ptr(out),
+                                            _stream(self.ctx, stream)))
+
+    def forward_block(self, target_features, token_input, ctx_len=None):
+        """m tokens over the cached context; returns the final hidden [m][n_embd]."""
+        t = np.ascontiguousarray(token_input, np.float32).reshape(-1, self.cfg.n_embd)
+        m = t.shape[0]
+        f = np.ascontiguousarray(target_features, np.float32).reshape(m, self.n_embd_inp())
+        fb, tb = upload_f32(self.ctx, f), upload_f32(self.ctx, t)
+        ob = GpuBuffer(self.ctx, 4 * m * self.cfg.n_embd)
+        self.forward_block_device(fb, tb, m, ob, ctx_len)
+        return ob.read_f32(m * self.cfg.n_embd).reshape(m, -1)
+
+    def forward_injected_decode_hidden(self, target_features, token_input):
+        """src/dflash.rs:877-976: one token, no cached context."""
+        return self.forward_block(target_features, token_input, ctx_len=0)[0]
+
+    def capture(self, feat, tok, m, out, stream, ctx_len=None):
+        """The block forward captured into a HIP graph on `stream` (a Stream)."""
+        return DFlashGraph(self, feat, tok, m, out, stream, self.ctx_len if ctx_len is None else ctx_len)
+
+    def free(self):
+        for b in self._bufs:
+            b.free()
+        self._bufs = []
+
+
+class DFlashGraph:
+    def __init__(self, model, feat, tok, m, out, stream, ctx_len):
+        self.model, self.stream = model, stream  # keep the tensors alive
+        g = ctypes.c_void_p()
+        check(lib().lg_dflash_graph_create(model.desc, _ptr(feat), _ptr(tok), m, ctx_len, _ptr(out), stream.ptr,
+                                           ctypes.byref(g)))
+        self.ptr = g.value
+
+    def launch(self):
+        check(lib().lg_dflash_graph_launch(self.ptr, self.stream.ptr))
+
+    def destroy(self):
+        if self.ptr:
+            lib().lg_dflash_graph_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass

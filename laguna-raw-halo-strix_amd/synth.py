@@ -104,3 +104,66 @@ def weight_bytes(dtype, k, n):
     if dtype == F32:
         return k * n * 4
     raise ValueError(dtype)
+
+
+# ---- DFlash draft model (random init) ------------------------------------------------
+
+DFLASH_PROJ = ("attn_q", "attn_k", "attn_v", "attn_gate", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+DFLASH_NORMS = ("attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm")
+
+
+def dflash_shapes(hp):
+    """(k, n) of each projection of a layer (src/dflash.rs:68-79)."""
+    E, QD, KVD = hp.n_embd, hp.n_heads * hp.head_dim, hp.n_kv * hp.head_dim
+    return {"attn_q": (E, QD), "attn_k": (E, KVD), "attn_v": (E, KVD), "attn_gate": (E, hp.n_heads),
+            "attn_output": (QD, E), "ffn_gate": (E, hp.n_ff), "ffn_up": (E, hp.n_ff), "ffn_down": (hp.n_ff, E)}
+
+
+def _weight(seed, dtype, k, n):
+    from laguna_hip import Q4_K, Q8_0, F32
+    if dtype == Q4_K:
+        return q4k_weight(seed, k, n)
+    if dtype == Q8_0:
+        return q8_0_weight(seed, k, n)
+    if dtype == F32:
+        return normal(seed, k * n, 0.02)
+    raise ValueError(dtype)
+
+
+def dflash_model(seed, hp, n_layers, types=None, norm_sigma=0.0):
+    """Random-init draft model: (encoder dict, list of layer dicts), keys as the
+    oracle's forward_block takes them.  Default types: Q4_K everywhere except
+    Q8_0 attn_output.  Norm weights are 1 + N(0, norm_sigma)."""
+    from laguna_hip import Q4_K, Q8_0
+    types = {**{p: Q4_K for p in DFLASH_PROJ}, "attn_output": Q8_0, "fc": Q4_K, **(types or {})}
+    shapes = dflash_shapes(hp)
+    sub = iter(splitmix64(seed, 64 + 16 * n_layers))
+
+    def norm(n):
+        return (1.0 + normal(int(next(sub)), n, norm_sigma)).astype(np.float32) if norm_sigma else np.ones(n, np.float32)
+
+    A = hp.n_aux * hp.n_embd
+    W = {"enc_aux_norm": norm(A), "fc": _weight(int(next(sub)), types["fc"], A, hp.n_embd), "fc_dtype": types["fc"],
+         "enc_output_norm": norm(hp.n_embd), "output_norm": norm(hp.n_embd)}
+    layers = []
+    for _ in range(n_layers):
+        L = {"attn_norm": norm(hp.n_embd), "attn_q_norm": norm(hp.head_dim), "attn_k_norm": norm(hp.head_dim),
+             "ffn_norm": norm(hp.n_embd)}
+        for p in DFLASH_PROJ:
+            k, n = shapes[p]
+            L[p] = _weight(int(next(sub)), types[p], k, n)
+            L[p + "_dtype"] = types[p]
+        layers.append(L)
+    return W, layers
+
+
+def dflash_inputs(seed, hp, n_layers, m, ctx_len):
+    """features [m][n_aux*n_embd], tokens [m][n_embd], per-layer context K and V
+    [ctx_len][n_kv*head_dim], all f32 N(0, 1)."""
+    s = splitmix64(seed, 4 + 2 * n_layers)
+    feat = normal(int(s[0]), m * hp.n_aux * hp.n_embd).reshape(m, -1)
+    tok = normal(int(s[1]), m * hp.n_embd).reshape(m, -1)
+    kvd = hp.n_kv * hp.head_dim
+    k_ctx = [normal(int(s[4 + 2 * i]), ctx_len * kvd).reshape(ctx_len, kvd) for i in range(n_layers)]
+    v_ctx = [normal(int(s[5 + 2 * i]), ctx_len * kvd).reshape(ctx_len, kvd) for i in range(n_layers)]
+    return feat, tok, k_ctx, v_ctx

@@ -99,3 +99,53 @@ def test_synth_q4k_blocks():
 def test_synth_normal_moments():
     z = synth.normal(0x5EED0002, 1 << 18).astype(np.float64)
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
+
+
+def test_dflash_struct_layout_matches_header(tmp_path):
+    """The ctypes mirrors of lg_dflash_hparams / lg_dflash_layer / lg_dflash_model
+    have the C compiler's sizes and field offsets."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    checks = []
+    for cname, cls in (("lg_dflash_hparams", lh._Hparams), ("lg_dflash_layer", lh._Layer),
+                       ("lg_dflash_model", lh._Model)):
+        checks.append((f"sizeof({cname})", ctypes.sizeof(cls)))
+        for fname, _ in cls._fields_:
+            checks.append((f"offsetof({cname}, {fname})", getattr(cls, fname).offset))
+    src = tmp_path / "layout.c"
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"laguna_hip.h\"\nint main(void) {\n"
+                   + "".join(f'    printf("%zu\\n", (size_t){expr});\n' for expr, _ in checks) + "    return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert got == [v for _, v in checks], [(e, g, v) for (e, v), g in zip(checks, got) if g != v]
+
+
+def test_dflash_rejects_bad_models_without_launching():
+    import synth
+
+    cfg = lh.DFlashConfig(n_embd=256, n_heads=4, n_kv=2, head_dim=64, rope_dim=32, n_ff=512, n_aux=2, n_layers=1)
+    desc = lh._Model()
+    desc.hp.n_embd, desc.hp.n_heads, desc.hp.n_kv_heads, desc.hp.head_dim = 256, 4, 2, 64
+    desc.hp.rope_dim, desc.hp.n_ff, desc.hp.n_aux, desc.hp.n_layers = 32, 512, 2, 1
+    layers = (lh._Layer * 1)()
+    desc.layers = layers
+    x = np.zeros(16, np.float32)
+    p = x.ctypes.data
+    # no layers' tensors, and a partial rotary dim: EINVAL before anything runs
+    assert lh.lib().lg_dflash_forward_block(ctypes.byref(desc), p, p, 1, 0, p, None) == lh.EINVAL
+    desc.hp.rope_dim = 64
+    desc.enc_aux_norm = desc.fc = desc.enc_output_norm = p
+    assert lh.lib().lg_dflash_forward_block(ctypes.byref(desc), p, p, 1, 0, p, None) == lh.EINVAL
+    assert b"missing a tensor" in lh.lib().lg_last_error()
+    assert lh.lib().lg_dflash_forward_block(ctypes.byref(desc), p, p, 33, 0, p, None) == lh.EINVAL
+    assert lh.lib().lg_dflash_graph_create(ctypes.byref(desc), p, p, 1, 0, p, None, None) == lh.EINVAL
+    assert lh.lib().lg_dispatch_qk_norm_rope(p, p, p, p, 2, 64, 32, 0, 1, 1e-6, None) == lh.EINVAL
+    assert lh.lib().lg_dispatch_mha_attn(p, p, p, p, 3, 2, 64, 4, 0, 1, 1, None) == lh.EINVAL
+    assert lh.lib().lg_dispatch_rmsnorm(None, p, p, 4, 1, 1e-5, None) == lh.EINVAL
+    assert lh.lib().lg_dflash_graph_destroy(None) == lh.OK
+    del cfg, synth
