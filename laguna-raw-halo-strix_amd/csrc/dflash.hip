@@ -524,23 +524,30 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
                                (uint64_t)m * hp.n_heads,          m * E,        m * E,  m * FF, m * FF, m * A,
                                attn_partial_floats(S, hp.n_kv_heads)};
     float **dst[] = {&L.xe, &L.nxe, &L.kk, &L.vv, &L.q, &L.att, &L.gate, &L.o, &L.h, &L.g, &L.u, &L.feat_n, &L.part};
-    // the RoPE table sits at offset 0 whatever (m, ctx_len) are, so an uploaded
-    // table stays valid across calls that lay the same workspace out differently
+    // The RoPE table and the small-M product workspace (whose arrival counters come
+    // first) sit at fixed offsets whatever (m, ctx_len) are: an uploaded table stays
+    // valid, and the counters stay zero, across calls that lay the rest out differently.
+    // Its size: the largest over the forward's product shapes (k, n, rows).
+    uint64_t pw = 0;
+    const uint32_t shapes[][3] = {{(uint32_t)E, (uint32_t)KVD, 2 * m}, {(uint32_t)E, (uint32_t)QD, m},
+                                  {(uint32_t)E, hp.n_heads, m},         {(uint32_t)QD, (uint32_t)E, m},
+                                  {(uint32_t)E, (uint32_t)FF, m},       {(uint32_t)FF, (uint32_t)E, m},
+                                  {(uint32_t)A, (uint32_t)E, m}};
+    for (const auto &sh : shapes)
+        for (int wt : {LG_Q4_K, LG_Q8_0}) {
+            const uint64_t c = proj_batch_ws_bytes(sh[0], sh[1], sh[2], LG_F32, wt);
+            pw = c > pw ? c : pw;
+        }
+    pw = pw > PROJ_WS_COUNTERS ? pw : PROJ_WS_COUNTERS;
     L.freq = reinterpret_cast<float *>(base);
-    uint64_t off = FREQ_BYTES;
+    L.pws = base + FREQ_BYTES;
+    L.pws_bytes = pw;
+    uint64_t off = FREQ_BYTES + ((pw + 255) & ~(uint64_t)255);
     for (size_t i = 0; i < sizeof(floats) / sizeof(floats[0]); i++) {
         *dst[i] = reinterpret_cast<float *>(base + off);
         off += (floats[i] * 4 + 255) & ~(uint64_t)255;
     }
-    uint64_t pw = 0;
-    const uint64_t cand[] = {proj_batch_ws_bytes(hp.n_embd, 2 * m, LG_F32), proj_batch_ws_bytes(hp.n_embd, m, LG_F32),
-                             proj_batch_ws_bytes(hp.n_heads * hp.head_dim, m, LG_F32),
-                             proj_batch_ws_bytes(hp.n_ff, m, LG_F32),
-                             proj_batch_ws_bytes(hp.n_aux * hp.n_embd, m, LG_F32)};
-    for (uint64_t c : cand) pw = c > pw ? c : pw;
-    L.pws = base + off;
-    L.pws_bytes = pw;
-    L.total = off + ((pw + 255) & ~(uint64_t)255);
+    L.total = off;
     return L.total;
 }
 
@@ -575,6 +582,7 @@ int ws_alloc(Ws &w, uint64_t need) {
         (void)hipGetLastError();
         return fail(LG_ENOMEM, "draft forward workspace (%llu bytes)", (unsigned long long)sz);
     }
+    LG_HIP_TRY(hipMemset(p, 0, sz));  // the small-M products' arrival counters start at zero
     w.base = static_cast<uint8_t *>(p);
     w.bytes = sz;
     return LG_OK;
@@ -628,9 +636,10 @@ int check_model(const lg_dflash_model *md, uint32_t m, const char *name, bool wi
     return LG_OK;
 }
 
+// c = W x, or c = res + W x
 int proj(const FwdLayout &W, const float *x, const void *w, int type, float *c, uint32_t k, uint32_t n, uint32_t m,
-         hipStream_t s) {
-    return proj_batch(x, LG_F32, w, c, k, n, m, type, W.pws, W.pws_bytes, s);
+         hipStream_t s, const float *res = nullptr) {
+    return proj_batch(x, LG_F32, w, c, k, n, m, type, W.pws, W.pws_bytes, s, res);
 }
 
 // DFlashModel::encode (src/dflash.rs:157-234) on m feature rows.
@@ -674,17 +683,13 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
         hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for((uint64_t)m * QD)), dim3(256), 0, s, W.att, W.gate, W.att, H,
                            HD, (uint64_t)m * QD, 1);
         LG_TRY(after_launch("softplus_gate_mul", s));
-        LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, W.o, QD, E, m, s));
-        hipLaunchKernelGGL(k_add, dim3(blocks_for(mE)), dim3(256), 0, s, x, W.o, x, mE);
-        LG_TRY(after_launch("residual", s));
+        LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, x, QD, E, m, s, x));  // x += o_proj
         // SwiGLU FFN (src/dflash.rs:962-968)
         LG_TRY(run_rmsnorm(x, L.ffn_norm, W.h, E, m, 1, E, hp.rms_eps, s));
         LG_TRY(proj(W, W.h, L.ffn_gate, L.ffn_gate_type, W.g, E, FF, m, s));
         LG_TRY(proj(W, W.h, L.ffn_up, L.ffn_up_type, W.u, E, FF, m, s));
         LG_TRY(lg_dispatch_activation(W.g, W.u, W.g, m * FF, s));
-        LG_TRY(proj(W, W.g, L.ffn_down, L.ffn_down_type, W.o, FF, E, m, s));
-        hipLaunchKernelGGL(k_add, dim3(blocks_for(mE)), dim3(256), 0, s, x, W.o, x, mE);
-        LG_TRY(after_launch("residual", s));
+        LG_TRY(proj(W, W.g, L.ffn_down, L.ffn_down_type, x, FF, E, m, s, x));  // x += ffn_down
     }
     if (md->output_norm) return run_rmsnorm(x, md->output_norm, out, E, m, 1, E, hp.rms_eps, s);
     hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, x, out, mE);

@@ -47,12 +47,18 @@ struct DeferSync {
                "%s: %llu bytes at %p run past the end of its lg_buf_alloc allocation",     \
                name, (unsigned long long)(bytes), (const void *)(ptr))
 
-// Small-M product behind lg_dispatch_proj_quant_batch.  ws == nullptr uses the
-// per-device workspace; otherwise ws holds at least proj_batch_ws_bytes(k, m,
-// x_dtype) bytes owned by the caller (graphs capture it, so it must outlive them).
-uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t m, int x_dtype);
+// Small-M product behind lg_dispatch_proj_quant_batch: c = W x, or c = res + W x
+// when res is given (res may be c).  ws == nullptr uses the per-device workspace;
+// otherwise ws holds at least proj_batch_ws_bytes(k, n, m, x_dtype, w_dtype) bytes
+// owned by the caller, zeroed before its first use and used by one call at a time
+// (graphs capture it, so it must outlive them).
+// A workspace starts with PROJ_WS_COUNTERS bytes of arrival counters that every
+// call expects to find zero (and leaves zero); callers that lay other data out
+// after a workspace keep that region at a fixed place.
+constexpr uint64_t PROJ_WS_COUNTERS = 65536;
+uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype);
 int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
-               void *ws, uint64_t ws_bytes, hipStream_t s);
+               void *ws, uint64_t ws_bytes, hipStream_t s, const float *res = nullptr);
 
 // ---- GGUF block geometry (src/gguf.rs:97,101,134,136)
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;

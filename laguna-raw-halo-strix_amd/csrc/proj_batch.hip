@@ -3,11 +3,11 @@
 // tiles on gfx950 (v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16]).
 //
 //   A = activations: 16 rows (tokens) x 32 k (one 32-element sub-block).  f32
-//       activations are split exactly into three bf16 parts hi + mid + lo (each the
-//       nearest bf16 of what the previous parts leave: together all 24 significant
-//       bits, so the products are f32-grade); bf16 activations use one part.  A prep kernel writes them once
-//       per call in MFMA operand order, with the per-sub-block sums X of the
-//       represented values, into a device workspace.
+//       activations are split exactly into three bf16 parts x = x0 + x1 + x2 (each
+//       the nearest bf16 of what the previous parts leave: together all 24
+//       significant bits, so the products are f32-grade); bf16 activations are one
+//       part.  Each workgroup builds the fragments of its slice of k straight from
+//       the activations, with the per-sub-block sums X, in LDS.
 //   B = weight codes of 16 output rows x the same 32 k, built in registers from
 //       the raw blocks:  Q4_K nibble q -> bf16 1 + q/16 (one shift and one and-or
 //       per pair);  Q8_0 int8 q -> bf16 of q + 128 (exact: 8 significant bits).
@@ -20,6 +20,14 @@
 // lane l, register r.  Inside a k-group the order of the 8 values only has to
 // agree between A and B; both use byte order {0,2,1,3,4,6,5,7}, which is the
 // order the nibble-pair encoding produces.
+//
+// Work split (split-K): workgroup (blockIdx.x, blockIdx.y) = 64*RT output rows (RT
+// 16-row tiles per wavefront) x slice blockIdx.y of k (CH chunks of 256 elements:
+// one Q4_K super-block or eight Q8_0 blocks per row and chunk).  With one slice
+// the workgroup writes the result; otherwise each writes its slice's partial sums
+// and the last workgroup of a row group to finish (a per-row-group arrival counter,
+// reset by that workgroup) adds the slices in slice order: the result does not
+// depend on which workgroup finishes last.
 #include <vector>
 
 #include "lg_common.hpp"
@@ -39,48 +47,6 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
-
-// Workspace layout, per 16-row tile tt and sub-block j (nsb = k/32 sub-blocks):
-//   frag[((tt*nsb + j)*parts + part)*64 + lane] : 8 bf16 (16 bytes)
-//   xsum[(tt*nsb + j)*16 + token]              : f32
-template <int PARTS>
-__global__ __launch_bounds__(64) void k_prep_x(const void *__restrict__ xv, uint32_t m, uint32_t k,
-                                               uint4 *__restrict__ frag, float *__restrict__ xsum) {
-    const uint32_t nsb = k / 32;
-    const uint32_t j = blockIdx.x, tt = blockIdx.y, l = threadIdx.x;
-    const uint32_t tok = tt * 16 + (l & 15u), kg = l >> 4;
-    uint32_t pc[PARTS][8];
-    float part = 0.0f;
-#pragma unroll
-    for (int v = 0; v < 8; v++) {
-        const uint32_t e = j * 32 + 8 * kg + PERM[v];
-#pragma unroll
-        for (int p = 0; p < PARTS; p++) pc[p][v] = 0;
-        if (tok < m) {
-            if constexpr (PARTS == 1) {
-                pc[0][v] = static_cast<const uint16_t *>(xv)[(uint64_t)tok * k + e];
-                part += bf16_to_f32(pc[0][v]);
-            } else {
-                const float x = static_cast<const float *>(xv)[(uint64_t)tok * k + e];
-                float r = x;
-#pragma unroll
-                for (int p = 0; p < PARTS; p++) {
-                    pc[p][v] = f32_to_bf16_rne(r);
-                    r -= bf16_to_f32(pc[p][v]);  // exact: r stays a multiple of x's last place
-                }
-                part += x;  // the parts sum to x exactly
-            }
-        }
-    }
-    const uint64_t base = ((uint64_t)tt * nsb + j) * PARTS;
-#pragma unroll
-    for (int p = 0; p < PARTS; p++)
-        frag[(base + p) * 64 + l] = make_uint4(pc[p][0] | pc[p][1] << 16, pc[p][2] | pc[p][3] << 16,
-                                               pc[p][4] | pc[p][5] << 16, pc[p][6] | pc[p][7] << 16);
-    part += __shfl_xor(part, 16);
-    part += __shfl_xor(part, 32);
-    if (l < 16) xsum[((uint64_t)tt * nsb + j) * 16 + l] = part;
-}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     uint4 u = make_uint4(a, b, c, d);
@@ -106,139 +72,345 @@ __device__ __forceinline__ void q8_codes(uint32_t v, uint32_t &p02, uint32_t &p1
     p13 = (f1 >> 16) | (f3 & 0xFFFF0000u);
 }
 
-// One wavefront = 16 output rows x all of k x up to TT 16-row activation tiles.
-template <int PARTS, int TT>
-__global__ __launch_bounds__(256) void k_q4k_batch(const uint4 *__restrict__ frag, const float *__restrict__ xsum,
-                                                   const uint8_t *__restrict__ w, float *__restrict__ c, uint32_t m,
-                                                   uint32_t k, uint32_t n, uint64_t row_bytes) {
-    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t row = (blockIdx.x * 4 + wave) * 16 + (l & 15u), kg = l >> 4;
-    const bool live = row < n;
-    const uint32_t nsb = k / 32, nb = k / QK_K;
-    const uint8_t *wr = w + (uint64_t)(live ? row : 0) * row_bytes;
-    float acc[TT][4];
-#pragma unroll
-    for (int t = 0; t < TT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
+// The activation fragments of a slice, built in LDS by the whole workgroup.
+//   lf[((t*SB + jj)*PARTS + p)*64 + lane] : part p of the A operand of token tile t,
+//                                          sub-block jj of the slice
+//   lx[(t*SB + jj)*16 + token]            : X, the sum of the 32 activations
+// A unit is (token tile t, sub-block jj, k-group kg, token tl): 8 activations.
+// load() issues the global loads (branch-free: tokens past m and sub-blocks past k
+// read a valid element and are zeroed at store()), store() splits and writes.
+template <int TT, int PARTS, int CH>
+struct Frags {
+    static constexpr int SB = 8 * CH;
+    static constexpr int PER = TT * 16 * SB * 4 / 256;  // units per thread
+    float4 r[PER][2];                                    // f32 activations
+    uint4 h[PER];                                        // bf16 activations
 
-    for (uint32_t b = 0; b < nb; b++) {
-        const uint8_t *blk = wr + (uint64_t)b * Q4K_BYTES;
-        uint4 hd = make_uint4(0, 0, 0, 0);
-        uint2 qv[4];
-        if (live) {
-            hd = *reinterpret_cast<const uint4 *>(blk);
+    __device__ __forceinline__ static void unit(int i, uint32_t &t, uint32_t &jj, uint32_t &kg, uint32_t &tl) {
+        const uint32_t u = i * 256 + threadIdx.x;
+        tl = u & 15u;
+        kg = (u >> 4) & 3u;
+        jj = (u >> 6) % SB;
+        t = u / (64 * SB);
+    }
+
+    __device__ __forceinline__ void load(const void *__restrict__ x, uint32_t m, uint32_t k, uint32_t sb0) {
+        const uint32_t nsb = k / 32;
 #pragma unroll
-            for (int g = 0; g < 4; g++) qv[g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kg);
-        } else {
-#pragma unroll
-            for (int g = 0; g < 4; g++) qv[g] = make_uint2(0, 0);
+        for (int i = 0; i < PER; i++) {
+            uint32_t t, jj, kg, tl;
+            unit(i, t, jj, kg, tl);
+            const uint32_t tok = t * 16 + tl < m ? t * 16 + tl : m - 1;
+            const uint32_t sb = sb0 + jj < nsb ? sb0 + jj : nsb - 1;
+            const uint64_t e = (uint64_t)tok * k + 32 * sb + 8 * kg;
+            if constexpr (PARTS == 1) {
+                h[i] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + e);
+            } else {
+                const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e);
+                r[i][0] = p[0];
+                r[i][1] = p[1];
+            }
         }
-        const float d16 = 16.0f * ref_half(hd.x & 0xFFFFu), dmin = ref_half(hd.x >> 16);
+    }
+
+    __device__ __forceinline__ void store(uint4 *lf, float *lx, uint32_t m, uint32_t k, uint32_t sb0) const {
+        const uint32_t nsb = k / 32;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            uint32_t t, jj, kg, tl;
+            unit(i, t, jj, kg, tl);
+            const bool valid = t * 16 + tl < m && sb0 + jj < nsb;
+            float v[8];
+            uint32_t code[PARTS][8];
+            if constexpr (PARTS == 1) {
+                const uint32_t wd[4] = {h[i].x, h[i].y, h[i].z, h[i].w};
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    code[0][q] = valid ? (wd[q / 2] >> (16 * (q % 2))) & 0xFFFFu : 0u;
+                    v[q] = bf16_to_f32(code[0][q]);
+                }
+            } else {
+                const float f[8] = {r[i][0].x, r[i][0].y, r[i][0].z, r[i][0].w,
+                                    r[i][1].x, r[i][1].y, r[i][1].z, r[i][1].w};
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    v[q] = valid ? f[q] : 0.0f;
+                    float rest = v[q];
+#pragma unroll
+                    for (int p = 0; p < PARTS; p++) {
+                        code[p][q] = f32_to_bf16_rne(rest);
+                        rest -= bf16_to_f32(code[p][q]);  // exact: rest stays a multiple of x's last place
+                    }
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < PARTS; p++) {
+                uint32_t c[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) c[q] = code[p][PERM[q]];
+                lf[((t * SB + jj) * PARTS + p) * 64 + kg * 16 + tl] =
+                    make_uint4(c[0] | c[1] << 16, c[2] | c[3] << 16, c[4] | c[5] << 16, c[6] | c[7] << 16);
+            }
+            float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            sum += __shfl_xor(sum, 16);  // the 4 k-groups of this token and sub-block
+            sum += __shfl_xor(sum, 32);
+            if (kg == 0) lx[(t * SB + jj) * 16 + tl] = sum;
+        }
+    }
+};
+
+// The workgroup's results: the output itself (one slice), or its slice's partial
+// sums and, in the last workgroup of the row group to finish, their ordered sum.
+template <int TT, int RT>
+__device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out, const float *res, float *part,
+                                       uint32_t *cnt, uint32_t rt0, uint32_t m, uint32_t n) {
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
+    const uint32_t S = gridDim.y, s = blockIdx.y;
+    const uint64_t mn = (uint64_t)m * n;
+    if (S > 1) {
+        float *ps = part + s * mn;
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t tok = t * 16 + 4 * kg + r;
+                    if (row < n && tok < m)
+                        __hip_atomic_store(ps + (uint64_t)tok * n + row, acc[i][t][r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+        }
+        // Partial sums and counter are device-coherent atomics (written through to,
+        // and read from, the device-wide level), so no cache write-back or
+        // invalidation is needed: each thread's stores complete before the
+        // workgroup's arrival is counted, and the last workgroup reads them after.
+        __shared__ uint32_t last;
+        __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(&cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1
+                       ? 1u
+                       : 0u;
+        __syncthreads();
+        if (!last) return;
+        if (threadIdx.x == 0) __hip_atomic_store(&cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+        const uint32_t rowc = row < n ? row : n - 1;
+        float v[TT][4];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[t][r] = S > 1 ? 0.0f : acc[i][t][r];
+        constexpr uint32_t G = 8 / TT;  // slices whose loads are in flight together
+        for (uint32_t q0 = 0; q0 < (S > 1 ? S : 0u); q0 += G) {
+            float pv[G][TT][4];
+#pragma unroll
+            for (uint32_t g = 0; g < G; g++) {
+                const uint32_t q = q0 + g < S ? q0 + g : S - 1;
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const uint32_t tok = t * 16 + 4 * kg + r;
+                        pv[g][t][r] = __hip_atomic_load(part + q * mn + (uint64_t)(tok < m ? tok : m - 1) * n + rowc,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+            }
+#pragma unroll
+            for (uint32_t g = 0; g < G; g++)  // slice order
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) v[t][r] += q0 + g < S ? pv[g][t][r] : 0.0f;
+        }
+        if (row >= n) continue;
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t tok = t * 16 + 4 * kg + r;
+                if (tok < m) {
+                    const uint64_t o = (uint64_t)tok * n + row;
+                    out[o] = res ? res[o] + v[t][r] : v[t][r];
+                }
+            }
+    }
+}
+
+// Q4_K.  Wavefront w owns row tiles (4*blockIdx.x + w)*RT .. +RT-1; each activation
+// fragment read from LDS serves all RT tiles.  Order of work: the activation loads,
+// every weight load of the slice (branch-free: rows past n and blocks past k read
+// row n-1 / the last block and are never used), the fragment build while the
+// weights are in flight, then the products.
+template <int TT, int PARTS, int CH, int RT>
+__global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const uint8_t *w, float *out,
+                                                const float *res, float *part, uint32_t *cnt, uint32_t m,
+                                                uint32_t k, uint32_t n, uint64_t row_bytes) {
+    constexpr int SB = 8 * CH;
+    __shared__ uint4 lf[TT * SB * PARTS * 64];
+    __shared__ float lx[TT * SB * 16];
+    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
+    const uint32_t rt0 = (blockIdx.x * 4 + wave) * RT;
+    const uint32_t nb = k / QK_K, b0 = blockIdx.y * CH;
+    Frags<TT, PARTS, CH> fr;
+    fr.load(x, m, k, 8 * b0);
+    uint4 hd[RT][CH];
+    uint2 qv[RT][CH][4];
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+        const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
+#pragma unroll
+        for (int cb = 0; cb < CH; cb++) {
+            const uint8_t *blk = wr + (uint64_t)(b0 + cb < nb ? b0 + cb : nb - 1) * Q4K_BYTES;
+            hd[i][cb] = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+            for (int g = 0; g < 4; g++) qv[i][cb][g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kg);
+        }
+    }
+    asm volatile("" ::: "memory");  // keep the weight loads issued ahead of the fragment build
+    fr.store(lf, lx, m, k, 8 * b0);
+    __syncthreads();
+    float acc[RT][TT][4];
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
+#pragma unroll
+    for (int cb = 0; cb < CH; cb++) {
+        if (b0 + cb >= nb) break;
+        float d16[RT], dmin[RT];
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            d16[i] = 16.0f * ref_half(hd[i][cb].x & 0xFFFFu);
+            dmin[i] = ref_half(hd[i][cb].x >> 16);
+        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            bf16x8 blo, bhi;
-            q4_codes(qv[g].x, qv[g].y, blo, bhi);
+            bf16x8 blo[RT], bhi[RT];
+#pragma unroll
+            for (int i = 0; i < RT; i++) q4_codes(qv[i][cb][g].x, qv[i][cb][g].y, blo[i], bhi[i]);
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t j = 2 * g + u;
-                uint32_t sc, mn;
-                scale_min_k4(j, hd.y, hd.z, hd.w, sc, mn);
-                const float a = d16 * (float)sc;
-                const float cc = __builtin_fmaf(dmin, (float)mn, a);
-                const uint32_t sb = b * 8 + j;
+                const uint32_t j = 2 * g + u, jj = cb * 8 + j;
+                bf16x8 A[TT][PARTS];
+                float4 X[TT];
 #pragma unroll
                 for (int t = 0; t < TT; t++) {
-                    const uint64_t fb = ((uint64_t)t * nsb + sb) * PARTS;
-                    f32x4 D = {0.f, 0.f, 0.f, 0.f};
-                    const bf16x8 a0 = __builtin_bit_cast(bf16x8, frag[fb * 64 + l]);
-                    D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, u ? bhi : blo, D, 0, 0, 0);
 #pragma unroll
-                    for (int p = 1; p < PARTS; p++) {
-                        const bf16x8 ap = __builtin_bit_cast(bf16x8, frag[(fb + p) * 64 + l]);
-                        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ap, u ? bhi : blo, D, 0, 0, 0);
+                    for (int p = 0; p < PARTS; p++)
+                        A[t][p] = __builtin_bit_cast(bf16x8, lf[((t * SB + jj) * PARTS + p) * 64 + l]);
+                    X[t] = *reinterpret_cast<const float4 *>(lx + (t * SB + jj) * 16 + 4 * kg);
+                }
+#pragma unroll
+                for (int i = 0; i < RT; i++) {
+                    uint32_t sc, mnv;
+                    scale_min_k4(j, hd[i][cb].y, hd[i][cb].z, hd[i][cb].w, sc, mnv);
+                    const float a = d16[i] * (float)sc;
+                    const float cc = __builtin_fmaf(dmin[i], (float)mnv, a);
+#pragma unroll
+                    for (int t = 0; t < TT; t++) {
+                        f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int p = 0; p < PARTS; p++)
+                            D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t][p], u ? bhi[i] : blo[i], D, 0, 0, 0);
+                        acc[i][t][0] = __builtin_fmaf(a, D[0], __builtin_fmaf(-cc, X[t].x, acc[i][t][0]));
+                        acc[i][t][1] = __builtin_fmaf(a, D[1], __builtin_fmaf(-cc, X[t].y, acc[i][t][1]));
+                        acc[i][t][2] = __builtin_fmaf(a, D[2], __builtin_fmaf(-cc, X[t].z, acc[i][t][2]));
+                        acc[i][t][3] = __builtin_fmaf(a, D[3], __builtin_fmaf(-cc, X[t].w, acc[i][t][3]));
                     }
-                    const float4 X = *reinterpret_cast<const float4 *>(xsum + ((uint64_t)t * nsb + sb) * 16 + 4 * kg);
-                    acc[t][0] = __builtin_fmaf(a, D[0], __builtin_fmaf(-cc, X.x, acc[t][0]));
-                    acc[t][1] = __builtin_fmaf(a, D[1], __builtin_fmaf(-cc, X.y, acc[t][1]));
-                    acc[t][2] = __builtin_fmaf(a, D[2], __builtin_fmaf(-cc, X.z, acc[t][2]));
-                    acc[t][3] = __builtin_fmaf(a, D[3], __builtin_fmaf(-cc, X.w, acc[t][3]));
                 }
             }
         }
     }
-    if (live) {
-#pragma unroll
-        for (int t = 0; t < TT; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t tok = t * 16 + 4 * kg + r;
-                if (tok < m) c[(uint64_t)tok * n + row] = acc[t][r];
-            }
-    }
+    finish<TT, RT>(acc, out, res, part, cnt, rt0, m, n);
 }
 
-template <int PARTS, int TT>
-__global__ __launch_bounds__(256) void k_q80_batch(const uint4 *__restrict__ frag, const float *__restrict__ xsum,
-                                                   const uint8_t *__restrict__ w, float *__restrict__ c, uint32_t m,
-                                                   uint32_t k, uint32_t n, uint64_t row_bytes) {
-    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t row = (blockIdx.x * 4 + wave) * 16 + (l & 15u), kg = l >> 4;
-    const bool live = row < n;
-    const uint32_t nsb = k / 32;
-    const uint8_t *wr = w + (uint64_t)(live ? row : 0) * row_bytes;
-    float acc[TT][4];
+// Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
+template <int TT, int PARTS, int CH, int RT>
+__global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const uint8_t *w, float *out,
+                                                const float *res, float *part, uint32_t *cnt, uint32_t m,
+                                                uint32_t k, uint32_t n, uint64_t row_bytes) {
+    constexpr int SB = 8 * CH;
+    __shared__ uint4 lf[TT * SB * PARTS * 64];
+    __shared__ float lx[TT * SB * 16];
+    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
+    const uint32_t rt0 = (blockIdx.x * 4 + wave) * RT;
+    const uint32_t nsb = k / 32, sb0 = blockIdx.y * SB;
+    Frags<TT, PARTS, CH> fr;
+    fr.load(x, m, k, sb0);
+    uint32_t dq[RT][SB], v0[RT][SB], v1[RT][SB];
 #pragma unroll
-    for (int t = 0; t < TT; t++)
+    for (int i = 0; i < RT; i++) {
+        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+        const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
-
-    for (uint32_t sb = 0; sb < nsb; sb++) {
-        const uint16_t *blk = reinterpret_cast<const uint16_t *>(wr + (uint64_t)sb * Q80_BYTES);  // 2-byte aligned
-        uint32_t v0 = 0, v1 = 0, dbits = 0;
-        if (live) {
-            dbits = blk[0];
+        for (int j = 0; j < SB; j++) {
+            const uint16_t *blk =
+                reinterpret_cast<const uint16_t *>(wr + (uint64_t)(sb0 + j < nsb ? sb0 + j : nsb - 1) * Q80_BYTES);
             const uint16_t *q = blk + 1 + 4 * kg;
-            v0 = q[0] | ((uint32_t)q[1] << 16);
-            v1 = q[2] | ((uint32_t)q[3] << 16);
-        }
-        const float d = ref_half(dbits);
-        uint32_t a0, a1, a2, a3;
-        q8_codes(v0, a0, a1);
-        q8_codes(v1, a2, a3);
-        const bf16x8 B = as_bf16x8(a0, a1, a2, a3);
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            const uint64_t fb = ((uint64_t)t * nsb + sb) * PARTS;
-            f32x4 D = {0.f, 0.f, 0.f, 0.f};
-            D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, frag[fb * 64 + l]), B, D, 0, 0, 0);
-#pragma unroll
-            for (int p = 1; p < PARTS; p++)
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, frag[(fb + p) * 64 + l]), B, D,
-                                                            0, 0, 0);
-            const float4 X = *reinterpret_cast<const float4 *>(xsum + ((uint64_t)t * nsb + sb) * 16 + 4 * kg);
-            acc[t][0] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X.x, D[0]), acc[t][0]);
-            acc[t][1] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X.y, D[1]), acc[t][1]);
-            acc[t][2] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X.z, D[2]), acc[t][2]);
-            acc[t][3] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X.w, D[3]), acc[t][3]);
+            dq[i][j] = blk[0];
+            v0[i][j] = q[0] | ((uint32_t)q[1] << 16);
+            v1[i][j] = q[2] | ((uint32_t)q[3] << 16);
         }
     }
-    if (live) {
+    asm volatile("" ::: "memory");  // keep the weight loads issued ahead of the fragment build
+    fr.store(lf, lx, m, k, sb0);
+    __syncthreads();
+    float acc[RT][TT][4];
+#pragma unroll
+    for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t tok = t * 16 + 4 * kg + r;
-                if (tok < m) c[(uint64_t)tok * n + row] = acc[t][r];
+            for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SB; j++) {
+        if (sb0 + j >= nsb) break;
+        bf16x8 A[TT][PARTS];
+        float4 X[TT];
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+#pragma unroll
+            for (int p = 0; p < PARTS; p++)
+                A[t][p] = __builtin_bit_cast(bf16x8, lf[((t * SB + j) * PARTS + p) * 64 + l]);
+            X[t] = *reinterpret_cast<const float4 *>(lx + (t * SB + j) * 16 + 4 * kg);
+        }
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const float d = ref_half(dq[i][j]);
+            uint32_t a0, a1, a2, a3;
+            q8_codes(v0[i][j], a0, a1);
+            q8_codes(v1[i][j], a2, a3);
+            const bf16x8 B = as_bf16x8(a0, a1, a2, a3);
+#pragma unroll
+            for (int t = 0; t < TT; t++) {
+                f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int p = 0; p < PARTS; p++) D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t][p], B, D, 0, 0, 0);
+                acc[i][t][0] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].x, D[0]), acc[i][t][0]);
+                acc[i][t][1] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].y, D[1]), acc[i][t][1]);
+                acc[i][t][2] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].z, D[2]), acc[i][t][2]);
+                acc[i][t][3] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].w, D[3]), acc[i][t][3]);
             }
+        }
     }
+    finish<TT, RT>(acc, out, res, part, cnt, rt0, m, n);
 }
 
 // Fallback for shapes outside the MFMA path (f32 weights, k not a multiple of the
-// block, unaligned pointers): one wavefront per output row, element-wise decode.
+// block, unaligned pointers, k = 0): one wavefront per output row, element-wise
+// decode.  c = res + W x when res is given.
 __global__ __launch_bounds__(256) void k_generic_batch(const void *__restrict__ xv, int x_bf16,
-                                                       const void *__restrict__ wv, float *__restrict__ c, uint32_t m,
-                                                       uint32_t k, uint32_t n, int dtype) {
+                                                       const void *__restrict__ wv, float *c, const float *res,
+                                                       uint32_t m, uint32_t k, uint32_t n, int dtype) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;
@@ -279,14 +451,18 @@ __global__ __launch_bounds__(256) void k_generic_batch(const void *__restrict__ 
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const float s = wave_sum(acc[t]);
-            if (lane == 0 && t0 + t < m) c[(uint64_t)(t0 + t) * n + row] = s;
+            if (lane == 0 && t0 + t < m) {
+                const uint64_t o = (uint64_t)(t0 + t) * n + row;
+                c[o] = res ? res[o] + s : s;
+            }
         }
     }
 }
 
-// Per-device workspace for activation fragments; grown on demand, kept for the
-// life of the process.  Calls on one device share it: calls that overlap in time
-// on different streams of the same device must be serialised by the caller.
+// Per-device workspace (arrival counters, partial sums); grown on demand, zeroed
+// when allocated, kept for the life of the process.  Calls on one device share it:
+// calls that overlap in time on different streams of the same device must be
+// serialised by the caller.
 struct Workspace {
     void *ptr = nullptr;
     uint64_t bytes = 0;
@@ -300,7 +476,7 @@ int workspace(uint64_t need, void **out) {
     Workspace &ws = g_ws[dev];
     if (ws.bytes < need) {
         if (ws.ptr) {
-            LG_HIP_TRY(hipDeviceSynchronize());  // earlier launches may still read it
+            LG_HIP_TRY(hipDeviceSynchronize());  // earlier launches may still use it
             LG_HIP_TRY(hipFree(ws.ptr));
         }
         ws.ptr = nullptr;
@@ -309,95 +485,136 @@ int workspace(uint64_t need, void **out) {
         hipError_t e = hipMalloc(&ws.ptr, sz);
         if (e != hipSuccess) return fail(LG_ENOMEM, "batch workspace (%llu bytes): %s", (unsigned long long)sz,
                                          hipGetErrorString(e));
+        LG_HIP_TRY(hipMemset(ws.ptr, 0, sz));  // arrival counters start at zero
         ws.bytes = sz;
     }
     *out = ws.ptr;
     return LG_OK;
 }
 
-template <int PARTS>
-int launch_main(int dtype, const uint4 *frag, const float *xs, const uint8_t *w, float *c, uint32_t m, uint32_t k,
-                uint32_t n, hipStream_t s) {
-    const uint32_t tiles = (m + 15) / 16;
-    const dim3 grid((n + 63) / 64), block(256);
-    if (dtype == LG_Q4_K) {
-        const uint64_t rb = (uint64_t)k / QK_K * Q4K_BYTES;
-        switch (tiles) {
-        case 1: hipLaunchKernelGGL((k_q4k_batch<PARTS, 1>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        case 2: hipLaunchKernelGGL((k_q4k_batch<PARTS, 2>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        case 3: hipLaunchKernelGGL((k_q4k_batch<PARTS, 3>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        default: hipLaunchKernelGGL((k_q4k_batch<PARTS, 4>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        }
-    } else {
-        const uint64_t rb = (uint64_t)k / QK8_0 * Q80_BYTES;
-        switch (tiles) {
-        case 1: hipLaunchKernelGGL((k_q80_batch<PARTS, 1>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        case 2: hipLaunchKernelGGL((k_q80_batch<PARTS, 2>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        case 3: hipLaunchKernelGGL((k_q80_batch<PARTS, 3>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        default: hipLaunchKernelGGL((k_q80_batch<PARTS, 4>), grid, block, 0, s, frag, xs, w, c, m, k, n, rb); break;
-        }
-    }
-    return after_launch(dtype == LG_Q4_K ? "proj_q4k_batch" : "proj_q8_0_batch", s);
+// Launch shape: CH chunks per slice (the slice's fragments fill LDS: 48 KB for f32
+// activations), one slice per workgroup column, RT row tiles per wavefront: the
+// most that still gives 256 workgroups.
+struct MmShape {
+    uint32_t ch, slices, tiles, rt, groups;
+};
+
+MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
+    const uint32_t tiles = (m + 15) / 16 > 2 ? 2 : (m + 15) / 16;  // per launch; larger m runs in pairs of tiles
+    const uint32_t ch = dtype == LG_Q4_K ? (tiles == 1 ? 2 : 1) : 1;
+    const uint32_t chunks = (k + 255) / 256, slices = (chunks + ch - 1) / ch;
+    uint32_t rt = 4;
+    while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 256) rt /= 2;
+    return {ch, slices, tiles, rt, (n + 64 * rt - 1) / (64 * rt)};
 }
+
+template <int TT, int PARTS, int CH>
+void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const uint8_t *w, float *out, const float *res,
+               float *part, uint32_t *cnt, uint32_t m, uint32_t k, uint32_t n, uint64_t rb, hipStream_t s) {
+#define LG_MM(K, R)                                                                                                    \
+    hipLaunchKernelGGL((K<TT, PARTS, CH, R>), grid, dim3(256), 0, s, x, w, out, res, part, cnt, m, k, n, rb)
+    if (dtype == LG_Q4_K) {
+        if (rt == 4) LG_MM(k_q4k_mm, 4);
+        else if (rt == 2) LG_MM(k_q4k_mm, 2);
+        else LG_MM(k_q4k_mm, 1);
+    } else {
+        if (rt == 4) LG_MM(k_q80_mm, 4);
+        else if (rt == 2) LG_MM(k_q80_mm, 2);
+        else LG_MM(k_q80_mm, 1);
+    }
+#undef LG_MM
+}
+
+template <int PARTS>
+int launch_mm(int dtype, const void *x, const uint8_t *w, float *out, const float *res, float *part, uint32_t *cnt,
+              uint32_t m, uint32_t k, uint32_t n, hipStream_t s) {
+    const MmShape sh = mm_shape(dtype, k, n, m);
+    const dim3 grid(sh.groups, sh.slices);
+    const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
+    if (dtype == LG_Q4_K) {
+        if (sh.tiles == 1) launch_rt<1, PARTS, 2>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
+        else launch_rt<2, PARTS, 1>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
+    } else {
+        if (sh.tiles == 1) launch_rt<1, PARTS, 1>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
+        else launch_rt<2, PARTS, 1>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
+    }
+    return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
+}
+
+uint64_t align256(uint64_t b) { return (b + 255) & ~(uint64_t)255; }
+
+// Workspace layout: the arrival counters at a fixed place (offset 0, one per row
+// group, for n up to 64 * CNT_MAX rows) so that every call finds them zero, then
+// the partial sums.
+constexpr uint64_t CNT_BYTES = PROJ_WS_COUNTERS;
+constexpr uint32_t CNT_MAX = CNT_BYTES / 4;
 
 }  // namespace
 
 namespace lg {
 
-uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t m, int x_dtype) {
-    const uint64_t tiles = (m + 15) / 16, nsb = k / 32;
-    const int parts = x_dtype == LG_BF16 ? 1 : 3;
-    return tiles * nsb * parts * 64 * 16 + tiles * nsb * 16 * 4;
+uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype) {
+    (void)x_dtype;
+    if (w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) return 0;
+    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32);
+    if (sh.slices <= 1) return 0;
+    const uint64_t ml = m < 32 ? m : 32;
+    return CNT_BYTES + align256((uint64_t)sh.slices * ml * n * 4);
 }
 
 int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
-               void *ws_given, uint64_t ws_bytes, hipStream_t s) {
+               void *ws_given, uint64_t ws_bytes, hipStream_t s, const float *res) {
     const char *name = "lg_dispatch_proj_quant_batch";
     if (n == 0 || m == 0) return LG_OK;
     LG_REQUIRE(m <= 64, "%s: m=%u exceeds 64", name, m);
+    LG_REQUIRE(n <= 64u * CNT_MAX, "%s: n=%u exceeds %u", name, n, 64u * CNT_MAX);
     LG_REQUIRE(x && w && c, "%s: null pointer", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
     LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32, "%s: weight dtype %d", name, w_dtype);
     const uint64_t xbytes = (uint64_t)m * k * (x_dtype == LG_F32 ? 4 : 2);
     LG_EXTENT(c, (uint64_t)m * n * 4, name);
-    if (k == 0) {
-        LG_HIP_TRY(hipMemsetAsync(c, 0, (uint64_t)m * n * 4, s));
-        return after_launch(name, s);
+    if (res) LG_EXTENT(res, (uint64_t)m * n * 4, name);
+    if (k) {
+        LG_EXTENT(x, xbytes, name);
+        LG_EXTENT(w, tensor_bytes(w_dtype, (uint64_t)n * k), name);
     }
-    LG_EXTENT(x, xbytes, name);
-    LG_EXTENT(w, tensor_bytes(w_dtype, (uint64_t)n * k), name);
     const uint32_t blk = w_dtype == LG_Q4_K ? QK_K : QK8_0;
-    const bool fast = w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 &&
+    const bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 &&
                       (w_dtype != LG_Q4_K || (reinterpret_cast<uintptr_t>(w) & 15u) == 0) &&
-                      (reinterpret_cast<uintptr_t>(w) & 1u) == 0;
+                      (reinterpret_cast<uintptr_t>(w) & 1u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (!fast) {
-        hipLaunchKernelGGL(k_generic_batch, dim3((n + 3) / 4), dim3(256), 0, s, x, (int)(x_dtype == LG_BF16), w, c, m,
-                           k, n, w_dtype);
+        hipLaunchKernelGGL(k_generic_batch, dim3((n + 3) / 4), dim3(256), 0, s, x, (int)(x_dtype == LG_BF16), w, c,
+                           res, m, k, n, w_dtype);
         return after_launch(name, s);
     }
-    const uint32_t tiles = (m + 15) / 16, nsb = k / 32;
-    const int parts = x_dtype == LG_BF16 ? 1 : 3;
-    const uint64_t frag_bytes = (uint64_t)tiles * nsb * parts * 64 * 16;
+    const uint64_t need = proj_batch_ws_bytes(k, n, m, x_dtype, w_dtype);
     void *ws = ws_given;
     int st = LG_OK;
-    if (ws) {
-        LG_REQUIRE(ws_bytes >= proj_batch_ws_bytes(k, m, x_dtype), "%s: workspace of %llu bytes too small", name,
-                   (unsigned long long)ws_bytes);
-    } else {
-        st = workspace(proj_batch_ws_bytes(k, m, x_dtype), &ws);
+    if (need) {
+        if (ws) {
+            LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small", name, (unsigned long long)ws_bytes);
+        } else {
+            st = workspace(need, &ws);
+            if (st != LG_OK) return st;
+        }
+    }
+    const uint32_t tiles = (m + 15) / 16;
+    const uint64_t xsz = x_dtype == LG_F32 ? 4 : 2;
+    for (uint32_t t0 = 0; t0 < tiles; t0 += 2) {  // pairs of 16-token tiles
+        const uint32_t ml = m - 16 * t0 < 32 ? m - 16 * t0 : 32;
+        const MmShape sh = mm_shape(w_dtype, k, n, ml);
+        uint32_t *cnt = static_cast<uint32_t *>(ws);
+        float *part = ws ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + CNT_BYTES) : nullptr;
+        if (sh.slices > 1) LG_REQUIRE(ws, "%s: no workspace for %u slices", name, sh.slices);
+        const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
+        float *ct = c + (uint64_t)16 * t0 * n;
+        const float *rt = res ? res + (uint64_t)16 * t0 * n : nullptr;
+        const uint8_t *wb = static_cast<const uint8_t *>(w);
+        st = x_dtype == LG_BF16 ? launch_mm<1>(w_dtype, xt, wb, ct, rt, part, cnt, ml, k, n, s)
+                                : launch_mm<3>(w_dtype, xt, wb, ct, rt, part, cnt, ml, k, n, s);
         if (st != LG_OK) return st;
     }
-    uint4 *frag = static_cast<uint4 *>(ws);
-    float *xs = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + frag_bytes);
-    if (parts == 1)
-        hipLaunchKernelGGL(k_prep_x<1>, dim3(nsb, tiles), dim3(64), 0, s, x, m, k, frag, xs);
-    else
-        hipLaunchKernelGGL(k_prep_x<3>, dim3(nsb, tiles), dim3(64), 0, s, x, m, k, frag, xs);
-    st = after_launch("prep_x", s);
-    if (st != LG_OK) return st;
-    const uint8_t *wb = static_cast<const uint8_t *>(w);
-    return parts == 1 ? launch_main<1>(w_dtype, frag, xs, wb, c, m, k, n, s)
-                      : launch_main<3>(w_dtype, frag, xs, wb, c, m, k, n, s);
+    return LG_OK;
 }
 
 }  // namespace lg
