@@ -37,12 +37,6 @@ using namespace lg;
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u) return (u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u);  // inf / NaN
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-__device__ __forceinline__ float bf16_f(uint32_t b) { return __uint_as_float(b << 16); }
 
 // Sum over the threads of a workgroup of THREADS; every thread receives it.
 template <int THREADS>
@@ -75,6 +69,35 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *x, const float *__
     const float ms = block_sum<256>(s, red) / (float)n;
     const float rms = 1.0f / sqrtf(ms + eps);
     for (uint32_t i = threadIdx.x; i < n; i += 256) out[base + i] = xr[i] * wr[i] * rms;
+}
+
+// The same for rows of n = 1024 * V4 floats (16-byte aligned): each thread keeps its
+// V4 float4 of the row in registers (one load each, all in flight together).
+template <int V4>
+__global__ __launch_bounds__(256) void k_rmsnorm4(const float *x, const float *__restrict__ w, float *out,
+                                                  uint32_t n, uint32_t ldx, float eps) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * ldx + (uint64_t)blockIdx.y * n;
+    const float4 *xr = reinterpret_cast<const float4 *>(x + base);
+    const float4 *wr = reinterpret_cast<const float4 *>(w + (uint64_t)blockIdx.y * n);
+    float4 v[V4], wv[V4];
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        v[i] = xr[i * 256 + threadIdx.x];
+        wv[i] = wr[i * 256 + threadIdx.x];
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V4; i++)
+        s = __builtin_fmaf(v[i].x, v[i].x, __builtin_fmaf(v[i].y, v[i].y,
+            __builtin_fmaf(v[i].z, v[i].z, __builtin_fmaf(v[i].w, v[i].w, s))));
+    const float ms = block_sum<256>(s, red) / (float)n;
+    const float rms = 1.0f / sqrtf(ms + eps);
+    float4 *o = reinterpret_cast<float4 *>(out + base);
+#pragma unroll
+    for (int i = 0; i < V4; i++)
+        o[i * 256 + threadIdx.x] = make_float4(v[i].x * wv[i].x * rms, v[i].y * wv[i].y * rms, v[i].z * wv[i].z * rms,
+                                               v[i].w * wv[i].w * rms);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -151,22 +174,29 @@ struct __attribute__((aligned(16))) AttnLds {
     uint16_t p[NP][AQ * PSTR];
 };
 
-__device__ __forceinline__ void split3(float x, uint32_t &a, uint32_t &b, uint32_t &c) {
-    a = bf16_rne(x);
-    float r = x - bf16_f(a);  // exact
-    b = bf16_rne(r);
-    r -= bf16_f(b);           // exact
-    c = bf16_rne(r);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32): a low, b high.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+// The three parts of the pair (a, b), each packed (a low, b high).
+__device__ __forceinline__ void split3x2(float a, float b, uint32_t &w0, uint32_t &w1, uint32_t &w2) {
+    w0 = pk_bf16(a, b);
+    a -= __uint_as_float(w0 << 16);  // exact
+    b -= __uint_as_float(w0 & 0xFFFF0000u);
+    w1 = pk_bf16(a, b);
+    a -= __uint_as_float(w1 << 16);
+    b -= __uint_as_float(w1 & 0xFFFF0000u);
+    w2 = pk_bf16(a, b);
 }
 
 __device__ __forceinline__ bf16x8 ld_frag(const uint16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(p));
 }
 
-__device__ __forceinline__ bf16x8 pack8(const uint32_t *h) {
-    return __builtin_bit_cast(bf16x8, make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16,
-                                                 h[6] | h[7] << 16));
-}
 
 // D += A B over the six part products that reach f32 precision (|a_i b_j| <= 2^-9(i+j)
 // |a b|; the three dropped ones are below 2^-26), smallest first.
@@ -196,51 +226,63 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
     const uint32_t l16 = lane & 15u, kg = lane >> 4;
     const uint32_t kvld = n_kv * AHD, qld = n_q * AHD;
 
-    // K and V of the chunk's 64 positions, 4 floats per step, as bf16 parts
-    for (uint32_t e = tid; e < ACH * AHD / 4; e += 256) {
-        const uint32_t pi = e / (AHD / 4), d = 4 * (e % (AHD / 4));
-        const uint32_t p = c * ACH + pi;
-        float4 kv = make_float4(0, 0, 0, 0), vv = kv;
-        if (p < S) {
-            const bool s0 = p < n0;
-            const uint64_t off = (uint64_t)(s0 ? p : p - n0) * kvld + h * AHD + d;
-            kv = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + off);
-            vv = *reinterpret_cast<const float4 *>((s0 ? v0 : v1) + off);
-        }
-        const float fk[4] = {kv.x, kv.y, kv.z, kv.w}, fv[4] = {vv.x, vv.y, vv.z, vv.w};
+    // K and V of the chunk's 64 positions as bf16 parts.  A thread takes blocks of 4
+    // positions x 4 dims: K rows and the transposed V rows go to LDS 4 values (8
+    // bytes) at a time.
+    for (uint32_t e = tid; e < (ACH / 4) * (AHD / 4); e += 256) {
+        const uint32_t pq = e / (AHD / 4), d = 4 * (e % (AHD / 4));
+        float fk[4][4], fv[4][4];  // [position][dim]
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t a, b, cc;
-            split3(fk[i], a, b, cc);
-            L.k[0][pi * KSTR + d + i] = (uint16_t)a;
-            L.k[1][pi * KSTR + d + i] = (uint16_t)b;
-            L.k[2][pi * KSTR + d + i] = (uint16_t)cc;
-            split3(fv[i], a, b, cc);
-            L.v[0][(d + i) * VSTR + pi] = (uint16_t)a;
-            L.v[1][(d + i) * VSTR + pi] = (uint16_t)b;
-            L.v[2][(d + i) * VSTR + pi] = (uint16_t)cc;
+        for (int i = 0; i < 4; i++) {  // branch-free: positions past S read position S-1, zeroed
+            const uint32_t p = c * ACH + 4 * pq + i, pc = p < S ? p : S - 1;
+            const bool s0 = pc < n0;
+            const uint64_t off = (uint64_t)(s0 ? pc : pc - n0) * kvld + h * AHD + d;
+            const float4 kv = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + off);
+            const float4 vv = *reinterpret_cast<const float4 *>((s0 ? v0 : v1) + off);
+            const bool ok = p < S;
+            fk[i][0] = ok ? kv.x : 0.f, fk[i][1] = ok ? kv.y : 0.f, fk[i][2] = ok ? kv.z : 0.f, fk[i][3] = ok ? kv.w : 0.f;
+            fv[i][0] = ok ? vv.x : 0.f, fv[i][1] = ok ? vv.y : 0.f, fv[i][2] = ok ? vv.z : 0.f, fv[i][3] = ok ? vv.w : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // K: position 4pq+i, dims d..d+3
+            uint32_t a[2], b[2], cc[2];
+            split3x2(fk[i][0], fk[i][1], a[0], b[0], cc[0]);
+            split3x2(fk[i][2], fk[i][3], a[1], b[1], cc[1]);
+            const uint32_t o = (4 * pq + i) * KSTR + d;
+            *reinterpret_cast<uint2 *>(L.k[0] + o) = make_uint2(a[0], a[1]);
+            *reinterpret_cast<uint2 *>(L.k[1] + o) = make_uint2(b[0], b[1]);
+            *reinterpret_cast<uint2 *>(L.k[2] + o) = make_uint2(cc[0], cc[1]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {  // V^T: dim d+j, positions 4pq..4pq+3
+            uint32_t a[2], b[2], cc[2];
+            split3x2(fv[0][j], fv[1][j], a[0], b[0], cc[0]);
+            split3x2(fv[2][j], fv[3][j], a[1], b[1], cc[1]);
+            const uint32_t o = (d + j) * VSTR + 4 * pq;
+            *reinterpret_cast<uint2 *>(L.v[0] + o) = make_uint2(a[0], a[1]);
+            *reinterpret_cast<uint2 *>(L.v[1] + o) = make_uint2(b[0], b[1]);
+            *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
         }
     }
     // this lane's query row: A operand fragments for the 4 k-steps, straight from HBM
     const uint32_t qr = 16 * wave + l16;
     bf16x8 qa[AHD / 32][NP];
     {
-        const bool live = qr < nq;
-        const uint32_t t = live ? qr / G : 0, hq = live ? h * G + qr % G : 0;
+        const bool live = qr < nq;  // branch-free: query rows past nq read row 0, zeroed
+        const uint32_t t = live ? qr / G : 0, hq = live ? h * G + qr % G : h * G;
         const float *qp = q + (uint64_t)t * qld + hq * AHD + 8 * kg;
 #pragma unroll
         for (int ks = 0; ks < (int)(AHD / 32); ks++) {
-            float4 x0 = make_float4(0, 0, 0, 0), x1 = x0;
-            if (live) {
-                x0 = *reinterpret_cast<const float4 *>(qp + 32 * ks);
-                x1 = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
-            }
-            const float f[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            uint32_t hp[NP][8];
+            const float4 x0 = *reinterpret_cast<const float4 *>(qp + 32 * ks);
+            const float4 x1 = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
+            const float f[8] = {live ? x0.x : 0.f, live ? x0.y : 0.f, live ? x0.z : 0.f, live ? x0.w : 0.f,
+                                live ? x1.x : 0.f, live ? x1.y : 0.f, live ? x1.z : 0.f, live ? x1.w : 0.f};
+            uint32_t wp[NP][4];
 #pragma unroll
-            for (int i = 0; i < 8; i++) split3(f[i], hp[0][i], hp[1][i], hp[2][i]);
+            for (int i = 0; i < 4; i++) split3x2(f[2 * i], f[2 * i + 1], wp[0][i], wp[1][i], wp[2][i]);
 #pragma unroll
-            for (int pp = 0; pp < NP; pp++) qa[ks][pp] = pack8(hp[pp]);
+            for (int pp = 0; pp < NP; pp++)
+                qa[ks][pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
         }
     }
     __syncthreads();
@@ -291,13 +333,15 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 #pragma unroll
     for (int pt = 0; pt < 4; pt++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
+        for (int r = 0; r < 4; r += 2) {  // rows r and r+1 converted together
             const uint32_t idx = (16 * wave + 4 * kg + r) * PSTR + 16 * pt + l16;
-            uint32_t a, b, cc;
-            split3(Sd[pt][r], a, b, cc);
-            L.p[0][idx] = (uint16_t)a;
-            L.p[1][idx] = (uint16_t)b;
-            L.p[2][idx] = (uint16_t)cc;
+            uint32_t w[NP];
+            split3x2(Sd[pt][r], Sd[pt][r + 1], w[0], w[1], w[2]);
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) {
+                L.p[pp][idx] = (uint16_t)w[pp];
+                L.p[pp][idx + PSTR] = (uint16_t)(w[pp] >> 16);
+            }
         }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -332,25 +376,45 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
     }
 }
 
-// out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c; one wavefront per query.
+// out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c; one wavefront per
+// query, the chunks' partials loaded CB at a time (all in flight together).
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
                                                       const float *__restrict__ part_ml, float *__restrict__ out,
                                                       uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch) {
+    constexpr uint32_t CB = 8;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t gq = blockIdx.x * 4 + (threadIdx.x >> 6);  // over n_kv * AQ
     const uint32_t G = n_q / n_kv;
     const uint32_t h = gq / AQ, qi = gq % AQ;
     if (h >= n_kv || qi >= rows * G) return;
+    const uint64_t q0 = (uint64_t)h * nch * AQ + qi;  // partial index of chunk c: q0 + c * AQ
     float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; c++) M = fmaxf(M, part_ml[2 * (((uint64_t)h * nch + c) * AQ + qi)]);
+    for (uint32_t c0 = 0; c0 < nch; c0 += CB) {
+        float mc[CB];
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) mc[b] = c0 + b < nch ? part_ml[2 * (q0 + (c0 + b) * AQ)] : -INFINITY;
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) M = fmaxf(M, mc[b]);
+    }
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (uint32_t c = 0; c < nch; c++) {
-        const uint64_t pq = ((uint64_t)h * nch + c) * AQ + qi;
-        const float mc = part_ml[2 * pq];
-        const float wgt = mc == -INFINITY ? 0.0f : expf(mc - M);
-        L = __builtin_fmaf(wgt, part_ml[2 * pq + 1], L);
-        o0 = __builtin_fmaf(wgt, part_o[pq * AHD + lane], o0);
-        o1 = __builtin_fmaf(wgt, part_o[pq * AHD + 64 + lane], o1);
+    for (uint32_t c0 = 0; c0 < nch; c0 += CB) {
+        float mc[CB], lc[CB], a0[CB], a1[CB];
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) {
+            const uint32_t c = c0 + b < nch ? c0 + b : nch - 1;
+            const uint64_t pq = q0 + (uint64_t)c * AQ;
+            mc[b] = c0 + b < nch ? part_ml[2 * pq] : -INFINITY;
+            lc[b] = part_ml[2 * pq + 1];
+            a0[b] = part_o[pq * AHD + lane];
+            a1[b] = part_o[pq * AHD + 64 + lane];
+        }
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) {  // chunk order
+            const float wgt = mc[b] == -INFINITY ? 0.0f : expf(mc[b] - M);
+            L = __builtin_fmaf(wgt, lc[b], L);
+            o0 = __builtin_fmaf(wgt, a0[b], o0);
+            o1 = __builtin_fmaf(wgt, a1[b], o1);
+        }
     }
     const uint32_t t = qi / G, hq = h * G + qi % G;
     float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
@@ -430,7 +494,19 @@ inline unsigned blocks_for(uint64_t n) { return (unsigned)((n + 255) / 256); }
 
 int run_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, uint32_t chunks, uint32_t ldx,
                 float eps, hipStream_t s) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(rows, chunks), dim3(256), 0, s, x, w, out, n, ldx, eps);
+    const bool vec = n % 1024 == 0 && ldx % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                                         reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+    const dim3 grid(rows, chunks);
+    if (vec && n == 4096)
+        hipLaunchKernelGGL(k_rmsnorm4<4>, grid, dim3(256), 0, s, x, w, out, n, ldx, eps);
+    else if (vec && n == 2048)
+        hipLaunchKernelGGL(k_rmsnorm4<2>, grid, dim3(256), 0, s, x, w, out, n, ldx, eps);
+    else if (vec && n == 1024)
+        hipLaunchKernelGGL(k_rmsnorm4<1>, grid, dim3(256), 0, s, x, w, out, n, ldx, eps);
+    else if (vec && n == 8192)
+        hipLaunchKernelGGL(k_rmsnorm4<8>, grid, dim3(256), 0, s, x, w, out, n, ldx, eps);
+    else
+        hipLaunchKernelGGL(k_rmsnorm, grid, dim3(256), 0, s, x, w, out, n, ldx, eps);
     return after_launch("rmsnorm", s);
 }
 

@@ -39,14 +39,34 @@ using namespace lg;
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
-constexpr int PERM[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7F800000u) == 0x7F800000u) return (u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u);  // inf / NaN
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32): a low, b high.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+// Scale factors of the 8 sub-blocks of a Q4_K super-block (ggml get_scale_min_k4,
+// kernels/proj_q4k.comp:46-58) from the scale dwords s0, s1, s2, all at once:
+// a[j] = 16 d sc_j and cc[j] = dmin m_j + a[j].
+__device__ __forceinline__ void q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2, float d16, float dmin, float (&a)[8],
+                                           float (&cc)[8]) {
+    const uint32_t sl = s0 & 0x3F3F3F3Fu, ml = s1 & 0x3F3F3F3Fu;
+    const uint32_t sh = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t mh = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    const float scf[8] = {ubyte_f<0>(sl), ubyte_f<1>(sl), ubyte_f<2>(sl), ubyte_f<3>(sl),
+                          ubyte_f<0>(sh), ubyte_f<1>(sh), ubyte_f<2>(sh), ubyte_f<3>(sh)};
+    const float mnf[8] = {ubyte_f<0>(ml), ubyte_f<1>(ml), ubyte_f<2>(ml), ubyte_f<3>(ml),
+                          ubyte_f<0>(mh), ubyte_f<1>(mh), ubyte_f<2>(mh), ubyte_f<3>(mh)};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        a[j] = d16 * scf[j];
+        cc[j] = __builtin_fmaf(dmin, mnf[j], a[j]);
+    }
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     uint4 u = make_uint4(a, b, c, d);
@@ -120,38 +140,46 @@ struct Frags {
             uint32_t t, jj, kg, tl;
             unit(i, t, jj, kg, tl);
             const bool valid = t * 16 + tl < m && sb0 + jj < nsb;
-            float v[8];
-            uint32_t code[PARTS][8];
+            float sum;
+            uint32_t wd[PARTS][4];  // fragment slots 0..7 hold activations 0,2,1,3,4,6,5,7
             if constexpr (PARTS == 1) {
-                const uint32_t wd[4] = {h[i].x, h[i].y, h[i].z, h[i].w};
+                const uint32_t raw[4] = {h[i].x, h[i].y, h[i].z, h[i].w};  // activations 0..7, two per word
+                // slot pairs (0,1), (2,3), (4,5), (6,7) hold activations (0,2), (1,3), (4,6), (5,7)
+                const uint32_t w0 = (raw[0] & 0xFFFFu) | (raw[1] << 16), w1 = (raw[0] >> 16) | (raw[1] & 0xFFFF0000u);
+                const uint32_t w2 = (raw[2] & 0xFFFFu) | (raw[3] << 16), w3 = (raw[2] >> 16) | (raw[3] & 0xFFFF0000u);
+                wd[0][0] = valid ? w0 : 0u;
+                wd[0][1] = valid ? w1 : 0u;
+                wd[0][2] = valid ? w2 : 0u;
+                wd[0][3] = valid ? w3 : 0u;
+                float v[8];
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    code[0][q] = valid ? (wd[q / 2] >> (16 * (q % 2))) & 0xFFFFu : 0u;
-                    v[q] = bf16_to_f32(code[0][q]);
+                for (int q = 0; q < 4; q++) {
+                    v[2 * q] = __uint_as_float(wd[0][q] << 16);
+                    v[2 * q + 1] = __uint_as_float(wd[0][q] & 0xFFFF0000u);
                 }
+                sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             } else {
-                const float f[8] = {r[i][0].x, r[i][0].y, r[i][0].z, r[i][0].w,
-                                    r[i][1].x, r[i][1].y, r[i][1].z, r[i][1].w};
+                float f[8] = {r[i][0].x, r[i][0].y, r[i][0].z, r[i][0].w, r[i][1].x, r[i][1].y, r[i][1].z, r[i][1].w};
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    v[q] = valid ? f[q] : 0.0f;
-                    float rest = v[q];
+                for (int q = 0; q < 8; q++) f[q] = valid ? f[q] : 0.0f;
+                sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+                // pairs in slot order: (0,2) (1,3) (4,6) (5,7); each part is the nearest
+                // bf16 of what the earlier parts leave (exact residuals)
+                float lo[4] = {f[0], f[1], f[4], f[5]}, hi[4] = {f[2], f[3], f[6], f[7]};
 #pragma unroll
-                    for (int p = 0; p < PARTS; p++) {
-                        code[p][q] = f32_to_bf16_rne(rest);
-                        rest -= bf16_to_f32(code[p][q]);  // exact: rest stays a multiple of x's last place
+                for (int p = 0; p < PARTS; p++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        wd[p][q] = pk_bf16(lo[q], hi[q]);
+                        if (p + 1 < PARTS) {
+                            lo[q] -= __uint_as_float(wd[p][q] << 16);
+                            hi[q] -= __uint_as_float(wd[p][q] & 0xFFFF0000u);
+                        }
                     }
-                }
             }
 #pragma unroll
-            for (int p = 0; p < PARTS; p++) {
-                uint32_t c[8];
-#pragma unroll
-                for (int q = 0; q < 8; q++) c[q] = code[p][PERM[q]];
-                lf[((t * SB + jj) * PARTS + p) * 64 + kg * 16 + tl] =
-                    make_uint4(c[0] | c[1] << 16, c[2] | c[3] << 16, c[4] | c[5] << 16, c[6] | c[7] << 16);
-            }
-            float sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            for (int p = 0; p < PARTS; p++)
+                lf[((t * SB + jj) * PARTS + p) * 64 + kg * 16 + tl] = make_uint4(wd[p][0], wd[p][1], wd[p][2], wd[p][3]);
             sum += __shfl_xor(sum, 16);  // the 4 k-groups of this token and sub-block
             sum += __shfl_xor(sum, 32);
             if (kg == 0) lx[(t * SB + jj) * 16 + tl] = sum;
@@ -285,13 +313,12 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
             for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
 #pragma unroll
     for (int cb = 0; cb < CH; cb++) {
-        if (b0 + cb >= nb) break;
-        float d16[RT], dmin[RT];
+        if (b0 + cb >= nb) continue;  // uniform: past the end of k
+        float sa[RT][8], scc[RT][8];
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-            d16[i] = 16.0f * ref_half(hd[i][cb].x & 0xFFFFu);
-            dmin[i] = ref_half(hd[i][cb].x >> 16);
-        }
+        for (int i = 0; i < RT; i++)
+            q4k_scales(hd[i][cb].y, hd[i][cb].z, hd[i][cb].w, 16.0f * ref_half(hd[i][cb].x & 0xFFFFu),
+                       ref_half(hd[i][cb].x >> 16), sa[i], scc[i]);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             bf16x8 blo[RT], bhi[RT];
@@ -311,10 +338,7 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
                 }
 #pragma unroll
                 for (int i = 0; i < RT; i++) {
-                    uint32_t sc, mnv;
-                    scale_min_k4(j, hd[i][cb].y, hd[i][cb].z, hd[i][cb].w, sc, mnv);
-                    const float a = d16[i] * (float)sc;
-                    const float cc = __builtin_fmaf(dmin[i], (float)mnv, a);
+                    const float a = sa[i][j], cc = scc[i][j];
 #pragma unroll
                     for (int t = 0; t < TT; t++) {
                         f32x4 D = {0.f, 0.f, 0.f, 0.f};
@@ -373,7 +397,7 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
             for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
 #pragma unroll
     for (int j = 0; j < SB; j++) {
-        if (sb0 + j >= nsb) break;
+        if (sb0 + j >= nsb) continue;  // uniform: past the end of k
         bf16x8 A[TT][PARTS];
         float4 X[TT];
 #pragma unroll
