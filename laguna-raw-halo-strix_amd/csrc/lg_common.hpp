@@ -56,6 +56,11 @@ struct DeferSync {
 // call expects to find zero (and leaves zero); callers that lay other data out
 // after a workspace keep that region at a fixed place.
 constexpr uint64_t PROJ_WS_COUNTERS = 65536;
+// The per-device workspace (arrival counters first, then partial sums) shared by
+// the product kernels that split k over workgroups: at least `need` bytes, grown
+// on demand (after a device synchronise), zeroed when allocated and kept for the
+// process.  Calls that overlap in time on one device must not share it.
+int device_workspace(uint64_t need, void **out);
 uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype);
 int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                void *ws, uint64_t ws_bytes, hipStream_t s, const float *res = nullptr);

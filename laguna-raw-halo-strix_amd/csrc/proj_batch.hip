@@ -493,7 +493,11 @@ struct Workspace {
 };
 std::vector<Workspace> g_ws;
 
-int workspace(uint64_t need, void **out) {
+}  // namespace
+
+namespace lg {
+
+int device_workspace(uint64_t need, void **out) {
     int dev = 0;
     LG_HIP_TRY(hipGetDevice(&dev));
     if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
@@ -515,6 +519,10 @@ int workspace(uint64_t need, void **out) {
     *out = ws.ptr;
     return LG_OK;
 }
+
+}  // namespace lg
+
+namespace {
 
 // Launch shape: CH chunks per slice (the slice's fragments fill LDS: 48 KB for f32
 // activations), one slice per workgroup column, RT row tiles per wavefront: the
@@ -618,7 +626,7 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
         if (ws) {
             LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small", name, (unsigned long long)ws_bytes);
         } else {
-            st = workspace(need, &ws);
+            st = device_workspace(need, &ws);
             if (st != LG_OK) return st;
         }
     }

@@ -2,35 +2,36 @@
 //
 // Replaces kernels/proj_q4k.comp, proj_q8_0.comp, proj.comp and activation.comp
 // (one invocation per output row, per-element byte decode, uncoalesced) with
-// wavefront-cooperative gfx950 kernels.
+// gfx950 kernels.
 //
-// Work split.  A "team" of TW = ceil(k/4096) waves covers one row: lane p of the
-// team owns the 64-element group p of the row (k/64 groups) and keeps the 64
-// activations of that group in registers; the team's partial sums meet in a
-// DPP/swizzle wavefront reduction (plus LDS across the TW waves).  A workgroup
-// holds TEAMS teams (8 waves) and normally there is one workgroup per CU: each
-// team owns a contiguous block of RPW rows (RPW <= 8, chosen so that the grid
-// covers the CUs once), and issues the loads of all RPW rows before anything else.
-// A matvec of this size is over in a few microseconds, so the whole share of a CU
-// (about 130 KB for Q4_K 4096 -> 14336) is in flight at once and each row is
-// computed as its bytes arrive.  The activations are read once per workgroup:
-// their global loads go out first, the row loads next, and only then is the
-// vector staged through LDS into registers.
+// Q4_K (k % 256 == 0, k <= 16384, 16-byte aligned tensor), two kernels chosen by
+// measurement:
+//  * plain projections: vector ALU (k_q4k_m1_rows, k_q4k_m1).  Lane p of a row
+//    team owns the 64-element group p of the row; a nibble masked in place is an
+//    f16 subnormal (q * 2^-24, or q * 2^-20 for a high nibble), so one AND gives two
+//    operands of v_fma_mix_f32 against the f32 activations, and the block's scale
+//    and min enter once per 32-element sub-block:
+//        sum_j x_j ((d sc) q_j - dmin m) = d sc 2^24 S - dmin m X,
+//        S = sum x q 2^-24,  X = sum x (per lane, once).
+//  * the fused SiLU(gate)*up down projection: int8 matrix cores (k_q4k_m1_mfma).
+//    The activations become exact integers (three signed byte digits per element,
+//    one power-of-two scale per 256-element super-block) and the raw nibbles are
+//    the other operand, so a byte product costs no decode; each (row, sub-block)
+//    pair gets its scale and min once, in an f32 epilogue.  Work is split over
+//    workgroups by rows and by k (each workgroup computes SiLU for, and converts,
+//    only its k slice); the slices of a row range are summed in slice order by
+//    the last workgroup to finish.
 //
-// Q4_K (k % 256 == 0, 16-byte aligned tensor): per row the lane loads the 16-byte
-// super-block header and the 32 quant bytes of its group with three 16-byte loads;
-// the team's loads cover the row's bytes exactly once.  A nibble masked in place
-// is an f16 subnormal (q * 2^-24, or q * 2^-20 for a high nibble), so one AND gives
-// two operands of v_fma_mix_f32 against the f32 activations, and the block's scale
-// and min enter once per 32-element sub-block:
-//     sum_j x_j ((d sc) q_j - dmin m) = d sc 2^24 S - dmin m X,
-//     S = sum x q 2^-24,  X = sum x (per lane, once).
-//
-// Q8_0: the same lane ownership (64 elements = two 34-byte blocks, 68 bytes, dword
-// aligned).  Each wave loads its 64-group share of a row with coalesced 16-byte
-// loads, writes it to its own LDS stage and each lane reads its 17 dwords back
-// (stride 17 dwords: no bank conflicts).  Bytes are biased to unsigned (q + 128),
-// converted with v_cvt_f32_ubyte and corrected by 128 X per block.
+// Q8_0: vector ALU.  A "team" of TW = ceil(k/4096) waves covers one row: lane p of
+// the team owns the 64-element group p of the row (two 34-byte blocks, 68 bytes,
+// dword aligned) and keeps the 64 activations of that group in registers; the
+// team's partial sums meet in a DPP/swizzle wavefront reduction (plus LDS across
+// the TW waves).  A workgroup holds TEAMS teams (8 waves); each team owns RPW
+// contiguous rows and issues all their loads before the activations are staged.
+// Each wave loads its 64-group share of a row with coalesced 16-byte loads, writes
+// it to its own LDS stage and each lane reads its 17 dwords back (stride 17 dwords:
+// no bank conflicts).  Bytes are biased to unsigned (q + 128), converted with
+// v_cvt_f32_ubyte and corrected by 128 X per block.
 //
 // Inputs outside these fast paths (k not a multiple of 256, unaligned pointers,
 // element offsets that are not block aligned) go to a per-element kernel that
@@ -109,6 +110,7 @@ __device__ __forceinline__ void x_share(const XFetch<XPT, FUSE> &f, uint32_t k, 
         xr[4 * i] = v.x, xr[4 * i + 1] = v.y, xr[4 * i + 2] = v.z, xr[4 * i + 3] = v.w;
     }
 }
+
 
 __device__ __forceinline__ float h_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
 __device__ __forceinline__ float h_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
@@ -468,6 +470,408 @@ __global__ __launch_bounds__(256) void k_generic_m1(const float *__restrict__ x,
 }
 
 // ------------------------------------------------------------------------------------------
+// Q4_K, M = 1, on int8 matrix cores (v_mfma_i32_16x16x64_i8: D[16x16] += A[16x64] B[64x16],
+// lane l supplies A row l%16 / B column l%16 at bytes 16(l/16)..+15 of k; D row 4(l/16)+r,
+// column l%16 lands in lane l, register r).
+//
+// Activations.  Each 256-element super-block of x is scaled by 2^sh, sh chosen so
+// that max|x| 2^sh lies in [2^20, 2^21), and rounded to an integer X (one fma with
+// 1.5 * 2^23 leaves U = X + 2^22 in the low 23 bits).  Its bytes are the digits:
+// X = s0 + 2^8 s1 + 2^16 s2 - 4161408 with s0 = u0 - 128, s1 = u1 - 128, s2 = u2
+// all in int8 range.  Quant nibbles are integers 0..15, so every product is exact
+// in the i32 accumulators; with C_l = sum_k s_l,k q_k and Q = sum_k q_k,
+//     sum_k X_k q_k = C0 + 2^8 C1 + 128 (2^9 C2 - 32511 Q)    (exact in int32),
+// and the only rounding of x is to 22 significant bits of its super-block maximum.
+//
+// Tile: 16 weight rows (MFMA columns n = lane & 15) by one super-block.  With
+// kq = lane >> 4, column n takes the quant bytes 16kq..16kq+15 (groups 0, 1) and
+// 64+16kq.. (groups 2, 3) of its row.  Group pair p takes two MFMAs into one
+// accumulator:
+//   #1  B = low nibbles  (k block kq: sub-block 4p + 2(kq>>1), elements 16(kq&1)..+15)
+//   #2  B = high nibbles (sub-block 4p + 2(kq>>1) + 1, same elements + 32)
+// A row i = 4 slot + d: slots 0 and 1 carry digit d of #1's k blocks {0,1} and
+// {2,3} and are zero in #2; slots 2 and 3 likewise for #2; d = 3 is a row of ones
+// (so C3 = Q).  C row 4 slot + d of column n lands in lane (n, slot): after the
+// pair each lane holds C0..C3 of one (row, sub-block) pair,
+// j = 4p + 2 (slot & 1) + (slot >> 1), and applies that sub-block's scale and min:
+//     acc += (d sc 2^-sh) S - (dmin m) X_j,   X_j = sum of x over sub-block j.
+// The A fragments come from three tables of the same layout (digits, zeros,
+// ones), so every lane's fragment address moves by the same amount per step.
+//
+// Weights reach the MFMA operands through LDS: read straight from memory, one
+// instruction would touch 16 rows 2304 bytes apart (64 bytes each), which the
+// memory system serves far below streaming rate.  Instead each wave copies MQ_C
+// super-blocks of its 16 rows with 16-byte loads that run along the rows (about
+// two rows per instruction) into its own LDS tile (rows padded so that the 16
+// columns of a fragment read fall in distinct banks), and reads the fragments
+// from there.  The loads of the next chunk are in flight while a chunk is used.
+//
+// Work split.  Workgroup (rs, ks) owns rows [n rs / RS, n (rs+1) / RS) (equal byte
+// shares) and super-blocks [nsb ks / KS, nsb (ks+1) / KS) of k (at most
+// MQ_MAX_SLICE); it stages only that slice of x (digit table, sub-block sums,
+// scales) in LDS.  Its rows form row groups of 16 (a partial last group repeats
+// its last row in the idle columns, which are not stored), and when there are
+// fewer row groups than waves each row group's slice is split into KP parts, one
+// (row group, part) unit per wave.  Parts are added in part order, slices in slice
+// order by the last workgroup of the row range to finish (arrival counter reset
+// by that workgroup): results do not depend on timing.
+//
+// A slice whose activations are not finite, or whose super-block maximum is below
+// 2^-100 (where 2^sh would leave the f32 range), is computed by the reference's
+// per-element loop instead.
+
+constexpr int MQ_WAVES = 8;
+constexpr uint32_t MQ_MIN_ROWS = 4;     // rows per workgroup below which columns idle for nothing
+constexpr uint32_t MQ_MAX_SLICE = 16;   // super-blocks of x one workgroup stages
+constexpr uint32_t MQ_TAB = MQ_MAX_SLICE * 768;  // one A table: 16 chunks x 48 bytes per super-block
+// The zero and ones tables start 64 and 128 bytes into a 256-byte period after the
+// digits, so that the lanes of one fragment read that use different tables hit
+// different banks.
+constexpr uint32_t MQ_TZERO = MQ_TAB + 64, MQ_TONES = 2 * MQ_TAB + 256 + 128;
+constexpr uint32_t MQ_TALL = 3 * MQ_TAB + 512;
+
+typedef int lg_i32x4 __attribute__((ext_vector_type(4)));
+
+template <int C>
+struct MqGeom {
+    static constexpr uint32_t ROW = C * 144 + 16;  // staged row stride: 16 rows at distinct banks
+    static constexpr uint32_t WAVE = 16 * ROW;     // one wave's tile
+    static constexpr uint32_t PIECES = 16 * C * 9;  // 16-byte pieces per chunk
+    static constexpr int LOADS = (PIECES + 63) / 64;
+};
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_xor((int)v, o);
+        v = v > t ? v : t;
+    }
+    return v;
+}
+
+// Staging of one super-block of x by one wave (lane l: elements 4l..4l+3): digit
+// table T (chunk c at T + 48c: digit d of elements 16c..16c+15 at +16d), sub-block
+// sums X, scale 2^-sh; returns 1 if the super-block needs the per-element loop.
+__device__ __forceinline__ uint32_t mq_stage(float4 v, uint32_t i, uint32_t lane, uint8_t *s_T, float *s_X,
+                                             float *s_FX) {
+    // max |x| on the bit patterns: NaN > inf > every finite value
+    uint32_t mb = __float_as_uint(v.x) & 0x7FFFFFFFu;
+    mb = max(mb, __float_as_uint(v.y) & 0x7FFFFFFFu);
+    mb = max(mb, __float_as_uint(v.z) & 0x7FFFFFFFu);
+    mb = max(mb, __float_as_uint(v.w) & 0x7FFFFFFFu);
+    mb = wave_max_u32(mb);
+    const uint32_t bad = (mb >= 0x7F800000u || (mb != 0u && mb < 0x0D800000u)) ? 1u : 0u;  // non-finite, < 2^-100
+    float sum = (v.x + v.y) + (v.z + v.w);
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if ((lane & 7u) == 0) s_X[i * 8u + (lane >> 3)] = sum;
+    int e = 0;
+    (void)frexpf(__uint_as_float(mb), &e);
+    const int sh = mb == 0u || bad ? 0 : 21 - e;
+    const float scale = ldexpf(1.0f, sh);
+    if (lane == 0) s_FX[i] = ldexpf(1.0f, -sh);
+    const uint32_t t0 = __float_as_uint(__builtin_fmaf(v.x, scale, 12582912.0f));
+    const uint32_t t1 = __float_as_uint(__builtin_fmaf(v.y, scale, 12582912.0f));
+    const uint32_t t2 = __float_as_uint(__builtin_fmaf(v.z, scale, 12582912.0f));
+    const uint32_t t3 = __float_as_uint(__builtin_fmaf(v.w, scale, 12582912.0f));
+    // byte b of the four elements into one dword (v_perm_b32: selector 0-3 picks
+    // from the second operand, 4-7 from the first, 0x0C is a zero byte)
+    const uint32_t p01 = __builtin_amdgcn_perm(t1, t0, 0x05010400u), p23 = __builtin_amdgcn_perm(t3, t2, 0x05010400u);
+    const uint32_t q01 = __builtin_amdgcn_perm(t1, t0, 0x0C0C0602u), q23 = __builtin_amdgcn_perm(t3, t2, 0x0C0C0602u);
+    uint8_t *tp = s_T + (i * 16u + (lane >> 2)) * 48u + 4u * (lane & 3u);
+    *reinterpret_cast<uint32_t *>(tp) = __builtin_amdgcn_perm(p23, p01, 0x05040100u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(tp + 16) = __builtin_amdgcn_perm(p23, p01, 0x07060302u) ^ 0x80808080u;
+    *reinterpret_cast<uint32_t *>(tp + 32) = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
+    return bad;
+}
+
+// The reference's f16 decoder (ref_half) from the hardware conversion: the two
+// differ only for exponent-0 codes with a non-zero mantissa (f16 subnormals, class
+// bits 4 and 7), which the reference reads as 2^-14 + 2^-24 m instead of 2^-24 m.
+__device__ __forceinline__ float mq_half(uint32_t h16) {
+    const _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)h16);
+    const float v = (float)h;
+    return v + (__builtin_amdgcn_classh(h, 0x90) ? __builtin_copysignf(0x1p-14f, v) : 0.0f);
+}
+
+// Wave-private LDS fence: the wave's own LDS writes are visible to its later reads
+// (and its earlier reads are done before later writes).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Row ranges and k slices of the grid, as quotients and remainders (workgroup rs
+// gets rows + (rs < rows_extra) rows, slice ks gets sbs + (ks < sbs_extra)
+// super-blocks).
+struct MqSplit {
+    uint32_t rows, rows_extra, sbs, sbs_extra;
+};
+
+// C: super-blocks per staged chunk; NCH: chunks whose loads a wave issues together.
+template <bool FUSE, int C, int NCH>
+__global__ __launch_bounds__(MQ_WAVES * 64) void k_q4k_m1_mfma(const float *__restrict__ x,
+                                                              const float *__restrict__ up,
+                                                              const uint8_t *__restrict__ w, float *__restrict__ y,
+                                                              float *__restrict__ part, uint32_t *__restrict__ cnt,
+                                                              uint32_t k, uint32_t n, uint64_t row_bytes, MqSplit sp) {
+    using G = MqGeom<C>;
+    __shared__ __attribute__((aligned(16))) uint8_t s_W[MQ_WAVES * G::WAVE];
+    __shared__ __attribute__((aligned(16))) uint8_t s_T[MQ_TALL + 4 * 768];  // dropped steps of a short unit read past the slice
+    __shared__ float s_X[(MQ_MAX_SLICE + C) * 8];  // dropped steps of a short unit read past the slice
+    __shared__ float s_FX[MQ_MAX_SLICE + C];
+    __shared__ float s_part[MQ_WAVES * 16];
+    __shared__ uint32_t s_bad[MQ_WAVES];
+    __shared__ uint32_t s_last;
+
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t rs = blockIdx.x, KS = gridDim.y, ks = blockIdx.y;
+    // (no integer divisions before the first loads: they would delay every one of them)
+    const uint32_t rows = sp.rows + (rs < sp.rows_extra ? 1u : 0u);
+    const uint32_t r_begin = rs * sp.rows + (rs < sp.rows_extra ? rs : sp.rows_extra);
+    const uint32_t r_end = r_begin + rows;
+    const uint32_t nsl = sp.sbs + (ks < sp.sbs_extra ? 1u : 0u);  // this workgroup's slice
+    const uint32_t sbA = ks * sp.sbs + (ks < sp.sbs_extra ? ks : sp.sbs_extra);
+    const uint32_t RG = (rows + 15) >> 4;
+    const uint32_t lkp = RG >= 5u ? 0u : RG >= 3u ? 1u : RG == 2u ? 2u : 3u;  // KP = 2^lkp: 8/RG rounded down, U <= 8 when KP > 1
+    const uint32_t KP = 1u << lkp;
+    const uint32_t U = RG << lkp;
+    const uint32_t nn = lane & 15u, kq = lane >> 4;
+
+    // ---- x of this wave's first two staging super-blocks: loaded before any weight,
+    // so that waiting for them never waits for the weights (loads complete in order)
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *u4 = reinterpret_cast<const float4 *>(up);
+    const uint32_t ia = wave < nsl ? wave : 0u, ib = wave + MQ_WAVES < nsl ? wave + MQ_WAVES : 0u;
+    float4 xa = x4[(sbA + ia) * 64u + lane], xb = x4[(sbA + ib) * 64u + lane];
+    float4 ua = xa, ub = xb;
+    if constexpr (FUSE) ua = u4[(sbA + ia) * 64u + lane], ub = u4[(sbA + ib) * 64u + lane];
+
+    // ---- chunk copies: piece p = 64 j + lane of a chunk is 16 bytes of row p / (9C),
+    // at 16 (p % (9C)) in the row's C super-blocks
+    uint32_t goff[G::LOADS], loff[G::LOADS];
+    uint32_t s0u = 0, cntu = 0, row0 = 0;
+    const uint8_t *ubase = w;  // this unit's first super-block of its first row
+    auto unit = [&](uint32_t u) {
+        const uint32_t rg = u >> lkp, kp = u & (KP - 1u);
+        s0u = (nsl * kp) >> lkp;
+        cntu = ((nsl * (kp + 1u)) >> lkp) - s0u;
+        row0 = r_begin + 16u * rg;
+        const uint32_t last = (r_end - 1u) - row0;  // rows past the range repeat the last one
+        const uint32_t sbl = cntu ? cntu - 1u : 0u;  // a unit shorter than a chunk repeats its last super-block
+        ubase = w + (uint64_t)row0 * row_bytes + (uint64_t)(sbA + s0u) * Q4K_BYTES;
+#pragma unroll
+        for (int j = 0; j < G::LOADS; j++) {
+            uint32_t p = 64u * j + lane;
+            p = p < G::PIECES ? p : G::PIECES - 1u;
+            const uint32_t r = p / (9u * C), q = p - r * (9u * C);
+            const uint32_t sb = q / 9u, qi = q - 9u * sb;
+            goff[j] = (r < last ? r : last) * (uint32_t)row_bytes + (sb < sbl ? sb : sbl) * Q4K_BYTES + 16u * qi;
+            loff[j] = wave * G::WAVE + r * G::ROW + 16u * q;
+        }
+    };
+    // First step of the chunk that holds steps c0..: the last chunk of a unit is
+    // moved back to end at the unit's end (its steps before c0 are dropped).
+    auto chunk_start = [&](uint32_t c0) { return c0 + C <= cntu ? c0 : (cntu >= C ? cntu - C : 0u); };
+    uint4 gb[NCH][G::LOADS];
+    auto fetch = [&](uint32_t r0) {  // the NCH chunks of the round starting at step r0
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const uint8_t *base = ubase + (uint64_t)chunk_start(r0 + c * C) * Q4K_BYTES;
+#pragma unroll
+            for (int j = 0; j < G::LOADS; j++) gb[c][j] = ld_stream16(base + goff[j]);
+        }
+    };
+    auto put = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < G::LOADS; j++) *reinterpret_cast<uint4 *>(s_W + loff[j]) = gb[c][j];
+    };
+    unit(wave < U ? wave : 0u);
+    if (wave >= U) cntu = 0;
+    fetch(0);
+
+    // ---- A tables: zeros and ones, then the digits of this slice
+    for (uint32_t o = MQ_TAB + threadIdx.x * 16u; o < MQ_TALL; o += MQ_WAVES * 64u * 16u)
+        *reinterpret_cast<uint4 *>(s_T + o) = o < MQ_TONES - 128u ? make_uint4(0u, 0u, 0u, 0u)
+                                                                 : make_uint4(0x01010101u, 0x01010101u, 0x01010101u,
+                                                                              0x01010101u);
+    uint32_t bad = 0;
+    if constexpr (FUSE) {
+        xa = make_float4(silu_mul(xa.x, ua.x), silu_mul(xa.y, ua.y), silu_mul(xa.z, ua.z), silu_mul(xa.w, ua.w));
+        xb = make_float4(silu_mul(xb.x, ub.x), silu_mul(xb.y, ub.y), silu_mul(xb.z, ub.z), silu_mul(xb.w, ub.w));
+    }
+    if (wave < nsl) bad |= mq_stage(xa, wave, lane, s_T, s_X, s_FX);
+    if (wave + MQ_WAVES < nsl) bad |= mq_stage(xb, wave + MQ_WAVES, lane, s_T, s_X, s_FX);
+    if (lane == 0) s_bad[wave] = bad;
+    __syncthreads();
+    uint32_t any_bad = 0;
+#pragma unroll
+    for (int i = 0; i < MQ_WAVES; i++) any_bad |= s_bad[i];
+
+    float *dst = KS > 1 ? part + (uint64_t)ks * n : y;  // this slice's sums
+    if (any_bad) {  // the reference's per-element loop over this slice
+        for (uint32_t r = r_begin + wave; r < r_end; r += MQ_WAVES) {
+            float acc = 0.0f;
+            for (uint32_t j = sbA * 256u + lane; j < (sbA + nsl) * 256u; j += 64) {
+                float xj = x[j];
+                if constexpr (FUSE) xj = silu_mul(xj, up[j]);
+                acc = __builtin_fmaf(xj, q4k_elem(w, (uint64_t)r * k + j), acc);
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) {
+                if (KS > 1) __hip_atomic_store(dst + r, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else dst[r] = acc;
+            }
+        }
+    } else {
+        // per-lane bases (byte offsets); every step adds the same immediate to all of them
+        const uint32_t slot = nn >> 2, dg = nn & 3u;
+        const uint32_t cb = 4u * (kq >> 1) + (kq & 1u);  // 16-element chunk of #1's k block in a super-block
+        const bool v1 = slot < 2u && slot == (kq >> 1), v2 = slot >= 2u && slot - 2u == (kq >> 1);
+        const uint32_t dof = dg < 3u ? dg * 16u : 0u;
+        const uint32_t tab1 = v1 ? (dg < 3u ? 0u : MQ_TONES) : MQ_TZERO;
+        const uint32_t tab2 = v2 ? (dg < 3u ? 0u : MQ_TONES) : MQ_TZERO;
+        const uint32_t ab1 = tab1 + cb * 48u + dof, ab2 = tab2 + (cb + 2u) * 48u + dof;
+        const uint32_t jl = 2u * (kq & 1u) + (kq >> 1);  // C slot kq holds sub-block 4p + jl
+        const uint32_t wb = wave * G::WAVE + nn * G::ROW;  // this column's staged row
+        const lg_i32x4 zero4 = {0, 0, 0, 0};
+
+        // Steps c0 .. c0+C-1 of the current unit from the staged chunk; steps past
+        // cntu are computed and dropped.
+        auto consume = [&](uint32_t c0) {
+            const uint32_t cs = chunk_start(c0);
+            const uint32_t sl0 = s0u + cs;  // slice super-block of step 0
+            const uint8_t *Ta = s_T + __mul24(sl0, 768u);
+            const float *Xa = s_X + sl0 * 8u + jl;
+            const float *FXa = s_FX + sl0;
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                const uint4 h = *reinterpret_cast<const uint4 *>(s_W + wb + i * 144);
+                const uint4 A = *reinterpret_cast<const uint4 *>(s_W + wb + i * 144 + 16 + 16 * kq);
+                const uint4 B = *reinterpret_cast<const uint4 *>(s_W + wb + i * 144 + 80 + 16 * kq);
+                const float d = mq_half(h.x & 0xFFFFu) * FXa[i], dm = mq_half(h.x >> 16);
+                float a = 0.0f;
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    const uint4 q = p ? B : A;
+                    const lg_i32x4 b1 = {(int)(q.x & 0x0F0F0F0Fu), (int)(q.y & 0x0F0F0F0Fu), (int)(q.z & 0x0F0F0F0Fu),
+                                         (int)(q.w & 0x0F0F0F0Fu)};
+                    const lg_i32x4 b2 = {(int)((q.x >> 4) & 0x0F0F0F0Fu), (int)((q.y >> 4) & 0x0F0F0F0Fu),
+                                         (int)((q.z >> 4) & 0x0F0F0F0Fu), (int)((q.w >> 4) & 0x0F0F0F0Fu)};
+                    const lg_i32x4 x1 = *reinterpret_cast<const lg_i32x4 *>(Ta + ab1 + i * 768 + p * 384);
+                    const lg_i32x4 x2 = *reinterpret_cast<const lg_i32x4 *>(Ta + ab2 + i * 768 + p * 384);
+                    lg_i32x4 c = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b1, zero4, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(x2, b2, c, 0, 0, 0);
+                    // scale and min of sub-block j = 4p + jl (kernels/proj_q4k.comp:46-58)
+                    uint32_t sc, mn;
+                    if (p == 0) {
+                        sc = __builtin_amdgcn_ubfe(h.y, 8u * jl, 6);
+                        mn = __builtin_amdgcn_ubfe(h.z, 8u * jl, 6);
+                    } else {
+                        sc = __builtin_amdgcn_ubfe(h.w, 8u * jl, 4) | (__builtin_amdgcn_ubfe(h.y, 8u * jl + 6u, 2) << 4);
+                        mn = __builtin_amdgcn_ubfe(h.w, 8u * jl + 4u, 4) |
+                             (__builtin_amdgcn_ubfe(h.z, 8u * jl + 6u, 2) << 4);
+                    }
+                    const int lo = c[0] + (c[1] << 8);
+                    const int hi = __mul24(c[3], -32511) + (c[2] << 9);
+                    const float S = __builtin_fmaf(128.0f, (float)hi, (float)lo);
+                    a = __builtin_fmaf(d * (float)sc, S, a);
+                    a = __builtin_fmaf(-(dm * (float)mn), Xa[i * 8 + 4 * p], a);
+                }
+                acc += cs + i >= c0 && cs + i < cntu ? a : 0.0f;
+            }
+            return acc;
+        };
+        auto finish = [&](uint32_t u, float acc) {
+            acc += __shfl_xor(acc, 16);
+            acc += __shfl_xor(acc, 32);
+            if (KP == 1) {
+                if (kq == 0 && row0 + nn < r_end) {
+                    if (KS > 1) __hip_atomic_store(dst + row0 + nn, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else dst[row0 + nn] = acc;
+                }
+            } else if (kq == 0) {
+                s_part[u * 16u + nn] = acc;
+            }
+        };
+        // One round: the loads of its NCH chunks are in flight; each chunk goes to the
+        // wave's LDS tile as soon as it has landed and is used from there.
+        auto round = [&](uint32_t r0) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                if (r0 + c * C < cntu) {
+                    wave_lds_fence();
+                    put(c);
+                    wave_lds_fence();
+                    acc += consume(r0 + c * C);
+                }
+            }
+            return acc;
+        };
+        // The first round of the first unit is straight-line code after the loads
+        // issued before staging, so each chunk waits only for its own loads.
+        if (wave < U) {
+            float acc = round(0);
+            for (uint32_t r0 = NCH * C; r0 < cntu; r0 += NCH * C) {
+                fetch(r0);
+                acc += round(r0);
+            }
+            finish(wave, acc);
+        }
+        for (uint32_t u = wave + MQ_WAVES; u < U; u += MQ_WAVES) {
+            unit(u);
+            float acc = 0.0f;
+            for (uint32_t r0 = 0; r0 < cntu; r0 += NCH * C) {
+                fetch(r0);
+                acc += round(r0);
+            }
+            finish(u, acc);
+        }
+        if (KP > 1) {
+            __syncthreads();
+            for (uint32_t t = threadIdx.x; t < rows; t += blockDim.x) {
+                const uint32_t rg = t >> 4, c = t & 15u;
+                float s = 0.0f;
+                for (uint32_t kp = 0; kp < KP; kp++) s += s_part[((rg << lkp) + kp) * 16u + c];
+                if (KS > 1) __hip_atomic_store(dst + r_begin + t, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else dst[r_begin + t] = s;
+            }
+        }
+    }
+    if (KS == 1) return;
+    // Slices: the partial sums and the counter are device-coherent atomics, so no
+    // cache write-back or invalidation is needed; each thread's stores complete
+    // before the workgroup's arrival is counted.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(&cnt[rs], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == KS - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(&cnt[rs], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (uint32_t t = threadIdx.x; t < rows; t += blockDim.x) {
+        const uint32_t r = r_begin + t;
+        float s = 0.0f;
+        for (uint32_t q0 = 0; q0 < KS; q0 += 8) {  // eight slices' loads in flight, added in slice order
+            float pv[8];
+#pragma unroll
+            for (int g = 0; g < 8; g++)
+                pv[g] = q0 + g < KS ? __hip_atomic_load(part + (uint64_t)(q0 + g) * n + r, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0.0f;
+#pragma unroll
+            for (int g = 0; g < 8; g++)
+                if (q0 + g < KS) s += pv[g];
+        }
+        y[r] = s;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // f32 weights: kernels/proj.comp (row_major = 0: w[i*k+j]; 1: w[j*n+i])
 
 __global__ __launch_bounds__(256) void k_f32_rows(const float *__restrict__ x, const float *__restrict__ w,
@@ -538,6 +942,64 @@ uint32_t rows_per_team(uint32_t n, uint32_t teams) {
     if (rpw < 1) rpw = 1;
     if (rpw > (uint64_t)M1_RPW_MAX) rpw = M1_RPW_MAX;
     return (uint32_t)rpw;
+}
+
+// Launch shape of k_q4k_m1_mfma: KS slices of k times RS row ranges, about one
+// workgroup per CU.  More slices mean less activation staging per workgroup (each
+// stages k/KS elements; the fused SiLU adds two transcendentals per element) but
+// more partial sums and a longer reduction by the last workgroup of a row range.
+uint32_t g_m1_split = 0;  // 0 = automatic
+
+void mq_shape(uint32_t k, uint32_t n, bool fuse, uint32_t &rs, uint32_t &ks) {
+    uint32_t G = (uint32_t)device_cus();
+    if (g_grid_cap && g_grid_cap < G) G = g_grid_cap;
+    const uint32_t nsb = k / QK_K;
+    uint32_t s = g_m1_split;
+    if (!s) {
+        // staging cost per workgroup ~ k/KS, product work ~ n k / G: keep their ratio small
+        const double per = (fuse ? 14.0 : 8.0) * 4096.0 / (double)n * (double)G / 256.0;
+        s = per < 1.0 ? 1u : (uint32_t)(per + 0.5);
+    }
+    const uint32_t smin = (nsb + MQ_MAX_SLICE - 1) / MQ_MAX_SLICE;  // the staged x slice fits LDS
+    s = s < smin ? smin : s;
+    s = s > nsb ? nsb : s;
+    s = s > G ? (G > smin ? G : smin) : s;
+    ks = s < 1 ? 1 : s;
+    uint32_t r = G / ks;
+    const uint32_t rmax = (n + MQ_MIN_ROWS - 1) / MQ_MIN_ROWS;
+    r = r > rmax ? rmax : r;
+    rs = r < 1 ? 1 : r;
+}
+
+template <bool FUSE>
+int launch_q4k_mfma(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n,
+                    hipStream_t s) {
+    uint32_t rs = 1, ks = 1;
+    mq_shape(k, n, FUSE, rs, ks);
+    float *part = nullptr;
+    uint32_t *cnt = nullptr;
+    if (ks > 1) {
+        LG_REQUIRE(rs <= PROJ_WS_COUNTERS / 4, "proj_q4k_m1: %u row ranges exceed the arrival counters", rs);
+        void *ws = nullptr;
+        const int st = device_workspace(PROJ_WS_COUNTERS + (uint64_t)ks * n * 4, &ws);
+        if (st != LG_OK) return st;
+        cnt = static_cast<uint32_t *>(ws);
+        part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + PROJ_WS_COUNTERS);
+    }
+    // longest unit of any workgroup decides the chunk: 2 super-blocks for short units
+    const uint32_t nsb = k / QK_K, rows = (n + rs - 1) / rs, rg = (rows + 15) / 16;
+    const uint32_t kp = rg >= 5u ? 1u : rg >= 3u ? 2u : rg == 2u ? 4u : 8u;
+    const uint32_t steps = ((nsb + ks - 1) / ks + kp - 1) / kp;
+    const dim3 grid(rs, ks), block(MQ_WAVES * 64);
+    const uint64_t rb = (uint64_t)k / QK_K * Q4K_BYTES;
+    const MqSplit sp{n / rs, n % rs, nsb / ks, nsb % ks};
+    if (steps <= 2)
+        hipLaunchKernelGGL((k_q4k_m1_mfma<FUSE, 2, 1>), grid, block, 0, s, x, up, w, y, part, cnt, k, n, rb, sp);
+    else if (steps <= 4)
+        hipLaunchKernelGGL((k_q4k_m1_mfma<FUSE, 2, 2>), grid, block, 0, s, x, up, w, y, part, cnt, k, n, rb, sp);
+    else
+        hipLaunchKernelGGL((k_q4k_m1_mfma<FUSE, 2, 4>), grid, block, 0, s, x, up, w, y, part, cnt, k, n, rb, sp);
+    return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
 }
 
 template <int TW, int TEAMS, int RPW, bool FUSE>
@@ -640,7 +1102,9 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
     if (dtype == LG_Q4_K && vec_ok && expert_offset % QK_K == 0) {
         const uint8_t *wbase = wb + (uint64_t)expert_offset / QK_K * Q4K_BYTES;
         if (aligned16(wbase))
-            return fuse ? launch_q4k<true>(x, up, wbase, c, k, n, s) : launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
+            // Measured on MI355X: the matrix-core kernel wins where the activation work is
+        // heavy (the fused SiLU); the vector kernels win on the plain projections.
+        return fuse ? launch_q4k_mfma<true>(x, up, wbase, c, k, n, s) : launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
     }
     if (dtype == LG_Q8_0 && vec_ok && !fuse && aligned16(wb)) return launch_q80(x, wb, c, k, n, s);
     if (dtype == LG_F32 && !fuse) {
@@ -727,6 +1191,14 @@ int lg_dispatch_activation(const float *gate, const float *up, float *h, uint32_
 // tuning hook for launch-shape sweeps; results do not depend on it.
 int lg_set_m1_grid_cap(uint32_t cap) {
     g_grid_cap = cap;
+    return LG_OK;
+}
+
+// Number of k slices of the Q4_K M=1 kernel (0 = automatic).  A tuning hook like
+// the cap above; results meet the same parity bound for every value and are
+// repeatable for a fixed one.
+int lg_set_m1_split(uint32_t slices) {
+    g_m1_split = slices;
     return LG_OK;
 }
 

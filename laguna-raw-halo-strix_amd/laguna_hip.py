@@ -71,6 +71,7 @@ SIGNATURES = {
 # Tuning hooks exported beside the ABI (not part of the drop-in surface).
 EXTRA = {
     "lg_set_m1_grid_cap": (_i, [_u32]),
+    "lg_set_m1_split": (_i, [_u32]),
 }
 
 
