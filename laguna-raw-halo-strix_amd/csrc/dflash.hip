@@ -28,11 +28,6 @@ namespace {
 
 using namespace lg;
 
-#define LG_TRY(expr)                                                                                                   \
-    do {                                                                                                               \
-        const int st_ = (expr);                                                                                        \
-        if (st_ != LG_OK) return st_;                                                                                  \
-    } while (0)
 
 typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -596,8 +591,8 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
     const uint64_t E = hp.n_embd, QD = (uint64_t)hp.n_heads * hp.head_dim, KVD = (uint64_t)hp.n_kv_heads * hp.head_dim;
     const uint64_t FF = hp.n_ff, A = (uint64_t)hp.n_aux * hp.n_embd;
     const uint32_t S = ctx_len + 2 * m;
-    const uint64_t floats[] = {2 * m * E, 2 * m * E, 2 * m * KVD, 2 * m * KVD,  m * QD, m * QD,
-                               (uint64_t)m * hp.n_heads,          m * E,        m * E,  m * FF, m * FF, m * A,
+    const uint64_t floats[] = {2 * m * E, 2 * m * E, 2 * m * KVD, 2 * m * KVD,  2 * m * QD, m * QD,
+                               2 * (uint64_t)m * hp.n_heads,      m * E,        m * E,  m * FF, m * FF, m * A,
                                attn_partial_floats(S, hp.n_kv_heads)};
     float **dst[] = {&L.xe, &L.nxe, &L.kk, &L.vv, &L.q, &L.att, &L.gate, &L.o, &L.h, &L.g, &L.u, &L.feat_n, &L.part};
     // The RoPE table and the small-M product workspace (whose arrival counters come
@@ -609,11 +604,17 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
                                   {(uint32_t)E, hp.n_heads, m},         {(uint32_t)QD, (uint32_t)E, m},
                                   {(uint32_t)E, (uint32_t)FF, m},       {(uint32_t)FF, (uint32_t)E, m},
                                   {(uint32_t)A, (uint32_t)E, m}};
-    for (const auto &sh : shapes)
-        for (int wt : {LG_Q4_K, LG_Q8_0}) {
+    const uint32_t qkvg[] = {(uint32_t)KVD, (uint32_t)KVD, (uint32_t)QD, hp.n_heads}, gu[] = {(uint32_t)FF, (uint32_t)FF};
+    for (int wt : {LG_Q4_K, LG_Q8_0}) {
+        for (const auto &sh : shapes) {
             const uint64_t c = proj_batch_ws_bytes(sh[0], sh[1], sh[2], LG_F32, wt);
             pw = c > pw ? c : pw;
         }
+        const uint64_t c1 = proj_batch_multi_ws_bytes((uint32_t)E, qkvg, 4, 2 * m, wt);
+        const uint64_t c2 = proj_batch_multi_ws_bytes((uint32_t)E, gu, 2, m, wt);
+        pw = c1 > pw ? c1 : pw;
+        pw = c2 > pw ? c2 : pw;
+    }
     pw = pw > PROJ_WS_COUNTERS ? pw : PROJ_WS_COUNTERS;
     L.freq = reinterpret_cast<float *>(base);
     L.pws = base + FREQ_BYTES;
@@ -746,26 +747,44 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
         const float *nx = W.nxe + mE;
         // attn_norm of the injected rows and the tokens in one launch (src/dflash.rs:917-923, :927)
         LG_TRY(run_rmsnorm(W.xe, L.attn_norm, W.nxe, E, 2 * m, 1, E, hp.rms_eps, s));
-        // K, V of [injected; tokens] at positions ctx_len .. ctx_len + 2m - 1 (src/dflash.rs:924-941)
-        LG_TRY(proj(W, W.nxe, L.attn_k, L.attn_k_type, W.kk, E, KVD, 2 * m, s));
-        LG_TRY(proj(W, W.nxe, L.attn_v, L.attn_v_type, W.vv, E, KVD, 2 * m, s));
-        LG_TRY(proj(W, nx, L.attn_q, L.attn_q_type, W.q, E, QD, m, s));
-        LG_TRY(proj(W, nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, m, s));
+        // K, V of [injected; tokens] at positions ctx_len .. ctx_len + 2m - 1 (src/dflash.rs:924-941),
+        // Q and the attention gate of the tokens (src/dflash.rs:942-944).  With one weight
+        // type the four share a launch over all 2m rows (Q and the gate of the injected
+        // rows are computed and not used: the weights are read once either way).
+        float *q = W.q, *gate = W.gate;
+        if (L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type && L.attn_k_type == L.attn_gate_type) {
+            const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                    {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
+            LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
+            q = W.q + (uint64_t)m * QD;
+            gate = W.gate + (uint64_t)m * H;
+        } else {
+            LG_TRY(proj(W, W.nxe, L.attn_k, L.attn_k_type, W.kk, E, KVD, 2 * m, s));
+            LG_TRY(proj(W, W.nxe, L.attn_v, L.attn_v_type, W.vv, E, KVD, 2 * m, s));
+            LG_TRY(proj(W, nx, L.attn_q, L.attn_q_type, W.q, E, QD, m, s));
+            LG_TRY(proj(W, nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, m, s));
+        }
         LG_TRY(run_qk_norm_rope(W.kk, L.attn_k_norm, W.freq, W.kk, KV, HD, hp.rope_dim, ctx_len, 2 * m, hp.qk_eps, s));
-        LG_TRY(run_qk_norm_rope(W.q, L.attn_q_norm, W.freq, W.q, H, HD, hp.rope_dim, ctx_len + m, m, hp.qk_eps, s));
+        LG_TRY(run_qk_norm_rope(q, L.attn_q_norm, W.freq, q, H, HD, hp.rope_dim, ctx_len + m, m, hp.qk_eps, s));
         // causal attention over [context; injected; tokens] (src/dflash.rs:945-954)
-        LG_TRY(run_attention(W.q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
+        LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
                              W.att, W.part, s));
-        hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for((uint64_t)m * QD)), dim3(256), 0, s, W.att, W.gate, W.att, H,
+        hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for((uint64_t)m * QD)), dim3(256), 0, s, W.att, gate, W.att, H,
                            HD, (uint64_t)m * QD, 1);
         LG_TRY(after_launch("softplus_gate_mul", s));
         LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, x, QD, E, m, s, x));  // x += o_proj
         // SwiGLU FFN (src/dflash.rs:962-968)
         LG_TRY(run_rmsnorm(x, L.ffn_norm, W.h, E, m, 1, E, hp.rms_eps, s));
-        LG_TRY(proj(W, W.h, L.ffn_gate, L.ffn_gate_type, W.g, E, FF, m, s));
-        LG_TRY(proj(W, W.h, L.ffn_up, L.ffn_up_type, W.u, E, FF, m, s));
-        LG_TRY(lg_dispatch_activation(W.g, W.u, W.g, m * FF, s));
-        LG_TRY(proj(W, W.g, L.ffn_down, L.ffn_down_type, x, FF, E, m, s, x));  // x += ffn_down
+        if (L.ffn_gate_type == L.ffn_up_type) {
+            const BatchJob jb[2] = {{L.ffn_gate, W.g, nullptr, FF}, {L.ffn_up, W.u, nullptr, FF}};
+            LG_TRY(proj_batch_multi(W.h, LG_F32, nullptr, jb, 2, E, m, L.ffn_gate_type, W.pws, W.pws_bytes, s));
+        } else {
+            LG_TRY(proj(W, W.h, L.ffn_gate, L.ffn_gate_type, W.g, E, FF, m, s));
+            LG_TRY(proj(W, W.h, L.ffn_up, L.ffn_up_type, W.u, E, FF, m, s));
+        }
+        // x += ffn_down(silu(gate) * up), the activation computed while staging the product's input
+        const BatchJob dj{L.ffn_down, x, x, E};
+        LG_TRY(proj_batch_multi(W.g, LG_F32, W.u, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
     }
     if (md->output_norm) return run_rmsnorm(x, md->output_norm, out, E, m, 1, E, hp.rms_eps, s);
     hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, x, out, mE);

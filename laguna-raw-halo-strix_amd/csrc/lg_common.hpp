@@ -37,6 +37,13 @@ struct DeferSync {
     ~DeferSync();
 };
 
+// Return the status of a call that fails.
+#define LG_TRY(expr)                                                                                                   \
+    do {                                                                                                               \
+        const int st_ = (expr);                                                                                        \
+        if (st_ != LG_OK) return st_;                                                                                  \
+    } while (0)
+
 #define LG_REQUIRE(cond, ...)                                                             \
     do {                                                                                  \
         if (!(cond)) return ::lg::fail(LG_EINVAL, __VA_ARGS__);                           \
@@ -64,6 +71,19 @@ int device_workspace(uint64_t need, void **out);
 uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype);
 int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                void *ws, uint64_t ws_bytes, hipStream_t s, const float *res = nullptr);
+
+// Up to 4 small-M products over the same activations in one launch: job j computes
+// c_j = W_j x (+ res_j) with W_j of n_j rows; all weights share k and w_dtype.
+// With `up` (f32 activations only), x is replaced by silu(x) * up (SiLU FFN input).
+struct BatchJob {
+    const void *w;
+    float *c;
+    const float *res;
+    uint32_t n;
+};
+uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype);
+int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jobs, uint32_t njobs, uint32_t k,
+                     uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s);
 
 // ---- GGUF block geometry (src/gguf.rs:97,101,134,136)
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;

@@ -92,6 +92,37 @@ __device__ __forceinline__ void q8_codes(uint32_t v, uint32_t &p02, uint32_t &p1
     p13 = (f1 >> 16) | (f3 & 0xFFFF0000u);
 }
 
+// A launch runs up to MM_JOBS products that share the activations x (and k): job
+// j owns workgroup columns g0 .. g0 + ceil(n / (64 RT)) - 1 and writes out[m][n]
+// (plus res, when given), using `part` for its slice partial sums.  Arrival
+// counters are indexed by the global workgroup column.
+constexpr int MM_JOBS = 4;
+struct MmJob {
+    const uint8_t *w;
+    float *out;
+    const float *res;
+    float *part;
+    uint32_t n, g0;
+};
+struct MmJobs {
+    MmJob j[MM_JOBS];
+    uint32_t count;
+};
+#define MM_JOB_SELECT                                                                     \
+    uint32_t J_ = 0;                                                                      \
+    _Pragma("unroll") for (int j_ = 1; j_ < MM_JOBS; j_++) if ((uint32_t)j_ < jobs.count && \
+                                                              blockIdx.x >= jobs.j[j_].g0) J_ = j_; \
+    const uint8_t *w = jobs.j[J_].w;                                                      \
+    float *out = jobs.j[J_].out;                                                          \
+    const float *res = jobs.j[J_].res;                                                    \
+    float *part = jobs.j[J_].part;                                                        \
+    const uint32_t n = jobs.j[J_].n, bx = blockIdx.x - jobs.j[J_].g0
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    // kernels/activation.comp:21-28: silu(g) * up, silu(x) = x * (1 / (1 + exp(-x)))
+    return g * (1.0f / (1.0f + expf(-g))) * u;
+}
+
 // The activation fragments of a slice, built in LDS by the whole workgroup.
 //   lf[((t*SB + jj)*PARTS + p)*64 + lane] : part p of the A operand of token tile t,
 //                                          sub-block jj of the slice
@@ -99,11 +130,12 @@ __device__ __forceinline__ void q8_codes(uint32_t v, uint32_t &p02, uint32_t &p1
 // A unit is (token tile t, sub-block jj, k-group kg, token tl): 8 activations.
 // load() issues the global loads (branch-free: tokens past m and sub-blocks past k
 // read a valid element and are zeroed at store()), store() splits and writes.
-template <int TT, int PARTS, int CH>
+template <int TT, int PARTS, int CH, bool FUSE = false>
 struct Frags {
     static constexpr int SB = 8 * CH;
     static constexpr int PER = TT * 16 * SB * 4 / 256;  // units per thread
-    float4 r[PER][2];                                    // f32 activations
+    float4 r[PER][2];                                    // f32 activations (FUSE: gate)
+    float4 ru[FUSE ? PER : 1][2];                        // FUSE: up
     uint4 h[PER];                                        // bf16 activations
 
     __device__ __forceinline__ static void unit(int i, uint32_t &t, uint32_t &jj, uint32_t &kg, uint32_t &tl) {
@@ -114,7 +146,8 @@ struct Frags {
         t = u / (64 * SB);
     }
 
-    __device__ __forceinline__ void load(const void *__restrict__ x, uint32_t m, uint32_t k, uint32_t sb0) {
+    __device__ __forceinline__ void load(const void *__restrict__ x, const float *__restrict__ up, uint32_t m,
+                                         uint32_t k, uint32_t sb0) {
         const uint32_t nsb = k / 32;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
@@ -129,6 +162,11 @@ struct Frags {
                 const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e);
                 r[i][0] = p[0];
                 r[i][1] = p[1];
+                if constexpr (FUSE) {
+                    const float4 *pu = reinterpret_cast<const float4 *>(up + e);
+                    ru[i][0] = pu[0];
+                    ru[i][1] = pu[1];
+                }
             }
         }
     }
@@ -160,6 +198,12 @@ struct Frags {
                 sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
             } else {
                 float f[8] = {r[i][0].x, r[i][0].y, r[i][0].z, r[i][0].w, r[i][1].x, r[i][1].y, r[i][1].z, r[i][1].w};
+                if constexpr (FUSE) {  // kernels/activation.comp:21-28
+                    const float u[8] = {ru[i][0].x, ru[i][0].y, ru[i][0].z, ru[i][0].w,
+                                        ru[i][1].x, ru[i][1].y, ru[i][1].z, ru[i][1].w};
+#pragma unroll
+                    for (int q = 0; q < 8; q++) f[q] = silu_mul(f[q], u[q]);
+                }
 #pragma unroll
                 for (int q = 0; q < 8; q++) f[q] = valid ? f[q] : 0.0f;
                 sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
@@ -275,18 +319,18 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 // every weight load of the slice (branch-free: rows past n and blocks past k read
 // row n-1 / the last block and are never used), the fragment build while the
 // weights are in flight, then the products.
-template <int TT, int PARTS, int CH, int RT>
-__global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const uint8_t *w, float *out,
-                                                const float *res, float *part, uint32_t *cnt, uint32_t m,
-                                                uint32_t k, uint32_t n, uint64_t row_bytes) {
+template <int TT, int PARTS, int CH, int RT, bool FUSE>
+__global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
+                                                uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
+    MM_JOB_SELECT;
     constexpr int SB = 8 * CH;
     __shared__ uint4 lf[TT * SB * PARTS * 64];
     __shared__ float lx[TT * SB * 16];
     const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
-    const uint32_t rt0 = (blockIdx.x * 4 + wave) * RT;
+    const uint32_t rt0 = (bx * 4 + wave) * RT;
     const uint32_t nb = k / QK_K, b0 = blockIdx.y * CH;
-    Frags<TT, PARTS, CH> fr;
-    fr.load(x, m, k, 8 * b0);
+    Frags<TT, PARTS, CH, FUSE> fr;
+    fr.load(x, up, m, k, 8 * b0);
     uint4 hd[RT][CH];
     uint2 qv[RT][CH][4];
 #pragma unroll
@@ -358,18 +402,18 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
 }
 
 // Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
-template <int TT, int PARTS, int CH, int RT>
-__global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const uint8_t *w, float *out,
-                                                const float *res, float *part, uint32_t *cnt, uint32_t m,
-                                                uint32_t k, uint32_t n, uint64_t row_bytes) {
+template <int TT, int PARTS, int CH, int RT, bool FUSE>
+__global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
+                                                uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
+    MM_JOB_SELECT;
     constexpr int SB = 8 * CH;
     __shared__ uint4 lf[TT * SB * PARTS * 64];
     __shared__ float lx[TT * SB * 16];
     const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
-    const uint32_t rt0 = (blockIdx.x * 4 + wave) * RT;
+    const uint32_t rt0 = (bx * 4 + wave) * RT;
     const uint32_t nsb = k / 32, sb0 = blockIdx.y * SB;
-    Frags<TT, PARTS, CH> fr;
-    fr.load(x, m, k, sb0);
+    Frags<TT, PARTS, CH, FUSE> fr;
+    fr.load(x, up, m, k, sb0);
     uint32_t dq[RT][SB], v0[RT][SB], v1[RT][SB];
 #pragma unroll
     for (int i = 0; i < RT; i++) {
@@ -431,10 +475,11 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
 
 // Fallback for shapes outside the MFMA path (f32 weights, k not a multiple of the
 // block, unaligned pointers, k = 0): one wavefront per output row, element-wise
-// decode.  c = res + W x when res is given.
+// decode.  c = res + W x when res is given; x = silu(x) * up when up is given.
 __global__ __launch_bounds__(256) void k_generic_batch(const void *__restrict__ xv, int x_bf16,
-                                                       const void *__restrict__ wv, float *c, const float *res,
-                                                       uint32_t m, uint32_t k, uint32_t n, int dtype) {
+                                                       const float *__restrict__ up, const void *__restrict__ wv,
+                                                       float *c, const float *res, uint32_t m, uint32_t k, uint32_t n,
+                                                       int dtype) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;
@@ -466,8 +511,9 @@ __global__ __launch_bounds__(256) void k_generic_batch(const void *__restrict__ 
             for (int t = 0; t < 8; t++) {
                 if (t0 + t < m) {
                     const uint64_t xi = (uint64_t)(t0 + t) * k + j;
-                    const float xj = x_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(xv)[xi])
-                                            : static_cast<const float *>(xv)[xi];
+                    float xj = x_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(xv)[xi])
+                                      : static_cast<const float *>(xv)[xi];
+                    if (up) xj = silu_mul(xj, up[xi]);
                     acc[t] = __builtin_fmaf(xj, wj, acc[t]);
                 }
             }
@@ -526,9 +572,9 @@ namespace {
 
 // Launch shape: CH chunks per slice (the slice's fragments fill LDS: 48 KB for f32
 // activations), one slice per workgroup column, RT row tiles per wavefront: the
-// most that still gives 256 workgroups.
+// most that still gives 256 workgroups (n is the jobs' total rows).
 struct MmShape {
-    uint32_t ch, slices, tiles, rt, groups;
+    uint32_t ch, slices, tiles, rt;
 };
 
 MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
@@ -537,14 +583,13 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     const uint32_t chunks = (k + 255) / 256, slices = (chunks + ch - 1) / ch;
     uint32_t rt = 4;
     while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 256) rt /= 2;
-    return {ch, slices, tiles, rt, (n + 64 * rt - 1) / (64 * rt)};
+    return {ch, slices, tiles, rt};
 }
 
-template <int TT, int PARTS, int CH>
-void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const uint8_t *w, float *out, const float *res,
-               float *part, uint32_t *cnt, uint32_t m, uint32_t k, uint32_t n, uint64_t rb, hipStream_t s) {
-#define LG_MM(K, R)                                                                                                    \
-    hipLaunchKernelGGL((K<TT, PARTS, CH, R>), grid, dim3(256), 0, s, x, w, out, res, part, cnt, m, k, n, rb)
+template <int TT, int PARTS, int CH, bool FUSE>
+void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt,
+               uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
+#define LG_MM(K, R) hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
     if (dtype == LG_Q4_K) {
         if (rt == 4) LG_MM(k_q4k_mm, 4);
         else if (rt == 2) LG_MM(k_q4k_mm, 2);
@@ -557,27 +602,26 @@ void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const uint8_t *
 #undef LG_MM
 }
 
-template <int PARTS>
-int launch_mm(int dtype, const void *x, const uint8_t *w, float *out, const float *res, float *part, uint32_t *cnt,
-              uint32_t m, uint32_t k, uint32_t n, hipStream_t s) {
-    const MmShape sh = mm_shape(dtype, k, n, m);
-    const dim3 grid(sh.groups, sh.slices);
+template <int PARTS, bool FUSE>
+int launch_mm(int dtype, const MmShape &sh, uint32_t groups, const void *x, const float *up, const MmJobs &jobs,
+              uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
+    const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
     if (dtype == LG_Q4_K) {
-        if (sh.tiles == 1) launch_rt<1, PARTS, 2>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
-        else launch_rt<2, PARTS, 1>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
+        if (sh.tiles == 1) launch_rt<1, PARTS, 2, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<2, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     } else {
-        if (sh.tiles == 1) launch_rt<1, PARTS, 1>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
-        else launch_rt<2, PARTS, 1>(dtype, sh.rt, grid, x, w, out, res, part, cnt, m, k, n, rb, s);
+        if (sh.tiles == 1) launch_rt<1, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<2, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     }
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
 }
 
 uint64_t align256(uint64_t b) { return (b + 255) & ~(uint64_t)255; }
 
-// Workspace layout: the arrival counters at a fixed place (offset 0, one per row
-// group, for n up to 64 * CNT_MAX rows) so that every call finds them zero, then
-// the partial sums.
+// Workspace layout: the arrival counters at a fixed place (offset 0, one per
+// workgroup column, CNT_MAX of them) so that every call finds them zero, then the
+// partial sums, job after job.
 constexpr uint64_t CNT_BYTES = PROJ_WS_COUNTERS;
 constexpr uint32_t CNT_MAX = CNT_BYTES / 4;
 
@@ -585,68 +629,110 @@ constexpr uint32_t CNT_MAX = CNT_BYTES / 4;
 
 namespace lg {
 
-uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype) {
-    (void)x_dtype;
+uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype) {
     if (w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) return 0;
-    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32);
+    uint64_t ntot = 0;
+    for (uint32_t j = 0; j < jobs; j++) ntot += n[j];
+    const uint32_t ml = m < 32 ? m : 32;
+    const MmShape sh = mm_shape(w_dtype, k, (uint32_t)ntot, ml);
     if (sh.slices <= 1) return 0;
-    const uint64_t ml = m < 32 ? m : 32;
-    return CNT_BYTES + align256((uint64_t)sh.slices * ml * n * 4);
+    uint64_t b = CNT_BYTES;
+    for (uint32_t j = 0; j < jobs; j++) b += align256((uint64_t)sh.slices * ml * n[j] * 4);
+    return b;
 }
 
-int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
-               void *ws_given, uint64_t ws_bytes, hipStream_t s, const float *res) {
+uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype) {
+    (void)x_dtype;
+    return proj_batch_multi_ws_bytes(k, &n, 1, m, w_dtype);
+}
+
+int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jb, uint32_t njobs, uint32_t k,
+                     uint32_t m, int w_dtype, void *ws_given, uint64_t ws_bytes, hipStream_t s) {
     const char *name = "lg_dispatch_proj_quant_batch";
-    if (n == 0 || m == 0) return LG_OK;
+    LG_REQUIRE(njobs >= 1 && njobs <= (uint32_t)MM_JOBS, "%s: %u jobs (1..%d)", name, njobs, MM_JOBS);
+    if (m == 0) return LG_OK;
     LG_REQUIRE(m <= 64, "%s: m=%u exceeds 64", name, m);
-    LG_REQUIRE(n <= 64u * CNT_MAX, "%s: n=%u exceeds %u", name, n, 64u * CNT_MAX);
-    LG_REQUIRE(x && w && c, "%s: null pointer", name);
+    LG_REQUIRE(x, "%s: null activations", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
+    LG_REQUIRE(!up || x_dtype == LG_F32, "%s: the fused SiLU(gate)*up takes f32 activations", name);
     LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32, "%s: weight dtype %d", name, w_dtype);
     const uint64_t xbytes = (uint64_t)m * k * (x_dtype == LG_F32 ? 4 : 2);
-    LG_EXTENT(c, (uint64_t)m * n * 4, name);
-    if (res) LG_EXTENT(res, (uint64_t)m * n * 4, name);
     if (k) {
         LG_EXTENT(x, xbytes, name);
-        LG_EXTENT(w, tensor_bytes(w_dtype, (uint64_t)n * k), name);
+        if (up) LG_EXTENT(up, xbytes, name);
     }
+    uint64_t ntot = 0;
+    uint32_t nv[MM_JOBS];
+    for (uint32_t j = 0; j < njobs; j++) {
+        const BatchJob &b = jb[j];
+        nv[j] = b.n;
+        ntot += b.n;
+        if (b.n == 0) continue;
+        LG_REQUIRE(b.w && b.c, "%s: null pointer in job %u", name, j);
+        LG_EXTENT(b.c, (uint64_t)m * b.n * 4, name);
+        if (b.res) LG_EXTENT(b.res, (uint64_t)m * b.n * 4, name);
+        if (k) LG_EXTENT(b.w, tensor_bytes(w_dtype, (uint64_t)b.n * k), name);
+    }
+    if (ntot == 0) return LG_OK;
     const uint32_t blk = w_dtype == LG_Q4_K ? QK_K : QK8_0;
-    const bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 &&
-                      (w_dtype != LG_Q4_K || (reinterpret_cast<uintptr_t>(w) & 15u) == 0) &&
-                      (reinterpret_cast<uintptr_t>(w) & 1u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                (!up || (reinterpret_cast<uintptr_t>(up) & 15u) == 0);
+    for (uint32_t j = 0; j < njobs; j++)
+        fast = fast && (w_dtype != LG_Q4_K || (reinterpret_cast<uintptr_t>(jb[j].w) & 15u) == 0) &&
+               (reinterpret_cast<uintptr_t>(jb[j].w) & 1u) == 0;
     if (!fast) {
-        hipLaunchKernelGGL(k_generic_batch, dim3((n + 3) / 4), dim3(256), 0, s, x, (int)(x_dtype == LG_BF16), w, c,
-                           res, m, k, n, w_dtype);
-        return after_launch(name, s);
+        for (uint32_t j = 0; j < njobs; j++) {
+            if (jb[j].n == 0) continue;
+            hipLaunchKernelGGL(k_generic_batch, dim3((jb[j].n + 3) / 4), dim3(256), 0, s, x, (int)(x_dtype == LG_BF16),
+                               up, jb[j].w, jb[j].c, jb[j].res, m, k, jb[j].n, w_dtype);
+            LG_TRY(after_launch(name, s));
+        }
+        return LG_OK;
     }
-    const uint64_t need = proj_batch_ws_bytes(k, n, m, x_dtype, w_dtype);
+    const uint64_t need = proj_batch_multi_ws_bytes(k, nv, njobs, m, w_dtype);
     void *ws = ws_given;
-    int st = LG_OK;
     if (need) {
         if (ws) {
             LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small", name, (unsigned long long)ws_bytes);
         } else {
-            st = device_workspace(need, &ws);
-            if (st != LG_OK) return st;
+            LG_TRY(device_workspace(need, &ws));
         }
     }
     const uint32_t tiles = (m + 15) / 16;
     const uint64_t xsz = x_dtype == LG_F32 ? 4 : 2;
     for (uint32_t t0 = 0; t0 < tiles; t0 += 2) {  // pairs of 16-token tiles
         const uint32_t ml = m - 16 * t0 < 32 ? m - 16 * t0 : 32;
-        const MmShape sh = mm_shape(w_dtype, k, n, ml);
+        const MmShape sh = mm_shape(w_dtype, k, (uint32_t)ntot, ml);
         uint32_t *cnt = static_cast<uint32_t *>(ws);
-        float *part = ws ? reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + CNT_BYTES) : nullptr;
+        uint8_t *pb = ws ? static_cast<uint8_t *>(ws) + CNT_BYTES : nullptr;
         if (sh.slices > 1) LG_REQUIRE(ws, "%s: no workspace for %u slices", name, sh.slices);
+        MmJobs jobs{};
+        uint32_t groups = 0;
+        for (uint32_t j = 0; j < njobs; j++) {
+            const uint64_t off = (uint64_t)16 * t0 * jb[j].n;
+            jobs.j[j] = {static_cast<const uint8_t *>(jb[j].w), jb[j].c + off, jb[j].res ? jb[j].res + off : nullptr,
+                         reinterpret_cast<float *>(pb), jb[j].n, groups};
+            if (pb) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
+            groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
+        }
+        jobs.count = njobs;
+        LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
         const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
-        float *ct = c + (uint64_t)16 * t0 * n;
-        const float *rt = res ? res + (uint64_t)16 * t0 * n : nullptr;
-        const uint8_t *wb = static_cast<const uint8_t *>(w);
-        st = x_dtype == LG_BF16 ? launch_mm<1>(w_dtype, xt, wb, ct, rt, part, cnt, ml, k, n, s)
-                                : launch_mm<3>(w_dtype, xt, wb, ct, rt, part, cnt, ml, k, n, s);
-        if (st != LG_OK) return st;
+        const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
+        if (x_dtype == LG_BF16) LG_TRY((launch_mm<1, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
+        else if (up) LG_TRY((launch_mm<3, true>(w_dtype, sh, groups, xt, ut, jobs, cnt, ml, k, s)));
+        else LG_TRY((launch_mm<3, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
     }
     return LG_OK;
+}
+
+int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
+               void *ws_given, uint64_t ws_bytes, hipStream_t s, const float *res) {
+    if (n == 0 || m == 0) return LG_OK;
+    LG_REQUIRE(n <= 64u * CNT_MAX, "lg_dispatch_proj_quant_batch: n=%u exceeds %u", n, 64u * CNT_MAX);
+    LG_REQUIRE(x && w && c, "lg_dispatch_proj_quant_batch: null pointer");
+    const BatchJob j{w, c, res, n};
+    return proj_batch_multi(x, x_dtype, nullptr, &j, 1, k, m, w_dtype, ws_given, ws_bytes, s);
 }
 
 }  // namespace lg
