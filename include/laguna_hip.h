@@ -200,6 +200,23 @@ int lg_dispatch_softplus_gate_mul(const float *v, const float *gate, float *out,
 /* dispatch_add (src/dflash.rs:1284-1303), kernels/add.comp: out = a + b. */
 int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream);
 
+/* ---- Launch-shape tuning hooks (no counterpart in the reference: the Vulkan
+ * shaders have fixed workgroup counts).  For launch-shape sweeps; 0 restores the
+ * automatic choice.  Every value meets the same parity bound, and results are
+ * repeatable for a fixed setting.  Process-wide, not thread-safe. */
+
+/* Upper bound on workgroups of the M = 1 quantized projections. */
+int lg_set_m1_grid_cap(uint32_t cap);
+/* Number of k slices of the Q4_K M = 1 matrix-core kernel (the fused SiLU down
+ * projection). */
+int lg_set_m1_split(uint32_t slices);
+/* Small-M products (lg_dispatch_proj_quant_batch, the draft forward): ch chunks of
+ * 256 elements per k slice (1, 2; 4 for Q4_K with m <= 16) and rt 16-row tiles per
+ * wavefront (1, 2, 4; clamped to the kernel's register budget).  A captured
+ * draft-forward graph keeps the workspace it was sized with: set this before
+ * lg_dflash_graph_create. */
+int lg_set_batch_shape(uint32_t ch, uint32_t rt);
+
 /* ---- DFlash draft model (src/dflash.rs DFlashModel) ---- */
 
 typedef struct {

@@ -269,37 +269,47 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
         if (!last) return;
         if (threadIdx.x == 0) __hip_atomic_store(&cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // Slices are added in slice order (the sum does not depend on arrival order);
+    // the loads of G slices for all RT row tiles are in flight together.
+    constexpr uint32_t G = RT * TT >= 16 ? 1u : 16u / (RT * TT);
+    float v[RT][TT][4];
 #pragma unroll
-    for (int i = 0; i < RT; i++) {
-        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
-        const uint32_t rowc = row < n ? row : n - 1;
-        float v[TT][4];
+    for (int i = 0; i < RT; i++)
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[t][r] = S > 1 ? 0.0f : acc[i][t][r];
-        constexpr uint32_t G = 8 / TT;  // slices whose loads are in flight together
-        for (uint32_t q0 = 0; q0 < (S > 1 ? S : 0u); q0 += G) {
-            float pv[G][TT][4];
+            for (int r = 0; r < 4; r++) v[i][t][r] = S > 1 ? 0.0f : acc[i][t][r];
+    for (uint32_t q0 = 0; q0 < (S > 1 ? S : 0u); q0 += G) {
+        float pv[G][RT][TT][4];
 #pragma unroll
-            for (uint32_t g = 0; g < G; g++) {
-                const uint32_t q = q0 + g < S ? q0 + g : S - 1;
+        for (uint32_t g = 0; g < G; g++) {
+            const uint32_t q = q0 + g < S ? q0 + g : S - 1;
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+                const uint32_t rowc = row < n ? row : n - 1;
 #pragma unroll
                 for (int t = 0; t < TT; t++)
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const uint32_t tok = t * 16 + 4 * kg + r;
-                        pv[g][t][r] = __hip_atomic_load(part + q * mn + (uint64_t)(tok < m ? tok : m - 1) * n + rowc,
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        pv[g][i][t][r] = __hip_atomic_load(part + q * mn + (uint64_t)(tok < m ? tok : m - 1) * n + rowc,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
             }
+        }
 #pragma unroll
-            for (uint32_t g = 0; g < G; g++)  // slice order
+        for (uint32_t g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < RT; i++)
 #pragma unroll
                 for (int t = 0; t < TT; t++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++) v[t][r] += q0 + g < S ? pv[g][t][r] : 0.0f;
-        }
+                    for (int r = 0; r < 4; r++) v[i][t][r] += q0 + g < S ? pv[g][i][t][r] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
         if (row >= n) continue;
 #pragma unroll
         for (int t = 0; t < TT; t++)
@@ -308,7 +318,7 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
                 const uint32_t tok = t * 16 + 4 * kg + r;
                 if (tok < m) {
                     const uint64_t o = (uint64_t)tok * n + row;
-                    out[o] = res ? res[o] + v[t][r] : v[t][r];
+                    out[o] = res ? res[o] + v[i][t][r] : v[i][t][r];
                 }
             }
     }
@@ -577,12 +587,21 @@ struct MmShape {
     uint32_t ch, slices, tiles, rt;
 };
 
+uint32_t g_mm_ch = 0, g_mm_rt = 0;  // launch-shape overrides (0 = automatic)
+
 MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     const uint32_t tiles = (m + 15) / 16 > 2 ? 2 : (m + 15) / 16;  // per launch; larger m runs in pairs of tiles
-    const uint32_t ch = dtype == LG_Q4_K ? (tiles == 1 ? 2 : 1) : 1;
+    uint32_t ch = dtype == LG_Q4_K ? (tiles == 1 ? 2 : 1) : 1;
+    // chunks of 8 sub-blocks per slice: 1, 2 or (one token tile only) 4
+    if (g_mm_ch) ch = g_mm_ch >= 4 && tiles == 1 ? 4 : g_mm_ch >= 2 ? 2 : 1;
+    if (dtype != LG_Q4_K && ch > 2) ch = 2;
     const uint32_t chunks = (k + 255) / 256, slices = (chunks + ch - 1) / ch;
+    // the most rows per wavefront that still give about three workgroups per CU per
+    // token tile (fewer, larger workgroups measured slower on every shape tried)
     uint32_t rt = 4;
-    while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 256) rt /= 2;
+    while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 768 * tiles) rt /= 2;
+    if (g_mm_rt) rt = g_mm_rt >= 4 ? 4 : g_mm_rt >= 2 ? 2 : 1;
+    while (rt * ch > (dtype == LG_Q4_K ? 8u : 4u)) rt /= 2;  // register budget
     return {ch, slices, tiles, rt};
 }
 
@@ -590,14 +609,31 @@ template <int TT, int PARTS, int CH, bool FUSE>
 void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt,
                uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
 #define LG_MM(K, R) hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
+    // mm_shape keeps rt * ch within each kernel's register budget
     if (dtype == LG_Q4_K) {
-        if (rt == 4) LG_MM(k_q4k_mm, 4);
-        else if (rt == 2) LG_MM(k_q4k_mm, 2);
-        else LG_MM(k_q4k_mm, 1);
+        if constexpr (4 * CH <= 8)
+            if (rt == 4) {
+                LG_MM(k_q4k_mm, 4);
+                return;
+            }
+        if constexpr (2 * CH <= 8)
+            if (rt == 2) {
+                LG_MM(k_q4k_mm, 2);
+                return;
+            }
+        LG_MM(k_q4k_mm, 1);
     } else {
-        if (rt == 4) LG_MM(k_q80_mm, 4);
-        else if (rt == 2) LG_MM(k_q80_mm, 2);
-        else LG_MM(k_q80_mm, 1);
+        if constexpr (4 * CH <= 4)
+            if (rt == 4) {
+                LG_MM(k_q80_mm, 4);
+                return;
+            }
+        if constexpr (2 * CH <= 4)
+            if (rt == 2) {
+                LG_MM(k_q80_mm, 2);
+                return;
+            }
+        if constexpr (CH <= 2) LG_MM(k_q80_mm, 1);
     }
 #undef LG_MM
 }
@@ -607,11 +643,12 @@ int launch_mm(int dtype, const MmShape &sh, uint32_t groups, const void *x, cons
               uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
     const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
-    if (dtype == LG_Q4_K) {
-        if (sh.tiles == 1) launch_rt<1, PARTS, 2, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<2, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+    if (sh.tiles == 1) {
+        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<1, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     } else {
-        if (sh.tiles == 1) launch_rt<1, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
         else launch_rt<2, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     }
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
@@ -736,6 +773,17 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
 }
 
 }  // namespace lg
+
+// Launch shape of the small-M products (0 = automatic): ch chunks of 8 sub-blocks
+// per k slice (1, 2, or 4 for Q4_K with one 16-token tile) and rt 16-row tiles per
+// wavefront (1, 2 or 4, clamped to the register budget).  A tuning hook for
+// launch-shape sweeps; results meet the same parity bound for every value.
+// Workspaces sized before a change may be too small afterwards (the call then fails).
+extern "C" int lg_set_batch_shape(uint32_t ch, uint32_t rt) {
+    g_mm_ch = ch;
+    g_mm_rt = rt;
+    return LG_OK;
+}
 
 extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k,
                                             uint32_t n, uint32_t m, int w_dtype, void *stream) {

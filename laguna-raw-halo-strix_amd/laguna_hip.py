@@ -67,11 +67,10 @@ SIGNATURES = {
     "lg_dflash_graph_create": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, ctypes.POINTER(_vp)]),
     "lg_dflash_graph_launch": (_i, [_vp, _vp]),
     "lg_dflash_graph_destroy": (_i, [_vp]),
-}
-# Tuning hooks exported beside the ABI (not part of the drop-in surface).
-EXTRA = {
+    # launch-shape tuning hooks (no counterpart in the reference)
     "lg_set_m1_grid_cap": (_i, [_u32]),
     "lg_set_m1_split": (_i, [_u32]),
+    "lg_set_batch_shape": (_i, [_u32, _u32]),
 }
 
 
@@ -91,7 +90,7 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise LagunaError(ENODEV, f"{LIB_PATH} is not built; run __graft_entry__.build() or make")
         L = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in {**SIGNATURES, **EXTRA}.items():
+        for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
