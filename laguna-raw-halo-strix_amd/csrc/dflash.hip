@@ -98,14 +98,26 @@ __global__ __launch_bounds__(256) void k_rmsnorm4(const float *x, const float *_
 // ------------------------------------------------------------------------------------------
 // QK-norm + NeoX RoPE (kernels/qk_norm_rope.comp:23-67): one wavefront per (row, head).
 
-// In place (out == x) is allowed: a wavefront reads its head before writing it.
-__global__ __launch_bounds__(256) void k_qk_norm_rope(const float *x, const float *__restrict__ w,
-                                                      const float *__restrict__ freq, float *out,
-                                                      uint32_t n_heads, uint32_t hd, uint32_t rope_dim, uint32_t pos0,
-                                                      uint32_t units, float eps) {
+// One tensor's share of a launch: rows x n_heads heads of hd floats, row r at
+// position pos0 + r.  In place (out == x) is allowed: a wavefront reads its head
+// before writing it.
+struct QkJob {
+    const float *x, *w;
+    float *out;
+    uint32_t n_heads, pos0, units, blocks;
+};
+
+// Job a takes workgroups 0 .. a.blocks-1, job b the rest (the forward's K and Q).
+__global__ __launch_bounds__(256) void k_qk_norm_rope(QkJob a, QkJob b, const float *__restrict__ freq, uint32_t hd,
+                                                      uint32_t rope_dim, float eps) {
     __shared__ float nrm[4][256];
+    const bool second = blockIdx.x >= a.blocks;
+    const QkJob &jb = second ? b : a;
+    const float *x = jb.x, *__restrict__ w = jb.w;
+    float *out = jb.out;
+    const uint32_t n_heads = jb.n_heads, pos0 = jb.pos0, units = jb.units;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t unit = blockIdx.x * 4 + wave;  // (row, head)
+    const uint32_t unit = (blockIdx.x - (second ? a.blocks : 0u)) * 4 + wave;  // (row, head)
     const bool live = unit < units;
     const uint32_t row = live ? unit / n_heads : 0, head = live ? unit % n_heads : 0;
     const float *xh = x + (uint64_t)row * n_heads * hd + (uint64_t)head * hd;
@@ -371,11 +383,16 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
     }
 }
 
+__device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g : logf(1.0f + expf(g)); }  // src/dflash.rs:957
+
 // out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c; one wavefront per
 // query, the chunks' partials loaded CB at a time (all in flight together).
+// With `gate` ([rows][n_q]), the result of head hq of row t is then multiplied by
+// softplus(gate[t][hq]) (the forward's attention gate, src/dflash.rs:956-959).
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
                                                       const float *__restrict__ part_ml, float *__restrict__ out,
-                                                      uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch) {
+                                                      uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch,
+                                                      const float *__restrict__ gate) {
     constexpr uint32_t CB = 8;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t gq = blockIdx.x * 4 + (threadIdx.x >> 6);  // over n_kv * AQ
@@ -414,8 +431,14 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     const uint32_t t = qi / G, hq = h * G + qi % G;
     float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    o[lane] = o0 * inv;
-    o[64 + lane] = o1 * inv;
+    if (gate) {
+        const float g = softplus_gate(gate[(uint64_t)t * n_q + hq]);
+        o[lane] = (o0 * inv) * g;
+        o[64 + lane] = (o1 * inv) * g;
+    } else {
+        o[lane] = o0 * inv;
+        o[64 + lane] = o1 * inv;
+    }
 }
 
 // Any head_dim <= 256: one wavefront per (row, q head), online softmax as mha_attn.comp.
@@ -467,9 +490,8 @@ __global__ __launch_bounds__(256) void k_gate_mul(const float *v, const float *_
     if (i >= total) return;
     const uint64_t row = i / ((uint64_t)n_heads * hd);
     const uint32_t head = (uint32_t)(i % ((uint64_t)n_heads * hd)) / hd;
-    float g = gate[row * n_heads + head];
-    if (softplus) g = g > 20.0f ? g : logf(1.0f + expf(g));  // src/dflash.rs:957
-    out[i] = v[i] * g;
+    const float g = gate[row * n_heads + head];
+    out[i] = v[i] * (softplus ? softplus_gate(g) : g);
 }
 
 __global__ __launch_bounds__(256) void k_add(const float *a, const float *b, float *out, uint64_t n) {
@@ -505,11 +527,16 @@ int run_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t
     return after_launch("rmsnorm", s);
 }
 
-int run_qk_norm_rope(const float *x, const float *w, const float *freq, float *out, uint32_t n_heads, uint32_t hd,
-                     uint32_t rope_dim, uint32_t pos, uint32_t rows, float eps, hipStream_t s) {
+QkJob qk_job(const float *x, const float *w, float *out, uint32_t n_heads, uint32_t pos, uint32_t rows) {
     const uint32_t units = rows * n_heads;
-    hipLaunchKernelGGL(k_qk_norm_rope, dim3((units + 3) / 4), dim3(256), 0, s, x, w, freq, out, n_heads, hd, rope_dim,
-                       pos, units, eps);
+    return {x, w, out, n_heads, pos, units, (units + 3) / 4};
+}
+
+// One or two tensors (b.blocks == 0: none) in one launch.
+int run_qk_norm_rope(const QkJob &a, const QkJob &b, const float *freq, uint32_t hd, uint32_t rope_dim, float eps,
+                     hipStream_t s) {
+    if (a.blocks + b.blocks == 0) return LG_OK;
+    hipLaunchKernelGGL(k_qk_norm_rope, dim3(a.blocks + b.blocks), dim3(256), 0, s, a, b, freq, hd, rope_dim, eps);
     return after_launch("qk_norm_rope", s);
 }
 
@@ -519,9 +546,10 @@ size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
 }
 
 // `part` holds attn_partial_floats(S, n_kv) floats when the matrix-core path applies.
+// With `gate` ([rows][n_q]) each head's result is multiplied by softplus of its gate.
 int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0, const float *k1, const float *v1,
                   uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t qpos0, int causal,
-                  float *out, float *part, hipStream_t s) {
+                  float *out, float *part, hipStream_t s, const float *gate = nullptr) {
     const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
     const uint32_t G = n_q / n_kv;
     if (part && hd == AHD && rows * G <= AQ) {
@@ -532,12 +560,16 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
         int st = after_launch("attn_chunk", s);
         if (st != LG_OK) return st;
         hipLaunchKernelGGL(k_attn_combine, dim3((n_kv * AQ + 3) / 4), dim3(256), 0, s, part, part_ml, out, rows, n_q,
-                           n_kv, nch);
+                           n_kv, nch, gate);
         return after_launch("attn_combine", s);
     }
     hipLaunchKernelGGL(k_attn_simple, dim3((rows * n_q + 3) / 4), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S, rows,
                        n_q, n_kv, hd, qpos0, causal, scale, out);
-    return after_launch("attn_simple", s);
+    LG_TRY(after_launch("attn_simple", s));
+    if (!gate) return LG_OK;
+    const uint64_t total = (uint64_t)rows * n_q * hd;
+    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, out, gate, out, n_q, hd, total, 1);
+    return after_launch("softplus_gate_mul", s);
 }
 
 // Per-device scratch for lg_dispatch_mha_attn's partials (grown on demand).
@@ -764,14 +796,12 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
             LG_TRY(proj(W, nx, L.attn_q, L.attn_q_type, W.q, E, QD, m, s));
             LG_TRY(proj(W, nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, m, s));
         }
-        LG_TRY(run_qk_norm_rope(W.kk, L.attn_k_norm, W.freq, W.kk, KV, HD, hp.rope_dim, ctx_len, 2 * m, hp.qk_eps, s));
-        LG_TRY(run_qk_norm_rope(q, L.attn_q_norm, W.freq, q, H, HD, hp.rope_dim, ctx_len + m, m, hp.qk_eps, s));
-        // causal attention over [context; injected; tokens] (src/dflash.rs:945-954)
+        LG_TRY(run_qk_norm_rope(qk_job(W.kk, L.attn_k_norm, W.kk, KV, ctx_len, 2 * m),
+                                qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim, hp.qk_eps, s));
+        // causal attention over [context; injected; tokens] (src/dflash.rs:945-954), each head
+        // scaled by softplus of its gate (src/dflash.rs:956-959)
         LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
-                             W.att, W.part, s));
-        hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for((uint64_t)m * QD)), dim3(256), 0, s, W.att, gate, W.att, H,
-                           HD, (uint64_t)m * QD, 1);
-        LG_TRY(after_launch("softplus_gate_mul", s));
+                             W.att, W.part, s, gate));
         LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, x, QD, E, m, s, x));  // x += o_proj
         // SwiGLU FFN (src/dflash.rs:962-968)
         LG_TRY(run_rmsnorm(x, L.ffn_norm, W.h, E, m, 1, E, hp.rms_eps, s));
@@ -854,7 +884,8 @@ int lg_dispatch_qk_norm_rope(const float *x, const float *norm_w, const float *f
     LG_EXTENT(x, tot, "lg_dispatch_qk_norm_rope x");
     LG_EXTENT(out, tot, "lg_dispatch_qk_norm_rope out");
     LG_EXTENT(norm_w, (uint64_t)head_dim * 4, "lg_dispatch_qk_norm_rope norm_w");
-    return run_qk_norm_rope(x, norm_w, freq, out, n_heads, head_dim, rope_dim, pos, rows, eps, (hipStream_t)stream);
+    return run_qk_norm_rope(qk_job(x, norm_w, out, n_heads, pos, rows), QkJob{}, freq, head_dim, rope_dim, eps,
+                            (hipStream_t)stream);
 }
 
 int lg_dispatch_mha_attn(const float *q, const float *k_seq, const float *v_seq, float *out, uint32_t n_q_heads,
