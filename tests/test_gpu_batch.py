@@ -104,3 +104,24 @@ def test_workspace_reuse_across_shapes(ctx):
     assert np.array_equal(small, again)
     y64, a = orc.proj_quant_f64(x, raw, lh.Q4_K, k, n)
     parity(big, y64, a, TOL)
+
+
+@pytest.mark.parametrize("ch,rt", [(1, 1), (1, 4), (2, 1), (2, 2), (2, 4), (4, 1), (4, 2)])
+@pytest.mark.parametrize("m", [16, 29])
+def test_launch_shapes(ctx, ch, rt, m):
+    # Every launch shape (k slice length, rows per wavefront) meets parity and is
+    # repeatable; k = 2816 is 11 super-blocks, so the last slice of a 2- or
+    # 4-super-block shape runs past the end of k.
+    k, n = 2816, 700
+    print(f"batch shape ch={ch} rt={rt} m={m}", flush=True)
+    raw = synth.q4k_weight(400 + m, k, n)
+    x = synth.normal(410 + m, m * k).reshape(m, k)
+    lh.check(lh.lib().lg_set_batch_shape(ch, rt))
+    try:
+        c1 = run_batch(ctx, x, lh.F32, raw, lh.Q4_K, k, n, m)
+        c2 = run_batch(ctx, x, lh.F32, raw, lh.Q4_K, k, n, m)
+    finally:
+        lh.check(lh.lib().lg_set_batch_shape(0, 0))
+    assert np.array_equal(c1, c2)
+    y64, a = orc.proj_quant_f64(x, raw, lh.Q4_K, k, n)
+    parity(c1, y64, a, TOL)
