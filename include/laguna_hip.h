@@ -53,7 +53,8 @@ typedef enum {
     LG_ENOMEM = 3,      /* device allocation failed */
     LG_EUNSUPPORTED = 4,/* valid request this build does not implement */
     LG_EIO = 5,         /* file I/O or format error (GGUF) */
-    LG_ENODEV = 6       /* no HIP device */
+    LG_ENODEV = 6,      /* no HIP device */
+    LG_ENOTFOUND = 7    /* no such tensor or metadata key (the reference's Option::None) */
 } lg_status;
 
 /* ---- runtime (replaces VulkanContext / GpuBuffer, src/vulkan.rs:16-452) ---- */
@@ -199,6 +200,114 @@ int lg_dispatch_softplus_gate_mul(const float *v, const float *gate, float *out,
 
 /* dispatch_add (src/dflash.rs:1284-1303), kernels/add.comp: out = a + b. */
 int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream);
+
+/* ---- GGUF v3 reader (replaces GGUFReader, src/gguf.rs:321-514, and the tensor
+ * loads of Model, src/model.rs:137-184).  Host code; only lg_gguf_upload_tensor
+ * touches the device.  The file stays open until lg_gguf_close; strings returned
+ * by the reader live as long as it does. ---- */
+
+typedef struct lg_gguf lg_gguf;
+
+#define LG_GGUF_MAX_DIMS 8
+#define LG_GGUF_MAX_TARGET_LAYERS 64
+
+/* TensorInfo (src/gguf.rs:172-201).  shape[0] is ne0, the contiguous dimension;
+ * data_offset is relative to the tensor data section; n_bytes = whole blocks of
+ * the type (the reference's table, lg_gguf_type_info). */
+typedef struct {
+    const char *name;
+    uint32_t n_dims;
+    uint64_t shape[LG_GGUF_MAX_DIMS];
+    int dtype;
+    uint64_t data_offset;
+    uint64_t n_elements;
+    uint64_t n_bytes;
+} lg_gguf_tensor;
+
+/* The GGUFMetadata fields the draft and target models read (populate_metadata,
+ * src/gguf.rs:517-637, with its key aliases: "laguna.", "dflash." or no prefix).
+ * A field is valid when its LG_GGUF_HAS_* bit is set in `present`.  Every other
+ * key is reachable through lg_gguf_field / lg_gguf_get_*. */
+enum {
+    LG_GGUF_HAS_ARCHITECTURE = 1u << 0,
+    LG_GGUF_HAS_GENERAL_NAME = 1u << 1,
+    LG_GGUF_HAS_FILE_TYPE = 1u << 2,
+    LG_GGUF_HAS_ALIGNMENT = 1u << 3,
+    LG_GGUF_HAS_BLOCK_COUNT = 1u << 4,
+    LG_GGUF_HAS_CONTEXT_LENGTH = 1u << 5,
+    LG_GGUF_HAS_EMBEDDING_LENGTH = 1u << 6,
+    LG_GGUF_HAS_FEED_FORWARD_LENGTH = 1u << 7,
+    LG_GGUF_HAS_HEAD_COUNT = 1u << 8,
+    LG_GGUF_HAS_HEAD_COUNT_KV = 1u << 9,
+    LG_GGUF_HAS_KEY_LENGTH = 1u << 10,
+    LG_GGUF_HAS_VALUE_LENGTH = 1u << 11,
+    LG_GGUF_HAS_RMS_EPSILON = 1u << 12,
+    LG_GGUF_HAS_ROPE_FREQ_BASE = 1u << 13,
+    LG_GGUF_HAS_ROPE_DIMENSION_COUNT = 1u << 14,
+    LG_GGUF_HAS_EXPERT_COUNT = 1u << 15,
+    LG_GGUF_HAS_EXPERT_USED_COUNT = 1u << 16,
+    LG_GGUF_HAS_VOCAB_SIZE = 1u << 17,
+    LG_GGUF_HAS_TARGET_LAYERS = 1u << 18,
+    LG_GGUF_HAS_DECODER_ARCH = 1u << 19,
+    LG_GGUF_HAS_EXPERT_WEIGHTS_NORM = 1u << 20
+};
+
+typedef struct {
+    uint32_t present;
+    char architecture[64], general_name[256], decoder_arch[64];
+    uint64_t file_type, alignment, block_count, context_length, embedding_length, feed_forward_length;
+    uint64_t head_count, head_count_kv, key_length, value_length, rope_dimension_count;
+    uint64_t expert_count, expert_used_count, vocab_size;
+    float rms_epsilon, rope_freq_base;
+    int expert_weights_norm;
+    uint32_t n_target_layers;
+    int64_t target_layers[LG_GGUF_MAX_TARGET_LAYERS];
+} lg_gguf_meta;
+
+/* TensorType::block_size / block_elements / is_supported / is_quantized
+ * (src/gguf.rs:91-170) for a GGUF type id; LG_EINVAL for ids from_u32 rejects. */
+int lg_gguf_type_info(int dtype, uint32_t *block_bytes, uint32_t *block_elements, int *supported, int *quantized);
+
+/* GGUFReader::open (src/gguf.rs:321-405): magic "GGUF", version 3 only, the
+ * metadata fields, the tensor infos, and the data section at the next multiple of
+ * general.alignment (default 32).  LG_EIO for a missing, foreign, truncated or
+ * inconsistent file (the reference returns io::Error or panics). */
+int lg_gguf_open(const char *path, lg_gguf **out);
+int lg_gguf_close(lg_gguf *g);
+int lg_gguf_header(const lg_gguf *g, uint32_t *version, uint64_t *tensor_count, uint64_t *field_count,
+                   uint64_t *tensor_data_offset);
+int lg_gguf_metadata(const lg_gguf *g, lg_gguf_meta *out);
+int lg_gguf_tensor_info(const lg_gguf *g, uint64_t index, lg_gguf_tensor *out);
+/* tensor_by_name (src/gguf.rs:407-409): the first tensor of that name, or LG_ENOTFOUND. */
+int lg_gguf_find_tensor(const lg_gguf *g, const char *name, uint64_t *index);
+/* read_tensor_data (src/gguf.rs:415-421): the tensor's n_bytes raw bytes into host
+ * memory `dst` (at least n_bytes).  LG_EIO when they run past the end of the file. */
+int lg_gguf_read_tensor(const lg_gguf *g, uint64_t index, void *dst, uint64_t dst_bytes);
+/* Model::upload_tensor_quantized (src/model.rs:174-184): the same bytes, unchanged,
+ * into device memory `dptr` (at least n_bytes), streamed through pinned staging
+ * memory; returns after the copy has completed. */
+int lg_gguf_upload_tensor(const lg_gguf *g, uint64_t index, void *dptr, uint64_t dst_bytes, void *stream);
+
+/* Raw metadata fields in file order (raw_fields, src/gguf.rs:341-355).  type is
+ * the GGUF value type (0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool,
+ * 8 string, 9 array, 10 u64, 11 i64, 12 f64); arrays report their length and the
+ * type of their first element. */
+int lg_gguf_field_count(const lg_gguf *g, uint64_t *count);
+int lg_gguf_field(const lg_gguf *g, uint64_t index, const char **key, int *type, uint64_t *n_elements,
+                  int *element_type);
+/* The index of the first field named `key`, or LG_ENOTFOUND. */
+int lg_gguf_find_field(const lg_gguf *g, const char *key, uint64_t *index);
+/* Typed reads of field `field`, or of element `elem` of an array field
+ * (elem = UINT64_MAX reads the field itself).  u64, f32 and bool convert as
+ * GGUFValue::as_u64 / as_f32 / as_bool (src/gguf.rs:232-272); i64 reads any
+ * integer (signed ones sign-extended); f64 reads f32 or f64.  LG_EINVAL for a
+ * value of another kind. */
+int lg_gguf_get_u64(const lg_gguf *g, uint64_t field, uint64_t elem, uint64_t *out);
+int lg_gguf_get_i64(const lg_gguf *g, uint64_t field, uint64_t elem, int64_t *out);
+int lg_gguf_get_f32(const lg_gguf *g, uint64_t field, uint64_t elem, float *out);
+int lg_gguf_get_f64(const lg_gguf *g, uint64_t field, uint64_t elem, double *out);
+int lg_gguf_get_bool(const lg_gguf *g, uint64_t field, uint64_t elem, int *out);
+int lg_gguf_get_str(const lg_gguf *g, uint64_t field, uint64_t elem, const char **out, uint64_t *len);
 
 /* ---- Launch-shape tuning hooks (no counterpart in the reference: the Vulkan
  * shaders have fixed workgroup counts).  For launch-shape sweeps; 0 restores the

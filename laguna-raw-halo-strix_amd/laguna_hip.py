@@ -27,7 +27,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblaguna_hip.so")
 
 F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
-OK, EINVAL, EHIP, ENOMEM, EUNSUPPORTED, EIO, ENODEV = range(7)
+OK, EINVAL, EHIP, ENOMEM, EUNSUPPORTED, EIO, ENODEV, ENOTFOUND = range(8)
 
 # C-ABI symbols declared in include/laguna_hip.h, with ctypes signatures.
 _vp, _u32, _u64, _i, _f = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
@@ -67,6 +67,27 @@ SIGNATURES = {
     "lg_dflash_graph_create": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, ctypes.POINTER(_vp)]),
     "lg_dflash_graph_launch": (_i, [_vp, _vp]),
     "lg_dflash_graph_destroy": (_i, [_vp]),
+    "lg_gguf_type_info": (_i, [_i, ctypes.POINTER(_u32), ctypes.POINTER(_u32), ctypes.POINTER(_i),
+                               ctypes.POINTER(_i)]),
+    "lg_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "lg_gguf_close": (_i, [_vp]),
+    "lg_gguf_header": (_i, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(_u64), ctypes.POINTER(_u64),
+                            ctypes.POINTER(_u64)]),
+    "lg_gguf_metadata": (_i, [_vp, _vp]),
+    "lg_gguf_tensor_info": (_i, [_vp, _u64, _vp]),
+    "lg_gguf_find_tensor": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
+    "lg_gguf_read_tensor": (_i, [_vp, _u64, _vp, _u64]),
+    "lg_gguf_upload_tensor": (_i, [_vp, _u64, _vp, _u64, _vp]),
+    "lg_gguf_field_count": (_i, [_vp, ctypes.POINTER(_u64)]),
+    "lg_gguf_field": (_i, [_vp, _u64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i), ctypes.POINTER(_u64),
+                           ctypes.POINTER(_i)]),
+    "lg_gguf_get_u64": (_i, [_vp, _u64, _u64, ctypes.POINTER(_u64)]),
+    "lg_gguf_get_i64": (_i, [_vp, _u64, _u64, ctypes.POINTER(ctypes.c_int64)]),
+    "lg_gguf_get_f32": (_i, [_vp, _u64, _u64, ctypes.POINTER(_f)]),
+    "lg_gguf_get_f64": (_i, [_vp, _u64, _u64, ctypes.POINTER(ctypes.c_double)]),
+    "lg_gguf_get_bool": (_i, [_vp, _u64, _u64, ctypes.POINTER(_i)]),
+    "lg_gguf_get_str": (_i, [_vp, _u64, _u64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_u64)]),
+    "lg_gguf_find_field": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
     # launch-shape tuning hooks (no counterpart in the reference)
     "lg_set_m1_grid_cap": (_i, [_u32]),
     "lg_set_m1_split": (_i, [_u32]),
@@ -412,10 +433,62 @@ class DFlashModel:
         self.ctx_len = 0
 
     def _up(self, a, dtype=None):
+        if isinstance(a, GpuBuffer):  # already on the device (e.g. uploaded from a GGUF file)
+            self._bufs.append(a)
+            return a
         a = np.ascontiguousarray(a if dtype is None else np.asarray(a, dtype))
         b = upload_bytes(self.ctx, a.view(np.uint8).ravel())
         self._bufs.append(b)
         return b
+
+    @classmethod
+    def load(cls, ctx, gguf_path):
+        """DFlashModel::load (src/dflash.rs:34-120) with Model::from_reader's
+        hyperparameters (src/model.rs:29-129).  Projections are uploaded as their raw
+        GGUF blocks (Q4_K, Q8_0 and F32 run as stored; other types are dequantized to
+        f32 on the device), norms as f32.  Unlike the reference, which keeps a
+        missing tensor as None and panics when the forward needs it, a missing
+        tensor raises here."""
+        with GGUFReader(gguf_path) as rd:
+            md = rd.metadata
+            need = {"block_count": md.block_count, "embedding_length": md.embedding_length,
+                    "feed_forward_length": md.feed_forward_length, "head_count": md.attention_head_count,
+                    "head_count_kv": md.attention_head_count_kv, "key_length": md.attention_key_length}
+            missing = [k for k, v in need.items() if not v]
+            if missing:
+                raise LagunaError(EIO, f"{gguf_path}: no {', '.join(missing)} in the metadata")
+            cfg = DFlashConfig(n_embd=md.embedding_length, n_heads=md.attention_head_count,
+                               n_kv=md.attention_head_count_kv, head_dim=md.attention_key_length,
+                               rope_dim=md.rope_dimension_count or 0, n_ff=md.feed_forward_length,
+                               n_aux=len(md.target_layers or []), n_layers=md.block_count,
+                               rope_base=md.rope_freq_base if md.rope_freq_base is not None else 500000.0)
+
+            def tensor(name, as_f32=False):
+                t = rd.tensor_by_name(name)
+                if t is None:
+                    raise LagunaError(ENOTFOUND, f"{gguf_path}: no tensor {name!r}")
+                raw = rd.upload_tensor_quantized(ctx, t)
+                if t.dtype == F32 or (not as_f32 and t.dtype in (Q4_K, Q8_0)):
+                    return raw, t.dtype
+                out = GpuBuffer(ctx, 4 * t.n_elements())  # dequant_to_f32 on the device
+                dequant_to_f32_device(ctx, raw, t.n_bytes(), t.dtype, t.n_elements(), out)
+                return out, F32
+
+            enc = {"enc_aux_norm": tensor("enc.aux_norm.weight", True)[0],
+                   "enc_output_norm": tensor("enc.output_norm.weight", True)[0],
+                   "output_norm": tensor("output_norm.weight", True)[0] if rd.tensor_by_name("output_norm.weight")
+                   else None}
+            enc["fc"], enc["fc_dtype"] = tensor("fc.weight")
+            layers = []
+            for i in range(cfg.n_layers):
+                L = {}
+                for n in DFLASH_NORMS:
+                    L[n] = tensor(f"blk.{i}.{n}.weight", True)[0]
+                for n in DFLASH_PROJ:
+                    L[n], L[n + "_dtype"] = tensor(f"blk.{i}.{n}.weight")
+                layers.append(L)
+        ctx.sync()
+        return cls(ctx, cfg, enc, layers)
 
     # accessors of src/dflash.rs:121-155
     def layer_count(self):
@@ -513,5 +586,211 @@ class DFlashGraph:
     def __del__(self):
         try:
             self.destroy()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------------------
+# GGUF v3 reader (GGUFReader / TensorInfo / GGUFMetadata, src/gguf.rs:172-514)
+
+GGUF_MAX_DIMS = 8
+WHOLE = 2**64 - 1  # "the field itself" for the typed metadata reads
+
+
+class _GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", _u32), ("shape", _u64 * GGUF_MAX_DIMS), ("dtype", _i),
+                ("data_offset", _u64), ("n_elements", _u64), ("n_bytes", _u64)]
+
+
+class _GgufMeta(ctypes.Structure):
+    _fields_ = [("present", _u32), ("architecture", ctypes.c_char * 64), ("general_name", ctypes.c_char * 256),
+                ("decoder_arch", ctypes.c_char * 64)] + \
+               [(n, _u64) for n in ("file_type", "alignment", "block_count", "context_length", "embedding_length",
+                                    "feed_forward_length", "head_count", "head_count_kv", "key_length",
+                                    "value_length", "rope_dimension_count", "expert_count", "expert_used_count",
+                                    "vocab_size")] + \
+               [("rms_epsilon", _f), ("rope_freq_base", _f), ("expert_weights_norm", _i),
+                ("n_target_layers", _u32), ("target_layers", ctypes.c_int64 * 64)]
+
+
+# LG_GGUF_HAS_* bits, in declaration order
+_META_FIELDS = ["architecture", "general_name", "file_type", "alignment", "block_count", "context_length",
+                "embedding_length", "feed_forward_length", "head_count", "head_count_kv", "key_length",
+                "value_length", "rms_epsilon", "rope_freq_base", "rope_dimension_count", "expert_count",
+                "expert_used_count", "vocab_size", "target_layers", "decoder_arch", "expert_weights_norm"]
+# GGUFMetadata's field names for the ones the C struct names differently
+_META_NAMES = {"head_count": "attention_head_count", "head_count_kv": "attention_head_count_kv",
+               "key_length": "attention_key_length", "value_length": "attention_value_length",
+               "rms_epsilon": "attention_layer_norm_rms_epsilon"}
+
+
+def gguf_type_info(dtype):
+    """(block_size, block_elements, is_supported, is_quantized) of a GGUF type id
+    (TensorType, src/gguf.rs:91-170)."""
+    bb, be, sup, q = _u32(), _u32(), _i(), _i()
+    check(lib().lg_gguf_type_info(dtype, ctypes.byref(bb), ctypes.byref(be), ctypes.byref(sup), ctypes.byref(q)))
+    return bb.value, be.value, bool(sup.value), bool(q.value)
+
+
+class TensorInfo:
+    """src/gguf.rs:172-201."""
+
+    def __init__(self, index, name, shape, dtype, data_offset, n_elements, n_bytes):
+        self.index, self.name, self.shape, self.dtype = index, name, shape, dtype
+        self.data_offset, self._n_elements, self._n_bytes = data_offset, n_elements, n_bytes
+
+    def n_elements(self):
+        return self._n_elements
+
+    def n_bytes(self):
+        return self._n_bytes
+
+    def __repr__(self):
+        return f"TensorInfo({self.name!r}, shape={self.shape}, dtype={self.dtype}, offset={self.data_offset})"
+
+
+class GGUFMetadata:
+    """The populated fields (None when absent) plus raw_fields: [(key, value)] in file order."""
+
+    def __init__(self, m, raw_fields):
+        for bit, f in enumerate(_META_FIELDS):
+            name = _META_NAMES.get(f, f)
+            if not m.present & (1 << bit):
+                setattr(self, name, None)
+            elif f in ("architecture", "general_name", "decoder_arch"):
+                setattr(self, name, getattr(m, f).decode())
+            elif f == "target_layers":
+                setattr(self, name, [int(m.target_layers[i]) for i in range(m.n_target_layers)])
+            elif f == "expert_weights_norm":
+                setattr(self, name, bool(m.expert_weights_norm))
+            else:
+                setattr(self, name, getattr(m, f))
+        self.raw_fields = raw_fields
+
+
+class GGUFReader:
+    """GGUFReader (src/gguf.rs:311-433) over the C reader.  Values of raw_fields are
+    Python ints, floats, bools, strs or lists of them."""
+
+    def __init__(self, path):
+        h = _vp()
+        check(lib().lg_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+        v, tc, fc, off = _u32(), _u64(), _u64(), _u64()
+        check(lib().lg_gguf_header(h, ctypes.byref(v), ctypes.byref(tc), ctypes.byref(fc), ctypes.byref(off)))
+        self.version, self.tensor_count, self.field_count = v.value, tc.value, fc.value
+        self.tensor_data_offset = off.value
+        self.tensors = []
+        for i in range(self.tensor_count):
+            t = _GgufTensor()
+            check(lib().lg_gguf_tensor_info(h, i, ctypes.byref(t)))
+            self.tensors.append(TensorInfo(i, t.name.decode(), [t.shape[d] for d in range(t.n_dims)], t.dtype,
+                                           t.data_offset, t.n_elements, t.n_bytes))
+        m = _GgufMeta()
+        check(lib().lg_gguf_metadata(h, ctypes.byref(m)))
+        self.metadata = GGUFMetadata(m, [(k, self.field_at(i)) for i, k in enumerate(self._keys())])
+
+    @classmethod
+    def open(cls, path):
+        return cls(path)
+
+    def _keys(self):
+        n = _u64()
+        check(lib().lg_gguf_field_count(self._h, ctypes.byref(n)))
+        keys = []
+        for i in range(n.value):
+            k = ctypes.c_char_p()
+            check(lib().lg_gguf_field(self._h, i, ctypes.byref(k), None, None, None))
+            keys.append(k.value.decode())
+        return keys
+
+    def find_field(self, key):
+        """Index of the first metadata field named `key`, or None."""
+        idx = _u64()
+        st = lib().lg_gguf_find_field(self._h, key.encode(), ctypes.byref(idx))
+        if st == ENOTFOUND:
+            return None
+        check(st)
+        return idx.value
+
+    def field(self, key):
+        """The value of the first metadata field named `key` (LagunaError if absent)."""
+        idx = self.find_field(key)
+        if idx is None:
+            raise LagunaError(ENOTFOUND, f"no metadata key {key!r}")
+        return self.field_at(idx)
+
+    def field_at(self, index):
+        """The value of the index-th metadata field."""
+        t, n, et = _i(), _u64(), _i()
+        check(lib().lg_gguf_field(self._h, index, None, ctypes.byref(t), ctypes.byref(n), ctypes.byref(et)))
+        if t.value == 9:
+            if et.value == 9:
+                return None  # arrays of arrays are not mirrored
+            return [self._scalar(index, et.value, j) for j in range(n.value)]
+        return self._scalar(index, t.value, WHOLE)
+
+    def _scalar(self, index, typ, elem):
+        h = self._h
+        if typ == 8:
+            out, n = ctypes.c_char_p(), _u64()
+            check(lib().lg_gguf_get_str(h, index, elem, ctypes.byref(out), ctypes.byref(n)))
+            return ctypes.string_at(out, n.value).decode("utf-8", "replace")
+        if typ in (6, 12):
+            out = ctypes.c_double()
+            check(lib().lg_gguf_get_f64(h, index, elem, ctypes.byref(out)))
+            return out.value
+        if typ == 7:
+            out = _i()
+            check(lib().lg_gguf_get_bool(h, index, elem, ctypes.byref(out)))
+            return bool(out.value)
+        out = ctypes.c_int64()
+        check(lib().lg_gguf_get_i64(h, index, elem, ctypes.byref(out)))
+        return out.value if typ in (1, 3, 5, 11) else out.value & (2**64 - 1)
+
+    def tensor_by_name(self, name):
+        """src/gguf.rs:407-409: the first tensor of that name, or None."""
+        idx = _u64()
+        st = lib().lg_gguf_find_tensor(self._h, name.encode(), ctypes.byref(idx))
+        if st == ENOTFOUND:
+            return None
+        check(st)
+        return self.tensors[idx.value]
+
+    def tensors_with_dtype(self, dtype):
+        return [t for t in self.tensors if t.dtype == dtype]
+
+    def read_tensor_data(self, tensor):
+        """src/gguf.rs:415-421: the tensor's n_bytes raw bytes."""
+        buf = np.empty(tensor.n_bytes(), np.uint8)
+        check(lib().lg_gguf_read_tensor(self._h, tensor.index, buf.ctypes.data, buf.size))
+        return buf
+
+    def upload_tensor_quantized(self, ctx, tensor, stream=None):
+        """Model::upload_tensor_quantized (src/model.rs:174-184): the raw bytes in a new device buffer."""
+        b = GpuBuffer(ctx, max(tensor.n_bytes(), 1))
+        check(lib().lg_gguf_upload_tensor(self._h, tensor.index, b.ptr, tensor.n_bytes(), stream))
+        return b
+
+    def layer_count(self):
+        return self.metadata.block_count
+
+    def embedding_length(self):
+        return self.metadata.embedding_length
+
+    def close(self):
+        if self._h:
+            check(lib().lg_gguf_close(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
