@@ -234,19 +234,46 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
     const uint32_t kvld = n_kv * AHD, qld = n_q * AHD;
 
     // K and V of the chunk's 64 positions as bf16 parts.  A thread takes blocks of 4
-    // positions x 4 dims: K rows and the transposed V rows go to LDS 4 values (8
-    // bytes) at a time.
-    for (uint32_t e = tid; e < (ACH / 4) * (AHD / 4); e += 256) {
-        const uint32_t pq = e / (AHD / 4), d = 4 * (e % (AHD / 4));
-        float fk[4][4], fv[4][4];  // [position][dim]
+    // positions x 4 dims (two rounds): K rows and the transposed V rows go to LDS 4
+    // values (8 bytes) at a time.  Every load of both rounds is issued first.
+    constexpr int KVR = (ACH / 4) * (AHD / 4) / 256;
+    float4 kq[KVR][4], vq[KVR][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {  // branch-free: positions past S read position S-1, zeroed
+    for (int rd = 0; rd < KVR; rd++) {
+        const uint32_t e = tid + 256u * rd;
+        const uint32_t pq = e / (AHD / 4), d = 4 * (e % (AHD / 4));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // branch-free: positions past S read position S-1 (zeroed below)
             const uint32_t p = c * ACH + 4 * pq + i, pc = p < S ? p : S - 1;
             const bool s0 = pc < n0;
             const uint64_t off = (uint64_t)(s0 ? pc : pc - n0) * kvld + h * AHD + d;
-            const float4 kv = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + off);
-            const float4 vv = *reinterpret_cast<const float4 *>((s0 ? v0 : v1) + off);
-            const bool ok = p < S;
+            kq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + off);
+            vq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? v0 : v1) + off);
+        }
+    }
+    // this lane's query row (A operand fragments for the 4 k-steps): loads issued
+    // first, with the chunk's K/V loads, so all of them are in flight together
+    const uint32_t qr = 16 * wave + l16;
+    const bool qlive = qr < nq;  // branch-free: query rows past nq read row 0, zeroed
+    float4 qx[AHD / 32][2];
+    {
+        const uint32_t t = qlive ? qr / G : 0, hq = qlive ? h * G + qr % G : h * G;
+        const float *qp = q + (uint64_t)t * qld + hq * AHD + 8 * kg;
+#pragma unroll
+        for (int ks = 0; ks < (int)(AHD / 32); ks++) {
+            qx[ks][0] = *reinterpret_cast<const float4 *>(qp + 32 * ks);
+            qx[ks][1] = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
+        }
+    }
+#pragma unroll
+    for (int rd = 0; rd < KVR; rd++) {
+        const uint32_t e = tid + 256u * rd;
+        const uint32_t pq = e / (AHD / 4), d = 4 * (e % (AHD / 4));
+        float fk[4][4], fv[4][4];  // [position][dim]
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool ok = c * ACH + 4 * pq + i < S;
+            const float4 kv = kq[rd][i], vv = vq[rd][i];
             fk[i][0] = ok ? kv.x : 0.f, fk[i][1] = ok ? kv.y : 0.f, fk[i][2] = ok ? kv.z : 0.f, fk[i][3] = ok ? kv.w : 0.f;
             fv[i][0] = ok ? vv.x : 0.f, fv[i][1] = ok ? vv.y : 0.f, fv[i][2] = ok ? vv.z : 0.f, fv[i][3] = ok ? vv.w : 0.f;
         }
@@ -271,26 +298,18 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
             *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
         }
     }
-    // this lane's query row: A operand fragments for the 4 k-steps, straight from HBM
-    const uint32_t qr = 16 * wave + l16;
     bf16x8 qa[AHD / 32][NP];
-    {
-        const bool live = qr < nq;  // branch-free: query rows past nq read row 0, zeroed
-        const uint32_t t = live ? qr / G : 0, hq = live ? h * G + qr % G : h * G;
-        const float *qp = q + (uint64_t)t * qld + hq * AHD + 8 * kg;
 #pragma unroll
-        for (int ks = 0; ks < (int)(AHD / 32); ks++) {
-            const float4 x0 = *reinterpret_cast<const float4 *>(qp + 32 * ks);
-            const float4 x1 = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
-            const float f[8] = {live ? x0.x : 0.f, live ? x0.y : 0.f, live ? x0.z : 0.f, live ? x0.w : 0.f,
-                                live ? x1.x : 0.f, live ? x1.y : 0.f, live ? x1.z : 0.f, live ? x1.w : 0.f};
-            uint32_t wp[NP][4];
+    for (int ks = 0; ks < (int)(AHD / 32); ks++) {
+        const float4 x0 = qx[ks][0], x1 = qx[ks][1];
+        const float f[8] = {qlive ? x0.x : 0.f, qlive ? x0.y : 0.f, qlive ? x0.z : 0.f, qlive ? x0.w : 0.f,
+                            qlive ? x1.x : 0.f, qlive ? x1.y : 0.f, qlive ? x1.z : 0.f, qlive ? x1.w : 0.f};
+        uint32_t wp[NP][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) split3x2(f[2 * i], f[2 * i + 1], wp[0][i], wp[1][i], wp[2][i]);
+        for (int i = 0; i < 4; i++) split3x2(f[2 * i], f[2 * i + 1], wp[0][i], wp[1][i], wp[2][i]);
 #pragma unroll
-            for (int pp = 0; pp < NP; pp++)
-                qa[ks][pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
-        }
+        for (int pp = 0; pp < NP; pp++)
+            qa[ks][pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
     }
     __syncthreads();
 
