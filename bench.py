@@ -191,6 +191,10 @@ WORKLOADS = {
     "q4k_m16_bf16": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008),
     "q4k_m16_f32": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008),
     "q8_0_m16_f32": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009),
+    # vocab-sized output projection (the LM head, src/target.rs:580-605): M=1 for one
+    # token, M=16 to verify a 16-token draft block
+    "q4k_lm_head_m1": lambda: MatvecM1(lh.Q4_K, 4096, 151936, 0x5EED000B),
+    "q4k_lm_head_m16": lambda: BatchM16(lh.Q4_K, 4096, 151936, lh.F32, 0x5EED000B),
     "dflash_block": lambda: DFlashBlock(),
     "dflash_block_eager": lambda: DFlashBlock(graph=False),
 }
@@ -323,7 +327,8 @@ def main():
     head = time_workload(ctx, ev, wl, args.steps, args.warmup)
     extra = {}
     if not args.no_extra:
-        for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32"]:
+        for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32", "q4k_lm_head_m1",
+                     "q4k_lm_head_m16"]:
             if name != args.workload:
                 extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(50, args.steps // 4), 20)
         for name in ["dflash_block", "dflash_block_eager"]:
