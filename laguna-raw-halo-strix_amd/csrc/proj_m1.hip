@@ -278,9 +278,38 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_rows(const float *__restr
     const uint32_t P = k >> 6;
     const uint32_t p = lane;
     const bool active = p < P;
-    for (uint32_t e4 = threadIdx.x; e4 < k / 4; e4 += blockDim.x) {
-        const uint32_t e = 4 * e4;
-        *reinterpret_cast<float4 *>(xs + e + 4 * (e >> 6)) = reinterpret_cast<const float4 *>(x)[e4];
+    const Q4Lane L = q4_lane(p & 3u);
+    const uint64_t lane_off = (uint64_t)(p >> 2) * Q4K_BYTES;
+    auto load_rows = [&](uint32_t r0, uint4 (&hd)[R], uint4 (&qa)[R], uint4 (&qb)[R]) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            if (active && r0 + r < n) {
+                const uint8_t *blk = w + (uint64_t)(r0 + r) * row_bytes + lane_off;
+                hd[r] = *reinterpret_cast<const uint4 *>(blk);
+                qa[r] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * L.g);
+                qb[r] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * L.g);
+            } else {
+                hd[r] = qa[r] = qb[r] = make_uint4(0, 0, 0, 0);  // idle lanes: zero scales, zero sums
+            }
+        }
+    };
+    // The activation loads go first, then the first rows' weight loads: the wait for
+    // the activations (loads complete in issue order) does not wait for the rows, and
+    // the rows are in flight while the activations are staged.
+    constexpr int XL = 4096 / 4 / (TEAMS * 64);  // float4 loads of x per thread (k <= 4096)
+    float4 xv[XL];
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+        const uint32_t e4 = threadIdx.x + i * TEAMS * 64;
+        xv[i] = e4 < k / 4 ? reinterpret_cast<const float4 *>(x)[e4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    uint32_t r0 = (blockIdx.x * TEAMS + team) * R;
+    uint4 hd[R], qa[R], qb[R];
+    if (r0 < n) load_rows(r0, hd, qa, qb);
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+        const uint32_t e4 = threadIdx.x + i * TEAMS * 64;
+        if (e4 < k / 4) *reinterpret_cast<float4 *>(xs + 4 * e4 + 4 * (e4 >> 4)) = xv[i];
     }
     __syncthreads();
     float xr[64];
@@ -298,26 +327,14 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_rows(const float *__restr
     float X0 = 0.f, X1 = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
-    const Q4Lane L = q4_lane(p & 3u);
-    const uint64_t lane_off = (uint64_t)(p >> 2) * Q4K_BYTES;
-    for (uint32_t r0 = (blockIdx.x * TEAMS + team) * R; r0 < n; r0 += gridDim.x * TEAMS * R) {
-        uint4 hd[R], qa[R], qb[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (active && r0 + r < n) {
-                const uint8_t *blk = w + (uint64_t)(r0 + r) * row_bytes + lane_off;
-                hd[r] = *reinterpret_cast<const uint4 *>(blk);
-                qa[r] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * L.g);
-                qb[r] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * L.g);
-            } else {
-                hd[r] = qa[r] = qb[r] = make_uint4(0, 0, 0, 0);  // idle lanes: zero scales, zero sums
-            }
-        }
+    for (; r0 < n; r0 += gridDim.x * TEAMS * R) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float v = wave_sum(q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L));
             if (lane == 0 && r0 + r < n) y[r0 + r] = v;
         }
+        const uint32_t rn = r0 + gridDim.x * TEAMS * R;
+        if (rn < n) load_rows(rn, hd, qa, qb);
     }
 }
 
