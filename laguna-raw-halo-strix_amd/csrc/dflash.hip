@@ -404,8 +404,9 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 
 __device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g : logf(1.0f + expf(g)); }  // src/dflash.rs:957
 
-// out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c; one wavefront per
-// query, the chunks' partials loaded CB at a time (all in flight together).
+// out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c.  One workgroup per
+// query: wave w takes the w-th quarter of the chunks (their partials loaded CB at a
+// time, all in flight together); the quarters meet in LDS, added in wave order.
 // With `gate` ([rows][n_q]), the result of head hq of row t is then multiplied by
 // softplus(gate[t][hq]) (the forward's attention gate, src/dflash.rs:956-959).
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
@@ -413,28 +414,33 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
                                                       uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch,
                                                       const float *__restrict__ gate) {
     constexpr uint32_t CB = 8;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t gq = blockIdx.x * 4 + (threadIdx.x >> 6);  // over n_kv * AQ
+    __shared__ float sm[4], sl[4], so[4][AHD];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t gq = blockIdx.x;  // over n_kv * AQ
     const uint32_t G = n_q / n_kv;
     const uint32_t h = gq / AQ, qi = gq % AQ;
-    if (h >= n_kv || qi >= rows * G) return;
+    if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup
     const uint64_t q0 = (uint64_t)h * nch * AQ + qi;  // partial index of chunk c: q0 + c * AQ
+    const uint32_t per = (nch + 3) / 4, cb0 = wave * per, cb1 = cb0 + per < nch ? cb0 + per : nch;
     float M = -INFINITY;
-    for (uint32_t c0 = 0; c0 < nch; c0 += CB) {
+    for (uint32_t c0 = cb0; c0 < cb1; c0 += CB) {
         float mc[CB];
 #pragma unroll
-        for (uint32_t b = 0; b < CB; b++) mc[b] = c0 + b < nch ? part_ml[2 * (q0 + (c0 + b) * AQ)] : -INFINITY;
+        for (uint32_t b = 0; b < CB; b++) mc[b] = c0 + b < cb1 ? part_ml[2 * (q0 + (c0 + b) * AQ)] : -INFINITY;
 #pragma unroll
         for (uint32_t b = 0; b < CB; b++) M = fmaxf(M, mc[b]);
     }
+    if (lane == 0) sm[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (uint32_t c0 = 0; c0 < nch; c0 += CB) {
+    for (uint32_t c0 = cb0; c0 < cb1; c0 += CB) {
         float mc[CB], lc[CB], a0[CB], a1[CB];
 #pragma unroll
         for (uint32_t b = 0; b < CB; b++) {
-            const uint32_t c = c0 + b < nch ? c0 + b : nch - 1;
+            const uint32_t c = c0 + b < cb1 ? c0 + b : cb1 - 1;
             const uint64_t pq = q0 + (uint64_t)c * AQ;
-            mc[b] = c0 + b < nch ? part_ml[2 * pq] : -INFINITY;
+            mc[b] = c0 + b < cb1 ? part_ml[2 * pq] : -INFINITY;
             lc[b] = part_ml[2 * pq + 1];
             a0[b] = part_o[pq * AHD + lane];
             a1[b] = part_o[pq * AHD + 64 + lane];
@@ -447,6 +453,14 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
             o1 = __builtin_fmaf(wgt, a1[b], o1);
         }
     }
+    if (lane == 0) sl[wave] = L;
+    so[wave][lane] = o0;
+    so[wave][64 + lane] = o1;
+    __syncthreads();
+    if (wave != 0) return;
+    L = ((sl[0] + sl[1]) + sl[2]) + sl[3];
+    o0 = ((so[0][lane] + so[1][lane]) + so[2][lane]) + so[3][lane];
+    o1 = ((so[0][64 + lane] + so[1][64 + lane]) + so[2][64 + lane]) + so[3][64 + lane];
     const uint32_t t = qi / G, hq = h * G + qi % G;
     float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
@@ -578,7 +592,7 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
                            rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
         int st = after_launch("attn_chunk", s);
         if (st != LG_OK) return st;
-        hipLaunchKernelGGL(k_attn_combine, dim3((n_kv * AQ + 3) / 4), dim3(256), 0, s, part, part_ml, out, rows, n_q,
+        hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, part, part_ml, out, rows, n_q,
                            n_kv, nch, gate);
         return after_launch("attn_combine", s);
     }
