@@ -155,6 +155,16 @@ int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, floa
                                  uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                  void *stream);
 
+/* The FFN's gate and up projections and dispatch_activation of a block in one
+ * launch (src/dflash.rs:963-965): h[r][i] = silu(g[r][i]) * u[r][i] with
+ * g[r][i] = sum_j x[r][j] W_gate[i,j] and u likewise with W_up (both n rows of
+ * w_dtype, f32 x [m][k], 1 <= m <= 64).  Each workgroup computes the same rows of
+ * both products, so g and u are never written; u_scratch (f32 [m][n]) is used
+ * only by inputs outside the matrix-core path, which compute g and u apart. */
+int lg_dispatch_silu_gate_up_batch(const float *x, const void *w_gate, const void *w_up, float *h,
+                                   float *u_scratch, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
+                                   void *stream);
+
 /* ---- DFlash draft glue (src/dflash.rs dispatch_* helpers, rows >= 1) ---- */
 
 /* dispatch_rmsnorm (src/dflash.rs:978-1007), kernels/rmsnorm.comp: for each of

@@ -838,16 +838,19 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
         LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, x, QD, E, m, s, x));  // x += o_proj
         // SwiGLU FFN (src/dflash.rs:962-968)
         LG_TRY(run_rmsnorm(x, L.ffn_norm, W.h, E, m, 1, E, hp.rms_eps, s));
+        const BatchJob dj{L.ffn_down, x, x, E};
         if (L.ffn_gate_type == L.ffn_up_type) {
+            // W.g = silu(gate) * up: each workgroup computes the same rows of both products
             const BatchJob jb[2] = {{L.ffn_gate, W.g, nullptr, FF}, {L.ffn_up, W.u, nullptr, FF}};
-            LG_TRY(proj_batch_multi(W.h, LG_F32, nullptr, jb, 2, E, m, L.ffn_gate_type, W.pws, W.pws_bytes, s));
+            LG_TRY(proj_batch_multi(W.h, LG_F32, nullptr, jb, 2, E, m, L.ffn_gate_type, W.pws, W.pws_bytes, s, true));
+            // x += ffn_down(silu(gate) * up)
+            LG_TRY(proj_batch_multi(W.g, LG_F32, nullptr, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
         } else {
             LG_TRY(proj(W, W.h, L.ffn_gate, L.ffn_gate_type, W.g, E, FF, m, s));
             LG_TRY(proj(W, W.h, L.ffn_up, L.ffn_up_type, W.u, E, FF, m, s));
+            // x += ffn_down(silu(gate) * up), the activation computed while staging the product's input
+            LG_TRY(proj_batch_multi(W.g, LG_F32, W.u, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
         }
-        // x += ffn_down(silu(gate) * up), the activation computed while staging the product's input
-        const BatchJob dj{L.ffn_down, x, x, E};
-        LG_TRY(proj_batch_multi(W.g, LG_F32, W.u, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
     }
     if (md->output_norm) return run_rmsnorm(x, md->output_norm, out, E, m, 1, E, hp.rms_eps, s);
     hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, x, out, mE);

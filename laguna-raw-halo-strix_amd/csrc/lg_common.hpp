@@ -75,6 +75,8 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
 // Up to 4 small-M products over the same activations in one launch: job j computes
 // c_j = W_j x (+ res_j) with W_j of n_j rows; all weights share k and w_dtype.
 // With `up` (f32 activations only), x is replaced by silu(x) * up (SiLU FFN input).
+// With `glu`, the two jobs are an FFN's gate and up products (equal n, f32 x, no
+// residuals): job 0's output receives silu(gate) * up and job 1's is scratch.
 struct BatchJob {
     const void *w;
     float *c;
@@ -83,7 +85,7 @@ struct BatchJob {
 };
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype);
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jobs, uint32_t njobs, uint32_t k,
-                     uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s);
+                     uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s, bool glu = false);
 
 // ---- GGUF block geometry (src/gguf.rs:97,101,134,136)
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;

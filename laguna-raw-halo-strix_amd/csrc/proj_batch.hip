@@ -108,9 +108,13 @@ struct MmJobs {
     MmJob j[MM_JOBS];
     uint32_t count;
 };
+// GLU launches pair two products of n rows each (gate: job 0, up: job 1): every
+// workgroup column covers the same 32*RT rows of both, wavefronts 0-1 the gate
+// rows and 2-3 the up rows, and writes only silu(gate) * up, to job 0's output.
 #define MM_JOB_SELECT                                                                     \
     uint32_t J_ = 0;                                                                      \
-    _Pragma("unroll") for (int j_ = 1; j_ < MM_JOBS; j_++) if ((uint32_t)j_ < jobs.count && \
+    if constexpr (GLU) J_ = threadIdx.x >> 7;                                             \
+    else _Pragma("unroll") for (int j_ = 1; j_ < MM_JOBS; j_++) if ((uint32_t)j_ < jobs.count && \
                                                               blockIdx.x >= jobs.j[j_].g0) J_ = j_; \
     const uint8_t *w = jobs.j[J_].w;                                                      \
     float *out = jobs.j[J_].out;                                                          \
@@ -233,9 +237,9 @@ struct Frags {
 
 // The workgroup's results: the output itself (one slice), or its slice's partial
 // sums and, in the last workgroup of the row group to finish, their ordered sum.
-template <int TT, int RT>
+template <int TT, int RT, bool GLU>
 __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out, const float *res, float *part,
-                                       uint32_t *cnt, uint32_t rt0, uint32_t m, uint32_t n) {
+                                       uint32_t *cnt, uint32_t rt0, uint32_t m, uint32_t n, float *xch) {
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
     const uint32_t S = gridDim.y, s = blockIdx.y;
     const uint64_t mn = (uint64_t)m * n;
@@ -307,6 +311,30 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 #pragma unroll
                     for (int r = 0; r < 4; r++) v[i][t][r] += q0 + g < S ? pv[g][i][t][r] : 0.0f;
     }
+    if constexpr (GLU) {
+        // wavefronts 2-3 pass their up sums through LDS (`xch`, free once every
+        // wavefront is past its products) to wavefronts 0-1, which hold the gate sums
+        // of the same rows and tokens (kernels/activation.comp:21-28)
+        const uint32_t wave = threadIdx.x >> 6;
+        __syncthreads();
+        if (wave >= 2) {
+#pragma unroll
+            for (int i = 0; i < RT; i++)
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) xch[(((wave - 2) * RT + i) * TT + t) * 256 + r * 64 + l] = v[i][t][r];
+        }
+        __syncthreads();
+        if (wave >= 2) return;
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    v[i][t][r] = silu_mul(v[i][t][r], xch[((wave * RT + i) * TT + t) * 256 + r * 64 + l]);
+    }
 #pragma unroll
     for (int i = 0; i < RT; i++) {
         const uint32_t row = (rt0 + i) * 16 + (l & 15u);
@@ -329,7 +357,7 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 // every weight load of the slice (branch-free: rows past n and blocks past k read
 // row n-1 / the last block and are never used), the fragment build while the
 // weights are in flight, then the products.
-template <int TT, int PARTS, int CH, int RT, bool FUSE>
+template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU>
 __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
     MM_JOB_SELECT;
@@ -337,7 +365,7 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
     __shared__ uint4 lf[TT * SB * PARTS * 64];
     __shared__ float lx[TT * SB * 16];
     const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
-    const uint32_t rt0 = (bx * 4 + wave) * RT;
+    const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
     const uint32_t nb = k / QK_K, b0 = blockIdx.y * CH;
     Frags<TT, PARTS, CH, FUSE> fr;
     fr.load(x, up, m, k, 8 * b0);
@@ -408,11 +436,12 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
             }
         }
     }
-    finish<TT, RT>(acc, out, res, part, cnt, rt0, m, n);
+    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
+    finish<TT, RT, GLU>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf));
 }
 
 // Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
-template <int TT, int PARTS, int CH, int RT, bool FUSE>
+template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU>
 __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
     MM_JOB_SELECT;
@@ -420,7 +449,7 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
     __shared__ uint4 lf[TT * SB * PARTS * 64];
     __shared__ float lx[TT * SB * 16];
     const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
-    const uint32_t rt0 = (bx * 4 + wave) * RT;
+    const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
     const uint32_t nsb = k / 32, sb0 = blockIdx.y * SB;
     Frags<TT, PARTS, CH, FUSE> fr;
     fr.load(x, up, m, k, sb0);
@@ -480,7 +509,8 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
             }
         }
     }
-    finish<TT, RT>(acc, out, res, part, cnt, rt0, m, n);
+    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
+    finish<TT, RT, GLU>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf));
 }
 
 // Fallback for shapes outside the MFMA path (f32 weights, k not a multiple of the
@@ -605,10 +635,10 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     return {ch, slices, tiles, rt};
 }
 
-template <int TT, int PARTS, int CH, bool FUSE>
+template <int TT, int PARTS, int CH, bool FUSE, bool GLU>
 void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt,
                uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
-#define LG_MM(K, R) hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
+#define LG_MM(K, R) hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE, GLU>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
     // mm_shape keeps rt * ch within each kernel's register budget
     if (dtype == LG_Q4_K) {
         if constexpr (4 * CH <= 8)
@@ -638,18 +668,18 @@ void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up
 #undef LG_MM
 }
 
-template <int PARTS, bool FUSE>
+template <int PARTS, bool FUSE, bool GLU = false>
 int launch_mm(int dtype, const MmShape &sh, uint32_t groups, const void *x, const float *up, const MmJobs &jobs,
               uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
     const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
     if (sh.tiles == 1) {
-        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<1, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<1, PARTS, 1, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     } else {
-        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<2, PARTS, 1, FUSE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<2, PARTS, 1, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     }
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
 }
@@ -684,9 +714,11 @@ uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, in
 }
 
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jb, uint32_t njobs, uint32_t k,
-                     uint32_t m, int w_dtype, void *ws_given, uint64_t ws_bytes, hipStream_t s) {
+                     uint32_t m, int w_dtype, void *ws_given, uint64_t ws_bytes, hipStream_t s, bool glu) {
     const char *name = "lg_dispatch_proj_quant_batch";
     LG_REQUIRE(njobs >= 1 && njobs <= (uint32_t)MM_JOBS, "%s: %u jobs (1..%d)", name, njobs, MM_JOBS);
+    LG_REQUIRE(!glu || (njobs == 2 && jb[0].n == jb[1].n && !up && x_dtype == LG_F32 && !jb[0].res && !jb[1].res),
+               "%s: a gate/up pair takes two products of equal n over f32 activations, without residuals", name);
     if (m == 0) return LG_OK;
     LG_REQUIRE(m <= 64, "%s: m=%u exceeds 64", name, m);
     LG_REQUIRE(x, "%s: null activations", name);
@@ -724,6 +756,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
                                up, jb[j].w, jb[j].c, jb[j].res, m, k, jb[j].n, w_dtype);
             LG_TRY(after_launch(name, s));
         }
+        if (glu) LG_TRY(lg_dispatch_activation(jb[0].c, jb[1].c, jb[0].c, m * jb[0].n, s));
         return LG_OK;
     }
     const uint64_t need = proj_batch_multi_ws_bytes(k, nv, njobs, m, w_dtype);
@@ -752,12 +785,17 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
             if (pb) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
             groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
         }
+        if (glu) {  // both products in every workgroup column
+            groups = (jb[0].n + 32 * sh.rt - 1) / (32 * sh.rt);
+            jobs.j[1].g0 = 0;
+        }
         jobs.count = njobs;
         LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
         const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
         const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
         if (x_dtype == LG_BF16) LG_TRY((launch_mm<1, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else if (up) LG_TRY((launch_mm<3, true>(w_dtype, sh, groups, xt, ut, jobs, cnt, ml, k, s)));
+        else if (glu) LG_TRY((launch_mm<3, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else LG_TRY((launch_mm<3, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
     }
     return LG_OK;
@@ -789,4 +827,15 @@ extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const vo
                                             uint32_t n, uint32_t m, int w_dtype, void *stream) {
     clear_error();
     return lg::proj_batch(x, x_dtype, w, c, k, n, m, w_dtype, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int lg_dispatch_silu_gate_up_batch(const float *x, const void *w_gate, const void *w_up, float *h,
+                                              float *u_scratch, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
+                                              void *stream) {
+    clear_error();
+    if (n == 0 || m == 0) return LG_OK;
+    LG_REQUIRE(n <= 32u * CNT_MAX, "lg_dispatch_silu_gate_up_batch: n=%u exceeds %u", n, 32u * CNT_MAX);
+    LG_REQUIRE(x && w_gate && w_up && h && u_scratch, "lg_dispatch_silu_gate_up_batch: null pointer");
+    const lg::BatchJob jb[2] = {{w_gate, h, nullptr, n}, {w_up, u_scratch, nullptr, n}};
+    return lg::proj_batch_multi(x, LG_F32, nullptr, jb, 2, k, m, w_dtype, nullptr, 0, (hipStream_t)stream, true);
 }

@@ -55,6 +55,7 @@ SIGNATURES = {
     "lg_dispatch_activation": (_i, [_vp, _vp, _vp, _u32, _vp]),
     "lg_dispatch_silu_mul_proj_quant": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _i, _vp]),
     "lg_dispatch_proj_quant_batch": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
+    "lg_dispatch_silu_gate_up_batch": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_rmsnorm": (_i, [_vp, _vp, _vp, _u32, _u32, _f, _vp]),
     "lg_dispatch_enc_aux_norm": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _f, _vp]),
     "lg_dispatch_qk_norm_rope": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f, _vp]),
@@ -254,6 +255,12 @@ def dispatch_silu_mul_proj_quant(ctx, gate, up, w, c, k, n, dtype):
 
 def dispatch_proj_quant_batch(ctx, x, x_dtype, w, c, k, n, m, w_dtype):
     check(lib().lg_dispatch_proj_quant_batch(_ptr(x), x_dtype, _ptr(w), _ptr(c), k, n, m, w_dtype, ctx.stream))
+
+
+def dispatch_silu_gate_up_batch(ctx, x, w_gate, w_up, h, u_scratch, k, n, m, w_dtype):
+    """h = silu(x W_gate^T) * (x W_up^T) for m rows of f32 x (src/dflash.rs:963-965)."""
+    check(lib().lg_dispatch_silu_gate_up_batch(_ptr(x), _ptr(w_gate), _ptr(w_up), _ptr(h), _ptr(u_scratch), k, n, m,
+                                               w_dtype, ctx.stream))
 
 
 def dequant_to_f32_device(ctx, data_buf, data_len, dtype, n_elements, out_buf):

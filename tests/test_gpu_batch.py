@@ -125,3 +125,58 @@ def test_launch_shapes(ctx, ch, rt, m):
     assert np.array_equal(c1, c2)
     y64, a = orc.proj_quant_f64(x, raw, lh.Q4_K, k, n)
     parity(c1, y64, a, TOL)
+
+
+def run_gate_up(ctx, x, raw_g, raw_u, w_dtype, k, n, m):
+    xb = lh.upload_f32(ctx, np.ascontiguousarray(x, np.float32).ravel())
+    gb, ub = lh.upload_bytes(ctx, np.ascontiguousarray(raw_g).view(np.uint8).ravel()), \
+        lh.upload_bytes(ctx, np.ascontiguousarray(raw_u).view(np.uint8).ravel())
+    hb, sb = lh.GpuBuffer(ctx, 4 * m * n), lh.GpuBuffer(ctx, 4 * m * n)
+    lh.dispatch_silu_gate_up_batch(ctx, xb, gb, ub, hb, sb, k, n, m, w_dtype)
+    return hb.read_f32(m * n).reshape(m, n)
+
+
+def gate_up_parity(h, x, raw_g, raw_u, w_dtype, k, n):
+    """h against silu(g) * u from the oracle's f64 products; the bound carries each
+    product's sum |W_ij x_j| through the activation (|silu'| < 1.1)."""
+    g64, ag = orc.proj_quant_f64(x, raw_g, w_dtype, k, n)
+    u64, au = orc.proj_quant_f64(x, raw_u, w_dtype, k, n)
+    sg = g64 / (1.0 + np.exp(-g64))
+    parity(h, sg * u64, 1.1 * np.abs(u64) * ag + np.abs(sg) * au, TOL)
+
+
+def weights(w_dtype, seed, k, n):
+    if w_dtype == lh.Q4_K:  # k = 96: blocks run across rows (the reference's linear addressing)
+        return synth.q4k_weight(seed, k, n) if k % 256 == 0 else synth.random_q4k(seed, -(-(k * n) // 256))
+    if w_dtype == lh.Q8_0:
+        return synth.q8_0_weight(seed, k, n)
+    return synth.normal(seed, k * n, 0.02)
+
+
+@pytest.mark.parametrize("w_dtype,k,n,m", [
+    (lh.Q4_K, 4096, 1536, 16), (lh.Q4_K, 4096, 1536, 1), (lh.Q4_K, 2816, 700, 29), (lh.Q4_K, 1024, 300, 40),
+    (lh.Q8_0, 1024, 700, 16), (lh.Q8_0, 4096, 512, 33),
+    (lh.F32, 512, 40, 7), (lh.Q4_K, 96, 8, 3),  # outside the matrix-core path
+])
+def test_silu_gate_up(ctx, w_dtype, k, n, m):
+    # The FFN's gate and up products with the activation (src/dflash.rs:963-965)
+    print(f"gate/up pair w={w_dtype} k={k} n={n} m={m}", flush=True)
+    raw_g, raw_u = weights(w_dtype, 500 + m, k, n), weights(w_dtype, 600 + m, k, n)
+    x = synth.normal(700 + m, m * k).reshape(m, k)
+    h = run_gate_up(ctx, x, raw_g, raw_u, w_dtype, k, n, m)
+    assert np.array_equal(h, run_gate_up(ctx, x, raw_g, raw_u, w_dtype, k, n, m))
+    gate_up_parity(h, x, raw_g, raw_u, w_dtype, k, n)
+
+
+@pytest.mark.parametrize("ch,rt", [(1, 1), (1, 4), (2, 2), (2, 4), (4, 2)])
+def test_silu_gate_up_launch_shapes(ctx, ch, rt):
+    k, n, m = 2816, 700, 29
+    print(f"gate/up pair shape ch={ch} rt={rt}", flush=True)
+    raw_g, raw_u = synth.q4k_weight(800, k, n), synth.q4k_weight(801, k, n)
+    x = synth.normal(802, m * k).reshape(m, k)
+    lh.check(lh.lib().lg_set_batch_shape(ch, rt))
+    try:
+        h = run_gate_up(ctx, x, raw_g, raw_u, lh.Q4_K, k, n, m)
+    finally:
+        lh.check(lh.lib().lg_set_batch_shape(0, 0))
+    gate_up_parity(h, x, raw_g, raw_u, lh.Q4_K, k, n)
