@@ -139,6 +139,25 @@ class BatchM16(Workload):
         lh.dispatch_proj_quant_batch(ctx, self.x, self.x_dtype, w, self.c, self.k, self.n, self.m, self.dtype)
 
 
+class VerifyBlock(BatchM16):
+    """Target-side block verify: the vocab-sized LM head over m draft hidden states
+    (src/target.rs:580-605), then the device argmax of each row of logits
+    (src/lib.rs:456-464); the indices stay on the device."""
+
+    def __init__(self, k, n, seed, m=16):
+        super().__init__(lh.Q4_K, k, n, lh.F32, seed, m)
+        self.bytes_per_call += 4 * m * n  # the argmax reads the logits back
+        self.name = f"Q4_K LM head {k}->{n} M={m} + argmax per row"
+
+    def setup(self, ctx):
+        super().setup(ctx)
+        self.idx = lh.GpuBuffer(ctx, 4 * self.m)
+
+    def step(self, ctx, i):
+        super().step(ctx, i)
+        lh.check(lh.lib().lg_dispatch_argmax(self.c.ptr, self.n, self.m, self.n, self.idx.ptr, ctx.stream))
+
+
 class DFlashBlock(Workload):
     """The 6-layer draft decoder's block forward: 16 tokens over a 2048-position f32
     K/V context, random-init weights (Q4_K except Q8_0 attn_output), replayed as a
@@ -195,6 +214,7 @@ WORKLOADS = {
     # token, M=16 to verify a 16-token draft block
     "q4k_lm_head_m1": lambda: MatvecM1(lh.Q4_K, 4096, 151936, 0x5EED000B),
     "q4k_lm_head_m16": lambda: BatchM16(lh.Q4_K, 4096, 151936, lh.F32, 0x5EED000B),
+    "lm_head_verify_m16": lambda: VerifyBlock(4096, 151936, 0x5EED000B),
     "dflash_block": lambda: DFlashBlock(),
     "dflash_block_eager": lambda: DFlashBlock(graph=False),
 }
@@ -328,7 +348,7 @@ def main():
     extra = {}
     if not args.no_extra:
         for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32", "q4k_lm_head_m1",
-                     "q4k_lm_head_m16"]:
+                     "q4k_lm_head_m16", "lm_head_verify_m16"]:
             if name != args.workload:
                 extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(50, args.steps // 4), 20)
         for name in ["dflash_block", "dflash_block_eager"]:

@@ -165,6 +165,16 @@ int lg_dispatch_silu_gate_up_batch(const float *x, const void *w_gate, const voi
                                    float *u_scratch, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                    void *stream);
 
+/* ---- target-side verify ---- */
+
+/* argmax (src/lib.rs:456-464) of each of `rows` rows of n logits (row r at
+ * logits + r*ld, ld >= n), on the device: out[r] is the reference's index bit for
+ * bit -- the last of equal maxima, and a NaN restarts the search after it (its
+ * fold with partial_cmp(..).unwrap_or(Equal)); n = 0 gives 0.  Used on the LM
+ * head's logits of the target (one row) and of a draft block (m rows). */
+int lg_dispatch_argmax(const float *logits, uint32_t n, uint32_t rows, uint64_t ld, uint32_t *out,
+                       void *stream);
+
 /* ---- DFlash draft glue (src/dflash.rs dispatch_* helpers, rows >= 1) ---- */
 
 /* dispatch_rmsnorm (src/dflash.rs:978-1007), kernels/rmsnorm.comp: for each of

@@ -56,6 +56,7 @@ SIGNATURES = {
     "lg_dispatch_silu_mul_proj_quant": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _i, _vp]),
     "lg_dispatch_proj_quant_batch": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_silu_gate_up_batch": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
+    "lg_dispatch_argmax": (_i, [_vp, _u32, _u32, _u64, _vp, _vp]),
     "lg_dispatch_rmsnorm": (_i, [_vp, _vp, _vp, _u32, _u32, _f, _vp]),
     "lg_dispatch_enc_aux_norm": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _f, _vp]),
     "lg_dispatch_qk_norm_rope": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f, _vp]),
@@ -261,6 +262,31 @@ def dispatch_silu_gate_up_batch(ctx, x, w_gate, w_up, h, u_scratch, k, n, m, w_d
     """h = silu(x W_gate^T) * (x W_up^T) for m rows of f32 x (src/dflash.rs:963-965)."""
     check(lib().lg_dispatch_silu_gate_up_batch(_ptr(x), _ptr(w_gate), _ptr(w_up), _ptr(h), _ptr(u_scratch), k, n, m,
                                                w_dtype, ctx.stream))
+
+
+def dispatch_argmax(ctx, logits, n, rows=1, ld=None, out=None):
+    """argmax (src/lib.rs:456-464) of each of `rows` rows of n logits on the device
+    (row r at float offset r * ld).  Returns the indices as int64 (and leaves them
+    in `out`, a GpuBuffer of 4 * rows bytes, when given)."""
+    ld = n if ld is None else ld
+    ob = out if out is not None else GpuBuffer(ctx, 4 * max(rows, 1))
+    try:
+        check(lib().lg_dispatch_argmax(_ptr(logits), n, rows, ld, _ptr(ob), ctx.stream))
+        return np.frombuffer(ob.download(4 * rows), np.uint32).astype(np.int64)
+    finally:
+        if out is None:
+            ob.free()
+
+
+def verify_step(ctx, draft_logits, target_logits, n_vocab):
+    """The decision of one run_target_dflash_verify step (src/lib.rs:497-503), taken
+    on the device logits of the draft (after project_normalized_hidden) and of the
+    target: both argmaxes, accepted when they agree, and the next token is the
+    draft's when accepted and the target's otherwise.
+    Returns (next_token, accepted, draft_token, target_token)."""
+    d = int(dispatch_argmax(ctx, draft_logits, n_vocab)[0])
+    t = int(dispatch_argmax(ctx, target_logits, n_vocab)[0])
+    return (d if d == t else t), d == t, d, t
 
 
 def dequant_to_f32_device(ctx, data_buf, data_len, dtype, n_elements, out_buf):

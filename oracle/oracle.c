@@ -288,3 +288,15 @@ void orc_silu_mul_f64(const float *g, const float *up, double *h, uint32_t n) {
         h[i] = x * (1.0 / (1.0 + exp(-x))) * (double)up[i];
     }
 }
+
+/* src/lib.rs:456-464: logits.iter().copied().enumerate().max_by(|a, b|
+ * a.1.partial_cmp(&b.1).unwrap_or(Equal)).map(|(i, _)| i).unwrap_or(0).
+ * Iterator::max_by keeps the running best only when compare(best, next) is
+ * Greater; Less, Equal and unordered (NaN, mapped to Equal) take the next. */
+size_t orc_argmax_f32(const float *v, size_t n) {
+    if (n == 0) return 0;
+    size_t best = 0;
+    for (size_t i = 1; i < n; i++)
+        if (!(v[best] > v[i])) best = i;
+    return best;
+}

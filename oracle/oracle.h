@@ -32,6 +32,9 @@
  *                         and the identity silu(x)-silu(-x)=x.
  *   orc_legacy_q4k        (the non-ggml Q4_K branch of dequant_to_f32) closed
  *                         forms only; it is recorded, not a product target.
+ *   orc_argmax_f32        numpy's last-occurrence argmax on NaN-free rows, and
+ *                         closed forms for ties, signed zeros, infinities, empty
+ *                         input and NaN positions (start, middle, end, all).
  */
 #ifndef LAGUNA_ORACLE_H
 #define LAGUNA_ORACLE_H
@@ -97,7 +100,11 @@ void orc_proj_quant_f64x(const double *x, const uint8_t *w, uint32_t dtype, uint
 void orc_silu_mul_f32(const float *g, const float *up, float *h, uint32_t n);
 void orc_silu_mul_f64(const float *g, const float *up, double *h, uint32_t n);
 
+/* src/lib.rs:456-464: the reference's argmax over n logits (0 when n = 0). */
+size_t orc_argmax_f32(const float *v, size_t n);
+
 #ifdef __cplusplus
 }
 #endif
+
 #endif

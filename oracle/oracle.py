@@ -45,6 +45,8 @@ def lib():
                                           _f64p, _f64p]
         L.orc_silu_mul_f32.argtypes = [_f32p, _f32p, _f32p, ctypes.c_uint32]
         L.orc_silu_mul_f64.argtypes = [_f32p, _f32p, _f64p, ctypes.c_uint32]
+        L.orc_argmax_f32.argtypes = [_f32p, ctypes.c_size_t]
+        L.orc_argmax_f32.restype = ctypes.c_size_t
         _LIB = L
     return _LIB
 
@@ -161,3 +163,9 @@ def silu_mul_f64(g, up):
     h = np.empty(g.size, np.float64)
     lib().orc_silu_mul_f64(_p(g, _f32p), _p(up, _f32p), _p(h, _f64p), g.size)
     return h
+
+
+def argmax(logits):
+    """src/lib.rs:456-464 (the reference's argmax over one row of logits)"""
+    v = np.ascontiguousarray(logits, np.float32).ravel()
+    return int(lib().orc_argmax_f32(_p(v, _f32p), v.size))

@@ -266,3 +266,30 @@ def test_silu_closed_forms():
     # silu(x) - silu(-x) = x
     assert abs((h64[3] - h64[4]) - 1.0) < 1e-15
     assert np.allclose(h, h64, rtol=1e-6, atol=1e-30)
+
+
+def test_argmax_nan_free_is_last_occurrence_of_max():
+    # max_by keeps the last of equal maxima (src/lib.rs:456-464); numpy's argmax
+    # over the reversed row finds that index independently
+    rng = np.random.default_rng(5)
+    for n in (1, 2, 3, 17, 1000, 151936):
+        for ties in (False, True):
+            v = (rng.integers(-4, 5, n) if ties else rng.standard_normal(n)).astype(np.float32)
+            assert orc.argmax(v) == n - 1 - int(np.argmax(v[::-1])), (n, ties)
+
+
+def test_argmax_closed_forms():
+    f = np.float32
+    nan, inf = f(np.nan), f(np.inf)
+    assert orc.argmax(np.zeros(0, f)) == 0                    # unwrap_or(0)
+    assert orc.argmax(np.full(7, 3.0, f)) == 6                # all equal: the last
+    assert orc.argmax(np.array([0.0, -0.0], f)) == 1          # -0 == +0: the later
+    assert orc.argmax(np.array([-0.0, 0.0, -0.0], f)) == 2
+    assert orc.argmax(np.array([1.0, inf, 2.0, inf, 3.0], f)) == 3
+    assert orc.argmax(np.array([-inf, -inf], f)) == 1
+    # a NaN is taken as Equal: it becomes the best and the next element replaces it
+    assert orc.argmax(np.array([5.0, nan, 1.0, 2.0], f)) == 3
+    assert orc.argmax(np.array([5.0, 1.0, nan], f)) == 2      # last element NaN
+    assert orc.argmax(np.array([nan, 1.0, 0.5], f)) == 1      # NaN first
+    assert orc.argmax(np.array([nan, nan, nan], f)) == 2
+    assert orc.argmax(np.array([3.0, nan, 9.0, nan, 4.0, 4.0, 1.0], f)) == 5  # after the last NaN only
