@@ -627,8 +627,9 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     if (dtype != LG_Q4_K && ch > 2) ch = 2;
     const uint32_t chunks = (k + 255) / 256, slices = (chunks + ch - 1) / ch;
     // the most rows per wavefront that still give about three workgroups per CU per
-    // token tile (fewer, larger workgroups measured slower on every shape tried)
-    uint32_t rt = 4;
+    // token tile (fewer, larger workgroups measured slower on every shape tried);
+    // four (two waves per SIMD) only when two already give twelve per CU
+    uint32_t rt = (n + 127) / 128 * slices >= 3072 * tiles ? 4 : 2;
     while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 768 * tiles) rt /= 2;
     if (g_mm_rt) rt = g_mm_rt >= 4 ? 4 : g_mm_rt >= 2 ? 2 : 1;
     while (rt * ch > (dtype == LG_Q4_K ? 8u : 4u)) rt /= 2;  // register budget
