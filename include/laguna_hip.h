@@ -43,7 +43,10 @@ typedef enum {
     LG_F16 = 1,
     LG_Q8_0 = 8,
     LG_Q4_K = 12,
-    LG_BF16 = 30
+    LG_BF16 = 30,
+    /* Not a GGUF type: Q4_K blocks repacked by lg_repack_tiled into 16-row tiles
+     * for the small-M products (block verify, the draft forward). */
+    LG_Q4_K_T16 = 1012
 } lg_dtype;
 
 typedef enum {
@@ -149,11 +152,27 @@ int lg_dispatch_silu_mul_proj_quant(const float *gate, const float *up, const vo
 
 /* Block-verify product: c[r][i] = sum_j x[r][j] * W[i,j] for r < m, i < n.
  * x is row-major [m][k] of x_dtype LG_F32 or LG_BF16 (raw bf16 bits); c is
- * f32 [m][n]; W is Q4_K or Q8_0 raw blocks or f32.  1 <= m <= 64; m = 1 is the
+ * f32 [m][n]; W is Q4_K or Q8_0 raw blocks, Q4_K repacked (LG_Q4_K_T16), or f32.  1 <= m <= 64; m = 1 is the
  * same product as lg_dispatch_proj_quant. */
 int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, float *c,
                                  uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                  void *stream);
+
+/* Q4_K weights repacked for the small-M products (no counterpart in the
+ * reference, which reads GGUF blocks in place; for callers that load a model once
+ * and run many block products).  Tile (t, b) -- rows 16t..16t+15, super-block b
+ * -- is 2304 contiguous bytes: the 16 rows' 16-byte block headers (d, dmin,
+ * scales) in row order, then their quant bytes as [32-byte group g][8-byte piece
+ * p][row r] (row r's bytes 32g+8p .. 32g+8p+7 at 256 + 512g + 128p + 8r).  Tiles
+ * are stored row tile by row tile, super-blocks in order; rows past n, up to a
+ * multiple of 16, are zero blocks.  The repack is a byte permutation, and the
+ * products over LG_Q4_K_T16 weights (lg_dispatch_proj_quant_batch,
+ * lg_dispatch_silu_gate_up_batch, the draft forward) equal those over the raw
+ * blocks bit for bit; each workgroup then reads its weights as whole 2304-byte
+ * tiles instead of 288-byte pieces of 2304-byte-apart rows.  dtype LG_Q4_K, k a
+ * multiple of 256. */
+uint64_t lg_tiled_bytes(int dtype, uint32_t k, uint32_t n);
+int lg_repack_tiled(const void *w, int dtype, uint32_t k, uint32_t n, void *out, void *stream);
 
 /* The FFN's gate and up projections and dispatch_activation of a block in one
  * launch (src/dflash.rs:963-965): h[r][i] = silu(g[r][i]) * u[r][i] with

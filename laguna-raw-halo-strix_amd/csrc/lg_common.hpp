@@ -91,6 +91,11 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;
 constexpr uint32_t QK8_0 = 32, Q80_BYTES = 34;
 
+constexpr uint32_t Q4K_TILE = 16 * Q4K_BYTES;  // LG_Q4_K_T16: 16 rows x one super-block
+
+// Bytes of a k x n LG_Q4_K_T16 tensor (rows padded to a multiple of 16).
+inline uint64_t tiled_bytes(uint32_t k, uint32_t n) { return (uint64_t)(n + 15) / 16 * (k / QK_K) * Q4K_TILE; }
+
 inline uint64_t tensor_bytes(int dtype, uint64_t elems) {
     switch (dtype) {
     case LG_Q4_K: return (elems + QK_K - 1) / QK_K * Q4K_BYTES;

@@ -107,6 +107,7 @@ struct MmJob {
 struct MmJobs {
     MmJob j[MM_JOBS];
     uint32_t count;
+    uint32_t tiled;  // Q4_K weights in LG_Q4_K_T16 tiles
 };
 // GLU launches pair two products of n rows each (gate: job 0, up: job 1): every
 // workgroup column covers the same 32*RT rows of both, wavefronts 0-1 the gate
@@ -371,16 +372,31 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
     fr.load(x, up, m, k, 8 * b0);
     uint4 hd[RT][CH];
     uint2 qv[RT][CH][4];
+    if (jobs.tiled) {  // 2304-byte tiles: each load is 512 (quants) or 256 (headers) contiguous bytes
+        const uint32_t ntiles = (n + 15) / 16;
 #pragma unroll
-    for (int i = 0; i < RT; i++) {
-        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
-        const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
+        for (int i = 0; i < RT; i++) {
+            const uint32_t t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
 #pragma unroll
-        for (int cb = 0; cb < CH; cb++) {
-            const uint8_t *blk = wr + (uint64_t)(b0 + cb < nb ? b0 + cb : nb - 1) * Q4K_BYTES;
-            hd[i][cb] = *reinterpret_cast<const uint4 *>(blk);
+            for (int cb = 0; cb < CH; cb++) {
+                const uint8_t *tb = w + ((uint64_t)t * nb + (b0 + cb < nb ? b0 + cb : nb - 1)) * Q4K_TILE;
+                hd[i][cb] = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
 #pragma unroll
-            for (int g = 0; g < 4; g++) qv[i][cb][g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kg);
+                for (int g = 0; g < 4; g++) qv[i][cb][g] = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * g + 8 * l);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+            const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
+#pragma unroll
+            for (int cb = 0; cb < CH; cb++) {
+                const uint8_t *blk = wr + (uint64_t)(b0 + cb < nb ? b0 + cb : nb - 1) * Q4K_BYTES;
+                hd[i][cb] = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+                for (int g = 0; g < 4; g++) qv[i][cb][g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kg);
+            }
         }
     }
     asm volatile("" ::: "memory");  // keep the weight loads issued ahead of the fragment build
@@ -698,6 +714,7 @@ constexpr uint32_t CNT_MAX = CNT_BYTES / 4;
 namespace lg {
 
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype) {
+    if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
     if (w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) return 0;
     uint64_t ntot = 0;
     for (uint32_t j = 0; j < jobs; j++) ntot += n[j];
@@ -725,7 +742,12 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     LG_REQUIRE(x, "%s: null activations", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
     LG_REQUIRE(!up || x_dtype == LG_F32, "%s: the fused SiLU(gate)*up takes f32 activations", name);
-    LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32, "%s: weight dtype %d", name, w_dtype);
+    LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32 || w_dtype == LG_Q4_K_T16,
+               "%s: weight dtype %d", name, w_dtype);
+    const bool tiled = w_dtype == LG_Q4_K_T16;
+    LG_REQUIRE(!tiled || (k % QK_K == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                          (!up || (reinterpret_cast<uintptr_t>(up) & 15u) == 0)),
+               "%s: LG_Q4_K_T16 weights take k a multiple of 256 (k=%u) and 16-byte aligned activations", name, k);
     const uint64_t xbytes = (uint64_t)m * k * (x_dtype == LG_F32 ? 4 : 2);
     if (k) {
         LG_EXTENT(x, xbytes, name);
@@ -741,9 +763,11 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         LG_REQUIRE(b.w && b.c, "%s: null pointer in job %u", name, j);
         LG_EXTENT(b.c, (uint64_t)m * b.n * 4, name);
         if (b.res) LG_EXTENT(b.res, (uint64_t)m * b.n * 4, name);
-        if (k) LG_EXTENT(b.w, tensor_bytes(w_dtype, (uint64_t)b.n * k), name);
+        if (k) LG_EXTENT(b.w, tiled ? tiled_bytes(k, b.n) : tensor_bytes(w_dtype, (uint64_t)b.n * k), name);
+        LG_REQUIRE(!tiled || (reinterpret_cast<uintptr_t>(b.w) & 15u) == 0, "%s: unaligned LG_Q4_K_T16 weights", name);
     }
     if (ntot == 0) return LG_OK;
+    if (tiled) w_dtype = LG_Q4_K;  // the Q4_K kernels, reading tiles
     const uint32_t blk = w_dtype == LG_Q4_K ? QK_K : QK8_0;
     bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                 (!up || (reinterpret_cast<uintptr_t>(up) & 15u) == 0);
@@ -791,6 +815,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
             jobs.j[1].g0 = 0;
         }
         jobs.count = njobs;
+        jobs.tiled = tiled ? 1u : 0u;
         LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
         const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
         const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
@@ -822,6 +847,52 @@ extern "C" int lg_set_batch_shape(uint32_t ch, uint32_t rt) {
     g_mm_ch = ch;
     g_mm_rt = rt;
     return LG_OK;
+}
+
+namespace {
+
+// LG_Q4_K_T16 repack: workgroup (b, t) writes tile (t, b).  Thread p moves quant
+// piece p = 64g + 16q + r (row r's bytes 32g + 8q .. +7, 8 bytes) to 256 + 8p;
+// threads 0-15 also move row p's 16-byte header.  Rows past n become zero blocks.
+__global__ __launch_bounds__(256) void k_repack_q4k_t16(const uint8_t *__restrict__ w, uint8_t *__restrict__ out,
+                                                         uint32_t nb, uint32_t n) {
+    const uint32_t b = blockIdx.x, t = blockIdx.y, p = threadIdx.x;
+    const uint32_t g = p >> 6, q = (p >> 4) & 3u, r = p & 15u, row = 16 * t + r;
+    uint8_t *tile = out + ((uint64_t)t * nb + b) * Q4K_TILE;
+    const bool live = row < n;
+    const uint8_t *blk = w + ((uint64_t)(live ? row : n - 1) * nb + b) * Q4K_BYTES;  // in bounds either way
+    const uint2 qv = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * q);
+    *reinterpret_cast<uint2 *>(tile + 256 + 8 * p) = live ? qv : make_uint2(0u, 0u);
+    if (p < 16) {
+        const bool hlive = 16 * t + p < n;
+        const uint8_t *hb = w + ((uint64_t)(hlive ? 16 * t + p : n - 1) * nb + b) * Q4K_BYTES;
+        const uint4 hv = *reinterpret_cast<const uint4 *>(hb);
+        *reinterpret_cast<uint4 *>(tile + 16 * p) = hlive ? hv : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+}  // namespace
+
+extern "C" uint64_t lg_tiled_bytes(int dtype, uint32_t k, uint32_t n) {
+    return dtype == LG_Q4_K && k % QK_K == 0 ? tiled_bytes(k, n) : 0;
+}
+
+extern "C" int lg_repack_tiled(const void *w, int dtype, uint32_t k, uint32_t n, void *out, void *stream) {
+    clear_error();
+    const char *name = "lg_repack_tiled";
+    LG_REQUIRE(dtype == LG_Q4_K, "%s: dtype %d (only Q4_K is tiled)", name, dtype);
+    LG_REQUIRE(k % QK_K == 0, "%s: k=%u is not a multiple of 256", name, k);
+    if (k == 0 || n == 0) return LG_OK;
+    LG_REQUIRE(w && out, "%s: null pointer", name);
+    LG_REQUIRE(((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0,
+               "%s: pointers must be 16-byte aligned", name);
+    LG_REQUIRE((n + 15) / 16 <= 65535u, "%s: n=%u exceeds %u rows", name, n, 65535u * 16);
+    LG_EXTENT(w, tensor_bytes(LG_Q4_K, (uint64_t)k * n), name);
+    LG_EXTENT(out, tiled_bytes(k, n), name);
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_repack_q4k_t16, dim3(k / QK_K, (n + 15) / 16), dim3(256), 0, s,
+                       static_cast<const uint8_t *>(w), static_cast<uint8_t *>(out), k / QK_K, n);
+    return after_launch(name, s);
 }
 
 extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k,

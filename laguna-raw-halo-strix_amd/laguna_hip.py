@@ -27,6 +27,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblaguna_hip.so")
 
 F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
+Q4_K_T16 = 1012  # Q4_K repacked into 16-row tiles by repack_tiled (not a GGUF type)
 OK, EINVAL, EHIP, ENOMEM, EUNSUPPORTED, EIO, ENODEV, ENOTFOUND = range(8)
 
 # C-ABI symbols declared in include/laguna_hip.h, with ctypes signatures.
@@ -57,6 +58,8 @@ SIGNATURES = {
     "lg_dispatch_proj_quant_batch": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_silu_gate_up_batch": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_argmax": (_i, [_vp, _u32, _u32, _u64, _vp, _vp]),
+    "lg_tiled_bytes": (_u64, [_i, _u32, _u32]),
+    "lg_repack_tiled": (_i, [_vp, _i, _u32, _u32, _vp, _vp]),
     "lg_dispatch_rmsnorm": (_i, [_vp, _vp, _vp, _u32, _u32, _f, _vp]),
     "lg_dispatch_enc_aux_norm": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _f, _vp]),
     "lg_dispatch_qk_norm_rope": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f, _vp]),
@@ -264,6 +267,14 @@ def dispatch_silu_gate_up_batch(ctx, x, w_gate, w_up, h, u_scratch, k, n, m, w_d
                                                w_dtype, ctx.stream))
 
 
+def repack_tiled(ctx, w, dtype, k, n):
+    """The k x n Q4_K tensor in `w` (raw GGUF blocks on the device) repacked into a
+    new buffer of 16-row tiles (Q4_K_T16), for the small-M products."""
+    out = GpuBuffer(ctx, lib().lg_tiled_bytes(dtype, k, n))
+    check(lib().lg_repack_tiled(_ptr(w), dtype, k, n, _ptr(out), ctx.stream))
+    return out
+
+
 def dispatch_argmax(ctx, logits, n, rows=1, ld=None, out=None):
     """argmax (src/lib.rs:456-464) of each of `rows` rows of n logits on the device
     (row r at float offset r * ld).  Returns the indices as int64 (and leaves them
@@ -434,14 +445,33 @@ class DFlashModel:
     output_norm; `layers` one dict per decoder layer with the f32 norms of
     DFLASH_NORMS and, for each projection p of DFLASH_PROJ, the raw GGUF bytes
     p and their type p + "_dtype" (tensor names of src/dflash.rs:68-79).  The
-    bytes are uploaded unchanged (Model::upload_tensor_quantized)."""
+    bytes are uploaded unchanged (Model::upload_tensor_quantized); with `tiled`
+    (the default) Q4_K projections are then repacked on the device into 16-row
+    tiles, which the forward's small-M products read as contiguous 2304-byte tiles
+    (the results are the same bit for bit)."""
 
-    def __init__(self, ctx, cfg, enc, layers):
+    def __init__(self, ctx, cfg, enc, layers, tiled=True):
         self.ctx, self.cfg = ctx, cfg
         self._bufs = []
         self.layers = []
         up = self._up
-        self._enc = {"enc_aux_norm": up(enc["enc_aux_norm"], np.float32), "fc": up(enc["fc"]),
+        E, QD, KVD = cfg.n_embd, cfg.n_heads * cfg.head_dim, cfg.n_kv * cfg.head_dim
+        shapes = {"attn_q": (E, QD), "attn_k": (E, KVD), "attn_v": (E, KVD), "attn_gate": (E, cfg.n_heads),
+                  "attn_output": (QD, E), "ffn_gate": (E, cfg.n_ff), "ffn_up": (E, cfg.n_ff), "ffn_down": (cfg.n_ff, E)}
+
+        def proj_w(a, dtype, k, n):
+            b = up(a)
+            if not tiled or int(dtype) != Q4_K or k % 256:
+                return b, int(dtype)
+            t = repack_tiled(ctx, b, Q4_K, k, n)
+            self._bufs.append(t)
+            self._bufs.remove(b)
+            ctx.sync()  # the repack has read the raw blocks
+            b.free()
+            return t, Q4_K_T16
+
+        fc_buf, fc_type = proj_w(enc["fc"], enc["fc_dtype"], cfg.n_aux * E, E)
+        self._enc = {"enc_aux_norm": up(enc["enc_aux_norm"], np.float32), "fc": fc_buf,
                      "enc_output_norm": up(enc["enc_output_norm"], np.float32),
                      "output_norm": up(enc["output_norm"], np.float32) if enc.get("output_norm") is not None else None}
         self._layer_desc = (_Layer * len(layers))()
@@ -450,8 +480,9 @@ class DFlashModel:
             for n in DFLASH_NORMS:
                 setattr(d, n, up(L[n], np.float32).ptr)
             for n in DFLASH_PROJ:
-                setattr(d, n, up(L[n]).ptr)
-                setattr(d, n + "_type", int(L[n + "_dtype"]))
+                b, t = proj_w(L[n], L[n + "_dtype"], *shapes[n])
+                setattr(d, n, b.ptr)
+                setattr(d, n + "_type", t)
         self._desc = _Model()
         h = self._desc.hp
         h.n_embd, h.n_heads, h.n_kv_heads, h.head_dim = cfg.n_embd, cfg.n_heads, cfg.n_kv, cfg.head_dim
@@ -459,7 +490,7 @@ class DFlashModel:
         h.rope_base, h.rms_eps, h.qk_eps = cfg.rope_base, cfg.rms_eps, cfg.qk_eps
         self._desc.enc_aux_norm = self._enc["enc_aux_norm"].ptr
         self._desc.fc = self._enc["fc"].ptr
-        self._desc.fc_type = int(enc["fc_dtype"])
+        self._desc.fc_type = fc_type
         self._desc.enc_output_norm = self._enc["enc_output_norm"].ptr
         self._desc.output_norm = self._enc["output_norm"].ptr if self._enc["output_norm"] else None
         self._desc.layers = self._layer_desc
@@ -475,7 +506,7 @@ class DFlashModel:
         return b
 
     @classmethod
-    def load(cls, ctx, gguf_path):
+    def load(cls, ctx, gguf_path, tiled=True):
         """DFlashModel::load (src/dflash.rs:34-120) with Model::from_reader's
         hyperparameters (src/model.rs:29-129).  Projections are uploaded as their raw
         GGUF blocks (Q4_K, Q8_0 and F32 run as stored; other types are dequantized to
@@ -521,7 +552,7 @@ class DFlashModel:
                     L[n], L[n + "_dtype"] = tensor(f"blk.{i}.{n}.weight")
                 layers.append(L)
         ctx.sync()
-        return cls(ctx, cfg, enc, layers)
+        return cls(ctx, cfg, enc, layers, tiled)
 
     # accessors of src/dflash.rs:121-155
     def layer_count(self):

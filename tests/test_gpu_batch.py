@@ -180,3 +180,77 @@ def test_silu_gate_up_launch_shapes(ctx, ch, rt):
     finally:
         lh.check(lh.lib().lg_set_batch_shape(0, 0))
     gate_up_parity(h, x, raw_g, raw_u, lh.Q4_K, k, n)
+
+
+def tile_q4k(raw, k, n):
+    """The LG_Q4_K_T16 layout restated in numpy: tile (t, b) = 16 row headers, then
+    quant bytes [group g][piece p][row r]; rows past n are zero blocks."""
+    nb, nt = k // 256, -(-n // 16)
+    blocks = np.zeros((nt * 16, nb, 144), np.uint8)
+    blocks[:n] = np.frombuffer(np.ascontiguousarray(raw).tobytes(), np.uint8).reshape(n, nb, 144)
+    blocks = blocks.reshape(nt, 16, nb, 144).transpose(0, 2, 1, 3)  # [t][b][r][144]
+    hdr = blocks[..., :16].reshape(nt, nb, 256)
+    q = blocks[..., 16:].reshape(nt, nb, 16, 4, 4, 8).transpose(0, 1, 3, 4, 2, 5).reshape(nt, nb, 2048)
+    return np.concatenate([hdr, q], axis=2).ravel()
+
+
+@pytest.mark.parametrize("k,n", [(4096, 1536), (2816, 700), (256, 5), (1024, 33)])
+def test_repack_tiled_layout(ctx, k, n):
+    print(f"repack Q4_K k={k} n={n}", flush=True)
+    raw = synth.q4k_weight(900 + n, k, n)
+    wb = lh.upload_bytes(ctx, raw)
+    tb = lh.repack_tiled(ctx, wb, lh.Q4_K, k, n)
+    assert tb.size == lh.lib().lg_tiled_bytes(lh.Q4_K, k, n) == -(-n // 16) * (k // 256) * 2304
+    assert np.array_equal(tb.download(), tile_q4k(raw, k, n))
+
+
+@pytest.mark.parametrize("k,n,m,x_dtype", [
+    (4096, 1536, 16, lh.F32), (4096, 1536, 16, lh.BF16), (2816, 700, 29, lh.F32), (1024, 33, 1, lh.F32),
+    (4096, 14336, 16, lh.F32), (256, 5, 40, lh.F32),
+])
+def test_tiled_products_equal_raw(ctx, k, n, m, x_dtype):
+    # the same kernels over tiles: results equal the raw layout's bit for bit
+    print(f"tiled product k={k} n={n} m={m} x={x_dtype}", flush=True)
+    raw = synth.q4k_weight(950 + n, k, n)
+    x32 = synth.normal(960 + m, m * k).reshape(m, k)
+    xin = bf16_bits(x32) if x_dtype == lh.BF16 else x32
+    xref = (xin.astype(np.uint32) << 16).view(np.float32) if x_dtype == lh.BF16 else x32
+    wb = lh.upload_bytes(ctx, raw)
+    tb = lh.repack_tiled(ctx, wb, lh.Q4_K, k, n)
+    xb = lh.upload_bytes(ctx, np.ascontiguousarray(xin).view(np.uint8).ravel())
+    c_raw, c_t = lh.GpuBuffer(ctx, 4 * m * n), lh.GpuBuffer(ctx, 4 * m * n)
+    lh.dispatch_proj_quant_batch(ctx, xb, x_dtype, wb, c_raw, k, n, m, lh.Q4_K)
+    lh.dispatch_proj_quant_batch(ctx, xb, x_dtype, tb, c_t, k, n, m, lh.Q4_K_T16)
+    ct = c_t.read_f32(m * n)
+    assert np.array_equal(ct, c_raw.read_f32(m * n))
+    y64, a = orc.proj_quant_f64(xref, raw, lh.Q4_K, k, n)
+    parity(ct.reshape(m, n), y64, a, TOL)
+
+
+@pytest.mark.parametrize("ch,rt", [(1, 1), (2, 4), (4, 2)])
+def test_tiled_launch_shapes_and_pair(ctx, ch, rt):
+    k, n, m = 2816, 700, 29
+    print(f"tiled shapes ch={ch} rt={rt}", flush=True)
+    rg, ru = synth.q4k_weight(970, k, n), synth.q4k_weight(971, k, n)
+    x = synth.normal(972, m * k).reshape(m, k)
+    gb, ub = lh.upload_bytes(ctx, rg), lh.upload_bytes(ctx, ru)
+    tg, tu = lh.repack_tiled(ctx, gb, lh.Q4_K, k, n), lh.repack_tiled(ctx, ub, lh.Q4_K, k, n)
+    xb = lh.upload_f32(ctx, x.ravel())
+    h1, h2, sc = (lh.GpuBuffer(ctx, 4 * m * n) for _ in range(3))
+    lh.check(lh.lib().lg_set_batch_shape(ch, rt))
+    try:
+        lh.dispatch_silu_gate_up_batch(ctx, xb, gb, ub, h1, sc, k, n, m, lh.Q4_K)
+        lh.dispatch_silu_gate_up_batch(ctx, xb, tg, tu, h2, sc, k, n, m, lh.Q4_K_T16)
+    finally:
+        lh.check(lh.lib().lg_set_batch_shape(0, 0))
+    h = h2.read_f32(m * n)
+    assert np.array_equal(h, h1.read_f32(m * n))
+    gate_up_parity(h.reshape(m, n), x, rg, ru, lh.Q4_K, k, n)
+
+
+def test_tiled_rejects_bad_input(ctx):
+    raw = synth.q4k_weight(980, 512, 16)
+    wb = lh.upload_bytes(ctx, raw)
+    with pytest.raises(lh.LagunaError):
+        lh.check(lh.lib().lg_repack_tiled(wb.ptr, lh.Q8_0, 512, 16, wb.ptr, ctx.stream))
+    assert lh.lib().lg_tiled_bytes(lh.Q4_K, 500, 16) == 0

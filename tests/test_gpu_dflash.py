@@ -217,6 +217,22 @@ def draft_full():
     return cfg, W, layers, feat, tok, kc, vc
 
 
+@pytest.mark.parametrize("m,ctx_len", [(16, 64), (1, 0), (32, 70)])
+def test_forward_tiled_equals_raw(ctx, m, ctx_len):
+    # Q4_K projections repacked into 16-row tiles (the default) against the raw
+    # GGUF blocks: the same forward bit for bit
+    print(f"forward tiled vs raw m={m} ctx={ctx_len}", flush=True)
+    W, layers = synth.dflash_model(0x5EED0260 + m, SMALL, SMALL.n_layers, norm_sigma=0.1)
+    feat, tok, kc, vc = synth.dflash_inputs(0x5EED0261 + m, SMALL, SMALL.n_layers, m, ctx_len)
+    ys = []
+    for tiled in (False, True):
+        model = lh.DFlashModel(ctx, SMALL, W, layers, tiled=tiled)
+        model.set_context(kc, vc)
+        ys.append(model.forward_block(feat, tok))
+        model.free()
+    np.testing.assert_array_equal(ys[0], ys[1])
+
+
 def test_forward_block_draft_full_size(ctx, draft_full):
     """6 layers, hidden 4096, 32/8 heads of 128, FFN 14336, Q4_K (o_proj Q8_0),
     16 tokens over a 2048-position context."""
