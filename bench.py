@@ -110,12 +110,14 @@ class MatvecM1(Workload):
 
 
 class BatchM16(Workload):
-    def __init__(self, dtype, k, n, x_dtype, seed, m=16):
+    def __init__(self, dtype, k, n, x_dtype, seed, m=16, tiled=False):
         self.dtype, self.k, self.n, self.x_dtype, self.seed, self.m = dtype, k, n, x_dtype, seed, m
+        self.tiled = tiled
         xb = 2 if x_dtype == lh.BF16 else 4
         self.bytes_per_call = synth.weight_bytes(dtype, k, n) + m * k * xb + 4 * m * n
         tag = {lh.Q4_K: "Q4_K", lh.Q8_0: "Q8_0"}[dtype]
-        self.name = f"{tag} block-verify {k}->{n} M={m} x={'bf16' if x_dtype == lh.BF16 else 'f32'}"
+        self.name = (f"{tag} block-verify {k}->{n} M={m} x={'bf16' if x_dtype == lh.BF16 else 'f32'}"
+                     + (" (16-row tiles)" if tiled else ""))
 
     def setup(self, ctx):
         k, n, m = self.k, self.n, self.m
@@ -125,6 +127,11 @@ class BatchM16(Workload):
         for _ in range(copies):
             b = lh.GpuBuffer(ctx, raw.nbytes)
             b.upload(raw)
+            if self.tiled:  # the same bytes, permuted into 16-row tiles
+                t = lh.repack_tiled(ctx, b, self.dtype, k, self.n)
+                ctx.sync()
+                b.free()
+                b = t
             self.pool.append(b)
         self.pool_bytes = copies * raw.nbytes
         x = synth.normal(self.seed + 0x100, m * k)
@@ -136,7 +143,8 @@ class BatchM16(Workload):
 
     def step(self, ctx, i):
         w = self.pool[i % len(self.pool)]
-        lh.dispatch_proj_quant_batch(ctx, self.x, self.x_dtype, w, self.c, self.k, self.n, self.m, self.dtype)
+        lh.dispatch_proj_quant_batch(ctx, self.x, self.x_dtype, w, self.c, self.k, self.n, self.m,
+                                     lh.TILED[self.dtype] if self.tiled else self.dtype)
 
 
 class VerifyBlock(BatchM16):
@@ -209,7 +217,9 @@ WORKLOADS = {
     "q4k_down_silu": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, fused=True),
     "q4k_m16_bf16": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008),
     "q4k_m16_f32": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008),
+    "q4k_m16_f32_tiled": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008, tiled=True),
     "q8_0_m16_f32": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009),
+    "q8_0_m16_f32_tiled": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009, tiled=True),
     # vocab-sized output projection (the LM head, src/target.rs:580-605): M=1 for one
     # token, M=16 to verify a 16-token draft block
     "q4k_lm_head_m1": lambda: MatvecM1(lh.Q4_K, 4096, 151936, 0x5EED000B),
@@ -347,8 +357,8 @@ def main():
     head = time_workload(ctx, ev, wl, args.steps, args.warmup)
     extra = {}
     if not args.no_extra:
-        for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q8_0_m16_f32", "q4k_lm_head_m1",
-                     "q4k_lm_head_m16", "lm_head_verify_m16"]:
+        for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled", "q8_0_m16_f32",
+                     "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16"]:
             if name != args.workload:
                 extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(50, args.steps // 4), 20)
         for name in ["dflash_block", "dflash_block_eager"]:

@@ -44,8 +44,9 @@ typedef enum {
     LG_Q8_0 = 8,
     LG_Q4_K = 12,
     LG_BF16 = 30,
-    /* Not a GGUF type: Q4_K blocks repacked by lg_repack_tiled into 16-row tiles
-     * for the small-M products (block verify, the draft forward). */
+    /* Not GGUF types: Q8_0 / Q4_K blocks repacked by lg_repack_tiled into 16-row
+     * tiles for the small-M products (block verify, the draft forward). */
+    LG_Q8_0_T16 = 1008,
     LG_Q4_K_T16 = 1012
 } lg_dtype;
 
@@ -152,25 +153,29 @@ int lg_dispatch_silu_mul_proj_quant(const float *gate, const float *up, const vo
 
 /* Block-verify product: c[r][i] = sum_j x[r][j] * W[i,j] for r < m, i < n.
  * x is row-major [m][k] of x_dtype LG_F32 or LG_BF16 (raw bf16 bits); c is
- * f32 [m][n]; W is Q4_K or Q8_0 raw blocks, Q4_K repacked (LG_Q4_K_T16), or f32.  1 <= m <= 64; m = 1 is the
+ * f32 [m][n]; W is Q4_K or Q8_0 raw blocks, repacked (LG_Q4_K_T16, LG_Q8_0_T16), or f32.  1 <= m <= 64; m = 1 is the
  * same product as lg_dispatch_proj_quant. */
 int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, float *c,
                                  uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                  void *stream);
 
-/* Q4_K weights repacked for the small-M products (no counterpart in the
+/* Q4_K and Q8_0 weights repacked for the small-M products (no counterpart in the
  * reference, which reads GGUF blocks in place; for callers that load a model once
- * and run many block products).  Tile (t, b) -- rows 16t..16t+15, super-block b
- * -- is 2304 contiguous bytes: the 16 rows' 16-byte block headers (d, dmin,
- * scales) in row order, then their quant bytes as [32-byte group g][8-byte piece
- * p][row r] (row r's bytes 32g+8p .. 32g+8p+7 at 256 + 512g + 128p + 8r).  Tiles
- * are stored row tile by row tile, super-blocks in order; rows past n, up to a
- * multiple of 16, are zero blocks.  The repack is a byte permutation, and the
- * products over LG_Q4_K_T16 weights (lg_dispatch_proj_quant_batch,
- * lg_dispatch_silu_gate_up_batch, the draft forward) equal those over the raw
- * blocks bit for bit; each workgroup then reads its weights as whole 2304-byte
- * tiles instead of 288-byte pieces of 2304-byte-apart rows.  dtype LG_Q4_K, k a
- * multiple of 256. */
+ * and run many block products).  Tiles hold 16 rows x 256 elements and are stored
+ * row tile by row tile, k in order; rows past n, up to a multiple of 16, are zero
+ * blocks.
+ *   LG_Q4_K_T16 tile (2304 bytes): the 16 rows' 16-byte block headers (d, dmin,
+ *     scales) in row order, then the quant bytes as [32-byte group g][8-byte
+ *     piece p][row r] (row r's bytes 32g+8p .. 32g+8p+7 at 256 + 512g + 128p + 8r).
+ *   LG_Q8_0_T16 tile (4352 bytes, blocks 8c..8c+7): the 16 rows' 8 f16 scales
+ *     (row r, block j at 16r + 2j), then the quants as [block j][8-byte piece p]
+ *     [row r] (row r's quants 8p .. 8p+7 of block j at 256 + 512j + 128p + 8r).
+ * The repack is a byte permutation, and the products over tiled weights
+ * (lg_dispatch_proj_quant_batch, lg_dispatch_silu_gate_up_batch, the draft
+ * forward) equal those over the raw blocks bit for bit; a workgroup then reads
+ * whole tiles instead of short pieces of rows that lie a row apart.  dtype
+ * LG_Q4_K or LG_Q8_0 (the raw type), k a multiple of 256; lg_tiled_bytes is 0
+ * for anything else. */
 uint64_t lg_tiled_bytes(int dtype, uint32_t k, uint32_t n);
 int lg_repack_tiled(const void *w, int dtype, uint32_t k, uint32_t n, void *out, void *stream);
 

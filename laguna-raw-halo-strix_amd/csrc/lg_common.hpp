@@ -91,10 +91,15 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;
 constexpr uint32_t QK8_0 = 32, Q80_BYTES = 34;
 
-constexpr uint32_t Q4K_TILE = 16 * Q4K_BYTES;  // LG_Q4_K_T16: 16 rows x one super-block
+constexpr uint32_t Q4K_TILE = 16 * Q4K_BYTES;      // LG_Q4_K_T16: 16 rows x one super-block
+constexpr uint32_t Q80_TILE = 16 * 8 * Q80_BYTES;  // LG_Q8_0_T16: 16 rows x 8 blocks
 
-// Bytes of a k x n LG_Q4_K_T16 tensor (rows padded to a multiple of 16).
-inline uint64_t tiled_bytes(uint32_t k, uint32_t n) { return (uint64_t)(n + 15) / 16 * (k / QK_K) * Q4K_TILE; }
+// Bytes of a k x n tensor repacked into 16-row tiles (rows padded to a multiple of
+// 16; dtype the raw type or its tiled id).
+inline uint64_t tiled_bytes(int dtype, uint32_t k, uint32_t n) {
+    const bool q4 = dtype == LG_Q4_K || dtype == LG_Q4_K_T16;
+    return (uint64_t)(n + 15) / 16 * (k / 256) * (q4 ? Q4K_TILE : Q80_TILE);
+}
 
 inline uint64_t tensor_bytes(int dtype, uint64_t elems) {
     switch (dtype) {

@@ -470,18 +470,40 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
     Frags<TT, PARTS, CH, FUSE> fr;
     fr.load(x, up, m, k, sb0);
     uint32_t dq[RT][SB], v0[RT][SB], v1[RT][SB];
+    if (jobs.tiled) {  // 4352-byte tiles: one 16-byte load for a row's 8 scales, 512 contiguous bytes per quant load
+        const uint32_t ntiles = (n + 15) / 16, nc = k / 256;
 #pragma unroll
-    for (int i = 0; i < RT; i++) {
-        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
-        const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
+        for (int i = 0; i < RT; i++) {
+            const uint32_t t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
 #pragma unroll
-        for (int j = 0; j < SB; j++) {
-            const uint16_t *blk =
-                reinterpret_cast<const uint16_t *>(wr + (uint64_t)(sb0 + j < nsb ? sb0 + j : nsb - 1) * Q80_BYTES);
-            const uint16_t *q = blk + 1 + 4 * kg;
-            dq[i][j] = blk[0];
-            v0[i][j] = q[0] | ((uint32_t)q[1] << 16);
-            v1[i][j] = q[2] | ((uint32_t)q[3] << 16);
+            for (int cc = 0; cc < CH; cc++) {
+                const uint32_t c = blockIdx.y * CH + cc;
+                const uint8_t *tb = w + ((uint64_t)t * nc + (c < nc ? c : nc - 1)) * Q80_TILE;
+                const uint4 sc = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
+                const uint32_t sw[4] = {sc.x, sc.y, sc.z, sc.w};
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    const uint2 q = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * jj + 8 * l);
+                    dq[i][8 * cc + jj] = (sw[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
+                    v0[i][8 * cc + jj] = q.x;
+                    v1[i][8 * cc + jj] = q.y;
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+            const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
+#pragma unroll
+            for (int j = 0; j < SB; j++) {
+                const uint16_t *blk =
+                    reinterpret_cast<const uint16_t *>(wr + (uint64_t)(sb0 + j < nsb ? sb0 + j : nsb - 1) * Q80_BYTES);
+                const uint16_t *q = blk + 1 + 4 * kg;
+                dq[i][j] = blk[0];
+                v0[i][j] = q[0] | ((uint32_t)q[1] << 16);
+                v1[i][j] = q[2] | ((uint32_t)q[3] << 16);
+            }
         }
     }
     asm volatile("" ::: "memory");  // keep the weight loads issued ahead of the fragment build
@@ -715,6 +737,7 @@ namespace lg {
 
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype) {
     if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
+    if (w_dtype == LG_Q8_0_T16) w_dtype = LG_Q8_0;
     if (w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) return 0;
     uint64_t ntot = 0;
     for (uint32_t j = 0; j < jobs; j++) ntot += n[j];
@@ -742,12 +765,13 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     LG_REQUIRE(x, "%s: null activations", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
     LG_REQUIRE(!up || x_dtype == LG_F32, "%s: the fused SiLU(gate)*up takes f32 activations", name);
-    LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32 || w_dtype == LG_Q4_K_T16,
+    LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32 || w_dtype == LG_Q4_K_T16 ||
+                   w_dtype == LG_Q8_0_T16,
                "%s: weight dtype %d", name, w_dtype);
-    const bool tiled = w_dtype == LG_Q4_K_T16;
+    const bool tiled = w_dtype == LG_Q4_K_T16 || w_dtype == LG_Q8_0_T16;
     LG_REQUIRE(!tiled || (k % QK_K == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                           (!up || (reinterpret_cast<uintptr_t>(up) & 15u) == 0)),
-               "%s: LG_Q4_K_T16 weights take k a multiple of 256 (k=%u) and 16-byte aligned activations", name, k);
+               "%s: tiled weights take k a multiple of 256 (k=%u) and 16-byte aligned activations", name, k);
     const uint64_t xbytes = (uint64_t)m * k * (x_dtype == LG_F32 ? 4 : 2);
     if (k) {
         LG_EXTENT(x, xbytes, name);
@@ -763,11 +787,11 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         LG_REQUIRE(b.w && b.c, "%s: null pointer in job %u", name, j);
         LG_EXTENT(b.c, (uint64_t)m * b.n * 4, name);
         if (b.res) LG_EXTENT(b.res, (uint64_t)m * b.n * 4, name);
-        if (k) LG_EXTENT(b.w, tiled ? tiled_bytes(k, b.n) : tensor_bytes(w_dtype, (uint64_t)b.n * k), name);
-        LG_REQUIRE(!tiled || (reinterpret_cast<uintptr_t>(b.w) & 15u) == 0, "%s: unaligned LG_Q4_K_T16 weights", name);
+        if (k) LG_EXTENT(b.w, tiled ? tiled_bytes(w_dtype, k, b.n) : tensor_bytes(w_dtype, (uint64_t)b.n * k), name);
+        LG_REQUIRE(!tiled || (reinterpret_cast<uintptr_t>(b.w) & 15u) == 0, "%s: unaligned tiled weights", name);
     }
     if (ntot == 0) return LG_OK;
-    if (tiled) w_dtype = LG_Q4_K;  // the Q4_K kernels, reading tiles
+    if (tiled) w_dtype = w_dtype == LG_Q4_K_T16 ? LG_Q4_K : LG_Q8_0;  // the same kernels, reading tiles
     const uint32_t blk = w_dtype == LG_Q4_K ? QK_K : QK8_0;
     bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                 (!up || (reinterpret_cast<uintptr_t>(up) & 15u) == 0);
@@ -871,27 +895,60 @@ __global__ __launch_bounds__(256) void k_repack_q4k_t16(const uint8_t *__restric
     }
 }
 
+// LG_Q8_0_T16 repack: workgroup (c, t) writes tile (t, c) -- rows 16t..16t+15,
+// blocks 8c..8c+7.  Thread p moves quant pieces p and p + 256 (piece
+// 64j + 16q + r: row r's bytes 2 + 8q .. 9 + 8q of block j, read as 16-bit
+// words since blocks are 2-byte aligned) and, for p < 128, the scale of row p/8,
+// block p%8.  Rows past n become zero blocks.
+__global__ __launch_bounds__(256) void k_repack_q80_t16(const uint8_t *__restrict__ w, uint8_t *__restrict__ out,
+                                                         uint32_t nc, uint32_t n) {
+    const uint32_t c = blockIdx.x, t = blockIdx.y;
+    uint8_t *tile = out + ((uint64_t)t * nc + c) * Q80_TILE;
+    const uint64_t rowb = (uint64_t)nc * 8 * Q80_BYTES;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; h++) {
+        const uint32_t p = threadIdx.x + 256 * h, j = p >> 6, q = (p >> 4) & 3u, r = p & 15u, row = 16 * t + r;
+        const bool live = row < n;
+        const uint16_t *src = reinterpret_cast<const uint16_t *>(w + (uint64_t)(live ? row : n - 1) * rowb +
+                                                                 (uint64_t)(8 * c + j) * Q80_BYTES + 2 + 8 * q);
+        const uint2 v = make_uint2(src[0] | ((uint32_t)src[1] << 16), src[2] | ((uint32_t)src[3] << 16));
+        *reinterpret_cast<uint2 *>(tile + 256 + 8 * p) = live ? v : make_uint2(0u, 0u);
+    }
+    if (threadIdx.x < 128) {
+        const uint32_t r = threadIdx.x >> 3, j = threadIdx.x & 7u, row = 16 * t + r;
+        const bool live = row < n;
+        const uint16_t d = *reinterpret_cast<const uint16_t *>(w + (uint64_t)(live ? row : n - 1) * rowb +
+                                                               (uint64_t)(8 * c + j) * Q80_BYTES);
+        *reinterpret_cast<uint16_t *>(tile + 2 * threadIdx.x) = live ? d : (uint16_t)0;
+    }
+}
+
 }  // namespace
 
 extern "C" uint64_t lg_tiled_bytes(int dtype, uint32_t k, uint32_t n) {
-    return dtype == LG_Q4_K && k % QK_K == 0 ? tiled_bytes(k, n) : 0;
+    return (dtype == LG_Q4_K || dtype == LG_Q8_0) && k % QK_K == 0 ? tiled_bytes(dtype, k, n) : 0;
 }
 
 extern "C" int lg_repack_tiled(const void *w, int dtype, uint32_t k, uint32_t n, void *out, void *stream) {
     clear_error();
     const char *name = "lg_repack_tiled";
-    LG_REQUIRE(dtype == LG_Q4_K, "%s: dtype %d (only Q4_K is tiled)", name, dtype);
+    LG_REQUIRE(dtype == LG_Q4_K || dtype == LG_Q8_0, "%s: dtype %d (Q4_K and Q8_0 are tiled)", name, dtype);
     LG_REQUIRE(k % QK_K == 0, "%s: k=%u is not a multiple of 256", name, k);
     if (k == 0 || n == 0) return LG_OK;
     LG_REQUIRE(w && out, "%s: null pointer", name);
-    LG_REQUIRE(((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0,
-               "%s: pointers must be 16-byte aligned", name);
+    LG_REQUIRE((reinterpret_cast<uintptr_t>(out) & 15u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w) & (dtype == LG_Q4_K ? 15u : 1u)) == 0,
+               "%s: misaligned pointer (out 16 bytes, w 16 for Q4_K and 2 for Q8_0)", name);
     LG_REQUIRE((n + 15) / 16 <= 65535u, "%s: n=%u exceeds %u rows", name, n, 65535u * 16);
-    LG_EXTENT(w, tensor_bytes(LG_Q4_K, (uint64_t)k * n), name);
-    LG_EXTENT(out, tiled_bytes(k, n), name);
+    LG_EXTENT(w, tensor_bytes(dtype, (uint64_t)k * n), name);
+    LG_EXTENT(out, tiled_bytes(dtype, k, n), name);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_repack_q4k_t16, dim3(k / QK_K, (n + 15) / 16), dim3(256), 0, s,
-                       static_cast<const uint8_t *>(w), static_cast<uint8_t *>(out), k / QK_K, n);
+    if (dtype == LG_Q4_K)
+        hipLaunchKernelGGL(k_repack_q4k_t16, dim3(k / QK_K, (n + 15) / 16), dim3(256), 0, s,
+                           static_cast<const uint8_t *>(w), static_cast<uint8_t *>(out), k / QK_K, n);
+    else
+        hipLaunchKernelGGL(k_repack_q80_t16, dim3(k / 256, (n + 15) / 16), dim3(256), 0, s,
+                           static_cast<const uint8_t *>(w), static_cast<uint8_t *>(out), k / 256, n);
     return after_launch(name, s);
 }
 

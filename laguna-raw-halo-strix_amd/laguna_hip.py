@@ -27,7 +27,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblaguna_hip.so")
 
 F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
-Q4_K_T16 = 1012  # Q4_K repacked into 16-row tiles by repack_tiled (not a GGUF type)
+Q8_0_T16, Q4_K_T16 = 1008, 1012  # Q8_0 / Q4_K repacked into 16-row tiles by repack_tiled (not GGUF types)
+TILED = {Q4_K: Q4_K_T16, Q8_0: Q8_0_T16}
 OK, EINVAL, EHIP, ENOMEM, EUNSUPPORTED, EIO, ENODEV, ENOTFOUND = range(8)
 
 # C-ABI symbols declared in include/laguna_hip.h, with ctypes signatures.
@@ -268,8 +269,8 @@ def dispatch_silu_gate_up_batch(ctx, x, w_gate, w_up, h, u_scratch, k, n, m, w_d
 
 
 def repack_tiled(ctx, w, dtype, k, n):
-    """The k x n Q4_K tensor in `w` (raw GGUF blocks on the device) repacked into a
-    new buffer of 16-row tiles (Q4_K_T16), for the small-M products."""
+    """The k x n Q4_K or Q8_0 tensor in `w` (raw GGUF blocks on the device) repacked
+    into a new buffer of 16-row tiles (type TILED[dtype]), for the small-M products."""
     out = GpuBuffer(ctx, lib().lg_tiled_bytes(dtype, k, n))
     check(lib().lg_repack_tiled(_ptr(w), dtype, k, n, _ptr(out), ctx.stream))
     return out
@@ -446,8 +447,8 @@ class DFlashModel:
     DFLASH_NORMS and, for each projection p of DFLASH_PROJ, the raw GGUF bytes
     p and their type p + "_dtype" (tensor names of src/dflash.rs:68-79).  The
     bytes are uploaded unchanged (Model::upload_tensor_quantized); with `tiled`
-    (the default) Q4_K projections are then repacked on the device into 16-row
-    tiles, which the forward's small-M products read as contiguous 2304-byte tiles
+    (the default) Q4_K and Q8_0 projections are then repacked on the device into
+    16-row tiles, which the forward's small-M products read as contiguous 2304-byte tiles
     (the results are the same bit for bit)."""
 
     def __init__(self, ctx, cfg, enc, layers, tiled=True):
@@ -461,14 +462,14 @@ class DFlashModel:
 
         def proj_w(a, dtype, k, n):
             b = up(a)
-            if not tiled or int(dtype) != Q4_K or k % 256:
+            if not tiled or int(dtype) not in TILED or k % 256:
                 return b, int(dtype)
-            t = repack_tiled(ctx, b, Q4_K, k, n)
+            t = repack_tiled(ctx, b, int(dtype), k, n)
             self._bufs.append(t)
             self._bufs.remove(b)
             ctx.sync()  # the repack has read the raw blocks
             b.free()
-            return t, Q4_K_T16
+            return t, TILED[int(dtype)]
 
         fc_buf, fc_type = proj_w(enc["fc"], enc["fc_dtype"], cfg.n_aux * E, E)
         self._enc = {"enc_aux_norm": up(enc["enc_aux_norm"], np.float32), "fc": fc_buf,

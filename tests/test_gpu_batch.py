@@ -194,6 +194,47 @@ def tile_q4k(raw, k, n):
     return np.concatenate([hdr, q], axis=2).ravel()
 
 
+def tile_q80(raw, k, n):
+    """The LG_Q8_0_T16 layout restated in numpy: tile (t, c) = the 16 rows' 8 f16
+    scales (row-major), then quants [block j][piece p][row r]."""
+    nc, nt = k // 256, -(-n // 16)
+    blocks = np.zeros((nt * 16, nc, 8, 34), np.uint8)
+    blocks[:n] = np.frombuffer(np.ascontiguousarray(raw).tobytes(), np.uint8).reshape(n, nc, 8, 34)
+    blocks = blocks.reshape(nt, 16, nc, 8, 34).transpose(0, 2, 1, 3, 4)  # [t][c][r][j][34]
+    sc = blocks[..., :2].reshape(nt, nc, 256)
+    q = blocks[..., 2:].reshape(nt, nc, 16, 8, 4, 8).transpose(0, 1, 3, 4, 2, 5).reshape(nt, nc, 4096)
+    return np.concatenate([sc, q], axis=2).ravel()
+
+
+@pytest.mark.parametrize("k,n", [(4096, 512), (2048, 37), (256, 3)])
+def test_repack_tiled_q80_layout(ctx, k, n):
+    print(f"repack Q8_0 k={k} n={n}", flush=True)
+    raw = synth.q8_0_weight(930 + n, k, n)
+    tb = lh.repack_tiled(ctx, lh.upload_bytes(ctx, raw), lh.Q8_0, k, n)
+    assert tb.size == lh.lib().lg_tiled_bytes(lh.Q8_0, k, n) == -(-n // 16) * (k // 256) * 4352
+    assert np.array_equal(tb.download(), tile_q80(raw, k, n))
+
+
+@pytest.mark.parametrize("k,n,m,ch", [(4096, 4096, 16, 0), (2048, 37, 29, 0), (4096, 700, 5, 2), (1024, 300, 40, 1)])
+def test_tiled_q80_products_equal_raw(ctx, k, n, m, ch):
+    print(f"tiled Q8_0 product k={k} n={n} m={m} ch={ch}", flush=True)
+    raw = synth.q8_0_weight(940 + n, k, n)
+    x = synth.normal(941 + m, m * k).reshape(m, k)
+    wb = lh.upload_bytes(ctx, raw)
+    tb = lh.repack_tiled(ctx, wb, lh.Q8_0, k, n)
+    lh.check(lh.lib().lg_set_batch_shape(ch, 0))
+    try:
+        c_raw = run_batch(ctx, x, lh.F32, raw, lh.Q8_0, k, n, m)
+        xb, c_t = lh.upload_f32(ctx, x.ravel()), lh.GpuBuffer(ctx, 4 * m * n)
+        lh.dispatch_proj_quant_batch(ctx, xb, lh.F32, tb, c_t, k, n, m, lh.Q8_0_T16)
+    finally:
+        lh.check(lh.lib().lg_set_batch_shape(0, 0))
+    ct = c_t.read_f32(m * n).reshape(m, n)
+    assert np.array_equal(ct, c_raw)
+    y64, a = orc.proj_quant_f64(x, raw, lh.Q8_0, k, n)
+    parity(ct, y64, a, TOL)
+
+
 @pytest.mark.parametrize("k,n", [(4096, 1536), (2816, 700), (256, 5), (1024, 33)])
 def test_repack_tiled_layout(ctx, k, n):
     print(f"repack Q4_K k={k} n={n}", flush=True)
@@ -252,5 +293,8 @@ def test_tiled_rejects_bad_input(ctx):
     raw = synth.q4k_weight(980, 512, 16)
     wb = lh.upload_bytes(ctx, raw)
     with pytest.raises(lh.LagunaError):
-        lh.check(lh.lib().lg_repack_tiled(wb.ptr, lh.Q8_0, 512, 16, wb.ptr, ctx.stream))
+        lh.check(lh.lib().lg_repack_tiled(wb.ptr, lh.F32, 512, 16, wb.ptr, ctx.stream))
+    with pytest.raises(lh.LagunaError):  # k not a multiple of 256
+        lh.check(lh.lib().lg_repack_tiled(wb.ptr, lh.Q8_0, 96, 16, wb.ptr, ctx.stream))
     assert lh.lib().lg_tiled_bytes(lh.Q4_K, 500, 16) == 0
+    assert lh.lib().lg_tiled_bytes(lh.F32, 512, 16) == 0
