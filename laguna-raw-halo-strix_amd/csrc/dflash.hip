@@ -235,20 +235,30 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 
     // K and V of the chunk's 64 positions as bf16 parts.  A thread takes blocks of 4
     // positions x 4 dims (two rounds): K rows and the transposed V rows go to LDS 4
-    // values (8 bytes) at a time.  Every load of both rounds is issued first.
+    // values (8 bytes) at a time.  Every load of both rounds is issued first.  K
+    // blocks run along the dims (a wavefront writes two whole K rows); V blocks run
+    // along the positions, so that the 16 lanes writing one V^T row write 128
+    // contiguous bytes (along the dims, lanes 576 bytes apart share banks 8 ways).
     constexpr int KVR = (ACH / 4) * (AHD / 4) / 256;
     float4 kq[KVR][4], vq[KVR][4];
+    auto kblk = [&](uint32_t e, uint32_t &pq, uint32_t &d) { pq = e / (AHD / 4), d = 4 * (e % (AHD / 4)); };
+    auto vblk = [&](uint32_t e, uint32_t &pq, uint32_t &d) { pq = e % (ACH / 4), d = 4 * (e / (ACH / 4)); };
 #pragma unroll
     for (int rd = 0; rd < KVR; rd++) {
         const uint32_t e = tid + 256u * rd;
-        const uint32_t pq = e / (AHD / 4), d = 4 * (e % (AHD / 4));
+        uint32_t pk, dk, pv, dv;
+        kblk(e, pk, dk);
+        vblk(e, pv, dv);
 #pragma unroll
         for (int i = 0; i < 4; i++) {  // branch-free: positions past S read position S-1 (zeroed below)
-            const uint32_t p = c * ACH + 4 * pq + i, pc = p < S ? p : S - 1;
+            const uint32_t p = c * ACH + 4 * pk + i, pc = p < S ? p : S - 1;
             const bool s0 = pc < n0;
-            const uint64_t off = (uint64_t)(s0 ? pc : pc - n0) * kvld + h * AHD + d;
-            kq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + off);
-            vq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? v0 : v1) + off);
+            kq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + (uint64_t)(s0 ? pc : pc - n0) * kvld +
+                                                          h * AHD + dk);
+            const uint32_t pw = c * ACH + 4 * pv + i, pwc = pw < S ? pw : S - 1;
+            const bool sv = pwc < n0;
+            vq[rd][i] = *reinterpret_cast<const float4 *>((sv ? v0 : v1) + (uint64_t)(sv ? pwc : pwc - n0) * kvld +
+                                                          h * AHD + dv);
         }
     }
     // this lane's query row (A operand fragments for the 4 k-steps): loads issued
@@ -268,31 +278,35 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 #pragma unroll
     for (int rd = 0; rd < KVR; rd++) {
         const uint32_t e = tid + 256u * rd;
-        const uint32_t pq = e / (AHD / 4), d = 4 * (e % (AHD / 4));
+        uint32_t pk, dk, pv, dv;
+        kblk(e, pk, dk);
+        vblk(e, pv, dv);
         float fk[4][4], fv[4][4];  // [position][dim]
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const bool ok = c * ACH + 4 * pq + i < S;
+            const bool okk = c * ACH + 4 * pk + i < S, okv = c * ACH + 4 * pv + i < S;
             const float4 kv = kq[rd][i], vv = vq[rd][i];
-            fk[i][0] = ok ? kv.x : 0.f, fk[i][1] = ok ? kv.y : 0.f, fk[i][2] = ok ? kv.z : 0.f, fk[i][3] = ok ? kv.w : 0.f;
-            fv[i][0] = ok ? vv.x : 0.f, fv[i][1] = ok ? vv.y : 0.f, fv[i][2] = ok ? vv.z : 0.f, fv[i][3] = ok ? vv.w : 0.f;
+            fk[i][0] = okk ? kv.x : 0.f, fk[i][1] = okk ? kv.y : 0.f, fk[i][2] = okk ? kv.z : 0.f;
+            fk[i][3] = okk ? kv.w : 0.f;
+            fv[i][0] = okv ? vv.x : 0.f, fv[i][1] = okv ? vv.y : 0.f, fv[i][2] = okv ? vv.z : 0.f;
+            fv[i][3] = okv ? vv.w : 0.f;
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {  // K: position 4pq+i, dims d..d+3
+        for (int i = 0; i < 4; i++) {  // K: position 4pk+i, dims dk..dk+3
             uint32_t a[2], b[2], cc[2];
             split3x2(fk[i][0], fk[i][1], a[0], b[0], cc[0]);
             split3x2(fk[i][2], fk[i][3], a[1], b[1], cc[1]);
-            const uint32_t o = (4 * pq + i) * KSTR + d;
+            const uint32_t o = (4 * pk + i) * KSTR + dk;
             *reinterpret_cast<uint2 *>(L.k[0] + o) = make_uint2(a[0], a[1]);
             *reinterpret_cast<uint2 *>(L.k[1] + o) = make_uint2(b[0], b[1]);
             *reinterpret_cast<uint2 *>(L.k[2] + o) = make_uint2(cc[0], cc[1]);
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {  // V^T: dim d+j, positions 4pq..4pq+3
+        for (int j = 0; j < 4; j++) {  // V^T: dim dv+j, positions 4pv..4pv+3
             uint32_t a[2], b[2], cc[2];
             split3x2(fv[0][j], fv[1][j], a[0], b[0], cc[0]);
             split3x2(fv[2][j], fv[3][j], a[1], b[1], cc[1]);
-            const uint32_t o = (d + j) * VSTR + 4 * pq;
+            const uint32_t o = (dv + j) * VSTR + 4 * pv;
             *reinterpret_cast<uint2 *>(L.v[0] + o) = make_uint2(a[0], a[1]);
             *reinterpret_cast<uint2 *>(L.v[1] + o) = make_uint2(b[0], b[1]);
             *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
