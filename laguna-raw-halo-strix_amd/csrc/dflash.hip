@@ -418,16 +418,25 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 
 __device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g : logf(1.0f + expf(g)); }  // src/dflash.rs:957
 
+// The block's own positions (the `tail`, at most ATAIL, after the n0 context
+// positions that the chunk kernel covers) are attended here, in f32: wave w takes
+// tail positions 16w .. 16w+15 and forms a partial like a chunk's.
+constexpr uint32_t ATAIL = 64;
+
 // out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c.  One workgroup per
 // query: wave w takes the w-th quarter of the chunks (their partials loaded CB at a
-// time, all in flight together); the quarters meet in LDS, added in wave order.
-// With `gate` ([rows][n_q]), the result of head hq of row t is then multiplied by
-// softplus(gate[t][hq]) (the forward's attention gate, src/dflash.rs:956-959).
+// time, all in flight together), then its part of the tail; the quarters meet in
+// LDS, added in wave order.  With `gate` ([rows][n_q]), the result of head hq of
+// row t is then multiplied by softplus(gate[t][hq]) (the forward's attention gate,
+// src/dflash.rs:956-959).
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
                                                       const float *__restrict__ part_ml, float *__restrict__ out,
                                                       uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch,
-                                                      const float *__restrict__ gate) {
-    constexpr uint32_t CB = 8;
+                                                      const float *__restrict__ gate, const float *__restrict__ q,
+                                                      const float *__restrict__ k1, const float *__restrict__ v1,
+                                                      uint32_t T, uint32_t n0, uint32_t qpos0, int causal,
+                                                      float scale) {
+    constexpr uint32_t CB = 8, TW = ATAIL / 4;
     __shared__ float sm[4], sl[4], so[4][AHD];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t gq = blockIdx.x;  // over n_kv * AQ
@@ -436,7 +445,41 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup
     const uint64_t q0 = (uint64_t)h * nch * AQ + qi;  // partial index of chunk c: q0 + c * AQ
     const uint32_t per = (nch + 3) / 4, cb0 = wave * per, cb1 = cb0 + per < nch ? cb0 + per : nch;
-    float M = -INFINITY;
+    // this wave's tail partial (tm, tl, t0, t1): scores made uniform over the wave
+    float tm = -INFINITY, tl = 0.0f, t0 = 0.0f, t1 = 0.0f;
+    if (T > wave * TW) {
+        const uint32_t t = qi / G, hq = h * G + qi % G, qpos = qpos0 + t, kvld = n_kv * AHD;
+        const float *qp = q + (uint64_t)t * n_q * AHD + hq * AHD;
+        const float qa = qp[lane], qb = qp[64 + lane];
+        float ka[TW], kb[TW], va[TW], vb[TW];
+#pragma unroll
+        for (uint32_t j = 0; j < TW; j++) {  // branch-free: positions past T read position T-1 (masked below)
+            const uint32_t jj = wave * TW + j < T ? wave * TW + j : T - 1;
+            const uint64_t o = (uint64_t)jj * kvld + h * AHD;
+            ka[j] = k1[o + lane], kb[j] = k1[o + 64 + lane];
+            va[j] = v1[o + lane], vb[j] = v1[o + 64 + lane];
+        }
+        float sc[TW];
+#pragma unroll
+        for (uint32_t j = 0; j < TW; j++) {
+            const uint32_t jj = wave * TW + j;
+            const float d = wave_sum(__builtin_fmaf(qa, ka[j], qb * kb[j]));
+            const float sv = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(d))) * scale;
+            const bool ok = jj < T && (!causal || n0 + jj <= qpos);
+            sc[j] = ok ? sv : -INFINITY;
+            tm = fmaxf(tm, sc[j]);
+        }
+        if (tm != -INFINITY) {
+#pragma unroll
+            for (uint32_t j = 0; j < TW; j++) {  // tail order
+                const float w = expf(sc[j] - tm);
+                tl += w;
+                t0 = __builtin_fmaf(w, va[j], t0);
+                t1 = __builtin_fmaf(w, vb[j], t1);
+            }
+        }
+    }
+    float M = tm;
     for (uint32_t c0 = cb0; c0 < cb1; c0 += CB) {
         float mc[CB];
 #pragma unroll
@@ -466,6 +509,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
             o0 = __builtin_fmaf(wgt, a0[b], o0);
             o1 = __builtin_fmaf(wgt, a1[b], o1);
         }
+    }
+    if (tm != -INFINITY) {  // the tail after the chunks
+        const float wgt = expf(tm - M);
+        L = __builtin_fmaf(wgt, tl, L);
+        o0 = __builtin_fmaf(wgt, t0, o0);
+        o1 = __builtin_fmaf(wgt, t1, o1);
     }
     if (lane == 0) sl[wave] = L;
     so[wave][lane] = o0;
@@ -600,14 +649,19 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
     const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
     const uint32_t G = n_q / n_kv;
     if (part && hd == AHD && rows * G <= AQ) {
-        const uint32_t nch = (S + ACH - 1) / ACH;
+        // The chunks cover the context; a short run of positions after it (the
+        // block's own keys in k1) is attended by the combine, so that the chunk
+        // grid does not spill a few workgroups into a second round.
+        const uint32_t T = k1 && S > n0 && S - n0 <= ATAIL ? S - n0 : 0;
+        const uint32_t Sc = T ? n0 : S, nch = (Sc + ACH - 1) / ACH;
         float *part_ml = part + (size_t)n_kv * nch * AQ * AHD;
-        hipLaunchKernelGGL(k_attn_chunk, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S,
-                           rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
-        int st = after_launch("attn_chunk", s);
-        if (st != LG_OK) return st;
+        if (nch) {
+            hipLaunchKernelGGL(k_attn_chunk, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, Sc,
+                               rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
+            LG_TRY(after_launch("attn_chunk", s));
+        }
         hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, part, part_ml, out, rows, n_q,
-                           n_kv, nch, gate);
+                           n_kv, nch, gate, q, k1, v1, T, n0, qpos0, causal, scale);
         return after_launch("attn_combine", s);
     }
     hipLaunchKernelGGL(k_attn_simple, dim3((rows * n_q + 3) / 4), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S, rows,
