@@ -68,6 +68,26 @@ __device__ __forceinline__ void q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2
     }
 }
 
+// a[j] = 16 d sc_j for the 8 sub-blocks (the code term's scales).
+__device__ __forceinline__ void q4k_scales_a(uint32_t s0, uint32_t s2, float d16, float (&a)[8]) {
+    const uint32_t sl = s0 & 0x3F3F3F3Fu, sh = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const float scf[8] = {ubyte_f<0>(sl), ubyte_f<1>(sl), ubyte_f<2>(sl), ubyte_f<3>(sl),
+                          ubyte_f<0>(sh), ubyte_f<1>(sh), ubyte_f<2>(sh), ubyte_f<3>(sh)};
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = d16 * scf[j];
+}
+
+// The X coefficients -(16 d sc_j + dmin m_j) of sub-blocks j = g and g + 4 (g < 4, a
+// lane's k-group): the B operand of the f32 product that adds the min terms.
+__device__ __forceinline__ void q4k_min_coef(uint32_t s0, uint32_t s1, uint32_t s2, float d16, float dmin,
+                                             uint32_t g, float &c_lo, float &c_hi) {
+    const uint32_t b0 = s0 >> (8 * g), b1 = s1 >> (8 * g), b2 = s2 >> (8 * g);
+    const uint32_t sc_lo = b0 & 63u, m_lo = b1 & 63u;
+    const uint32_t sc_hi = (b2 & 15u) | (((b0 >> 6) & 3u) << 4), m_hi = ((b2 >> 4) & 15u) | (((b1 >> 6) & 3u) << 4);
+    c_lo = -__builtin_fmaf(dmin, (float)m_lo, d16 * (float)sc_lo);
+    c_hi = -__builtin_fmaf(dmin, (float)m_hi, d16 * (float)sc_hi);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     uint4 u = make_uint4(a, b, c, d);
     return __builtin_bit_cast(bf16x8, u);
@@ -412,11 +432,16 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
 #pragma unroll
     for (int cb = 0; cb < CH; cb++) {
         if (b0 + cb >= nb) continue;  // uniform: past the end of k
-        float sa[RT][8], scc[RT][8];
+        // code terms a_j D_j per sub-block on the VALU; the super-block's min terms
+        // -(a_j + dmin m_j) X_j as two f32 matrix products (k = the 8 sub-blocks)
+        // accumulated into acc: A = X[token][sub-block], B = coefficient[sub-block][row]
+        float sa[RT][8], cmin[RT][2];
 #pragma unroll
-        for (int i = 0; i < RT; i++)
-            q4k_scales(hd[i][cb].y, hd[i][cb].z, hd[i][cb].w, 16.0f * ref_half(hd[i][cb].x & 0xFFFFu),
-                       ref_half(hd[i][cb].x >> 16), sa[i], scc[i]);
+        for (int i = 0; i < RT; i++) {
+            const float d16 = 16.0f * ref_half(hd[i][cb].x & 0xFFFFu), dmin = ref_half(hd[i][cb].x >> 16);
+            q4k_scales_a(hd[i][cb].y, hd[i][cb].w, d16, sa[i]);
+            q4k_min_coef(hd[i][cb].y, hd[i][cb].z, hd[i][cb].w, d16, dmin, kg, cmin[i][0], cmin[i][1]);
+        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             bf16x8 blo[RT], bhi[RT];
@@ -426,29 +451,37 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
             for (int u = 0; u < 2; u++) {
                 const uint32_t j = 2 * g + u, jj = cb * 8 + j;
                 bf16x8 A[TT][PARTS];
-                float4 X[TT];
 #pragma unroll
-                for (int t = 0; t < TT; t++) {
+                for (int t = 0; t < TT; t++)
 #pragma unroll
                     for (int p = 0; p < PARTS; p++)
                         A[t][p] = __builtin_bit_cast(bf16x8, lf[((t * SB + jj) * PARTS + p) * 64 + l]);
-                    X[t] = *reinterpret_cast<const float4 *>(lx + (t * SB + jj) * 16 + 4 * kg);
-                }
 #pragma unroll
                 for (int i = 0; i < RT; i++) {
-                    const float a = sa[i][j], cc = scc[i][j];
+                    const float a = sa[i][j];
 #pragma unroll
                     for (int t = 0; t < TT; t++) {
                         f32x4 D = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int p = 0; p < PARTS; p++)
                             D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t][p], u ? bhi[i] : blo[i], D, 0, 0, 0);
-                        acc[i][t][0] = __builtin_fmaf(a, D[0], __builtin_fmaf(-cc, X[t].x, acc[i][t][0]));
-                        acc[i][t][1] = __builtin_fmaf(a, D[1], __builtin_fmaf(-cc, X[t].y, acc[i][t][1]));
-                        acc[i][t][2] = __builtin_fmaf(a, D[2], __builtin_fmaf(-cc, X[t].z, acc[i][t][2]));
-                        acc[i][t][3] = __builtin_fmaf(a, D[3], __builtin_fmaf(-cc, X[t].w, acc[i][t][3]));
+#pragma unroll
+                        for (int r = 0; r < 4; r++) acc[i][t][r] = __builtin_fmaf(a, D[r], acc[i][t][r]);
                     }
                 }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const float x_lo = lx[(t * SB + cb * 8 + kg) * 16 + (l & 15u)];
+            const float x_hi = lx[(t * SB + cb * 8 + kg + 4) * 16 + (l & 15u)];
+#pragma unroll
+            for (int i = 0; i < RT; i++) {
+                f32x4 C = {acc[i][t][0], acc[i][t][1], acc[i][t][2], acc[i][t][3]};
+                C = __builtin_amdgcn_mfma_f32_16x16x4f32(x_lo, cmin[i][0], C, 0, 0, 0);
+                C = __builtin_amdgcn_mfma_f32_16x16x4f32(x_hi, cmin[i][1], C, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[i][t][r] = C[r];
             }
         }
     }
