@@ -25,6 +25,10 @@
  *     extent the call reads or writes lies inside that allocation and returns
  *     LG_EINVAL otherwise (the reference binds whole buffers and never checks).
  *   - A library instance is not thread-safe per device; callers serialise.
+ *     The small-M products and lg_dispatch_argmax share one per-device
+ *     workspace (arrival counters that each call leaves at zero, and partial
+ *     sums), so their calls on one device must not overlap in time, on any
+ *     stream.  The draft forward and its graphs use workspaces of their own.
  */
 #ifndef LAGUNA_HIP_H
 #define LAGUNA_HIP_H

@@ -107,10 +107,64 @@ struct QkJob {
     uint32_t n_heads, pos0, units, blocks;
 };
 
-// Job a takes workgroups 0 .. a.blocks-1, job b the rest (the forward's K and Q).
+// The forward's attention gate of the tokens, when its weights are raw Q4_K blocks:
+// out[r][h] = sum_j x[r][j] W[h][j] (src/dflash.rs:942-944), one wavefront per
+// (row, head), lane p taking the 64-element groups p, p + 64, ... of the row.
+struct GateJob {
+    const float *x;
+    const uint8_t *w;
+    float *out;
+    uint32_t n_heads, k, units, blocks;
+};
+
+__device__ __forceinline__ void gate_dot(const GateJob &g, uint32_t unit, uint32_t lane) {
+    if (unit >= g.units) return;
+    const uint32_t row = unit / g.n_heads, head = unit % g.n_heads;
+    const float *xr = g.x + (uint64_t)row * g.k;
+    const uint8_t *wr = g.w + (uint64_t)head * (g.k / QK_K) * Q4K_BYTES;
+    float acc = 0.0f;
+    for (uint32_t p = lane; p < g.k / 64; p += 64) {
+        const uint8_t *blk = wr + (uint64_t)(p >> 2) * Q4K_BYTES;
+        const uint32_t gi = p & 3u;
+        const uint4 hd = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qa = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * gi);
+        const uint4 qb = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * gi);
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr + 64 * p);
+        float xv[64];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 t = x4[i];
+            xv[4 * i] = t.x, xv[4 * i + 1] = t.y, xv[4 * i + 2] = t.z, xv[4 * i + 3] = t.w;
+        }
+        const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        float slo = 0.0f, shi = 0.0f, xlo = 0.0f, xhi = 0.0f;  // sub-blocks 2gi (low nibbles), 2gi+1 (high)
+#pragma unroll
+        for (int b = 0; b < 32; b++) {
+            const uint32_t byte = (qw[b >> 2] >> (8 * (b & 3))) & 0xFFu;
+            slo = __builtin_fmaf(xv[b], (float)(byte & 15u), slo);
+            shi = __builtin_fmaf(xv[32 + b], (float)(byte >> 4), shi);
+            xlo += xv[b];
+            xhi += xv[32 + b];
+        }
+        uint32_t sc0, m0, sc1, m1;
+        scale_min_k4(2 * gi, hd.y, hd.z, hd.w, sc0, m0);
+        scale_min_k4(2 * gi + 1, hd.y, hd.z, hd.w, sc1, m1);
+        const float d = ref_half(hd.x & 0xFFFFu), dmin = ref_half(hd.x >> 16);
+        acc += (d * (float)sc0) * slo - (dmin * (float)m0) * xlo + (d * (float)sc1) * shi - (dmin * (float)m1) * xhi;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) g.out[(uint64_t)row * g.n_heads + head] = acc;
+}
+
+// Job a takes workgroups 0 .. a.blocks-1, job b the next b.blocks (the forward's K
+// and Q), and the gate job the rest.
 __global__ __launch_bounds__(256) void k_qk_norm_rope(QkJob a, QkJob b, const float *__restrict__ freq, uint32_t hd,
-                                                      uint32_t rope_dim, float eps) {
+                                                      uint32_t rope_dim, float eps, GateJob gj) {
     __shared__ float nrm[4][256];
+    if (blockIdx.x >= a.blocks + b.blocks) {  // uniform over the workgroup
+        gate_dot(gj, (blockIdx.x - a.blocks - b.blocks) * 4 + (threadIdx.x >> 6), threadIdx.x & 63u);
+        return;
+    }
     const bool second = blockIdx.x >= a.blocks;
     const QkJob &jb = second ? b : a;
     const float *x = jb.x, *__restrict__ w = jb.w;
@@ -628,11 +682,13 @@ QkJob qk_job(const float *x, const float *w, float *out, uint32_t n_heads, uint3
     return {x, w, out, n_heads, pos, units, (units + 3) / 4};
 }
 
-// One or two tensors (b.blocks == 0: none) in one launch.
+// One or two tensors (b.blocks == 0: none) in one launch, and the attention gate
+// when gj.blocks > 0.
 int run_qk_norm_rope(const QkJob &a, const QkJob &b, const float *freq, uint32_t hd, uint32_t rope_dim, float eps,
-                     hipStream_t s) {
-    if (a.blocks + b.blocks == 0) return LG_OK;
-    hipLaunchKernelGGL(k_qk_norm_rope, dim3(a.blocks + b.blocks), dim3(256), 0, s, a, b, freq, hd, rope_dim, eps);
+                     hipStream_t s, const GateJob &gj = GateJob{}) {
+    if (a.blocks + b.blocks + gj.blocks == 0) return LG_OK;
+    hipLaunchKernelGGL(k_qk_norm_rope, dim3(a.blocks + b.blocks + gj.blocks), dim3(256), 0, s, a, b, freq, hd,
+                       rope_dim, eps, gj);
     return after_launch("qk_norm_rope", s);
 }
 
@@ -744,6 +800,8 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
             pw = c > pw ? c : pw;
         }
         const uint64_t c1 = proj_batch_multi_ws_bytes((uint32_t)E, qkvg, 4, 2 * m, wt);
+        const uint64_t c3 = proj_batch_multi_ws_bytes((uint32_t)E, qkvg, 3, 2 * m, wt);  // gate apart
+        pw = c3 > pw ? c3 : pw;
         const uint64_t c2 = proj_batch_multi_ws_bytes((uint32_t)E, gu, 2, m, wt);
         pw = c1 > pw ? c1 : pw;
         pw = c2 > pw ? c2 : pw;
@@ -885,7 +943,18 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
         // type the four share a launch over all 2m rows (Q and the gate of the injected
         // rows are computed and not used: the weights are read once either way).
         float *q = W.q, *gate = W.gate;
-        if (L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type && L.attn_k_type == L.attn_gate_type) {
+        GateJob gj{};
+        const bool kvq = L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type;
+        if (kvq && L.attn_gate_type == LG_Q4_K && E % QK_K == 0 && (reinterpret_cast<uintptr_t>(L.attn_gate) & 15u) == 0) {
+            // K, V, Q in one launch; the gate (H rows) is computed with the QK norms
+            // below, which keeps the grouped launch's workgroups to whole rounds
+            const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                    {L.attn_q, W.q, nullptr, QD}};
+            LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
+            q = W.q + (uint64_t)m * QD;
+            gate = W.gate + (uint64_t)m * H;
+            gj = {nx, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4};
+        } else if (kvq && L.attn_k_type == L.attn_gate_type) {
             const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
                                     {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
             LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
@@ -898,7 +967,8 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
             LG_TRY(proj(W, nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, m, s));
         }
         LG_TRY(run_qk_norm_rope(qk_job(W.kk, L.attn_k_norm, W.kk, KV, ctx_len, 2 * m),
-                                qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim, hp.qk_eps, s));
+                                qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim, hp.qk_eps, s,
+                                gj));
         // causal attention over [context; injected; tokens] (src/dflash.rs:945-954), each head
         // scaled by softplus of its gate (src/dflash.rs:956-959)
         LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
