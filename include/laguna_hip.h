@@ -24,11 +24,21 @@
  *   - When a pointer was returned by lg_buf_alloc, the library checks that the
  *     extent the call reads or writes lies inside that allocation and returns
  *     LG_EINVAL otherwise (the reference binds whole buffers and never checks).
- *   - A library instance is not thread-safe per device; callers serialise.
- *     The small-M products and lg_dispatch_argmax share one per-device
- *     workspace (arrival counters that each call leaves at zero, and partial
- *     sums), so their calls on one device must not overlap in time, on any
- *     stream.  The draft forward and its graphs use workspaces of their own.
+ *   - Device workspaces belong to a stream.  The entry points that split work
+ *     over workgroups (the small-M products, the fused SiLU down projection,
+ *     lg_dispatch_argmax, lg_dispatch_mha_attn, the eager draft forward) keep
+ *     partial results and arrival counters in memory the library owns per
+ *     (device, stream): calls on different streams may run at the same time;
+ *     calls on one stream run in order.  A workspace grows between calls (the
+ *     stream is synchronised first) and never while its stream is being
+ *     captured: make the same call once before capturing it into a HIP graph.
+ *     A graph captured from a stream uses that stream's workspace, so it must
+ *     not run at the same time as direct calls on that stream.  A draft-forward
+ *     graph (lg_dflash_graph_create) owns its workspace.  lg_stream_destroy
+ *     releases a stream's workspaces; a stream destroyed without it leaves them
+ *     to the next stream that gets the same handle.
+ *   - Registries inside the library are locked; the launch-shape hooks of
+ *     laguna_hip_tuning.h are atomic.
  */
 #ifndef LAGUNA_HIP_H
 #define LAGUNA_HIP_H
@@ -211,11 +221,13 @@ int lg_dispatch_argmax(const float *logits, uint32_t n, uint32_t rows, uint64_t 
 int lg_dispatch_rmsnorm(const float *w, const float *x, float *out, uint32_t n, uint32_t rows, float eps,
                         void *stream);
 
-/* dispatch_enc_aux_norm (src/dflash.rs:1196-1236), kernels/enc_aux_norm.comp: RMSNorm
- * of each n_feat chunk of the n_aux*n_feat features of each of n_tokens rows,
- * times aux_norm_w[aux*n_feat + feat]. */
+/* dispatch_enc_aux_norm (src/dflash.rs:1200-1233), kernels/enc_aux_norm.comp:
+ * out[i] = x[i] * (mean(x[chunk]^2) + 1e-5)^-1/2 * aux_norm_w[i % (n_aux*n_feat)]
+ * for i < n_total, where chunk is the n_feat-float chunk that holds i.  Same
+ * arguments as the reference (n_total = n_aux*n_feat for its one token); n_total
+ * may be any whole number of tokens. */
 int lg_dispatch_enc_aux_norm(const float *x, const float *aux_norm_w, float *out, uint32_t n_feat,
-                             uint32_t n_aux, uint32_t n_tokens, float eps, void *stream);
+                             uint32_t n_aux, uint32_t n_total, void *stream);
 
 /* dispatch_qk_norm_rope (src/dflash.rs:1092-1128), kernels/qk_norm_rope.comp:
  * per-head RMSNorm times norm_w[dim], then GPT-NeoX rotation of dims < rope_dim
@@ -236,15 +248,18 @@ int lg_dispatch_mha_attn(const float *q, const float *k_seq, const float *v_seq,
                          uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq_len, uint32_t q_pos,
                          uint32_t rows, int causal, void *stream);
 
-/* dispatch_gate_mul (src/dflash.rs:1238-1270), kernels/gate_mul.comp:
- * out[r][i] = v[r][i] * gate[r][i / head_dim]. */
-int lg_dispatch_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
-                         uint32_t rows, void *stream);
+/* dispatch_gate_mul (src/dflash.rs:1236-1266), kernels/gate_mul.comp, same
+ * argument order: attn_out[i] = v_rep[i] * gate[i / head_dim] for i < n_hd
+ * (n_heads does not enter the result, as in the shader). */
+int lg_dispatch_gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd,
+                         uint32_t n_heads, uint32_t head_dim, void *stream);
 
-/* The attention gate of src/dflash.rs:956-959 on the device: the reference
- * applies softplus on the host (g > 20 ? g : ln(1 + e^g)) and then gate_mul. */
-int lg_dispatch_softplus_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads,
-                                  uint32_t head_dim, uint32_t rows, void *stream);
+/* The attention gate of src/dflash.rs:956-959 on the device, arguments as
+ * dispatch_gate_mul: the reference applies softplus on the host
+ * (g > 20 ? g : ln(1 + e^g)) and then gate_mul;
+ * attn_out[i] = v_rep[i] * softplus(gate[i / head_dim]). */
+int lg_dispatch_softplus_gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd,
+                                  uint32_t n_heads, uint32_t head_dim, void *stream);
 
 /* dispatch_add (src/dflash.rs:1284-1303), kernels/add.comp: out = a + b. */
 int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream);
@@ -357,22 +372,6 @@ int lg_gguf_get_f64(const lg_gguf *g, uint64_t field, uint64_t elem, double *out
 int lg_gguf_get_bool(const lg_gguf *g, uint64_t field, uint64_t elem, int *out);
 int lg_gguf_get_str(const lg_gguf *g, uint64_t field, uint64_t elem, const char **out, uint64_t *len);
 
-/* ---- Launch-shape tuning hooks (no counterpart in the reference: the Vulkan
- * shaders have fixed workgroup counts).  For launch-shape sweeps; 0 restores the
- * automatic choice.  Every value meets the same parity bound, and results are
- * repeatable for a fixed setting.  Process-wide, not thread-safe. */
-
-/* Upper bound on workgroups of the M = 1 quantized projections. */
-int lg_set_m1_grid_cap(uint32_t cap);
-/* Number of k slices of the Q4_K M = 1 matrix-core kernel (the fused SiLU down
- * projection). */
-int lg_set_m1_split(uint32_t slices);
-/* Small-M products (lg_dispatch_proj_quant_batch, the draft forward): ch chunks of
- * 256 elements per k slice (1, 2; 4 for Q4_K with m <= 16) and rt 16-row tiles per
- * wavefront (1, 2, 4; clamped to the kernel's register budget).  A captured
- * draft-forward graph keeps the workspace it was sized with: set this before
- * lg_dflash_graph_create. */
-int lg_set_batch_shape(uint32_t ch, uint32_t rt);
 
 /* ---- DFlash draft model (src/dflash.rs DFlashModel) ---- */
 

@@ -19,6 +19,7 @@
 //   attention (other head_dim)  one wavefront per (row, head), online softmax
 //   softplus gate, add          elementwise
 #include <cmath>
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -729,38 +730,6 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
     return after_launch("softplus_gate_mul", s);
 }
 
-// Per-device scratch for lg_dispatch_mha_attn's partials (grown on demand).
-struct Scratch {
-    void *ptr = nullptr;
-    size_t bytes = 0;
-};
-std::vector<Scratch> g_attn_scratch;
-std::mutex g_scratch_mu;
-
-int scratch(std::vector<Scratch> &v, size_t need, void **out) {
-    int dev = 0;
-    LG_HIP_TRY(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if ((size_t)dev >= v.size()) v.resize(dev + 1);
-    Scratch &sc = v[dev];
-    if (sc.bytes < need) {
-        if (sc.ptr) {
-            LG_HIP_TRY(hipDeviceSynchronize());  // earlier launches may still use it
-            LG_HIP_TRY(hipFree(sc.ptr));
-        }
-        sc.ptr = nullptr;
-        sc.bytes = 0;
-        const size_t sz = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-        if (hipMalloc(&sc.ptr, sz) != hipSuccess) {
-            (void)hipGetLastError();
-            return fail(LG_ENOMEM, "scratch (%zu bytes)", sz);
-        }
-        sc.bytes = sz;
-    }
-    *out = sc.ptr;
-    return LG_OK;
-}
-
 // ------------------------------------------------------------------------------------------
 // forward
 
@@ -829,7 +798,7 @@ std::vector<float> rope_table(const lg_dflash_hparams &hp) {
     return f;
 }
 
-// A workspace with its table uploaded for (rope_dim, rope_base).
+// A graph's own workspace, with its table uploaded for (rope_dim, rope_base).
 struct Ws {
     uint8_t *base = nullptr;
     uint64_t bytes = 0;
@@ -856,28 +825,35 @@ int ws_alloc(Ws &w, uint64_t need) {
     return LG_OK;
 }
 
-int ws_table(Ws &w, const lg_dflash_hparams &hp, const FwdLayout &L, hipStream_t s) {
-    if (w.rope_dim == hp.rope_dim && w.rope_base == hp.rope_base) return LG_OK;
+// The f32 RoPE table at L.freq, uploaded unless the (rope_dim, rope_base) in tag already is.
+int upload_table(uint64_t (&tag)[2], const lg_dflash_hparams &hp, const FwdLayout &L, hipStream_t s) {
+    uint32_t bb = 0;
+    std::memcpy(&bb, &hp.rope_base, 4);
+    if (tag[0] == hp.rope_dim && tag[1] == bb) return LG_OK;
     const std::vector<float> f = rope_table(hp);
     LG_HIP_TRY(hipMemcpyAsync(L.freq, f.data(), f.size() * 4, hipMemcpyHostToDevice, s));
     LG_HIP_TRY(hipStreamSynchronize(s));  // f is released on return
+    tag[0] = hp.rope_dim;
+    tag[1] = bb;
+    return LG_OK;
+}
+
+int ws_table(Ws &w, const lg_dflash_hparams &hp, const FwdLayout &L, hipStream_t s) {
+    uint64_t tag[2] = {w.rope_dim, 0};
+    std::memcpy(&tag[1], &w.rope_base, 4);
+    LG_TRY(upload_table(tag, hp, L, s));
     w.rope_dim = hp.rope_dim;
     w.rope_base = hp.rope_base;
     return LG_OK;
 }
 
-std::vector<Ws> g_ws;  // eager calls, per device (guarded by g_scratch_mu)
-
-// The per-device eager workspace laid out for (hp, m, ctx_len), table uploaded.
+// The eager workspace of stream s laid out for (hp, m, ctx_len), table uploaded.
+// Eager calls on one stream share it; calls on different streams never do.
 int eager_ws(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, FwdLayout &L, hipStream_t s) {
-    int dev = 0;
-    LG_HIP_TRY(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
-    Ws &w = g_ws[dev];
-    LG_TRY(ws_alloc(w, layout(hp, m, ctx_len, nullptr, L)));
-    layout(hp, m, ctx_len, w.base, L);
-    return ws_table(w, hp, L, s);
+    BufLease lease;
+    LG_TRY(stream_buffer(BUF_DRAFT, s, layout(hp, m, ctx_len, nullptr, L), lease, "draft forward"));
+    layout(hp, m, ctx_len, static_cast<uint8_t *>(lease.buf->ptr), L);
+    return upload_table(lease.buf->tag, hp, L, s);
 }
 
 // with_layers = false checks what the encoder needs only.
@@ -1034,15 +1010,18 @@ int lg_dispatch_rmsnorm(const float *w, const float *x, float *out, uint32_t n, 
 }
 
 int lg_dispatch_enc_aux_norm(const float *x, const float *aux_norm_w, float *out, uint32_t n_feat, uint32_t n_aux,
-                             uint32_t n_tokens, float eps, void *stream) {
+                             uint32_t n_total, void *stream) {
     clear_error();
-    if (n_feat == 0 || n_aux == 0 || n_tokens == 0) return LG_OK;
+    if (n_feat == 0 || n_aux == 0 || n_total == 0) return LG_OK;
     LG_REQUIRE(x && aux_norm_w && out, "lg_dispatch_enc_aux_norm: null pointer");
-    const uint64_t tot = (uint64_t)n_feat * n_aux * n_tokens * 4;
-    LG_EXTENT(x, tot, "lg_dispatch_enc_aux_norm x");
-    LG_EXTENT(out, tot, "lg_dispatch_enc_aux_norm out");
-    LG_EXTENT(aux_norm_w, (uint64_t)n_feat * n_aux * 4, "lg_dispatch_enc_aux_norm w");
-    return run_rmsnorm(x, aux_norm_w, out, n_feat, n_tokens, n_aux, n_feat * n_aux, eps, (hipStream_t)stream);
+    const uint64_t per = (uint64_t)n_feat * n_aux;
+    LG_REQUIRE(n_total % per == 0, "lg_dispatch_enc_aux_norm: n_total=%u is not a whole number of tokens of %llu",
+               n_total, (unsigned long long)per);
+    const uint32_t n_tokens = (uint32_t)(n_total / per);
+    LG_EXTENT(x, (uint64_t)n_total * 4, "lg_dispatch_enc_aux_norm x");
+    LG_EXTENT(out, (uint64_t)n_total * 4, "lg_dispatch_enc_aux_norm out");
+    LG_EXTENT(aux_norm_w, per * 4, "lg_dispatch_enc_aux_norm w");
+    return run_rmsnorm(x, aux_norm_w, out, n_feat, n_tokens, n_aux, n_feat * n_aux, 1e-5f, (hipStream_t)stream);
 }
 
 int lg_dispatch_qk_norm_rope(const float *x, const float *norm_w, const float *freq, float *out, uint32_t n_heads,
@@ -1082,39 +1061,42 @@ int lg_dispatch_mha_attn(const float *q, const float *k_seq, const float *v_seq,
     const uint32_t G = n_q_heads / n_kv_heads;
     if (head_dim == AHD && rows * G <= AQ && seq_len) {
         void *p = nullptr;
-        LG_TRY(scratch(g_attn_scratch, attn_partial_floats(seq_len, n_kv_heads) * 4, &p));
+        BufLease lease;
+        LG_TRY(stream_buffer(BUF_ATTN, s, attn_partial_floats(seq_len, n_kv_heads) * 4, lease, "lg_dispatch_mha_attn"));
+        p = lease.buf->ptr;
         part = static_cast<float *>(p);
     }
     return run_attention(q, k_seq, v_seq, seq_len, nullptr, nullptr, seq_len, rows, n_q_heads, n_kv_heads, head_dim,
                          q_pos, causal, out, part, s);
 }
 
-int lg_dispatch_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
-                         uint32_t rows, void *stream) {
+// dispatch_gate_mul / the softplus gate (src/dflash.rs:1236-1266, 956-959):
+// attn_out[i] = v_rep[i] * g(gate[i / head_dim]) for i < n_hd, g = identity or
+// softplus.  As in kernels/gate_mul.comp, n_heads does not enter the result.
+static int gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd, uint32_t n_heads,
+                    uint32_t head_dim, int softplus, void *stream, const char *name) {
     clear_error();
-    const uint64_t total = (uint64_t)rows * n_heads * head_dim;
-    if (total == 0) return LG_OK;
-    LG_REQUIRE(v && gate && out, "lg_dispatch_gate_mul: null pointer");
-    LG_EXTENT(v, total * 4, "lg_dispatch_gate_mul v");
-    LG_EXTENT(out, total * 4, "lg_dispatch_gate_mul out");
-    LG_EXTENT(gate, (uint64_t)rows * n_heads * 4, "lg_dispatch_gate_mul gate");
+    (void)n_heads;
+    if (n_hd == 0) return LG_OK;
+    LG_REQUIRE(attn_out && v_rep && gate, "%s: null pointer", name);
+    LG_REQUIRE(head_dim, "%s: head_dim = 0", name);
+    LG_EXTENT(v_rep, (uint64_t)n_hd * 4, name);
+    LG_EXTENT(attn_out, (uint64_t)n_hd * 4, name);
+    LG_EXTENT(gate, (uint64_t)((n_hd + head_dim - 1) / head_dim) * 4, name);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, v, gate, out, n_heads, head_dim, total, 0);
-    return after_launch("lg_dispatch_gate_mul", s);
+    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(n_hd)), dim3(256), 0, s, v_rep, gate, attn_out, 1u, head_dim,
+                       (uint64_t)n_hd, softplus);
+    return after_launch(name, s);
 }
 
-int lg_dispatch_softplus_gate_mul(const float *v, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
-                                  uint32_t rows, void *stream) {
-    clear_error();
-    const uint64_t total = (uint64_t)rows * n_heads * head_dim;
-    if (total == 0) return LG_OK;
-    LG_REQUIRE(v && gate && out, "lg_dispatch_softplus_gate_mul: null pointer");
-    LG_EXTENT(v, total * 4, "lg_dispatch_softplus_gate_mul v");
-    LG_EXTENT(out, total * 4, "lg_dispatch_softplus_gate_mul out");
-    LG_EXTENT(gate, (uint64_t)rows * n_heads * 4, "lg_dispatch_softplus_gate_mul gate");
-    hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, v, gate, out, n_heads, head_dim, total, 1);
-    return after_launch("lg_dispatch_softplus_gate_mul", s);
+int lg_dispatch_gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd, uint32_t n_heads,
+                         uint32_t head_dim, void *stream) {
+    return gate_mul(attn_out, v_rep, gate, n_hd, n_heads, head_dim, 0, stream, "lg_dispatch_gate_mul");
+}
+
+int lg_dispatch_softplus_gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd,
+                                  uint32_t n_heads, uint32_t head_dim, void *stream) {
+    return gate_mul(attn_out, v_rep, gate, n_hd, n_heads, head_dim, 1, stream, "lg_dispatch_softplus_gate_mul");
 }
 
 int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream) {

@@ -4,10 +4,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
 #include "laguna_hip.h"
+#include "laguna_hip_tuning.h"
 
 namespace lg {
 
@@ -54,20 +56,62 @@ struct DeferSync {
                "%s: %llu bytes at %p run past the end of its lg_buf_alloc allocation",     \
                name, (unsigned long long)(bytes), (const void *)(ptr))
 
+// A product workspace starts with PROJ_WS_COUNTERS bytes of arrival counters that
+// every call expects to find zero (and leaves zero); callers that lay other data out
+// after a workspace keep that region at a fixed place.
+constexpr uint64_t PROJ_WS_COUNTERS = 65536;
+
+// Device memory the library owns for one purpose on one stream of one device, so
+// that calls on different streams never share it.  It grows on demand: the stream
+// is synchronised and the old allocation freed, unless a graph captured from that
+// stream may still use it (then it is kept until the process ends).  It cannot grow
+// while the stream is being captured (LG_EINVAL: make the same call once on that
+// stream before capturing).  New memory is zeroed on the stream.  The lease holds
+// the registry lock; `tag` is free for the purpose's own bookkeeping.
+enum BufPurpose { BUF_PRODUCT = 0, BUF_ATTN = 1, BUF_DRAFT = 2 };
+struct StreamBuf {
+    void *ptr = nullptr;
+    uint64_t bytes = 0;
+    bool captured = false;
+    uint64_t tag[2] = {~0ull, ~0ull};
+};
+struct BufLease {
+    StreamBuf *buf = nullptr;
+    void *lock = nullptr;  // std::unique_lock<std::mutex>, released by the destructor
+    BufLease() = default;
+    BufLease(const BufLease &) = delete;
+    BufLease &operator=(const BufLease &) = delete;
+    ~BufLease();
+};
+int stream_buffer(int purpose, hipStream_t s, uint64_t need, BufLease &lease, const char *what);
+// The product kernels' workspace on stream s (arrival counters first, then partial
+// sums): at least `need` bytes.  Every call finds the counters zero and leaves them
+// zero.
+int stream_workspace(hipStream_t s, uint64_t need, void **out);
+
+// Split-k arrival, called by every thread of a (one-dimensional) workgroup after its
+// partial results are stored with device-coherent atomic stores.  True in every
+// thread of the last workgroup to arrive at *cnt (of `total`), which resets the
+// counter; that workgroup then observes every other workgroup's partial results:
+// each thread's stores are released at agent scope before the barrier, the counter
+// update is acquire-release, and the last workgroup acquires before reading.
+__device__ __forceinline__ bool arrive_last(uint32_t *cnt, uint32_t total, uint32_t *s_flag) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *s_flag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == total - 1 ? 1u : 0u;
+    __syncthreads();
+    if (*s_flag == 0u) return false;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 // Small-M product behind lg_dispatch_proj_quant_batch: c = W x, or c = res + W x
-// when res is given (res may be c).  ws == nullptr uses the per-device workspace;
+// when res is given (res may be c).  ws == nullptr uses stream s's workspace;
 // otherwise ws holds at least proj_batch_ws_bytes(k, n, m, x_dtype, w_dtype) bytes
 // owned by the caller, zeroed before its first use and used by one call at a time
 // (graphs capture it, so it must outlive them).
-// A workspace starts with PROJ_WS_COUNTERS bytes of arrival counters that every
-// call expects to find zero (and leaves zero); callers that lay other data out
-// after a workspace keep that region at a fixed place.
-constexpr uint64_t PROJ_WS_COUNTERS = 65536;
-// The per-device workspace (arrival counters first, then partial sums) shared by
-// the product kernels that split k over workgroups: at least `need` bytes, grown
-// on demand (after a device synchronise), zeroed when allocated and kept for the
-// process.  Calls that overlap in time on one device must not share it.
-int device_workspace(uint64_t need, void **out);
 uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype);
 int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                void *ws, uint64_t ws_bytes, hipStream_t s, const float *res = nullptr);

@@ -49,25 +49,6 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 
-// Scale factors of the 8 sub-blocks of a Q4_K super-block (ggml get_scale_min_k4,
-// kernels/proj_q4k.comp:46-58) from the scale dwords s0, s1, s2, all at once:
-// a[j] = 16 d sc_j and cc[j] = dmin m_j + a[j].
-__device__ __forceinline__ void q4k_scales(uint32_t s0, uint32_t s1, uint32_t s2, float d16, float dmin, float (&a)[8],
-                                           float (&cc)[8]) {
-    const uint32_t sl = s0 & 0x3F3F3F3Fu, ml = s1 & 0x3F3F3F3Fu;
-    const uint32_t sh = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-    const uint32_t mh = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-    const float scf[8] = {ubyte_f<0>(sl), ubyte_f<1>(sl), ubyte_f<2>(sl), ubyte_f<3>(sl),
-                          ubyte_f<0>(sh), ubyte_f<1>(sh), ubyte_f<2>(sh), ubyte_f<3>(sh)};
-    const float mnf[8] = {ubyte_f<0>(ml), ubyte_f<1>(ml), ubyte_f<2>(ml), ubyte_f<3>(ml),
-                          ubyte_f<0>(mh), ubyte_f<1>(mh), ubyte_f<2>(mh), ubyte_f<3>(mh)};
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        a[j] = d16 * scf[j];
-        cc[j] = __builtin_fmaf(dmin, mnf[j], a[j]);
-    }
-}
-
 // a[j] = 16 d sc_j for the 8 sub-blocks (the code term's scales).
 __device__ __forceinline__ void q4k_scales_a(uint32_t s0, uint32_t s2, float d16, float (&a)[8]) {
     const uint32_t sl = s0 & 0x3F3F3F3Fu, sh = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
@@ -279,20 +260,9 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
                                            __HIP_MEMORY_SCOPE_AGENT);
                 }
         }
-        // Partial sums and counter are device-coherent atomics (written through to,
-        // and read from, the device-wide level), so no cache write-back or
-        // invalidation is needed: each thread's stores complete before the
-        // workgroup's arrival is counted, and the last workgroup reads them after.
+        // the last workgroup of the column to arrive adds the slices
         __shared__ uint32_t last;
-        __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(&cnt[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1
-                       ? 1u
-                       : 0u;
-        __syncthreads();
-        if (!last) return;
-        if (threadIdx.x == 0) __hip_atomic_store(&cnt[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!arrive_last(&cnt[blockIdx.x], S, &last)) return;
     }
     // Slices are added in slice order (the sum does not depend on arrival order);
     // the loads of G slices for all RT row tiles are in flight together.
@@ -640,47 +610,6 @@ __global__ __launch_bounds__(256) void k_generic_batch(const void *__restrict__ 
     }
 }
 
-// Per-device workspace (arrival counters, partial sums); grown on demand, zeroed
-// when allocated, kept for the life of the process.  Calls on one device share it:
-// calls that overlap in time on different streams of the same device must be
-// serialised by the caller.
-struct Workspace {
-    void *ptr = nullptr;
-    uint64_t bytes = 0;
-};
-std::vector<Workspace> g_ws;
-
-}  // namespace
-
-namespace lg {
-
-int device_workspace(uint64_t need, void **out) {
-    int dev = 0;
-    LG_HIP_TRY(hipGetDevice(&dev));
-    if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
-    Workspace &ws = g_ws[dev];
-    if (ws.bytes < need) {
-        if (ws.ptr) {
-            LG_HIP_TRY(hipDeviceSynchronize());  // earlier launches may still use it
-            LG_HIP_TRY(hipFree(ws.ptr));
-        }
-        ws.ptr = nullptr;
-        ws.bytes = 0;
-        const uint64_t sz = (need + (1u << 20) - 1) & ~(uint64_t)((1u << 20) - 1);
-        hipError_t e = hipMalloc(&ws.ptr, sz);
-        if (e != hipSuccess) return fail(LG_ENOMEM, "batch workspace (%llu bytes): %s", (unsigned long long)sz,
-                                         hipGetErrorString(e));
-        LG_HIP_TRY(hipMemset(ws.ptr, 0, sz));  // arrival counters start at zero
-        ws.bytes = sz;
-    }
-    *out = ws.ptr;
-    return LG_OK;
-}
-
-}  // namespace lg
-
-namespace {
-
 // Launch shape: CH chunks per slice (the slice's fragments fill LDS: 48 KB for f32
 // activations), one slice per workgroup column, RT row tiles per wavefront: the
 // most that still gives 256 workgroups (n is the jobs' total rows).
@@ -688,13 +617,14 @@ struct MmShape {
     uint32_t ch, slices, tiles, rt;
 };
 
-uint32_t g_mm_ch = 0, g_mm_rt = 0;  // launch-shape overrides (0 = automatic)
+std::atomic<uint32_t> g_mm_ch{0}, g_mm_rt{0};  // launch-shape overrides (0 = automatic)
 
 MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     const uint32_t tiles = (m + 15) / 16 > 2 ? 2 : (m + 15) / 16;  // per launch; larger m runs in pairs of tiles
     uint32_t ch = dtype == LG_Q4_K ? (tiles == 1 ? 2 : 1) : 1;
     // chunks of 8 sub-blocks per slice: 1, 2 or (one token tile only) 4
-    if (g_mm_ch) ch = g_mm_ch >= 4 && tiles == 1 ? 4 : g_mm_ch >= 2 ? 2 : 1;
+    const uint32_t och = g_mm_ch.load(std::memory_order_relaxed), ort = g_mm_rt.load(std::memory_order_relaxed);
+    if (och) ch = och >= 4 && tiles == 1 ? 4 : och >= 2 ? 2 : 1;
     if (dtype != LG_Q4_K && ch > 2) ch = 2;
     const uint32_t chunks = (k + 255) / 256, slices = (chunks + ch - 1) / ch;
     // the most rows per wavefront that still give about three workgroups per CU per
@@ -702,7 +632,7 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     // four (two waves per SIMD) only when two already give twelve per CU
     uint32_t rt = (n + 127) / 128 * slices >= 3072 * tiles ? 4 : 2;
     while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 768 * tiles) rt /= 2;
-    if (g_mm_rt) rt = g_mm_rt >= 4 ? 4 : g_mm_rt >= 2 ? 2 : 1;
+    if (ort) rt = ort >= 4 ? 4 : ort >= 2 ? 2 : 1;
     while (rt * ch > (dtype == LG_Q4_K ? 8u : 4u)) rt /= 2;  // register budget
     return {ch, slices, tiles, rt};
 }
@@ -847,7 +777,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         if (ws) {
             LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small", name, (unsigned long long)ws_bytes);
         } else {
-            LG_TRY(device_workspace(need, &ws));
+            LG_TRY(stream_workspace(s, need, &ws));
         }
     }
     const uint32_t tiles = (m + 15) / 16;
@@ -901,8 +831,8 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
 // launch-shape sweeps; results meet the same parity bound for every value.
 // Workspaces sized before a change may be too small afterwards (the call then fails).
 extern "C" int lg_set_batch_shape(uint32_t ch, uint32_t rt) {
-    g_mm_ch = ch;
-    g_mm_rt = rt;
+    g_mm_ch.store(ch, std::memory_order_relaxed);
+    g_mm_rt.store(rt, std::memory_order_relaxed);
     return LG_OK;
 }
 

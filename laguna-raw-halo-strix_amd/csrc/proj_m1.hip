@@ -45,7 +45,7 @@ namespace {
 
 using namespace lg;
 
-uint32_t g_grid_cap = 0;  // 0 = automatic
+std::atomic<uint32_t> g_grid_cap{0};  // 0 = automatic
 
 constexpr uint32_t M1_MAX_K = 16384;  // 4 waves x 64 lanes x 64 elements
 constexpr int M1_RPW_MAX = 8;         // rows per team whose loads are in flight together
@@ -860,16 +860,8 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void k_q4k_m1_mfma(const float *__re
         }
     }
     if (KS == 1) return;
-    // Slices: the partial sums and the counter are device-coherent atomics, so no
-    // cache write-back or invalidation is needed; each thread's stores complete
-    // before the workgroup's arrival is counted.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(&cnt[rs], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == KS - 1 ? 1u : 0u;
-    __syncthreads();
-    if (!s_last) return;
-    if (threadIdx.x == 0) __hip_atomic_store(&cnt[rs], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last workgroup of the row range to arrive adds the slices
+    if (!arrive_last(&cnt[rs], KS, &s_last)) return;
     for (uint32_t t = threadIdx.x; t < rows; t += blockDim.x) {
         const uint32_t r = r_begin + t;
         float s = 0.0f;
@@ -954,7 +946,8 @@ int device_cus() {
 // workgroups), at most M1_RPW_MAX; larger n simply launches more workgroups.
 uint32_t rows_per_team(uint32_t n, uint32_t teams) {
     uint64_t wgs = (uint64_t)device_cus();
-    if (g_grid_cap && g_grid_cap < wgs) wgs = g_grid_cap;
+    const uint32_t cap = g_grid_cap.load(std::memory_order_relaxed);
+    if (cap && cap < wgs) wgs = cap;
     uint64_t rpw = (n + wgs * teams - 1) / (wgs * teams);
     if (rpw < 1) rpw = 1;
     if (rpw > (uint64_t)M1_RPW_MAX) rpw = M1_RPW_MAX;
@@ -965,13 +958,14 @@ uint32_t rows_per_team(uint32_t n, uint32_t teams) {
 // workgroup per CU.  More slices mean less activation staging per workgroup (each
 // stages k/KS elements; the fused SiLU adds two transcendentals per element) but
 // more partial sums and a longer reduction by the last workgroup of a row range.
-uint32_t g_m1_split = 0;  // 0 = automatic
+std::atomic<uint32_t> g_m1_split{0};  // 0 = automatic
 
 void mq_shape(uint32_t k, uint32_t n, bool fuse, uint32_t &rs, uint32_t &ks) {
     uint32_t G = (uint32_t)device_cus();
-    if (g_grid_cap && g_grid_cap < G) G = g_grid_cap;
+    const uint32_t cap = g_grid_cap.load(std::memory_order_relaxed);
+    if (cap && cap < G) G = cap;
     const uint32_t nsb = k / QK_K;
-    uint32_t s = g_m1_split;
+    uint32_t s = g_m1_split.load(std::memory_order_relaxed);
     if (!s) {
         // staging cost per workgroup ~ k/KS, product work ~ n k / G: keep their ratio small
         const double per = (fuse ? 14.0 : 8.0) * 4096.0 / (double)n * (double)G / 256.0;
@@ -998,7 +992,7 @@ int launch_q4k_mfma(const float *x, const float *up, const uint8_t *w, float *y,
     if (ks > 1) {
         LG_REQUIRE(rs <= PROJ_WS_COUNTERS / 4, "proj_q4k_m1: %u row ranges exceed the arrival counters", rs);
         void *ws = nullptr;
-        const int st = device_workspace(PROJ_WS_COUNTERS + (uint64_t)ks * n * 4, &ws);
+        const int st = stream_workspace(s, PROJ_WS_COUNTERS + (uint64_t)ks * n * 4, &ws);
         if (st != LG_OK) return st;
         cnt = static_cast<uint32_t *>(ws);
         part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + PROJ_WS_COUNTERS);
@@ -1050,7 +1044,8 @@ int launch_q4k(const float *x, const float *up, const uint8_t *w, float *y, uint
     if (P <= 64 && !FUSE) {
         constexpr int TEAMS = 4, R = 2;
         uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
-        const uint32_t cap = g_grid_cap ? g_grid_cap : 1024;
+        const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed);
+        const uint32_t cap = gc ? gc : 1024;
         grid = grid < cap ? grid : cap;
         hipLaunchKernelGGL((k_q4k_m1_rows<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
                            (uint64_t)k / QK_K * Q4K_BYTES);
@@ -1180,16 +1175,16 @@ int lg_dispatch_proj_read(const float *x, const float *w, uint32_t k, uint32_t n
     clear_error();
     if (n == 0) return LG_OK;
     LG_REQUIRE(out, "lg_dispatch_proj_read: null out");
-    float *tmp = nullptr;
-    LG_HIP_TRY(hipMalloc(&tmp, (uint64_t)n * 4));
-    int st = lg_dispatch_proj_row(x, w, tmp, k, n, 0, stream);
-    if (st == LG_OK) {
-        hipError_t e = hipMemcpyAsync(out, tmp, (uint64_t)n * 4, hipMemcpyDeviceToHost, (hipStream_t)stream);
-        if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream);
-        if (e != hipSuccess) st = fail(LG_EHIP, "lg_dispatch_proj_read: %s", hipGetErrorString(e));
-    }
-    (void)hipFree(tmp);
-    return st;
+    hipStream_t s = (hipStream_t)stream;
+    // the result lands in this stream's workspace, after its arrival counters (the f32
+    // projection itself uses no workspace), and is copied to the host from there
+    void *ws = nullptr;
+    LG_TRY(stream_workspace(s, PROJ_WS_COUNTERS + (uint64_t)n * 4, &ws));
+    float *tmp = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + PROJ_WS_COUNTERS);
+    LG_TRY(lg_dispatch_proj_row(x, w, tmp, k, n, 0, stream));
+    LG_HIP_TRY(hipMemcpyAsync(out, tmp, (uint64_t)n * 4, hipMemcpyDeviceToHost, s));
+    LG_HIP_TRY(hipStreamSynchronize(s));
+    return LG_OK;
 }
 
 int lg_dispatch_activation(const float *gate, const float *up, float *h, uint32_t n, void *stream) {
@@ -1207,7 +1202,7 @@ int lg_dispatch_activation(const float *gate, const float *up, float *h, uint32_
 // Upper bound on workgroups of the M=1 quantized kernels (0 = automatic).  A
 // tuning hook for launch-shape sweeps; results do not depend on it.
 int lg_set_m1_grid_cap(uint32_t cap) {
-    g_grid_cap = cap;
+    g_grid_cap.store(cap, std::memory_order_relaxed);
     return LG_OK;
 }
 
@@ -1215,7 +1210,7 @@ int lg_set_m1_grid_cap(uint32_t cap) {
 // the cap above; results meet the same parity bound for every value and are
 // repeatable for a fixed one.
 int lg_set_m1_split(uint32_t slices) {
-    g_m1_split = slices;
+    g_m1_split.store(slices, std::memory_order_relaxed);
     return LG_OK;
 }
 

@@ -5,6 +5,8 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
+#include <vector>
 
 #include "lg_common.hpp"
 
@@ -57,6 +59,85 @@ int after_launch(const char *what, hipStream_t s) {
         e = hipStreamSynchronize(s);
         if (e != hipSuccess) return fail(LG_EHIP, "%s: %s", what, hipGetErrorString(e));
     }
+    return LG_OK;
+}
+
+// ---- library-owned device buffers, one per (purpose, device, stream)
+
+static std::mutex g_sb_mu;
+static std::map<std::tuple<int, int, uintptr_t>, StreamBuf> g_sb;
+static std::vector<void *> g_retired;  // buffers a captured graph may still use: never freed
+
+BufLease::~BufLease() { delete static_cast<std::unique_lock<std::mutex> *>(lock); }
+
+int stream_buffer(int purpose, hipStream_t s, uint64_t need, BufLease &lease, const char *what) {
+    int dev = 0;
+    LG_HIP_TRY(hipGetDevice(&dev));
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    LG_HIP_TRY(hipStreamIsCapturing(s, &cs));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    auto *lk = new std::unique_lock<std::mutex>(g_sb_mu);
+    lease.lock = lk;
+    StreamBuf &b = g_sb[std::make_tuple(purpose, dev, reinterpret_cast<uintptr_t>(s))];
+    if (b.bytes < need) {
+        if (capturing)
+            return fail(LG_EINVAL,
+                        "%s: its device workspace must grow to %llu bytes while the stream is being captured; make "
+                        "the same call once on this stream before capturing",
+                        what, (unsigned long long)need);
+        if (b.ptr) {
+            if (b.captured) {
+                g_retired.push_back(b.ptr);
+            } else {
+                LG_HIP_TRY(hipStreamSynchronize(s));  // earlier launches on this stream may still use it
+                LG_HIP_TRY(hipFree(b.ptr));
+            }
+        }
+        b = StreamBuf();
+        const uint64_t sz = (need + (1u << 20) - 1) & ~(uint64_t)((1u << 20) - 1);
+        void *p = nullptr;
+        if (hipMalloc(&p, sz) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(LG_ENOMEM, "%s: device workspace of %llu bytes", what, (unsigned long long)sz);
+        }
+        LG_HIP_TRY(hipMemsetAsync(p, 0, sz, s));  // arrival counters start at zero
+        b.ptr = p;
+        b.bytes = sz;
+    }
+    if (capturing) b.captured = true;
+    lease.buf = &b;
+    return LG_OK;
+}
+
+// Drops the buffers of stream s on every device (lg_stream_destroy): freed after the
+// stream's work, or retired when a captured graph may still use them.
+static int release_stream_buffers(hipStream_t s) {
+    std::lock_guard<std::mutex> lk(g_sb_mu);
+    bool synced = false;
+    for (auto it = g_sb.begin(); it != g_sb.end();) {
+        if (std::get<2>(it->first) != reinterpret_cast<uintptr_t>(s)) {
+            ++it;
+            continue;
+        }
+        StreamBuf &b = it->second;
+        if (b.ptr) {
+            if (b.captured) {
+                g_retired.push_back(b.ptr);
+            } else {
+                if (!synced) LG_HIP_TRY(hipStreamSynchronize(s));
+                synced = true;
+                LG_HIP_TRY(hipFree(b.ptr));
+            }
+        }
+        it = g_sb.erase(it);
+    }
+    return LG_OK;
+}
+
+int stream_workspace(hipStream_t s, uint64_t need, void **out) {
+    BufLease lease;
+    LG_TRY(stream_buffer(BUF_PRODUCT, s, need, lease, "product workspace"));
+    *out = lease.buf->ptr;
     return LG_OK;
 }
 
@@ -186,6 +267,7 @@ int lg_stream_create(void **stream) {
 
 int lg_stream_destroy(void *stream) {
     if (!stream) return LG_OK;
+    LG_TRY(release_stream_buffers((hipStream_t)stream));
     LG_HIP_TRY(hipStreamDestroy((hipStream_t)stream));
     return LG_OK;
 }

@@ -103,19 +103,14 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const float *__restrict__ x
         } else {
             const uint4 st = make_uint4(__float_as_uint(t.v), t.i, t.f, 0u);
             uint32_t *pw = reinterpret_cast<uint32_t *>(part + (uint64_t)row * nch + c);
-            // device-coherent stores and counter: no cache maintenance between them
             __hip_atomic_store(pw, st.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(pw + 1, st.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(pw + 2, st.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-            last = __hip_atomic_fetch_add(&cnt[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1 ? 1u
-                                                                                                                : 0u;
         }
     }
     if (nch == 1) return;
-    __syncthreads();
-    if (!last || wave != 0) return;
-    if (lane == 0) __hip_atomic_store(&cnt[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the last workgroup of the row to arrive combines the chunk states
+    if (!arrive_last(&cnt[row], nch, &last) || wave != 0) return;
     // the chunk states in chunk order, 64 at a time
     ArgState acc{0.0f, 0u, 0u};
     for (uint32_t c0 = 0; c0 < nch; c0 += 64) {
@@ -158,7 +153,7 @@ extern "C" int lg_dispatch_argmax(const float *logits, uint32_t n, uint32_t rows
     LG_EXTENT(out, (uint64_t)rows * 4, "lg_dispatch_argmax out");
     const uint32_t nch = (n + ARG_CHUNK - 1) / ARG_CHUNK;
     void *ws = nullptr;
-    if (nch > 1) LG_TRY(device_workspace(PROJ_WS_COUNTERS + (uint64_t)rows * nch * 16, &ws));
+    if (nch > 1) LG_TRY(stream_workspace(s, PROJ_WS_COUNTERS + (uint64_t)rows * nch * 16, &ws));
     uint32_t *cnt = static_cast<uint32_t *>(ws);
     uint4 *part = ws ? reinterpret_cast<uint4 *>(static_cast<uint8_t *>(ws) + PROJ_WS_COUNTERS) : nullptr;
     hipLaunchKernelGGL(k_argmax_rows, dim3(nch, rows), dim3(256), 0, s, logits, ld, n, part, cnt, out);

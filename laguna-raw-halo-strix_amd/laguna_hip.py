@@ -62,7 +62,7 @@ SIGNATURES = {
     "lg_tiled_bytes": (_u64, [_i, _u32, _u32]),
     "lg_repack_tiled": (_i, [_vp, _i, _u32, _u32, _vp, _vp]),
     "lg_dispatch_rmsnorm": (_i, [_vp, _vp, _vp, _u32, _u32, _f, _vp]),
-    "lg_dispatch_enc_aux_norm": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _f, _vp]),
+    "lg_dispatch_enc_aux_norm": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "lg_dispatch_qk_norm_rope": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f, _vp]),
     "lg_dispatch_mha_attn": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_gate_mul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
@@ -360,11 +360,10 @@ def dispatch_rmsnorm(ctx, w, x, out, n, rows=1, eps=RMS_EPS):
     check(lib().lg_dispatch_rmsnorm(_ptr(w), _ptr(x), _ptr(out), n, rows, eps, ctx.stream))
 
 
-def dispatch_enc_aux_norm(ctx, x, aux_norm_w, out, n_feat, n_aux, n_total, eps=RMS_EPS):
-    """dispatch_enc_aux_norm (src/dflash.rs:1201-1234); n_total = n_aux * n_feat per token."""
-    n_tokens = n_total // (n_aux * n_feat) if n_aux * n_feat else 0
-    check(lib().lg_dispatch_enc_aux_norm(_ptr(x), _ptr(aux_norm_w), _ptr(out), n_feat, n_aux, n_tokens, eps,
-                                         ctx.stream))
+def dispatch_enc_aux_norm(ctx, x, aux_norm_w, out, n_feat, n_aux, n_total):
+    """dispatch_enc_aux_norm (src/dflash.rs:1200-1233); n_total = n_aux * n_feat per token
+    (eps 1e-5, as the reference)."""
+    check(lib().lg_dispatch_enc_aux_norm(_ptr(x), _ptr(aux_norm_w), _ptr(out), n_feat, n_aux, n_total, ctx.stream))
 
 
 def dispatch_qk_norm_rope(ctx, x, norm_w, freq, out, n_heads, head_dim, rope_dim, pos, rows=1, eps=QK_EPS):
@@ -381,16 +380,14 @@ def dispatch_mha_attn_seq(ctx, q_normed, k_seq, v_seq, out, n_q_heads, n_kv_head
 
 
 def dispatch_gate_mul(ctx, attn_out, v_rep, gate, n_hd, n_heads, head_dim):
-    """dispatch_gate_mul(ctx, shader, attn_out, v_rep, gate, ...) (src/dflash.rs:1236-1266):
-    attn_out[i] = v_rep[i] * gate[i / head_dim] over n_hd = rows * n_heads * head_dim."""
-    rows = n_hd // (n_heads * head_dim) if n_heads * head_dim else 0
-    check(lib().lg_dispatch_gate_mul(_ptr(v_rep), _ptr(gate), _ptr(attn_out), n_heads, head_dim, rows, ctx.stream))
+    """dispatch_gate_mul(ctx, shader, attn_out, v_rep, gate, n_hd, n_heads, head_dim)
+    (src/dflash.rs:1236-1266): attn_out[i] = v_rep[i] * gate[i / head_dim], i < n_hd."""
+    check(lib().lg_dispatch_gate_mul(_ptr(attn_out), _ptr(v_rep), _ptr(gate), n_hd, n_heads, head_dim, ctx.stream))
 
 
 def dispatch_softplus_gate_mul(ctx, attn_out, v_rep, gate, n_hd, n_heads, head_dim):
     """src/dflash.rs:956-959 on the device: gate -> softplus (threshold 20), then gate_mul."""
-    rows = n_hd // (n_heads * head_dim) if n_heads * head_dim else 0
-    check(lib().lg_dispatch_softplus_gate_mul(_ptr(v_rep), _ptr(gate), _ptr(attn_out), n_heads, head_dim, rows,
+    check(lib().lg_dispatch_softplus_gate_mul(_ptr(attn_out), _ptr(v_rep), _ptr(gate), n_hd, n_heads, head_dim,
                                               ctx.stream))
 
 
