@@ -173,6 +173,19 @@ int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, floa
                                  uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                  void *stream);
 
+/* lg_dispatch_proj_quant_batch without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results, bit for bit; the partial sums and arrival counters live
+ * in a fixed 16 MiB + 64 KiB device array that every GPU the library runs on holds
+ * until the process ends (set up by lg_init, or by the first call on a device).
+ * Shapes whose workspace would exceed it (about m * n * 32 bytes for k = 4096,
+ * m <= 32) are LG_EINVAL.  Calls on one GPU share the array: calls that overlap in
+ * time on one GPU, on any stream, race. */
+int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, const void *w, float *c,
+                                        uint32_t k, uint32_t n, uint32_t m, int w_dtype,
+                                        void *stream);
+
 /* Q4_K and Q8_0 weights repacked for the small-M products (no counterpart in the
  * reference, which reads GGUF blocks in place; for callers that load a model once
  * and run many block products).  Tiles hold 16 rows x 256 elements and are stored

@@ -117,6 +117,9 @@ __device__ __forceinline__ bool arrive_last(uint32_t *cnt, uint32_t total, uint3
 // owned by the caller, zeroed before its first use and used by one call at a time
 // (graphs capture it, so it must outlive them).
 uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype);
+// Sets up the allocation-free product's scratch on device `dev` (current); lg_init
+// calls it, and the entry point's first call on a device does otherwise.
+int static_scratch_setup(int dev);
 int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                void *ws, uint64_t ws_bytes, hipStream_t s, const float *res = nullptr);
 

@@ -28,6 +28,7 @@
 // and the last workgroup of a row group to finish (a per-row-group arrival counter,
 // reset by that workgroup) adds the slices in slice order: the result does not
 // depend on which workgroup finishes last.
+#include <mutex>
 #include <vector>
 
 #include "lg_common.hpp"
@@ -919,6 +920,76 @@ extern "C" int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const vo
                                             uint32_t n, uint32_t m, int w_dtype, void *stream) {
     clear_error();
     return lg::proj_batch(x, x_dtype, w, c, k, n, m, w_dtype, nullptr, 0, (hipStream_t)stream);
+}
+
+// ---- allocation-free small-M product
+//
+// lg_dispatch_proj_quant_batch_static runs the same kernels with their arrival
+// counters and partial sums in `scratch`, a file-scope device array that every GPU
+// holds for the life of the process, so the call makes no allocation (for code
+// under HIP graph capture, serving loops and callers that may not allocate).  Host
+// code uses the address hipGetSymbolAddress returns for the current device, never
+// the array's name.  Calls on one GPU share the array: calls that overlap in time on
+// that GPU, on any stream, race.
+constexpr uint64_t STATIC_SCRATCH_BYTES = PROJ_WS_COUNTERS + (16ull << 20);
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int STATIC_MAX_DEVICES = 64;
+std::mutex g_static_mu;
+void *g_static_ptr[STATIC_MAX_DEVICES] = {};
+
+__global__ __launch_bounds__(256) void k_zero_words(uint32_t *p, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// The scratch address on device `dev` (current), set up once: its arrival counters
+// are cleared on stream s with a kernel (the set-up may happen inside a capture,
+// where a memset node must not be recorded).
+int static_scratch(int dev, hipStream_t s, bool wait, void **out) {
+    LG_REQUIRE(dev >= 0 && dev < STATIC_MAX_DEVICES, "static scratch: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void *p = nullptr;
+        LG_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        LG_REQUIRE(p, "static scratch: no address on device %d", dev);
+        const uint32_t words = (uint32_t)(PROJ_WS_COUNTERS / 4);
+        hipLaunchKernelGGL(k_zero_words, dim3((words + 255) / 256), dim3(256), 0, s, static_cast<uint32_t *>(p), words);
+        LG_HIP_TRY(hipGetLastError());
+        if (wait) LG_HIP_TRY(hipStreamSynchronize(s));
+        g_static_ptr[dev] = p;
+    }
+    *out = g_static_ptr[dev];
+    return LG_OK;
+}
+
+}  // namespace
+
+namespace lg {
+
+int static_scratch_setup(int dev) {
+    void *p = nullptr;
+    return static_scratch(dev, nullptr, true, &p);
+}
+
+}  // namespace lg
+
+extern "C" int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, const void *w, float *c, uint32_t k,
+                                                   uint32_t n, uint32_t m, int w_dtype, void *stream) {
+    clear_error();
+    const char *name = "lg_dispatch_proj_quant_batch_static";
+    if (n == 0 || m == 0) return LG_OK;
+    const uint64_t need = lg::proj_batch_ws_bytes(k, n, m < 32 ? m : 32, x_dtype, w_dtype);
+    LG_REQUIRE(need <= STATIC_SCRATCH_BYTES,
+               "%s: k=%u n=%u m=%u needs %llu bytes of scratch, more than the %llu this entry point has", name, k, n,
+               m, (unsigned long long)need, (unsigned long long)STATIC_SCRATCH_BYTES);
+    int dev = 0;
+    LG_HIP_TRY(hipGetDevice(&dev));
+    void *ws = nullptr;
+    LG_TRY(static_scratch(dev, (hipStream_t)stream, false, &ws));
+    return lg::proj_batch(x, x_dtype, w, c, k, n, m, w_dtype, ws, STATIC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
 extern "C" int lg_dispatch_silu_gate_up_batch(const float *x, const void *w_gate, const void *w_up, float *h,

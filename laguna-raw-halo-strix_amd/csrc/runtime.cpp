@@ -175,6 +175,7 @@ int lg_init(int device) {
     LG_REQUIRE(device >= 0 && device < n, "lg_init: device %d out of range (%d devices)", device, n);
     LG_HIP_TRY(hipSetDevice(device));
     LG_HIP_TRY(hipFree(nullptr));  // create the context now, not inside the first timed call
+    LG_TRY(static_scratch_setup(device));
     clear_error();
     return LG_OK;
 }

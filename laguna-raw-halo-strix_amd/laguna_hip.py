@@ -57,6 +57,7 @@ SIGNATURES = {
     "lg_dispatch_activation": (_i, [_vp, _vp, _vp, _u32, _vp]),
     "lg_dispatch_silu_mul_proj_quant": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _i, _vp]),
     "lg_dispatch_proj_quant_batch": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
+    "lg_dispatch_proj_quant_batch_static": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_silu_gate_up_batch": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_argmax": (_i, [_vp, _u32, _u32, _u64, _vp, _vp]),
     "lg_tiled_bytes": (_u64, [_i, _u32, _u32]),
