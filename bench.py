@@ -3,28 +3,48 @@
 Headline (`value`): GGUF Q4_K matvec, 4096 -> 14336, M = 1, in GB/s of algorithmic
 bytes (raw weight blocks + activations read + outputs written) with the inputs
 resident in HBM.  A step is one call of the hot path on one weight copy; the
-copies rotate through a pool of more than 1 GiB so that no timed call is served
-from the 256 MB Infinity Cache.  Kernel time is taken with HIP events recorded on
-the stream the kernels run on.
+copies rotate through a pool of more than 1 GiB, so no timed call is served from
+the 256 MB Infinity Cache.
 
-Also reported under "extra": the Q8_0 4096x4096 M=1 matvec, the fused
-SiLU(gate)*up + Q4_K 14336 -> 4096 down projection, the M = 16 block-verify
-products (Q4_K 4096 -> 14336 with bf16 and f32 activations, Q8_0 4096 -> 4096
-with f32 activations), and the 6-layer draft decoder's 16-token block forward
-over a 2048-position context (HIP graph replay and eager), in us per block, draft
-tokens/s and GB/s of algorithmic bytes (every weight, the context K/V, inputs
-and outputs once per block).
+Method, for every workload: W warmup calls, then R = 10 repetitions of
+L = max(--steps, 200) back-to-back calls, each repetition timed with HIP events
+recorded on the stream the calls are issued on; the per-call time is the median
+over the repetitions.  The same L calls are also captured once into a HIP graph
+on that stream and the graph replayed R times ("graph" figures: the host's
+issue cost is then out of the picture).  `value` and `ms_per_step` are the
+stream figures.  One window of exactly --steps calls between two stream
+synchronisations is reported beside them.
 
-`cpu_baseline`: the same Q4_K matvec computed by the oracle (a C restatement of
-kernels/proj_q4k.comp's per-element decode and f32 accumulation) on the host
-cores, over a bounded sample of output rows.
+Also reported under "extra":
+* the Q8_0 4096x4096 M=1 matvec, the fused SiLU(gate)*up + Q4_K 14336 -> 4096
+  down projection, and Q4_K 20480 -> 4096 (k above 16384: the per-element path);
+* the M = 16 block-verify products (Q4_K 4096 -> 14336 with bf16 and f32
+  activations, Q8_0 4096 -> 4096 with f32 activations, raw blocks and 16-row
+  tiles), the vocab-sized LM head at M = 1 and M = 16, and that head plus the
+  argmax of every row;
+* the 6-layer draft decoder's 16-token block forward over a 2048-position
+  context (HIP graph replay and eager), in us per block, draft tokens/s and
+  GB/s of algorithmic bytes (every weight, the context K/V, inputs and outputs
+  once per block);
+* ceilings: an empty kernel, and a plain streaming read (lg_bench_read) of
+  17.8, 33.0 and 350 MB buffers through the same kind of rotating pool; the
+  headline's roofline carries its fraction of both 8 TB/s and the measured read
+  of its own byte count.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+`cpu_baseline`: the oracle (the C restatement of the reference's CPU and shader
+arithmetic) on the host cores: Q8_0 dequant_to_f32 of the 4096x4096 tensor, the
+f32 matvec in proj.comp order on 4096x4096 f32 weights, and the fused Q4_K matvec
+in proj_q4k.comp order on the headline workload, each on one thread and on the
+process's CPU share.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-extra] [--no-cpu]
 """
 import argparse
 import ctypes
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 
@@ -39,80 +59,130 @@ import synth  # noqa: E402
 PEAK_HBM_GBS = 8000.0
 METRIC = "Q4_K/Q8_0 matvec HBM GB/s (% of peak) M=1; 6-layer draft block fwd µs"
 POOL_BYTES = 1 << 30
+REPS = 10
+MIN_LAUNCHES = 200
+CAPTURE_THREAD_LOCAL = 1
 
 
-class HipEvents:
-    """hipEvent timing through the HIP runtime the library itself uses."""
+class Hip:
+    """HIP events, stream capture and graphs through the runtime the library uses."""
 
     def __init__(self):
-        self.hip = ctypes.CDLL("libamdhip64.so")
-        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
-        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
-        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
-        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        h = ctypes.CDLL("libamdhip64.so")
+        vp, pvp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        h.hipEventCreate.argtypes = [pvp]
+        h.hipEventRecord.argtypes = [vp, vp]
+        h.hipEventSynchronize.argtypes = [vp]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        h.hipEventDestroy.argtypes = [vp]
+        h.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        h.hipStreamEndCapture.argtypes = [vp, pvp]
+        h.hipGraphInstantiate.argtypes = [pvp, vp, vp, vp, ctypes.c_size_t]
+        h.hipGraphLaunch.argtypes = [vp, vp]
+        h.hipGraphExecDestroy.argtypes = [vp]
+        h.hipGraphDestroy.argtypes = [vp]
+        self.h = h
+        self.a, self.b = self._event(), self._event()
 
-    def new(self):
+    def _event(self):
         e = ctypes.c_void_p()
-        assert self.hip.hipEventCreate(ctypes.byref(e)) == 0
+        assert self.h.hipEventCreate(ctypes.byref(e)) == 0
         return e
 
-    def record(self, e, stream):
-        assert self.hip.hipEventRecord(e, stream) == 0
-
-    def elapsed_ms(self, a, b):
-        assert self.hip.hipEventSynchronize(b) == 0
+    def time_ms(self, stream, fn):
+        """Elapsed GPU time of the work fn() issues on `stream`."""
+        assert self.h.hipEventRecord(self.a, stream) == 0
+        fn()
+        assert self.h.hipEventRecord(self.b, stream) == 0
+        assert self.h.hipEventSynchronize(self.b) == 0
         ms = ctypes.c_float()
-        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        assert self.h.hipEventElapsedTime(ctypes.byref(ms), self.a, self.b) == 0
         return ms.value
+
+    def capture(self, stream, fn):
+        """A graph executable holding the work fn() issues on `stream`."""
+        g, ge = ctypes.c_void_p(), ctypes.c_void_p()
+        assert self.h.hipStreamBeginCapture(stream, CAPTURE_THREAD_LOCAL) == 0
+        try:
+            fn()
+        finally:
+            st = self.h.hipStreamEndCapture(stream, ctypes.byref(g))
+        assert st == 0, f"hipStreamEndCapture {st}"
+        assert self.h.hipGraphInstantiate(ctypes.byref(ge), g, None, None, 0) == 0
+        self.h.hipGraphDestroy(g)
+        return ge
+
+
+def _pool(ctx, raw, tiled=None):
+    """Copies of `raw` (device buffers) filling more than POOL_BYTES; `tiled` =
+    (dtype, k, n) repacks each copy into 16-row tiles."""
+    copies = max(2, -(-POOL_BYTES // raw.nbytes))
+    pool = []
+    for _ in range(copies):
+        b = lh.GpuBuffer(ctx, raw.nbytes)
+        b.upload(raw)
+        if tiled is not None:
+            t = lh.repack_tiled(ctx, b, *tiled)
+            ctx.sync()
+            b.free()
+            b = t
+        pool.append(b)
+    return pool, copies * raw.nbytes
 
 
 class Workload:
     name = ""
     bytes_per_call = 0
+    graph_mode = True  # the calls can be captured into a HIP graph
+    kernel = None      # the kernel a rocprof trace of this workload shows
 
     def setup(self, ctx):
         raise NotImplementedError
 
-    def step(self, ctx, i):
+    def step(self, i, stream):
         raise NotImplementedError
+
+    def teardown(self):
+        for p in getattr(self, "pool", []):
+            p.free()
+        self.pool = []
 
 
 class MatvecM1(Workload):
-    def __init__(self, dtype, k, n, seed, fused=False):
-        self.dtype, self.k, self.n, self.seed, self.fused = dtype, k, n, seed, fused
-        wbytes = synth.weight_bytes(dtype, k, n)
-        xbytes = 4 * k * (2 if fused else 1)
-        self.bytes_per_call = wbytes + xbytes + 4 * n
+    def __init__(self, dtype, k, n, seed, fused=False, kernel=None):
+        self.dtype, self.k, self.n, self.seed, self.fused, self.kernel = dtype, k, n, seed, fused, kernel
+        self.bytes_per_call = synth.weight_bytes(dtype, k, n) + 4 * k * (2 if fused else 1) + 4 * n
         tag = {lh.Q4_K: "Q4_K", lh.Q8_0: "Q8_0"}[dtype]
         self.name = (f"fused SiLU(gate)*up + {tag} matvec {k}->{n} M=1" if fused else f"{tag} matvec {k}->{n} M=1")
 
     def setup(self, ctx):
         k, n = self.k, self.n
         raw = synth.q4k_weight(self.seed, k, n) if self.dtype == lh.Q4_K else synth.q8_0_weight(self.seed, k, n)
-        copies = max(2, -(-POOL_BYTES // raw.nbytes))
-        self.pool = []
-        for _ in range(copies):
-            b = lh.GpuBuffer(ctx, raw.nbytes)
-            b.upload(raw)
-            self.pool.append(b)
-        self.pool_bytes = copies * raw.nbytes
+        self.pool, self.pool_bytes = _pool(ctx, raw)
         self.x = lh.upload_f32(ctx, synth.normal(self.seed + 1, k))
         self.up = lh.upload_f32(ctx, synth.normal(self.seed + 2, k)) if self.fused else None
         self.c = lh.GpuBuffer(ctx, 4 * n)
 
-    def step(self, ctx, i):
+    def step(self, i, stream):
         w = self.pool[i % len(self.pool)]
+        L = lh.lib()
         if self.fused:
-            lh.dispatch_silu_mul_proj_quant(ctx, self.x, self.up, w, self.c, self.k, self.n, self.dtype)
+            lh.check(L.lg_dispatch_silu_mul_proj_quant(self.x.ptr, self.up.ptr, w.ptr, self.c.ptr, self.k, self.n,
+                                                       self.dtype, stream))
         else:
-            lh.dispatch_proj_quant(ctx, self.x, w, self.c, self.k, self.n, self.dtype)
+            lh.check(L.lg_dispatch_proj_quant(self.x.ptr, w.ptr, self.c.ptr, self.k, self.n, self.dtype, stream))
+
+    def teardown(self):
+        super().teardown()
+        for b in (self.x, self.up, self.c):
+            if b is not None:
+                b.free()
 
 
 class BatchM16(Workload):
-    def __init__(self, dtype, k, n, x_dtype, seed, m=16, tiled=False):
+    def __init__(self, dtype, k, n, x_dtype, seed, m=16, tiled=False, kernel=None):
         self.dtype, self.k, self.n, self.x_dtype, self.seed, self.m = dtype, k, n, x_dtype, seed, m
-        self.tiled = tiled
+        self.tiled, self.kernel = tiled, kernel
         xb = 2 if x_dtype == lh.BF16 else 4
         self.bytes_per_call = synth.weight_bytes(dtype, k, n) + m * k * xb + 4 * m * n
         tag = {lh.Q4_K: "Q4_K", lh.Q8_0: "Q8_0"}[dtype]
@@ -122,18 +192,7 @@ class BatchM16(Workload):
     def setup(self, ctx):
         k, n, m = self.k, self.n, self.m
         raw = synth.q4k_weight(self.seed, k, n) if self.dtype == lh.Q4_K else synth.q8_0_weight(self.seed, k, n)
-        copies = max(2, -(-POOL_BYTES // raw.nbytes))
-        self.pool = []
-        for _ in range(copies):
-            b = lh.GpuBuffer(ctx, raw.nbytes)
-            b.upload(raw)
-            if self.tiled:  # the same bytes, permuted into 16-row tiles
-                t = lh.repack_tiled(ctx, b, self.dtype, k, self.n)
-                ctx.sync()
-                b.free()
-                b = t
-            self.pool.append(b)
-        self.pool_bytes = copies * raw.nbytes
+        self.pool, self.pool_bytes = _pool(ctx, raw, (self.dtype, k, n) if self.tiled else None)
         x = synth.normal(self.seed + 0x100, m * k)
         if self.x_dtype == lh.BF16:
             u = x.view(np.uint32).astype(np.uint64)
@@ -141,10 +200,16 @@ class BatchM16(Workload):
         self.x = lh.upload_bytes(ctx, x.view(np.uint8))
         self.c = lh.GpuBuffer(ctx, 4 * m * n)
 
-    def step(self, ctx, i):
+    def step(self, i, stream):
         w = self.pool[i % len(self.pool)]
-        lh.dispatch_proj_quant_batch(ctx, self.x, self.x_dtype, w, self.c, self.k, self.n, self.m,
-                                     lh.TILED[self.dtype] if self.tiled else self.dtype)
+        wt = lh.TILED[self.dtype] if self.tiled else self.dtype
+        lh.check(lh.lib().lg_dispatch_proj_quant_batch(self.x.ptr, self.x_dtype, w.ptr, self.c.ptr, self.k, self.n,
+                                                       self.m, wt, stream))
+
+    def teardown(self):
+        super().teardown()
+        self.x.free()
+        self.c.free()
 
 
 class VerifyBlock(BatchM16):
@@ -161,25 +226,30 @@ class VerifyBlock(BatchM16):
         super().setup(ctx)
         self.idx = lh.GpuBuffer(ctx, 4 * self.m)
 
-    def step(self, ctx, i):
-        super().step(ctx, i)
-        lh.check(lh.lib().lg_dispatch_argmax(self.c.ptr, self.n, self.m, self.n, self.idx.ptr, ctx.stream))
+    def step(self, i, stream):
+        super().step(i, stream)
+        lh.check(lh.lib().lg_dispatch_argmax(self.c.ptr, self.n, self.m, self.n, self.idx.ptr, stream))
+
+    def teardown(self):
+        super().teardown()
+        self.idx.free()
 
 
 class DFlashBlock(Workload):
     """The 6-layer draft decoder's block forward: 16 tokens over a 2048-position f32
-    K/V context, random-init weights (Q4_K except Q8_0 attn_output), replayed as a
-    captured HIP graph.  One forward reads every weight once (917 MB > the 256 MB
-    Infinity Cache), so a single model copy needs no rotation."""
+    K/V context, random-init weights (Q4_K except Q8_0 attn_output), either replayed
+    as the captured HIP graph or launched eagerly.  One forward reads every weight
+    once (917 MB > the 256 MB Infinity Cache), so one model copy needs no rotation."""
+
+    graph_mode = False  # the forward is itself a graph (or its eager launches)
 
     def __init__(self, m=16, ctx_len=2048, seed=0x5EED000A, graph=True):
-        self.m, self.ctx_len, self.seed, self.graph_mode = m, ctx_len, seed, graph
+        self.m, self.ctx_len, self.seed, self.as_graph = m, ctx_len, seed, graph
         self.cfg = lh.DFlashConfig()
-        self.k, self.n = self.cfg.n_embd, self.cfg.n_embd
         self.name = (f"DFlash 6-layer block forward, {m} tokens over {ctx_len}-position f32 KV "
                      f"({'HIP graph' if graph else 'eager'})")
 
-    def setup(self, ctx):
+    def setup(self, ctx, stream=None):
         cfg, m = self.cfg, self.m
         W, layers = synth.dflash_model(self.seed, cfg, cfg.n_layers)
         feat, tok, kc, vc = synth.dflash_inputs(self.seed + 1, cfg, cfg.n_layers, m, self.ctx_len)
@@ -193,111 +263,208 @@ class DFlashBlock(Workload):
         del W, layers, kc, vc
         self.fb, self.tb = lh.upload_f32(ctx, feat), lh.upload_f32(ctx, tok)
         self.ob = lh.GpuBuffer(ctx, 4 * m * cfg.n_embd)
-        self.stream = lh.Stream()
-        self.g = self.model.capture(self.fb, self.tb, m, self.ob, self.stream) if self.graph_mode else None
-        self.pool = [self.fb, self.tb, self.ob]
         self.pool_bytes = self.bytes_per_call
+        if self.as_graph and stream is None:
+            self.own_stream = stream = lh.Stream()
+        self.g = self.model.capture(self.fb, self.tb, m, self.ob, stream) if self.as_graph else None
 
-    def step(self, ctx, i):
+    def step(self, i, stream):
         if self.g is not None:
-            self.g.launch()
+            lh.check(lh.lib().lg_dflash_graph_launch(self.g.ptr, stream))
         else:
-            self.model.forward_block_device(self.fb, self.tb, self.m, self.ob, stream=self.stream)
+            self.model.forward_block_device(self.fb, self.tb, self.m, self.ob, stream=stream)
 
     def teardown(self):
         if self.g is not None:
             self.g.destroy()
         self.model.free()
-        self.stream.sync()
+        for b in (self.fb, self.tb, self.ob):
+            b.free()
 
 
+class Empty(Workload):
+    def __init__(self, workgroups=256):
+        self.wg = workgroups
+        self.name = f"empty kernel, {workgroups} workgroups"
+        self.kernel = "k_empty"
+
+    def setup(self, ctx):
+        self.pool, self.pool_bytes = [], 0
+
+    def step(self, i, stream):
+        lh.check(lh.lib().lg_bench_empty(self.wg, stream))
+
+
+class Read(Workload):
+    def __init__(self, nbytes):
+        self.bytes_per_call = nbytes
+        self.name = f"streaming read of {nbytes / 1e6:.1f} MB (one-shot, 32 KiB per workgroup)"
+        self.kernel = "k_read"
+
+    def setup(self, ctx):
+        copies = max(2, -(-POOL_BYTES // self.bytes_per_call))
+        self.pool = [lh.GpuBuffer(ctx, self.bytes_per_call) for _ in range(copies)]
+        for p in self.pool:
+            p.fill(1)
+        ctx.sync()
+        self.pool_bytes = copies * self.bytes_per_call
+
+    def step(self, i, stream):
+        w = self.pool[i % len(self.pool)]
+        lh.check(lh.lib().lg_bench_read(w.ptr, self.bytes_per_call, stream))
+
+
+HEAD_KERNEL = "k_q4k_m1_rows"
 WORKLOADS = {
-    "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003),
-    "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001),
-    "q4k_down_silu": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, fused=True),
-    "q4k_m16_bf16": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008),
-    "q4k_m16_f32": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008),
-    "q4k_m16_f32_tiled": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008, tiled=True),
-    "q8_0_m16_f32": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009),
-    "q8_0_m16_f32_tiled": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009, tiled=True),
+    "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003, kernel=HEAD_KERNEL),
+    "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001, kernel="k_q80_m1"),
+    "q4k_down_silu": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, fused=True, kernel="k_q4k_m1_mfma"),
+    "q4k_m1_k20480": lambda: MatvecM1(lh.Q4_K, 20480, 4096, 0x5EED000C, kernel="k_generic_m1"),
+    "q4k_m16_bf16": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.BF16, 0x5EED0008, kernel="k_q4k_mm"),
+    "q4k_m16_f32": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008, kernel="k_q4k_mm"),
+    "q4k_m16_f32_tiled": lambda: BatchM16(lh.Q4_K, 4096, 14336, lh.F32, 0x5EED0008, tiled=True, kernel="k_q4k_mm"),
+    "q8_0_m16_f32": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009, kernel="k_q80_mm"),
+    "q8_0_m16_f32_tiled": lambda: BatchM16(lh.Q8_0, 4096, 4096, lh.F32, 0x5EED0009, tiled=True, kernel="k_q80_mm"),
     # vocab-sized output projection (the LM head, src/target.rs:580-605): M=1 for one
     # token, M=16 to verify a 16-token draft block
-    "q4k_lm_head_m1": lambda: MatvecM1(lh.Q4_K, 4096, 151936, 0x5EED000B),
-    "q4k_lm_head_m16": lambda: BatchM16(lh.Q4_K, 4096, 151936, lh.F32, 0x5EED000B),
+    "q4k_lm_head_m1": lambda: MatvecM1(lh.Q4_K, 4096, 151936, 0x5EED000B, kernel=HEAD_KERNEL),
+    "q4k_lm_head_m16": lambda: BatchM16(lh.Q4_K, 4096, 151936, lh.F32, 0x5EED000B, kernel="k_q4k_mm"),
     "lm_head_verify_m16": lambda: VerifyBlock(4096, 151936, 0x5EED000B),
     "dflash_block": lambda: DFlashBlock(),
     "dflash_block_eager": lambda: DFlashBlock(graph=False),
+    "ceil_empty": lambda: Empty(256),
+    "ceil_read_17.8MB": lambda: Read(17858560),
+    "ceil_read_33.1MB": lambda: Read(33103872),
+    "ceil_read_350MB": lambda: Read(350684672),
 }
+EXTRA = ["q8_0_m1", "q4k_down_silu", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
+         "q8_0_m16_f32", "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16",
+         "dflash_block", "dflash_block_eager", "ceil_empty", "ceil_read_17.8MB", "ceil_read_33.1MB",
+         "ceil_read_350MB"]
 
 
-def time_workload(ctx, ev, wl, steps, warmup):
-    wl.setup(ctx)
-    stream = wl.stream.ptr if getattr(wl, "stream", None) is not None else ctx.stream
-    sync = wl.stream.sync if getattr(wl, "stream", None) is not None else ctx.sync
-    for i in range(warmup):
-        wl.step(ctx, i)
-    sync()
-    a, b = ev.new(), ev.new()
+def time_workload(ctx, hip, wl, steps, warmup, launches=None):
+    """Per-call us: median over REPS repetitions of `launches` back-to-back calls,
+    issued from the host (stream) and replayed from one captured graph (graph), plus
+    one window of exactly `steps` calls."""
+    L = launches or max(steps, MIN_LAUNCHES)
+    stream = lh.Stream()
+    s = stream.ptr
     t0 = time.perf_counter()
-    ev.record(a, stream)
-    for i in range(steps):
-        wl.step(ctx, warmup + i)
-    ev.record(b, stream)
-    sync()
-    wall = time.perf_counter() - t0
-    ms = ev.elapsed_ms(a, b)
-    us = 1000.0 * ms / steps
-    gbs = wl.bytes_per_call / (us * 1e-6) / 1e9
-    for p in wl.pool:
-        p.free()
-    wl.pool = []
-    if hasattr(wl, "teardown"):
-        wl.teardown()
-    r = {"workload": wl.name, "us_per_call": round(us, 3), "GBps": round(gbs, 1),
-         "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_call": wl.bytes_per_call,
-         "pool_MB": round(wl.pool_bytes / 2 ** 20, 1), "host_wall_s": round(wall, 4)}
+    if isinstance(wl, DFlashBlock):
+        wl.setup(ctx, stream)
+    else:
+        wl.setup(ctx)
+    for i in range(warmup):
+        wl.step(i, s)
+    stream.sync()
+    t_issue0 = time.perf_counter()
+    ms_window = hip.time_ms(s, lambda: [wl.step(warmup + i, s) for i in range(steps)])
+    reps = []
+    for r in range(REPS):
+        reps.append(1000.0 * hip.time_ms(s, lambda: [wl.step(r * L + i, s) for i in range(L)]) / L)
+    host_s = time.perf_counter() - t_issue0
+    us = statistics.median(reps)
+    r = {"workload": wl.name, "us_per_call": round(us, 3), "launches_per_rep": L, "reps": REPS,
+         "us_spread": [round(min(reps), 3), round(max(reps), 3)],
+         "us_per_call_steps_window": round(1000.0 * ms_window / max(steps, 1), 3), "steps_window": steps}
+    if wl.graph_mode:
+        ge = hip.capture(s, lambda: [wl.step(i, s) for i in range(L)])
+        hip.h.hipGraphLaunch(ge, s)
+        stream.sync()
+        g = [1000.0 * hip.time_ms(s, lambda: hip.h.hipGraphLaunch(ge, s)) / L for _ in range(REPS)]
+        hip.h.hipGraphExecDestroy(ge)
+        r["us_per_call_graph"] = round(statistics.median(g), 3)
+    if wl.bytes_per_call:
+        gbs = wl.bytes_per_call / (us * 1e-6) / 1e9
+        r.update({"GBps": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4),
+                  "bytes_per_call": wl.bytes_per_call, "pool_MB": round(wl.pool_bytes / 2 ** 20, 1)})
+        if "us_per_call_graph" in r:
+            r["GBps_graph"] = round(wl.bytes_per_call / (r["us_per_call_graph"] * 1e-6) / 1e9, 1)
     if isinstance(wl, DFlashBlock):
         r["draft_tokens_per_s"] = round(wl.m / (us * 1e-6), 1)
+    if wl.kernel:
+        r["kernel"] = wl.kernel
+    r["host_wall_s"] = round(time.perf_counter() - t0, 3)
+    r["host_issue_s"] = round(host_s, 3)
+    wl.teardown()
+    stream.sync()
+    stream.destroy()
     return r
 
 
-def cpu_baseline(budget_s=12.0):
-    """The oracle's proj_q4k.comp-order matvec (per-element decode, f32 accumulation)
-    on the host cores, on the same 4096 -> 14336 Q4_K workload: the whole matvec
-    repeated on `threads` OpenMP threads for about budget_s/2 seconds, and a
-    bounded sample of output rows on one thread for the other half."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_threads():
+    """The process's CPU share: OMP_NUM_THREADS when set, else the CPUs it may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def _rate(fn, nbytes, budget_s):
+    """Bytes per second of fn() repeated for at least budget_s (at least twice)."""
+    reps, t = 0, 0.0
+    while t < budget_s or reps < 2:
+        t0 = time.perf_counter()
+        fn()
+        t += time.perf_counter() - t0
+        reps += 1
+    return reps * nbytes / t, reps, t
+
+
+def cpu_baseline(budget_s=2.0):
+    """The oracle on the host: three legs, each on one thread and on the CPU share."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as orc
 
+    nthr = cpu_threads()
+    legs = {}
+    # 1. dequant_to_f32 of a Q8_0 tensor (src/dflash.rs:379-397), the load-time cost
+    q8 = synth.q8_0_weight(0x5EED0001, 4096, 4096)
+    n_el = 4096 * 4096
+    for t in (1, nthr):
+        fn = (lambda: orc.dequant_to_f32(q8, orc.Q8_0, n_el)) if t == 1 else (lambda: orc.dequant_q8_0_mt(q8, n_el, t))
+        bps, reps, secs = _rate(fn, q8.nbytes, budget_s)
+        legs[f"dequant_q8_0_4096x4096_t{t}"] = {"GBps": round(bps / 1e9, 4), "Melem_per_s": round(bps / q8.nbytes *
+                                                                                                 n_el / 1e6, 1),
+                                                "threads": t, "calls": reps, "seconds": round(secs, 2)}
+    # 2. the f32 matvec in kernels/proj.comp order (the reference draft's projections)
+    wf = synth.normal(0x5EED0101, 4096 * 4096, 0.02)
+    xf = synth.normal(0x5EED0102, 4096)
+    for t in (1, nthr):
+        bps, reps, secs = _rate(lambda: orc.proj_f32(xf, wf, 4096, 4096, threads=t), wf.nbytes + 4 * 4096 + 4 * 4096,
+                                budget_s)
+        legs[f"proj_f32_4096x4096_t{t}"] = {"GBps": round(bps / 1e9, 4), "threads": t, "calls": reps,
+                                            "seconds": round(secs, 2)}
+    del wf
+    # 3. the fused Q4_K matvec in kernels/proj_q4k.comp order on the headline workload
     k, n = 4096, 14336
-    threads = max(1, min(16, os.cpu_count() or 1))
-    raw = synth.q4k_weight(0x5EED0003, k, n)
+    q4 = synth.q4k_weight(0x5EED0003, k, n)
     x = synth.normal(0x5EED0004, k)
-    bytes_per_row = (k // 256) * 144 + 4
-    # multi-threaded: whole matvecs
-    reps, t_mt = 0, 0.0
-    while t_mt < budget_s / 2 or reps < 2:
-        t0 = time.perf_counter()
-        orc.proj_q4k(x, raw, k, n, threads=threads)
-        t_mt += time.perf_counter() - t0
-        reps += 1
-    gbs_mt = reps * (n * bytes_per_row + 4 * k) / t_mt / 1e9
-    # single thread: consecutive 512-row blocks (wrapping) until the budget is spent
-    rows, t_st = 0, 0.0
-    while t_st < budget_s / 2:
-        r0 = rows % n
-        r = min(512, n - r0)
-        sub = raw[r0 * (k // 256) * 144:(r0 + r) * (k // 256) * 144]
-        t0 = time.perf_counter()
-        orc.proj_q4k(x, sub, k, r, threads=1)
-        t_st += time.perf_counter() - t0
-        rows += r
-    gbs_st = (rows * bytes_per_row + 4 * k) / t_st / 1e9
-    return {"value": round(gbs_mt, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "single_thread_GBps": round(gbs_st, 4),
-            "sample": f"oracle restatement of kernels/proj_q4k.comp (f32 per-element decode) on Q4_K "
-                      f"4096->14336 M=1: {reps} full matvecs on {threads} threads in {t_mt:.1f} s; "
-                      f"single thread {rows} rows in {t_st:.1f} s"}
+    nbytes = q4.nbytes + 4 * k + 4 * n
+    for t in (1, nthr):
+        bps, reps, secs = _rate(lambda: orc.proj_q4k(x, q4, k, n, threads=t), nbytes, budget_s)
+        legs[f"proj_q4k_4096x14336_t{t}"] = {"GBps": round(bps / 1e9, 4), "threads": t, "calls": reps,
+                                             "seconds": round(secs, 2)}
+    head = legs[f"proj_q4k_4096x14336_t{nthr}"]
+    return {"value": head["GBps"], "unit": "GB/s", "cores": nthr, "kind": "port",
+            "cpu_model": cpu_model(), "cpu_count": os.cpu_count(), "legs": legs,
+            "sample": f"oracle (C, -O2, no FMA contraction) on the host: Q8_0 dequant_to_f32 of 4096x4096, f32 "
+                      f"proj.comp-order matvec 4096x4096, fused Q4_K proj_q4k.comp-order matvec 4096->14336 (the "
+                      f"value); whole calls repeated for about {budget_s:.0f} s each on 1 and {nthr} threads"}
 
 
 CAL_BYTES = 64 << 20  # lg_buf_copy size that hardware traffic counters are calibrated against
@@ -325,18 +492,19 @@ def pmc_run(ctx, wl, steps):
     ctx.sync()
     a.free()
     b.free()
-    wl.setup(ctx)
+    wl.setup(ctx) if not isinstance(wl, DFlashBlock) else wl.setup(ctx, None)
     for i in range(steps):
-        wl.step(ctx, i)
+        wl.step(i, None)
     ctx.sync()
+    wl.teardown()
     print(json.dumps({"pmc_run": wl.name, "steps": steps, "calibration_copy_bytes": CAL_BYTES}), flush=True)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="q4k_m1", choices=sorted(WORKLOADS))
     ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -352,18 +520,29 @@ def main():
     if args.pmc:
         pmc_run(ctx, WORKLOADS[args.workload](), args.steps)
         return
-    ev = HipEvents()
+    hip = Hip()
     wl = WORKLOADS[args.workload]()
-    head = time_workload(ctx, ev, wl, args.steps, args.warmup)
+    head = time_workload(ctx, hip, wl, args.steps, args.warmup)
+    print(f"# {args.workload}: {head['us_per_call']} us/call (graph {head.get('us_per_call_graph')})",
+          file=sys.stderr, flush=True)
     extra = {}
     if not args.no_extra:
-        for name in ["q8_0_m1", "q4k_down_silu", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled", "q8_0_m16_f32",
-                     "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16"]:
+        for name in EXTRA:
             if name != args.workload:
-                extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(50, args.steps // 4), 20)
-        for name in ["dflash_block", "dflash_block_eager"]:
-            if name != args.workload:
-                extra[name] = time_workload(ctx, ev, WORKLOADS[name](), max(10, args.steps // 40), 3)
+                w = WORKLOADS[name]()
+                extra[name] = time_workload(ctx, hip, w, args.steps, max(3, args.warmup // 4))
+                print(f"# {name}: {extra[name]['us_per_call']} us/call", file=sys.stderr, flush=True)
+    roof = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": head["frac_of_peak"], "traffic": traffic_from_profile(args.workload),
+            "us_per_call": head["us_per_call"], "algorithmic_bytes": head["bytes_per_call"],
+            "kernel": wl.kernel}
+    ceil = extra.get("ceil_read_33.1MB") if args.workload == "q4k_m1" else None
+    if ceil:
+        roof.update({"ceiling_read_GBps": ceil["GBps"], "frac_of_ceiling_read": round(head["GBps"] / ceil["GBps"], 4),
+                     "ceiling_read_us": ceil["us_per_call"]})
+    if "ceil_empty" in extra:
+        roof["empty_launch_us"] = extra["ceil_empty"]["us_per_call"]
+        roof["empty_launch_us_graph"] = extra["ceil_empty"].get("us_per_call_graph")
     line = {
         "metric": METRIC,
         "value": head["GBps"],
@@ -378,10 +557,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded SplitMix64: random valid Q4_K blocks, ggml-quantized Q8_0, N(0,1) activations)",
         "config": {"workload": head["workload"], "k": wl.k, "n": wl.n, "m": getattr(wl, "m", 1),
-                   "weight_pool_MB": head["pool_MB"], "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": traffic_from_profile(args.workload),
-                     "us_per_call": head["us_per_call"], "algorithmic_bytes": head["bytes_per_call"]},
+                   "weight_pool_MB": head["pool_MB"], "parallelism": "single GPU",
+                   "timing": f"median of {REPS} x {head['launches_per_rep']} back-to-back calls"},
+        "graph_us_per_call": head.get("us_per_call_graph"),
+        "roofline": roof,
         "extra": extra,
     }
     if not args.no_cpu:

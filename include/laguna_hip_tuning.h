@@ -1,11 +1,9 @@
 /*
- * laguna_hip_tuning.h -- launch-shape hooks of liblaguna_hip.so for sweeps.
+ * laguna_hip_tuning.h -- launch-shape hooks and ceiling kernels of
+ * liblaguna_hip.so, for sweeps and measurement.
  *
- * Not part of the drop-in boundary (laguna_hip.h): the reference's Vulkan shaders
- * have fixed workgroup counts, and these hooks have no counterpart there.  Each
- * sets a process-wide value (an atomic, read at every launch); 0 restores the
- * automatic choice.  Every setting meets the same parity bound, and results are
- * repeatable for a fixed setting.
+ * Not part of the drop-in boundary (laguna_hip.h), and without counterparts in the
+ * reference, whose Vulkan shaders have fixed workgroup counts.
  */
 #ifndef LAGUNA_HIP_TUNING_H
 #define LAGUNA_HIP_TUNING_H
@@ -15,6 +13,10 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* ---- launch-shape hooks.  Each sets a process-wide value (an atomic, read at
+ * every launch); 0 restores the automatic choice.  Every setting meets the same
+ * parity bound, and results are repeatable for a fixed setting. */
 
 /* Upper bound on workgroups of the M = 1 quantized projections. */
 int lg_set_m1_grid_cap(uint32_t cap);
@@ -27,6 +29,15 @@ int lg_set_m1_split(uint32_t slices);
  * draft-forward graph keeps the workspace it was sized with: set this before
  * lg_dflash_graph_create. */
 int lg_set_batch_shape(uint32_t ch, uint32_t rt);
+
+/* ---- ceiling kernels: what one launch, and one read of a buffer, cost. */
+
+/* An empty kernel of `workgroups` x 256 threads on `stream`. */
+int lg_bench_empty(uint32_t workgroups, void *stream);
+/* Reads `bytes` (a positive multiple of 16) of device memory at `buf` (16-byte
+ * aligned) once: each workgroup streams a contiguous 32 KiB run, every load issued
+ * up front. */
+int lg_bench_read(const void *buf, uint64_t bytes, void *stream);
 
 #ifdef __cplusplus
 }

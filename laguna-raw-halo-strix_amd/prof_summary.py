@@ -6,6 +6,10 @@
         two --pmc runs of `bench.py --pmc` (FETCH_SIZE, WRITE_SIZE): HBM bytes per
         launch of the kernel whose name contains NAME, each counter scaled by what it
         reads for lg_buf_copy (kernel k_copy16) of a known size.
+    python prof_summary.py counters --dirs D1 [D2 ...] --kernel NAME --weights W --out FILE --cmd "..."
+        --pmc runs of `bench.py --pmc` with SQ_* counters: each counter's average per
+        dispatch of the kernel whose name contains NAME, and per wavefront and per
+        weight (W weights per launch).
 """
 import argparse
 import csv
@@ -63,6 +67,26 @@ def traffic(args):
     print("\n".join(out))
 
 
+def counters(args):
+    vals = {}
+    for d in args.dirs:
+        for r in _rows(d, "*counter_collection.csv"):
+            if args.kernel in r["Kernel_Name"] and "k_copy16" not in r["Kernel_Name"]:
+                vals.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    if not vals:
+        raise SystemExit(f"no counter samples for {args.kernel}")
+    avg = {k: sum(v) / len(v) for k, v in vals.items()}
+    out = ["# Counters per launch (rocprofv3 --pmc)", "", f"command: {args.cmd}", "",
+           f"kernel: names containing `{args.kernel}`; {args.weights} weights per launch", "",
+           "| counter | per launch | per wavefront | per 1000 weights | dispatches |", "|---|---|---|---|---|"]
+    waves = avg.get("SQ_WAVES")
+    for k in sorted(avg):
+        pw = f"{avg[k] / waves:.1f}" if waves else "-"
+        out.append(f"| {k} | {avg[k]:.0f} | {pw} | {1000.0 * avg[k] / args.weights:.3f} | {len(vals[k])} |")
+    open(args.out, "w").write("\n".join(out) + "\n")
+    print("\n".join(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -76,8 +100,14 @@ def main():
     p.add_argument("--kernel", required=True)
     p.add_argument("--out", required=True)
     p.add_argument("--cmd", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("--dirs", nargs="+", required=True)
+    c.add_argument("--kernel", required=True)
+    c.add_argument("--weights", type=float, required=True)
+    c.add_argument("--out", required=True)
+    c.add_argument("--cmd", required=True)
     args = ap.parse_args()
-    trace(args) if args.mode == "trace" else traffic(args)
+    {"trace": trace, "traffic": traffic, "counters": counters}[args.mode](args)
 
 
 if __name__ == "__main__":

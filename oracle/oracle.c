@@ -170,9 +170,45 @@ void orc_dequant_q4k(const uint8_t *data, size_t len, size_t n, float *out) {
     }
 }
 
+/* The Q8_0 arm of orc_dequant_to_f32 (src/dflash.rs:379-397) on `threads` OpenMP
+ * threads: block b is decoded alone, and the serial loop's `break` at the first
+ * block that runs past len becomes the bound b < len / 34.  Same values. */
+void orc_dequant_q8_0_mt(const uint8_t *data, size_t len, size_t n, float *out, int threads) {
+    memset(out, 0, n * sizeof(float));
+    size_t n_blocks = (n + 31) / 32, whole = len / 34;
+    if (n_blocks > whole) n_blocks = whole;
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (size_t b = 0; b < n_blocks; b++) {
+        size_t off = b * 34;
+        float d = orc_half_to_f32(rd16(data + off));
+        size_t start = b * 32;
+        size_t end = start + 32 < n ? start + 32 : n;
+        for (size_t i = 0; i < end - start; i++) {
+            float q = (float)(int8_t)data[off + 2 + i];
+            out[start + i] = q * d;
+        }
+    }
+}
+
 /* kernels/proj.comp:23-33 */
 void orc_proj_f32(const float *x, const float *w, float *c, uint32_t k, uint32_t n,
                   uint32_t row_major) {
+    for (uint32_t i = 0; i < n; i++) {
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < k; j++) {
+            uint32_t idx = row_major ? (j * n + i) : (j + i * k);
+            float p = x[j] * w[idx];
+            acc += p;
+        }
+        c[i] = acc;
+    }
+}
+
+/* orc_proj_f32 with its rows on `threads` OpenMP threads (each row's sum in the
+ * shader's order, so the same values). */
+void orc_proj_f32_mt(const float *x, const float *w, float *c, uint32_t k, uint32_t n, uint32_t row_major,
+                     int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
     for (uint32_t i = 0; i < n; i++) {
         float acc = 0.0f;
         for (uint32_t j = 0; j < k; j++) {

@@ -73,6 +73,11 @@ void orc_dequant_q4k(const uint8_t *data, size_t len, size_t n_elements, float *
 void orc_proj_f32(const float *x, const float *w, float *c, uint32_t k, uint32_t n,
                   uint32_t row_major);
 /* kernels/proj_q8_0.comp:47-66. */
+/* Multi-threaded forms (OpenMP, for the benchmark's CPU baseline); the same values
+ * as orc_dequant_to_f32 (Q8_0) and orc_proj_f32. */
+void orc_dequant_q8_0_mt(const uint8_t *data, size_t len, size_t n, float *out, int threads);
+void orc_proj_f32_mt(const float *x, const float *w, float *c, uint32_t k, uint32_t n, uint32_t row_major,
+                     int threads);
 void orc_proj_q8_0(const float *x, const uint8_t *w, float *c, uint32_t k, uint32_t n);
 /* kernels/proj_q4k.comp:60-92 (uint32 linear index, as the shader). */
 void orc_proj_q4k(const float *x, const uint8_t *w, float *c, uint32_t k, uint32_t n,

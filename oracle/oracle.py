@@ -35,6 +35,9 @@ def lib():
         L.orc_q8_0_value.restype = ctypes.c_float
         L.orc_dequant_q4k.argtypes = [_u8p, ctypes.c_size_t, ctypes.c_size_t, _f32p]
         L.orc_proj_f32.argtypes = [_f32p, _f32p, _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        L.orc_proj_f32_mt.argtypes = [_f32p, _f32p, _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                      ctypes.c_int]
+        L.orc_dequant_q8_0_mt.argtypes = [_u8p, ctypes.c_size_t, ctypes.c_size_t, _f32p, ctypes.c_int]
         L.orc_proj_q8_0.argtypes = [_f32p, _u8p, _f32p, ctypes.c_uint32, ctypes.c_uint32]
         L.orc_proj_q4k.argtypes = [_f32p, _u8p, _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
         L.orc_proj_q4k_mt.argtypes = [_f32p, _u8p, _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
@@ -88,13 +91,24 @@ def dequant(data, dtype, n):
     return dequant_to_f32(data, dtype, n)
 
 
-def proj_f32(x, w, k, n, row_major=0):
+def proj_f32(x, w, k, n, row_major=0, threads=1):
     """kernels/proj.comp:23-33"""
     x = np.ascontiguousarray(x, np.float32)
     w = np.ascontiguousarray(w, np.float32)
     c = np.empty(n, np.float32)
-    lib().orc_proj_f32(_p(x, _f32p), _p(w, _f32p), _p(c, _f32p), k, n, row_major)
+    if threads > 1:
+        lib().orc_proj_f32_mt(_p(x, _f32p), _p(w, _f32p), _p(c, _f32p), k, n, row_major, threads)
+    else:
+        lib().orc_proj_f32(_p(x, _f32p), _p(w, _f32p), _p(c, _f32p), k, n, row_major)
     return c
+
+
+def dequant_q8_0_mt(data, n, threads):
+    """The Q8_0 arm of dequant_to_f32 (src/dflash.rs:379-397) on `threads` threads."""
+    d = _u8(data)
+    out = np.empty(n, np.float32)
+    lib().orc_dequant_q8_0_mt(_p(d, _u8p), d.size, n, _p(out, _f32p), threads)
+    return out
 
 
 def proj_q8_0(x, w, k, n, threads=1):

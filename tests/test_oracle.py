@@ -293,3 +293,21 @@ def test_argmax_closed_forms():
     assert orc.argmax(np.array([nan, 1.0, 0.5], f)) == 1      # NaN first
     assert orc.argmax(np.array([nan, nan, nan], f)) == 2
     assert orc.argmax(np.array([3.0, nan, 9.0, nan, 4.0, 4.0, 1.0], f)) == 5  # after the last NaN only
+
+
+def test_multithreaded_legs_equal_serial():
+    """The benchmark's multi-threaded CPU legs compute the same values as the serial
+    restatements: Q8_0 dequant_to_f32 (including a tensor cut short, where the serial
+    loop stops at the first short block) and the proj.comp-order f32 matvec."""
+    raw = synth.q8_0_weight(0x5EED0101, 1024, 64)
+    n = 1024 * 64
+    for data in (raw, raw[: 34 * 1000 + 20]):
+        a = orc.dequant_to_f32(data, orc.Q8_0, n)
+        b = orc.dequant_q8_0_mt(data, n, 4)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    w = synth.normal(0x5EED0102, 512 * 96)
+    x = synth.normal(0x5EED0103, 512)
+    for rm in (0, 1):
+        a = orc.proj_f32(x, w, 512, 96, row_major=rm)
+        b = orc.proj_f32(x, w, 512, 96, row_major=rm, threads=4)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
