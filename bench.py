@@ -532,10 +532,13 @@ def main():
                 w = WORKLOADS[name]()
                 extra[name] = time_workload(ctx, hip, w, args.steps, max(3, args.warmup // 4))
                 print(f"# {name}: {extra[name]['us_per_call']} us/call", file=sys.stderr, flush=True)
-    roof = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": head["frac_of_peak"], "traffic": traffic_from_profile(args.workload),
-            "us_per_call": head["us_per_call"], "algorithmic_bytes": head["bytes_per_call"],
-            "kernel": wl.kernel}
+    if "GBps" in head:
+        roof = {"bound": "hbm", "achieved": head["GBps"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": head["frac_of_peak"], "traffic": traffic_from_profile(args.workload),
+                "us_per_call": head["us_per_call"], "algorithmic_bytes": head["bytes_per_call"],
+                "kernel": wl.kernel}
+    else:  # a workload that moves no data (the empty kernel)
+        roof = {"bound": "launch", "us_per_call": head["us_per_call"], "kernel": wl.kernel}
     ceil = extra.get("ceil_read_33.1MB") if args.workload == "q4k_m1" else None
     if ceil:
         roof.update({"ceiling_read_GBps": ceil["GBps"], "frac_of_ceiling_read": round(head["GBps"] / ceil["GBps"], 4),
@@ -545,7 +548,7 @@ def main():
         roof["empty_launch_us_graph"] = extra["ceil_empty"].get("us_per_call_graph")
     line = {
         "metric": METRIC,
-        "value": head["GBps"],
+        "value": head.get("GBps"),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -556,8 +559,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded SplitMix64: random valid Q4_K blocks, ggml-quantized Q8_0, N(0,1) activations)",
-        "config": {"workload": head["workload"], "k": wl.k, "n": wl.n, "m": getattr(wl, "m", 1),
-                   "weight_pool_MB": head["pool_MB"], "parallelism": "single GPU",
+        "config": {"workload": head["workload"], "k": getattr(wl, "k", None), "n": getattr(wl, "n", None),
+                   "m": getattr(wl, "m", 1),
+                   "weight_pool_MB": head.get("pool_MB"), "parallelism": "single GPU",
                    "timing": f"median of {REPS} x {head['launches_per_rep']} back-to-back calls"},
         "graph_us_per_call": head.get("us_per_call_graph"),
         "roofline": roof,

@@ -3,6 +3,7 @@
 # named below, SQ counter passes and HBM traffic (FETCH_SIZE, WRITE_SIZE) for the
 # headline kernels.  Run from the repository root on a GPU host:
 #     bash laguna-raw-halo-strix_amd/profile_runs.sh OUTDIR [traces|counters|traffic|all]
+# (TRACES="w1 w2 ..." in the environment replaces the list of traced workloads.)
 # Raw profiler output and the text summaries go to OUTDIR (the summaries as
 # OUTDIR/summaries/*.txt, to be copied into profiles/).  Each profiler run has its
 # own time limit; the script stops at the first run that fails.
@@ -30,8 +31,8 @@ run() {  # run NAME ARGS...: one rocprofv3 invocation, stop on failure
 }
 
 if [ "$WHAT" = all ] || [ "$WHAT" = traces ]; then
-    for W in q4k_m1 q8_0_m1 q4k_down_silu q4k_m16_f32 q4k_m16_f32_tiled q8_0_m16_f32_tiled lm_head_verify_m16 \
-             dflash_block_eager ceil_read_33.1MB ceil_empty; do
+    for W in ${TRACES:-q4k_m1 q8_0_m1 q4k_down_silu q4k_m16_f32 q4k_m16_f32_tiled q8_0_m16_f32_tiled \
+             lm_head_verify_m16 dflash_block_eager ceil_read_33.1MB ceil_empty}; do
         ARGS=(--kernel-trace --stats --output-format csv -d "$OUT/tr_$W" -o run -- $BENCH --workload $W --no-extra --no-cpu)
         run "tr_$W" "${ARGS[@]}"
         $PS trace --dir "$OUT/tr_$W" --out "$SUM/kernel_trace_$W.txt" \
