@@ -314,7 +314,7 @@ class Read(Workload):
         lh.check(lh.lib().lg_bench_read(w.ptr, self.bytes_per_call, stream))
 
 
-HEAD_KERNEL = "k_q4k_m1_rows"
+HEAD_KERNEL = "k_q4k_m1_dig"
 WORKLOADS = {
     "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003, kernel=HEAD_KERNEL),
     "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001, kernel="k_q80_m1"),

@@ -4,9 +4,11 @@
 // (one invocation per output row, per-element byte decode, uncoalesced) with
 // gfx950 kernels.
 //
-// Q4_K (k % 256 == 0, k <= 16384, 16-byte aligned tensor), two kernels chosen by
+// Q4_K (k % 256 == 0, k <= 16384, 16-byte aligned tensor), kernels chosen by
 // measurement:
-//  * plain projections: vector ALU (k_q4k_m1_rows, k_q4k_m1).  Lane p of a row
+//  * plain projections with k <= 4096: integer dot products of the raw nibbles
+//    against byte digits of the activations (k_q4k_m1_dig, described there).
+//  * plain projections with k > 4096: vector ALU (k_q4k_m1).  Lane p of a row
 //    team owns the 64-element group p of the row; a nibble masked in place is an
 //    f16 subnormal (q * 2^-24, or q * 2^-20 for a high nibble), so one AND gives two
 //    operands of v_fma_mix_f32 against the f32 activations, and the block's scale
@@ -262,80 +264,6 @@ __global__ __launch_bounds__(TW *TEAMS * 64) void k_q4k_m1(const float *__restri
         acc[r] = active ? v : 0.0f;
     }
     team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
-}
-
-// Q4_K with k <= 4096, not fused: one wave per row, x staged once per workgroup
-// in LDS, grid-stride rows, R per team per iteration.  Written so that the
-// compiler re-reads the activations from LDS instead of holding all 64 in
-// registers: at about 60 VGPRs all 16 waves of a CU stay resident, which hides
-// the latency of the small per-row loads better than a register-resident vector.
-template <int TEAMS, int R>
-__global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_rows(const float *__restrict__ x, const uint8_t *__restrict__ w,
-                                                             float *__restrict__ y, uint32_t k, uint32_t n,
-                                                             uint64_t row_bytes) {
-    __shared__ __attribute__((aligned(16))) float xs[64 * 68];
-    const uint32_t lane = threadIdx.x & 63u, team = threadIdx.x >> 6;
-    const uint32_t P = k >> 6;
-    const uint32_t p = lane;
-    const bool active = p < P;
-    const Q4Lane L = q4_lane(p & 3u);
-    const uint64_t lane_off = (uint64_t)(p >> 2) * Q4K_BYTES;
-    auto load_rows = [&](uint32_t r0, uint4 (&hd)[R], uint4 (&qa)[R], uint4 (&qb)[R]) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (active && r0 + r < n) {
-                const uint8_t *blk = w + (uint64_t)(r0 + r) * row_bytes + lane_off;
-                hd[r] = *reinterpret_cast<const uint4 *>(blk);
-                qa[r] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * L.g);
-                qb[r] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * L.g);
-            } else {
-                hd[r] = qa[r] = qb[r] = make_uint4(0, 0, 0, 0);  // idle lanes: zero scales, zero sums
-            }
-        }
-    };
-    // The activation loads go first, then the first rows' weight loads: the wait for
-    // the activations (loads complete in issue order) does not wait for the rows, and
-    // the rows are in flight while the activations are staged.
-    constexpr int XL = 4096 / 4 / (TEAMS * 64);  // float4 loads of x per thread (k <= 4096)
-    float4 xv[XL];
-#pragma unroll
-    for (int i = 0; i < XL; i++) {
-        const uint32_t e4 = threadIdx.x + i * TEAMS * 64;
-        xv[i] = e4 < k / 4 ? reinterpret_cast<const float4 *>(x)[e4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    uint32_t r0 = (blockIdx.x * TEAMS + team) * R;
-    uint4 hd[R], qa[R], qb[R];
-    if (r0 < n) load_rows(r0, hd, qa, qb);
-#pragma unroll
-    for (int i = 0; i < XL; i++) {
-        const uint32_t e4 = threadIdx.x + i * TEAMS * 64;
-        if (e4 < k / 4) *reinterpret_cast<float4 *>(xs + 4 * e4 + 4 * (e4 >> 4)) = xv[i];
-    }
-    __syncthreads();
-    float xr[64];
-    if (active) {
-        const float4 *s4 = reinterpret_cast<const float4 *>(xs + 68 * p);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float4 v = s4[i];
-            xr[4 * i] = v.x, xr[4 * i + 1] = v.y, xr[4 * i + 2] = v.z, xr[4 * i + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
-    }
-    float X0 = 0.f, X1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
-    for (; r0 < n; r0 += gridDim.x * TEAMS * R) {
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float v = wave_sum(q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L));
-            if (lane == 0 && r0 + r < n) y[r0 + r] = v;
-        }
-        const uint32_t rn = r0 + gridDim.x * TEAMS * R;
-        if (rn < n) load_rows(rn, hd, qa, qb);
-    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -881,6 +809,179 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void k_q4k_m1_mfma(const float *__re
 }
 
 // ------------------------------------------------------------------------------------------
+// Q4_K with k <= 4096, not fused: integer dot products (v_dot4_i32_i8) of the raw
+// nibbles against three signed byte digits of the activations.
+//
+// Each 64-element group p of x is scaled by 2^sh_p, sh_p chosen so that the group's
+// max|x| 2^sh lies in [2^20, 2^21), and rounded to an integer X (one fma with
+// 1.5 * 2^23: the low 24 bits of the result are X + 0x808080).  Bytes XOR 0x80 are
+// signed digits with X = t0 + 2^8 t1 + 2^16 t2, so per 32-element sub-block
+//     sum_j X_j q_j = C0 + 2^8 C1 + 2^16 C2,   C_l = sum_j t_l,j q_j  (exact in int32:
+//     |X| <= 2^21, q <= 15),
+// and the row's term is d sc 2^-sh (C0 + 2^8 C1 + 2^16 C2) - dmin m sum_j x_j.
+// The rounding of x to 21 significant bits of its group maximum is the only
+// approximation (|error| <= 2^-22 max|x_group| per element).  Groups holding a
+// non-finite value, a magnitude >= 2^21 or a nonzero magnitude below 2^-60 cannot
+// be scaled that way: if x holds one, every row takes the reference's per-element
+// loop instead.
+//
+// Lane p of a wave owns group p of a row (k/64 <= 64 lanes); the workgroup converts
+// x once into an LDS table of 48 digit dwords per group, each lane keeps its group's
+// 48 dwords in registers, and the waves stride over rows R at a time with the next
+// rows' loads in flight while the current rows are reduced.
+template <int TEAMS, int R>
+__global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restrict__ x, const uint8_t *__restrict__ w,
+                                                            float *__restrict__ y, uint32_t k, uint32_t n,
+                                                            uint64_t row_bytes) {
+    static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
+    __shared__ __attribute__((aligned(16))) uint32_t s_dig[64 * 48];  // group p: digit planes 0, 1, 2 x 16 dwords
+    __shared__ float s_xf[64 * 4];                                       // group p: X0, X1, 2^-sh
+    __shared__ uint32_t s_bad;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, team = tid >> 6;
+    const uint32_t P = k >> 6;
+    const bool active = lane < P;
+    const uint32_t p = active ? lane : 0u;  // idle lanes read group 0 and contribute 0
+    const Q4Lane L = q4_lane(p & 3u);
+    const uint32_t lane_off = (p >> 2) * Q4K_BYTES;
+    const uint32_t stride = gridDim.x * TEAMS * R;
+
+    // thread t converts elements 16t .. 16t+15 (group t/4, quarter t%4); threads past
+    // k/16 read element 0 and fill table entries that only idle lanes read
+    float4 xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t e4 = 4 * tid + j;
+        xv[j] = reinterpret_cast<const float4 *>(x)[e4 < k / 4 ? e4 : 0];
+    }
+    // the first rows' weights are in flight while x is converted
+    uint32_t r0 = (blockIdx.x * TEAMS + team) * R;
+    uint4 hd[2][R], qa[2][R], qb[2][R];
+    auto load = [&](int b, uint32_t rr) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = min(rr + r, n - 1u);  // rows past n re-read row n-1 and are not stored
+            const uint8_t *blk = w + (uint64_t)row * row_bytes + lane_off;
+            hd[b][r] = *reinterpret_cast<const uint4 *>(blk);
+            qa[b][r] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * L.g);
+            qb[b][r] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * L.g);
+        }
+    };
+    load(0, r0);
+    if (tid == 0) s_bad = 0u;
+    __syncthreads();
+    {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            v[4 * j] = xv[j].x, v[4 * j + 1] = xv[j].y, v[4 * j + 2] = xv[j].z, v[4 * j + 3] = xv[j].w;
+        uint32_t mb = 0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) mb = max(mb, __float_as_uint(v[j]) & 0x7FFFFFFFu);
+        // the group's maximum over its four threads (a quad)
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+        const bool outside = mb >= 0x4A000000u || (mb != 0u && mb < 0x21800000u);  // >= 2^21 or NaN/inf; < 2^-60
+        const int E = (int)(mb >> 23) - 127;
+        const int sh = (mb == 0u || outside) ? 0 : 20 - E;
+        const float scale = __uint_as_float((uint32_t)(127 + sh) << 23);
+        uint32_t U[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) U[j] = __float_as_uint(__builtin_fmaf(v[j], scale, 12582912.0f)) - 0x4ABF7F80u;
+        uint32_t *dg = s_dig + (tid >> 2) * 48 + 4 * (tid & 3u);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {  // elements 4q .. 4q+3 of this thread's 16: one dword per digit plane
+            const uint32_t lo01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x05010400u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(U[4 * q + 3], U[4 * q + 2], 0x05010400u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x0C0C0602u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(U[4 * q + 3], U[4 * q + 2], 0x0C0C0602u);
+            dg[q] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+            dg[16 + q] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+            dg[32 + q] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) sum += v[j];
+        sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+        if ((tid & 3u) == 0) s_xf[(tid >> 2) * 4 + 0] = sum;  // elements 0-31 of the group (sub-block 2g)
+        if ((tid & 3u) == 2) s_xf[(tid >> 2) * 4 + 1] = sum;  // elements 32-63 (sub-block 2g+1)
+        if ((tid & 3u) == 0) s_xf[(tid >> 2) * 4 + 2] = __uint_as_float((uint32_t)(127 - sh) << 23);
+        if (tid < k / 16 && outside) s_bad = 1u;
+    }
+    __syncthreads();
+    uint32_t D[48];
+    {
+        const uint4 *src = reinterpret_cast<const uint4 *>(s_dig + p * 48);
+#pragma unroll
+        for (int i = 0; i < 12; i++) {
+            const uint4 u = src[i];
+            D[4 * i] = u.x, D[4 * i + 1] = u.y, D[4 * i + 2] = u.z, D[4 * i + 3] = u.w;
+        }
+    }
+    const float X0 = s_xf[p * 4], X1 = s_xf[p * 4 + 1], F = s_xf[p * 4 + 2];
+    if (s_bad) {  // the reference's per-element loop (kernels/proj_q4k.comp:60-75)
+        for (uint32_t rr = blockIdx.x * TEAMS + team; rr < n; rr += gridDim.x * TEAMS) {
+            float a = 0.0f;
+            for (uint32_t j = lane; j < k; j += 64) a = __builtin_fmaf(x[j], q4k_elem(w, (uint64_t)rr * k + j), a);
+            a = wave_sum(a);
+            if (lane == 0) y[rr] = a;
+        }
+        return;
+    }
+    auto dotrow = [&](const uint4 &h, const uint4 &A, const uint4 &B) -> float {
+        const uint32_t q[8] = {A.x, A.y, A.z, A.w, B.x, B.y, B.z, B.w};
+        int c0 = 0, c1 = 0, c2 = 0, e0 = 0, e1 = 0, e2 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int lo = (int)(q[t] & 0x0F0F0F0Fu), hi = (int)((q[t] >> 4) & 0x0F0F0F0Fu);
+            c0 = __builtin_amdgcn_sdot4(lo, (int)D[t], c0, false);
+            c1 = __builtin_amdgcn_sdot4(lo, (int)D[16 + t], c1, false);
+            c2 = __builtin_amdgcn_sdot4(lo, (int)D[32 + t], c2, false);
+            e0 = __builtin_amdgcn_sdot4(hi, (int)D[8 + t], e0, false);
+            e1 = __builtin_amdgcn_sdot4(hi, (int)D[24 + t], e1, false);
+            e2 = __builtin_amdgcn_sdot4(hi, (int)D[40 + t], e2, false);
+        }
+        const float S0 = (float)(c0 + (c1 << 8) + (c2 << 16)), S1 = (float)(e0 + (e1 << 8) + (e2 << 16));
+        // scales and mins of sub-blocks 2g and 2g+1 (kernels/proj_q4k.comp:46-58)
+        const bool lo = L.g < 2;
+        const uint32_t srcA = lo ? h.y : h.w, srcM = lo ? h.z : h.w;
+        const float d = mq_half(h.x & 0xFFFFu) * F, dmin = mq_half(h.x >> 16);
+        const float sc0 = (float)(__builtin_amdgcn_ubfe(srcA, L.sa[0], 4) | (__builtin_amdgcn_ubfe(h.y, L.sb[0], 2) << 4));
+        const float sc1 = (float)(__builtin_amdgcn_ubfe(srcA, L.sa[1], 4) | (__builtin_amdgcn_ubfe(h.y, L.sb[1], 2) << 4));
+        const float m0 = (float)(__builtin_amdgcn_ubfe(srcM, L.ma[0], 4) | (__builtin_amdgcn_ubfe(h.z, L.mb[0], 2) << 4));
+        const float m1 = (float)(__builtin_amdgcn_ubfe(srcM, L.ma[1], 4) | (__builtin_amdgcn_ubfe(h.z, L.mb[1], 2) << 4));
+        const float ts = __builtin_fmaf(sc1, S1, sc0 * S0);
+        const float tm = __builtin_fmaf(m1, X1, m0 * X0);
+        return __builtin_fmaf(d, ts, -(dmin * tm));
+    };
+    // Idle lanes contribute an explicit 0, not 0 * (a scale that may be inf or NaN).
+    auto reduce = [&](int b, uint32_t rr) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float v = dotrow(hd[b][r], qa[b][r], qb[b][r]);
+            v = wave_sum(active ? v : 0.0f);
+            if (lane == 0 && rr + r < n) y[rr + r] = v;
+        }
+    };
+    for (;;) {  // every wave leaves once its next rows start at or past n
+        const uint32_t r1 = r0 + stride;
+        if (r1 >= n) {
+            reduce(0, r0);
+            break;
+        }
+        load(1, r1);
+        reduce(0, r0);
+        const uint32_t r2 = r1 + stride;
+        if (r2 >= n) {
+            reduce(1, r1);
+            break;
+        }
+        load(0, r2);
+        reduce(1, r1);
+        r0 = r2;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // f32 weights: kernels/proj.comp (row_major = 0: w[i*k+j]; 1: w[j*n+i])
 
 __global__ __launch_bounds__(256) void k_f32_rows(const float *__restrict__ x, const float *__restrict__ w,
@@ -1045,9 +1146,9 @@ int launch_q4k(const float *x, const float *up, const uint8_t *w, float *y, uint
         constexpr int TEAMS = 4, R = 2;
         uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
         const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed);
-        const uint32_t cap = gc ? gc : 1024;
+        const uint32_t cap = gc ? gc : 512;  // two workgroups per CU: measured best for 14336 rows
         grid = grid < cap ? grid : cap;
-        hipLaunchKernelGGL((k_q4k_m1_rows<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
+        hipLaunchKernelGGL((k_q4k_m1_dig<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
                            (uint64_t)k / QK_K * Q4K_BYTES);
         return after_launch("proj_q4k_m1", s);
     }

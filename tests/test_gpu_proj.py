@@ -53,6 +53,58 @@ def test_config_shapes(ctx, dtype, k, n, seed):
     parity(y, y64, a, TOL)
 
 
+def assert_same_non_finite(y, y64):
+    y = np.asarray(y, np.float64)
+    assert np.array_equal(np.isnan(y), np.isnan(y64)), "NaN pattern differs"
+    assert np.array_equal(np.isinf(y), np.isinf(y64)), "inf pattern differs"
+    inf = np.isinf(y64)
+    assert np.array_equal(np.sign(y[inf]), np.sign(y64[inf]))
+
+
+@pytest.mark.parametrize("k,n", [(4096, 300), (1024, 37)])
+def test_q4k_activations_outside_the_digit_range(ctx, k, n):
+    # Q4_K with k <= 4096 converts x to byte digits per 64-element group; values it
+    # cannot scale (non-finite, >= 2^21, nonzero below 2^-60) send the call to the
+    # reference's per-element loop, whose results the f64 accumulation matches.
+    raw = synth.q4k_weight(300 + k, k, n)
+    x = synth.normal(301 + k, k)
+    for idx, val in [(5, np.inf), (k - 3, -np.inf), (k // 3, np.nan)]:
+        print(f"proj q4k k={k} x[{idx}]={val}", flush=True)
+        xs = x.copy()
+        xs[idx] = val
+        y64, _ = orc.proj_quant_f64(xs, raw, orc.Q4_K, k, n)
+        assert_same_non_finite(run_proj(ctx, lh.Q4_K, raw, xs, k, n), y64)
+    cases = {
+        "huge": lambda v: np.where(np.arange(k) == 77, np.float32(3e6), v),       # one value >= 2^21
+        "tiny": lambda v: (v * 1e-20).astype(np.float32),                           # all below 2^-60
+        "wide": lambda v: np.where(np.arange(k) % 64 == 9, np.float32(30.0), v * np.float32(1e-3)),
+        "zero_groups": lambda v: np.where((np.arange(k) // 64) % 3 == 1, np.float32(0.0), v),
+        "mixed_scales": lambda v: (v * np.exp2(np.arange(k) // 64 % 40 - 30.0)).astype(np.float32),
+    }
+    for name, f in cases.items():
+        print(f"proj q4k k={k} {name} activations", flush=True)
+        xs = f(x).astype(np.float32)
+        y64, a = orc.proj_quant_f64(xs, raw, orc.Q4_K, k, n)
+        parity(run_proj(ctx, lh.Q4_K, raw, xs, k, n), y64, a, TOL)
+
+
+def test_q4k_exponent0_scales(ctx):
+    # d and dmin codes with exponent 0 and a non-zero mantissa, which the reference
+    # decodes as 2^-14 * (1 + m/1024) (src/dflash.rs:314-329), on the k <= 4096 path
+    k, n = 4096, 256
+    print("proj q4k exponent-0 f16 scales", flush=True)
+    raw = synth.q4k_weight(310, k, n).reshape(-1, 144).copy()
+    h = np.frombuffer(raw[:, 0:4].tobytes(), np.uint16).reshape(-1, 2).copy()
+    sel = np.arange(raw.shape[0])
+    h[sel % 7 == 0, 0] = 0x0001 + (sel[sel % 7 == 0] % 0x3FF).astype(np.uint16)
+    h[sel % 5 == 0, 1] = 0x8000 | (0x0100 + (sel[sel % 5 == 0] % 0x2FF)).astype(np.uint16)
+    raw[:, 0:4] = h.view(np.uint8).reshape(-1, 4)
+    raw = raw.ravel()
+    x = synth.normal(311, k)
+    y64, a = orc.proj_quant_f64(x, raw, orc.Q4_K, k, n)
+    parity(run_proj(ctx, lh.Q4_K, raw, x, k, n), y64, a, TOL)
+
+
 @pytest.mark.parametrize("dtype", [lh.Q4_K, lh.Q8_0])
 @pytest.mark.parametrize("k,n", [(256, 1), (256, 7), (512, 33), (768, 5), (1024, 64), (2048, 9),
                                  (2304, 11), (3072, 13), (4352, 3), (6144, 17), (16384, 5)])
