@@ -274,6 +274,13 @@ int lg_dispatch_gate_mul(float *attn_out, const float *v_rep, const float *gate,
 int lg_dispatch_softplus_gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd,
                                   uint32_t n_heads, uint32_t head_dim, void *stream);
 
+/* dispatch_gate_attn (src/target.rs:992-1020), kernels/gate_attn.comp, same
+ * argument order: result[i] = attn_out[i] * log(1 + exp(gate[i / head_dim])) for
+ * i < n_heads*head_dim.  No threshold, as in the shader: a gate above about 88.7
+ * gives an infinite factor.  result may be attn_out (the target's in-place call). */
+int lg_dispatch_gate_attn(const float *attn_out, const float *gate, float *result, uint32_t n_heads,
+                          uint32_t head_dim, void *stream);
+
 /* dispatch_add (src/dflash.rs:1284-1303), kernels/add.comp: out = a + b. */
 int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream);
 
@@ -440,6 +447,70 @@ int lg_dflash_graph_create(const lg_dflash_model *model, const float *features, 
                            uint32_t ctx_len, float *out, void *stream, void **graph);
 int lg_dflash_graph_launch(void *graph, void *stream);
 int lg_dflash_graph_destroy(void *graph);
+
+/* ---- Dense target model (src/target.rs TargetModel, dense layers) ---- */
+
+typedef struct {
+    uint32_t n_embd, n_heads, n_kv_heads, head_dim, n_ff, n_layers;
+    uint32_t n_vocab;      /* rows of `output` (vocab_size, src/target.rs:287-291) */
+    uint32_t rope_dim;     /* rope.dimension_count: 0 or head_dim */
+    uint32_t rope_dim_swa; /* rope.dimension_count_swa: 0 or head_dim */
+    int swa;               /* rope_dim_swa > 0 or attention.sliding_window > 0 (src/target.rs:331);
+                            * layers whose index % 4 != 0 then use the SWA table (:440) */
+    float rope_base;       /* rope.freq_base, 0 = the reference's default 500000 (:350) */
+    float rope_base_swa;   /* rope.freq_base_swa, 0 = 10000 (:366) */
+    float rms_eps;         /* 1e-5 (src/target.rs:970) */
+    float qk_eps;          /* 1e-6 (src/target.rs:897) */
+} lg_target_hparams;
+
+/* One dense layer (TargetDenseLayer, src/target.rs:30-43): f32 norms, raw GGUF
+ * blocks (LG_Q4_K, LG_Q8_0) or f32 for the projections, attn_gate optional (NULL:
+ * no gate), and the layer's query head count (attn_q rows / head_dim,
+ * src/target.rs:236-246). */
+typedef struct {
+    const float *attn_norm, *attn_q_norm, *attn_k_norm, *ffn_norm;
+    const void *attn_q, *attn_k, *attn_v, *attn_gate, *attn_output, *ffn_gate, *ffn_up, *ffn_down;
+    int attn_q_type, attn_k_type, attn_v_type, attn_gate_type, attn_output_type, ffn_gate_type, ffn_up_type,
+        ffn_down_type;
+    uint32_t n_q_heads;
+} lg_target_layer;
+
+typedef struct {
+    lg_target_hparams hp;
+    const lg_target_layer *layers;
+    const float *output_norm; /* [n_embd] or NULL */
+    const void *output;       /* LM head [n_vocab][n_embd] or NULL (logits = final hidden) */
+    int output_type;
+} lg_target_model;
+
+/* Device-resident K/V cache (replaces TargetKvCache, src/target.rs:74-101, which
+ * the reference keeps on the host and re-uploads whole every token): layer l's
+ * normed, roped key and raw value of position p at [l][p][n_kv_heads*head_dim]
+ * of k and v, for p < len. */
+typedef struct {
+    float *k, *v;
+    uint32_t capacity; /* positions per layer */
+    uint32_t len;      /* tokens cached: the position of the next token */
+} lg_target_kv_cache;
+
+/* TargetModel::forward_token (cache NULL) and forward_token_cached
+ * (src/target.rs:298-578) for a dense model: one token `input` [n_embd] at
+ * position cache ? cache->len : 0.  Hidden states are captured as they enter
+ * layer l for each l in capture_layers (every layer when capture_layers is NULL,
+ * the reference's None), in ascending l, plus the final state (before
+ * output_norm) when n_layers is listed; *n_captured receives their number and
+ * captured[i*n_embd ..] the states.  logits: [n_vocab] (LM head of the normed
+ * final state), or [n_embd] holding that normed state when the model has no
+ * output weight; hidden (optional): the normed final state.  With a cache, the
+ * token's K/V are stored at position len, attention runs over 0..len, and len
+ * is incremented.  MoE layers are not supported. */
+int lg_target_forward_token(const lg_target_model *model, const float *input, const uint32_t *capture_layers,
+                            uint32_t n_capture, float *captured, uint32_t *n_captured, float *logits, float *hidden,
+                            lg_target_kv_cache *cache, void *stream);
+
+/* The number of states lg_target_forward_token captures for this list (host only). */
+int lg_target_capture_count(uint32_t n_layers, const uint32_t *capture_layers, uint32_t n_capture,
+                            uint32_t *count);
 
 #ifdef __cplusplus
 }

@@ -642,7 +642,9 @@ __global__ __launch_bounds__(256) void k_gate_mul(const float *v, const float *_
     const uint64_t row = i / ((uint64_t)n_heads * hd);
     const uint32_t head = (uint32_t)(i % ((uint64_t)n_heads * hd)) / hd;
     const float g = gate[row * n_heads + head];
-    out[i] = v[i] * (softplus ? softplus_gate(g) : g);
+    // softplus 1: the draft's host softplus (src/dflash.rs:957); 2: kernels/gate_attn.comp:27,
+    // log(1 + exp(g)) with no threshold (infinite for g above about 88.7)
+    out[i] = v[i] * (softplus == 1 ? softplus_gate(g) : softplus == 2 ? logf(1.0f + expf(g)) : g);
 }
 
 __global__ __launch_bounds__(256) void k_add(const float *a, const float *b, float *out, uint64_t n) {
@@ -792,9 +794,7 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
 // (src/dflash.rs:898-904: 1.0 / base.powf((2.0 * i as f32) / rope_dim as f32)).
 std::vector<float> rope_table(const lg_dflash_hparams &hp) {
     std::vector<float> f(hp.rope_dim / 2 + 1, 0.0f);
-    const float base = hp.rope_base > 0.0f ? hp.rope_base : 500000.0f;
-    for (uint32_t i = 0; i < hp.rope_dim / 2; i++)
-        f[i] = 1.0f / std::pow(base, (2.0f * (float)i) / (float)hp.rope_dim);
+    glue_rope_table(hp.rope_dim, hp.rope_base > 0.0f ? hp.rope_base : 500000.0f, f.data());
     return f;
 }
 
@@ -996,6 +996,51 @@ int check_forward(const lg_dflash_model *md, const float *features, const float 
 
 }  // namespace
 
+// ------------------------------------------------------------------------------------------
+// the launchers, for the target forward (one row each unless stated)
+
+namespace lg {
+
+int glue_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps, hipStream_t s) {
+    return run_rmsnorm(x, w, out, n, rows, 1, n, eps, s);
+}
+
+int glue_qk_norm_rope(const float *x, const float *w, float *out, uint32_t n_heads, uint32_t head_dim,
+                      uint32_t rope_dim, uint32_t pos, const float *freq, float eps, hipStream_t s) {
+    return run_qk_norm_rope(qk_job(x, w, out, n_heads, pos, 1), QkJob{}, freq, head_dim, rope_dim, eps, s);
+}
+
+uint64_t glue_attn_partial_bytes(uint32_t seq_len, uint32_t n_kv) { return attn_partial_floats(seq_len, n_kv) * 4; }
+
+int glue_attention(const float *q, const float *k, const float *v, uint32_t seq_len, uint32_t q_pos, uint32_t n_q,
+                   uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s) {
+    return run_attention(q, k, v, seq_len, nullptr, nullptr, seq_len, 1, n_q, n_kv, head_dim, q_pos, 1, out, part, s);
+}
+
+int glue_gate_attn(const float *attn, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
+                   hipStream_t s) {
+    const uint64_t total = (uint64_t)n_heads * head_dim;
+    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, attn, gate, out, n_heads, head_dim, total,
+                       2);
+    return after_launch("gate_attn", s);
+}
+
+int glue_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_add, dim3(blocks_for(n)), dim3(256), 0, s, a, b, out, n);
+    return after_launch("add", s);
+}
+
+int glue_copy(const float *src, float *dst, uint64_t n, hipStream_t s) {
+    hipLaunchKernelGGL(k_copy, dim3(blocks_for(n)), dim3(256), 0, s, src, dst, n);
+    return after_launch("copy", s);
+}
+
+void glue_rope_table(uint32_t rope_dim, float base, float *out) {
+    for (uint32_t i = 0; i < rope_dim / 2; i++) out[i] = 1.0f / std::pow(base, (2.0f * (float)i) / (float)rope_dim);
+}
+
+}  // namespace lg
+
 extern "C" {
 
 int lg_dispatch_rmsnorm(const float *w, const float *x, float *out, uint32_t n, uint32_t rows, float eps,
@@ -1097,6 +1142,19 @@ int lg_dispatch_gate_mul(float *attn_out, const float *v_rep, const float *gate,
 int lg_dispatch_softplus_gate_mul(float *attn_out, const float *v_rep, const float *gate, uint32_t n_hd,
                                   uint32_t n_heads, uint32_t head_dim, void *stream) {
     return gate_mul(attn_out, v_rep, gate, n_hd, n_heads, head_dim, 1, stream, "lg_dispatch_softplus_gate_mul");
+}
+
+int lg_dispatch_gate_attn(const float *attn_out, const float *gate, float *result, uint32_t n_heads,
+                          uint32_t head_dim, void *stream) {
+    clear_error();
+    const char *name = "lg_dispatch_gate_attn";
+    const uint64_t n = (uint64_t)n_heads * head_dim;
+    if (n == 0) return LG_OK;
+    LG_REQUIRE(attn_out && gate && result, "%s: null pointer", name);
+    LG_EXTENT(attn_out, n * 4, name);
+    LG_EXTENT(result, n * 4, name);
+    LG_EXTENT(gate, (uint64_t)n_heads * 4, name);
+    return glue_gate_attn(attn_out, gate, result, n_heads, head_dim, (hipStream_t)stream);
 }
 
 int lg_dispatch_add(const float *a, const float *b, float *out, uint32_t n, void *stream) {

@@ -68,7 +68,7 @@ constexpr uint64_t PROJ_WS_COUNTERS = 65536;
 // while the stream is being captured (LG_EINVAL: make the same call once on that
 // stream before capturing).  New memory is zeroed on the stream.  The lease holds
 // the registry lock; `tag` is free for the purpose's own bookkeeping.
-enum BufPurpose { BUF_PRODUCT = 0, BUF_ATTN = 1, BUF_DRAFT = 2 };
+enum BufPurpose { BUF_PRODUCT = 0, BUF_ATTN = 1, BUF_DRAFT = 2, BUF_TARGET = 3 };
 struct StreamBuf {
     void *ptr = nullptr;
     uint64_t bytes = 0;
@@ -137,6 +137,23 @@ struct BatchJob {
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype);
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jobs, uint32_t njobs, uint32_t k,
                      uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s, bool glu = false);
+
+// ---- launchers of the draft's glue kernels, used by the target forward (one row each;
+// in place allowed where the kernels allow it: rmsnorm, qk_norm_rope, gate_attn, add)
+int glue_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps, hipStream_t s);
+int glue_qk_norm_rope(const float *x, const float *w, float *out, uint32_t n_heads, uint32_t head_dim,
+                      uint32_t rope_dim, uint32_t pos, const float *freq, float eps, hipStream_t s);
+// Causal attention of one query row at q_pos over seq_len keys/values; `part` holds
+// glue_attn_partial_bytes(seq_len, n_kv) bytes (or is null: the plain kernel).
+uint64_t glue_attn_partial_bytes(uint32_t seq_len, uint32_t n_kv);
+int glue_attention(const float *q, const float *k, const float *v, uint32_t seq_len, uint32_t q_pos, uint32_t n_q,
+                   uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s);
+int glue_gate_attn(const float *attn, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
+                   hipStream_t s);
+int glue_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);
+int glue_copy(const float *src, float *dst, uint64_t n, hipStream_t s);
+// The reference's f32 RoPE table: out[i] = 1 / base^(2i / rope_dim), i < rope_dim / 2.
+void glue_rope_table(uint32_t rope_dim, float base, float *out);
 
 // ---- GGUF block geometry (src/gguf.rs:97,101,134,136)
 constexpr uint32_t QK_K = 256, Q4K_BYTES = 144;

@@ -69,6 +69,9 @@ SIGNATURES = {
     "lg_dispatch_gate_mul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "lg_dispatch_softplus_gate_mul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "lg_dispatch_add": (_i, [_vp, _vp, _vp, _u32, _vp]),
+    "lg_dispatch_gate_attn": (_i, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "lg_target_forward_token": (_i, [_vp, _vp, _vp, _u32, _vp, ctypes.POINTER(_u32), _vp, _vp, _vp, _vp]),
+    "lg_target_capture_count": (_i, [_u32, _vp, _u32, ctypes.POINTER(_u32)]),
     "lg_dflash_encode": (_i, [_vp, _vp, _u32, _vp, _vp]),
     "lg_dflash_forward_block": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
     "lg_dflash_graph_create": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, ctypes.POINTER(_vp)]),
@@ -395,6 +398,11 @@ def dispatch_softplus_gate_mul(ctx, attn_out, v_rep, gate, n_hd, n_heads, head_d
                                               ctx.stream))
 
 
+def dispatch_gate_attn(ctx, attn_out, gate, result, n_heads, head_dim):
+    """dispatch_gate_attn (src/target.rs:992-1020): result = attn_out * log(1 + exp(gate[head]))."""
+    check(lib().lg_dispatch_gate_attn(_ptr(attn_out), _ptr(gate), _ptr(result), n_heads, head_dim, ctx.stream))
+
+
 def dispatch_add(ctx, a, b, out, n):
     """dispatch_add (src/dflash.rs:1281-1303)."""
     check(lib().lg_dispatch_add(_ptr(a), _ptr(b), _ptr(out), n, ctx.stream))
@@ -452,8 +460,9 @@ class DFlashModel:
     16-row tiles, which the forward's small-M products read as contiguous 2304-byte tiles
     (the results are the same bit for bit)."""
 
-    def __init__(self, ctx, cfg, enc, layers, tiled=True):
+    def __init__(self, ctx, cfg, enc, layers, tiled=True, target_layers=None):
         self.ctx, self.cfg = ctx, cfg
+        self._tl = list(target_layers or [])
         self._bufs = []
         self.layers = []
         up = self._up
@@ -556,7 +565,7 @@ class DFlashModel:
                     L[n], L[n + "_dtype"] = tensor(f"blk.{i}.{n}.weight")
                 layers.append(L)
         ctx.sync()
-        return cls(ctx, cfg, enc, layers, tiled)
+        return cls(ctx, cfg, enc, layers, tiled, target_layers=md.target_layers or [])
 
     # accessors of src/dflash.rs:121-155
     def layer_count(self):
@@ -582,6 +591,11 @@ class DFlashModel:
 
     def n_embd_inp(self):
         return self.cfg.n_aux * self.cfg.n_embd
+
+    def target_layers(self):
+        """The target layers whose hidden states feed the encoder (metadata
+        target_layers, src/dflash.rs:149-151)."""
+        return list(self._tl)
 
     def set_context(self, k_ctx, v_ctx):
         """Per-layer cached context keys (normed, roped) and values, [ctx_len][n_kv*head_dim] f32."""
@@ -656,6 +670,353 @@ class DFlashGraph:
             self.destroy()
         except Exception:
             pass
+
+
+# ---------------------------------------------------------------------------------------
+# Dense target model (src/target.rs TargetModel) and the verify loop (src/lib.rs:466-520)
+
+TARGET_NORMS = ("attn_norm", "attn_q_norm", "attn_k_norm", "ffn_norm")
+TARGET_PROJ = ("attn_q", "attn_k", "attn_v", "attn_gate", "attn_output", "ffn_gate", "ffn_up", "ffn_down")
+
+
+class TargetConfig:
+    """Dense target hyperparameters (Model::from_reader, src/model.rs:29-129, and the
+    forward's RoPE set-up, src/target.rs:321-376)."""
+
+    def __init__(self, n_embd, n_heads, n_kv, head_dim, n_ff, n_layers, n_vocab, rope_dim, rope_dim_swa=0,
+                 swa=False, rope_base=500000.0, rope_base_swa=10000.0, rms_eps=RMS_EPS, qk_eps=QK_EPS):
+        self.n_embd, self.n_heads, self.n_kv, self.head_dim = n_embd, n_heads, n_kv, head_dim
+        self.n_ff, self.n_layers, self.n_vocab = n_ff, n_layers, n_vocab
+        self.rope_dim, self.rope_dim_swa, self.swa = rope_dim, rope_dim_swa, bool(swa)
+        self.rope_base, self.rope_base_swa, self.rms_eps, self.qk_eps = rope_base, rope_base_swa, rms_eps, qk_eps
+
+
+class _TgtHparams(ctypes.Structure):
+    _fields_ = [(n, _u32) for n in ("n_embd", "n_heads", "n_kv_heads", "head_dim", "n_ff", "n_layers", "n_vocab",
+                                    "rope_dim", "rope_dim_swa")] + \
+               [("swa", _i), ("rope_base", _f), ("rope_base_swa", _f), ("rms_eps", _f), ("qk_eps", _f)]
+
+
+class _TgtLayer(ctypes.Structure):
+    _fields_ = ([(n, _vp) for n in TARGET_NORMS] + [(n, _vp) for n in TARGET_PROJ]
+                + [(n + "_type", _i) for n in TARGET_PROJ] + [("n_q_heads", _u32)])
+
+
+class _TgtModel(ctypes.Structure):
+    _fields_ = [("hp", _TgtHparams), ("layers", ctypes.POINTER(_TgtLayer)), ("output_norm", _vp), ("output", _vp),
+                ("output_type", _i)]
+
+
+class _TgtKv(ctypes.Structure):
+    _fields_ = [("k", _vp), ("v", _vp), ("capacity", _u32), ("len", _u32)]
+
+
+class TargetKvCache:
+    """TargetKvCache (src/target.rs:74-101) in device memory: per layer, `capacity`
+    positions of normed, roped keys and raw values."""
+
+    def __init__(self, target, capacity):
+        cfg = target.cfg
+        n = cfg.n_layers * capacity * cfg.n_kv * cfg.head_dim * 4
+        self.k, self.v = GpuBuffer(target.ctx, max(n, 4)), GpuBuffer(target.ctx, max(n, 4))
+        self._c = _TgtKv(self.k.ptr, self.v.ptr, capacity, 0)
+
+    @property
+    def len(self):
+        return self._c.len
+
+    @property
+    def capacity(self):
+        return self._c.capacity
+
+    def clear(self):
+        """src/target.rs:92-100 (the stored values are overwritten as tokens arrive)."""
+        self._c.len = 0
+
+    def free(self):
+        self.k.free()
+        self.v.free()
+
+
+class TargetModel:
+    """TargetModel (src/target.rs:103-605) over device tensors, dense layers.
+
+    `layers`: one dict per layer with the f32 norms of TARGET_NORMS and, for each
+    projection p of TARGET_PROJ, its raw GGUF bytes p and type p + "_dtype"
+    (attn_gate may be absent or None: no gate); "n_q_heads" defaults to
+    cfg.n_heads.  `tok_embd` (+ tok_embd_dtype) is the token embedding tensor,
+    `output` (+ output_dtype) the LM head [n_vocab][n_embd], `output_norm` its
+    norm.  Weights are uploaded as their raw GGUF bytes (load_weight,
+    src/target.rs:114-127)."""
+
+    def __init__(self, ctx, cfg, layers, tok_embd=None, tok_embd_dtype=F32, output_norm=None, output=None,
+                 output_dtype=None, target_layers=None):
+        self.ctx, self.cfg = ctx, cfg
+        self._bufs = []
+        self._tl = list(target_layers or [])
+        up = self._up
+        self._layer_desc = (_TgtLayer * len(layers))()
+        for i, L in enumerate(layers):
+            d = self._layer_desc[i]
+            for n in TARGET_NORMS:
+                setattr(d, n, up(L[n], np.float32).ptr)
+            for n in TARGET_PROJ:
+                if L.get(n) is None:
+                    assert n == "attn_gate", f"layer {i}: no {n}"
+                    continue
+                setattr(d, n, up(L[n]).ptr)
+                setattr(d, n + "_type", int(L[n + "_dtype"]))
+            d.n_q_heads = int(L.get("n_q_heads", cfg.n_heads))
+        self._desc = _TgtModel()
+        h = self._desc.hp
+        h.n_embd, h.n_heads, h.n_kv_heads, h.head_dim = cfg.n_embd, cfg.n_heads, cfg.n_kv, cfg.head_dim
+        h.n_ff, h.n_layers, h.n_vocab = cfg.n_ff, len(layers), cfg.n_vocab
+        h.rope_dim, h.rope_dim_swa, h.swa = cfg.rope_dim, cfg.rope_dim_swa, int(cfg.swa)
+        h.rope_base, h.rope_base_swa, h.rms_eps, h.qk_eps = cfg.rope_base, cfg.rope_base_swa, cfg.rms_eps, cfg.qk_eps
+        self._desc.layers = self._layer_desc
+        self._desc.output_norm = up(output_norm, np.float32).ptr if output_norm is not None else None
+        if output is not None:
+            self._desc.output = up(output).ptr
+            self._desc.output_type = int(output_dtype)
+        self._emb = up(tok_embd) if tok_embd is not None else None
+        self._emb_dtype = int(tok_embd_dtype)
+
+    def _up(self, a, dtype=None):
+        if isinstance(a, GpuBuffer):  # already on the device (e.g. uploaded from a GGUF file)
+            self._bufs.append(a)
+            return a
+        a = np.ascontiguousarray(a if dtype is None else np.asarray(a, dtype))
+        b = upload_bytes(self.ctx, a.view(np.uint8).ravel())
+        self._bufs.append(b)
+        return b
+
+    @classmethod
+    def load(cls, ctx, gguf_path):
+        """TargetModel::load (src/target.rs:129-261) for a dense model, with
+        Model::from_reader's hyperparameters (src/model.rs:29-129).  Projections stay
+        raw GGUF blocks (Q4_K, Q8_0, F32; other types are dequantized to f32 on the
+        device, as load_weight's F32 arm does on the host); norms are f32.  MoE
+        models (ffn_gate_exps tensors) are refused; a missing tensor raises."""
+        with GGUFReader(gguf_path) as rd:
+            md = rd.metadata
+            if any("ffn_gate_exps" in t.name for t in rd.tensors):
+                raise LagunaError(EUNSUPPORTED, f"{gguf_path}: MoE layers are not supported")
+            need = {"block_count": md.block_count, "embedding_length": md.embedding_length,
+                    "feed_forward_length": md.feed_forward_length, "head_count": md.attention_head_count,
+                    "head_count_kv": md.attention_head_count_kv, "key_length": md.attention_key_length}
+            missing = [k for k, v in need.items() if not v]
+            if missing:
+                raise LagunaError(EIO, f"{gguf_path}: no {', '.join(missing)} in the metadata")
+
+            def meta(*keys):  # the key aliases of GGUFReader's metadata parser (src/gguf.rs:570-604)
+                for key in keys:
+                    if rd.find_field(key) is not None:
+                        return rd.field(key)
+                return None
+
+            rope_dim_swa = int(meta("laguna.rope.dimension_count_swa", "dflash.rope.dimension_count_swa",
+                                    "rope.dimension_count_swa") or 0)
+            window = meta("laguna.attention.sliding_window", "dflash.attention.sliding_window")
+            base_swa = meta("laguna.rope.freq_base_swa", "dflash.rope.freq_base_swa", "rope.freq_base_swa")
+            E, HD = md.embedding_length, md.attention_key_length
+
+            def tensor(name, as_f32=False, required=True):
+                t = rd.tensor_by_name(name)
+                if t is None:
+                    if required:
+                        raise LagunaError(ENOTFOUND, f"{gguf_path}: no tensor {name!r}")
+                    return None, None, None
+                raw = rd.upload_tensor_quantized(ctx, t)
+                if t.dtype == F32 or (not as_f32 and t.dtype in (Q4_K, Q8_0)):
+                    return raw, t.dtype, t
+                out = GpuBuffer(ctx, 4 * t.n_elements())  # dequant_to_f32 on the device
+                dequant_to_f32_device(ctx, raw, t.n_bytes(), t.dtype, t.n_elements(), out)
+                raw.free()
+                return out, F32, t
+
+            layers = []
+            for i in range(md.block_count):
+                L = {}
+                for n in TARGET_NORMS:
+                    L[n] = tensor(f"blk.{i}.{n}.weight", True)[0]
+                for n in TARGET_PROJ:
+                    b, dt, t = tensor(f"blk.{i}.{n}.weight", required=n != "attn_gate")
+                    L[n], L[n + "_dtype"] = b, dt
+                    if n == "attn_q":  # src/target.rs:236-246
+                        L["n_q_heads"] = t.shape[1] // HD if len(t.shape) >= 2 else md.attention_head_count
+                layers.append(L)
+            emb, emb_dt, emb_t = tensor("token_embd.weight", required=False)
+            if emb_t is not None and emb_dt != emb_t.dtype:  # keep the embedding raw: rows decode on demand
+                emb.free()
+                emb, emb_dt = rd.upload_tensor_quantized(ctx, emb_t), emb_t.dtype
+            out_norm = tensor("output_norm.weight", True, required=False)[0]
+            out, out_dt, _ = tensor("output.weight", required=False)
+            n_vocab = emb_t.n_elements() // E if emb_t is not None else (md.vocab_size or 0)
+            cfg = TargetConfig(n_embd=E, n_heads=md.attention_head_count, n_kv=md.attention_head_count_kv,
+                               head_dim=HD, n_ff=md.feed_forward_length, n_layers=md.block_count, n_vocab=n_vocab,
+                               rope_dim=md.rope_dimension_count or 0, rope_dim_swa=rope_dim_swa,
+                               swa=rope_dim_swa > 0 or int(window or 0) > 0,
+                               rope_base=md.rope_freq_base if md.rope_freq_base is not None else 500000.0,
+                               rope_base_swa=float(base_swa) if base_swa is not None else 10000.0)
+            tl = md.target_layers or []
+            model = cls(ctx, cfg, layers, tok_embd=emb, tok_embd_dtype=emb_dt if emb_dt is not None else F32,
+                        output_norm=out_norm, output=out, output_dtype=out_dt, target_layers=tl)
+            model._emb_tensor = emb_t
+        ctx.sync()
+        return model
+
+    # accessors of src/target.rs:263-296
+    def layer_count(self):
+        return self._desc.hp.n_layers
+
+    def embedding_length(self):
+        return self.cfg.n_embd
+
+    def vocab_size(self):
+        return self.cfg.n_vocab
+
+    def target_layers(self):
+        return list(self._tl)
+
+    @property
+    def desc(self):
+        return ctypes.byref(self._desc)
+
+    def capture_count(self, layer_indices):
+        lst = None if layer_indices is None else np.ascontiguousarray(layer_indices, np.uint32)
+        c = _u32()
+        check(lib().lg_target_capture_count(self.layer_count(), _ptr(lst), 0 if lst is None else lst.size,
+                                            ctypes.byref(c)))
+        return c.value
+
+    def forward_token_device(self, inp, layer_indices, captured, logits, hidden=None, cache=None, stream=None):
+        """The forward on device buffers; returns the number of captured states."""
+        lst = None if layer_indices is None else np.ascontiguousarray(layer_indices, np.uint32)
+        nc = _u32()
+        check(lib().lg_target_forward_token(self.desc, _ptr(inp), _ptr(lst), 0 if lst is None else lst.size,
+                                            _ptr(captured), ctypes.byref(nc), _ptr(logits), _ptr(hidden),
+                                            ctypes.byref(cache._c) if cache is not None else None,
+                                            _stream(self.ctx, stream)))
+        return nc.value
+
+    def _forward(self, inp, layer_indices, cache):
+        E = self.cfg.n_embd
+        nc = self.capture_count(layer_indices)
+        xb = upload_f32(self.ctx, np.asarray(inp, np.float32).reshape(E))
+        cb = GpuBuffer(self.ctx, 4 * max(nc, 1) * E)
+        n_out = self.cfg.n_vocab if self._desc.output else E
+        lb = GpuBuffer(self.ctx, 4 * n_out)
+        self.forward_token_device(xb, layer_indices, cb, lb, cache=cache)
+        cap = cb.read_f32(nc * E).reshape(nc, E) if nc else np.zeros((0, E), np.float32)
+        return lb.read_f32(n_out).copy(), [c.copy() for c in cap]
+
+    def forward_token(self, inp, layer_indices=None):
+        """src/target.rs:298-300: (logits, captured hidden states)."""
+        return self._forward(inp, layer_indices, None)
+
+    def forward_token_cached(self, inp, layer_indices, cache):
+        """src/target.rs:305-312 over a TargetKvCache."""
+        return self._forward(inp, layer_indices, cache)
+
+    def project_normalized_hidden_device(self, hidden, logits):
+        check(lib().lg_dispatch_proj_quant(_ptr(hidden), self._desc.output, _ptr(logits), self.cfg.n_embd,
+                                           self.cfg.n_vocab, self._desc.output_type, self.ctx.stream))
+
+    def project_normalized_hidden(self, hidden):
+        """src/target.rs:580-605: the LM head applied to a normed hidden state."""
+        if not self._desc.output:
+            raise LagunaError(EINVAL, "project_normalized_hidden: the model has no output weight")
+        hb = upload_f32(self.ctx, np.asarray(hidden, np.float32).reshape(self.cfg.n_embd))
+        lb = GpuBuffer(self.ctx, 4 * self.cfg.n_vocab)
+        self.project_normalized_hidden_device(hb, lb)
+        return lb.read_f32(self.cfg.n_vocab).copy()
+
+    def token_embedding_device(self, token, out):
+        """target_token_embedding (src/lib.rs:431-454) into a device buffer: row
+        `token` of token_embd, decoded on the device (Q4_K as ggml blocks)."""
+        E = self.cfg.n_embd
+        if self._emb is None:
+            raise LagunaError(EINVAL, "token_embedding: the model has no token_embd tensor")
+        if not 0 <= token < self.cfg.n_vocab:
+            raise LagunaError(EINVAL, f"token_id {token} >= vocab_size {self.cfg.n_vocab}")
+        bb, be, _, _ = gguf_type_info(self._emb_dtype)
+        if (token * E) % be == 0 and E % be == 0:  # the row is whole blocks: decode only it
+            off, nbytes = token * E // be * bb, E // be * bb
+            dequant_to_f32_device(self.ctx, self._emb.ptr + off, nbytes, self._emb_dtype, E, out)
+            return
+        full = GpuBuffer(self.ctx, 4 * (token + 1) * E)
+        dequant_to_f32_device(self.ctx, self._emb, self._emb.size, self._emb_dtype, (token + 1) * E, full)
+        check(lib().lg_buf_copy(_ptr(out), full.ptr + 4 * token * E, 4 * E, self.ctx.stream))
+        self.ctx.sync()
+        full.free()
+
+    def token_embedding(self, token):
+        ob = GpuBuffer(self.ctx, 4 * self.cfg.n_embd)
+        self.token_embedding_device(token, ob)
+        return ob.read_f32(self.cfg.n_embd).copy()
+
+    def free(self):
+        for b in self._bufs:
+            b.free()
+        self._bufs = []
+
+
+class VerifyLoop:
+    """run_target_dflash_verify (src/lib.rs:466-520) with every step on the device:
+    token embedding, the target forward capturing the draft's target layers (as the
+    draft's features, [n_aux][n_embd] in layer order), the draft forward of that
+    token (forward_injected_decode_hidden), the LM head on the draft's hidden state,
+    and both argmaxes; only the two token ids come back to the host."""
+
+    def __init__(self, target, draft, target_layers=None):
+        self.target, self.draft = target, draft
+        self.layers = [int(v) for v in (target_layers if target_layers is not None else draft.target_layers())]
+        E, ctx = target.cfg.n_embd, target.ctx
+        nc = target.capture_count(self.layers)
+        if nc * E != draft.n_embd_inp():
+            raise LagunaError(EINVAL, f"the draft takes {draft.n_embd_inp()} features; the target captures "
+                                      f"{nc} states of {E} for layers {self.layers}")
+        V = target.cfg.n_vocab
+        self.emb, self.feat, self.hidden = GpuBuffer(ctx, 4 * E), GpuBuffer(ctx, 4 * nc * E), GpuBuffer(ctx, 4 * E)
+        self.logits = GpuBuffer(ctx, 4 * 2 * V)  # row 0: target, row 1: draft
+        self.tok = GpuBuffer(ctx, 8)
+
+    def step(self, token):
+        """One step: (next_token, accepted, draft_token, target_token)."""
+        t, ctx, V = self.target, self.target.ctx, self.target.cfg.n_vocab
+        t.token_embedding_device(token, self.emb)
+        t.forward_token_device(self.emb, self.layers, self.feat, self.logits)
+        self.draft.forward_block_device(self.feat, self.emb, 1, self.hidden, ctx_len=0)
+        t.project_normalized_hidden_device(self.hidden, self.logits.ptr + 4 * V)
+        tgt, drf = (int(v) for v in dispatch_argmax(ctx, self.logits, V, rows=2, out=self.tok))
+        accept = drf == tgt
+        return (drf if accept else tgt), accept, drf, tgt
+
+    def free(self):
+        for b in (self.emb, self.feat, self.hidden, self.logits, self.tok):
+            b.free()
+
+
+def run_target_dflash_verify(target, draft, start_token, n_steps, target_layers=None, log=None):
+    """src/lib.rs:466-520: returns (accepted tokens, exact accepts, per-step
+    (input, draft, target, accept)); `log` (e.g. print) receives the reference's lines."""
+    loop = VerifyLoop(target, draft, target_layers)
+    token, accepted, exact, steps = start_token, [], 0, []
+    try:
+        for step in range(n_steps):
+            nxt, ok, d, t = loop.step(token)
+            exact += int(ok)
+            accepted.append(nxt)
+            steps.append((token, d, t, ok))
+            if log:
+                log(f"step {step}: input={token} draft={d} target={t} {'ACCEPT' if ok else 'REJECT'} -> accepted={nxt}")
+            token = nxt
+    finally:
+        loop.free()
+    if log:
+        log(f"accepted tokens: {accepted}")
+        log(f"exact draft accept rate: {exact}/{n_steps}")
+    return accepted, exact, steps
 
 
 # ---------------------------------------------------------------------------------------

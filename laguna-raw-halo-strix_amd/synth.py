@@ -95,6 +95,45 @@ def q4k_weight(seed, k, n):
     return random_q4k(seed, k * n // QK_K)
 
 
+def quantize_q4k(x):
+    """f32 values (a multiple of 256) -> ggml Q4_K blocks: per 32-element sub-block
+    an offset m >= -min and a scale (max + m) / 15, both as 6-bit multiples of the
+    super-block's f16 dmin and d; nibbles q = round((x + dmin m) / (d sc)).
+    Decodes (kernels/proj_q4k.comp:46-87) to d sc q - dmin m."""
+    x = np.asarray(x, np.float32).reshape(-1, 8, 32).astype(np.float64)
+    nb = x.shape[0]
+    mn = np.maximum(-x.min(axis=2), 0.0)                     # [nb, 8]
+    sc = (x.max(axis=2) + mn) / 15.0
+    d = (sc.max(axis=1) / 63.0).astype(np.float16)
+    dmin = (mn.max(axis=1) / 63.0).astype(np.float16)
+    d64, dm64 = d.astype(np.float64)[:, None], dmin.astype(np.float64)[:, None]
+    sc6 = np.clip(np.rint(np.divide(sc, d64, out=np.zeros_like(sc), where=d64 > 0)), 0, 63).astype(np.uint32)
+    m6 = np.clip(np.rint(np.divide(mn, dm64, out=np.zeros_like(mn), where=dm64 > 0)), 0, 63).astype(np.uint32)
+    step = (d64 * sc6)[:, :, None]
+    q = np.clip(np.rint(np.divide(x + (dm64 * m6)[:, :, None], step, out=np.zeros_like(x), where=step > 0)), 0,
+                15).astype(np.uint8)
+    out = np.zeros((nb, Q4_K_BYTES), np.uint8)
+    out[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    out[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+    sb = np.zeros((nb, 12), np.uint32)
+    for j in range(4):
+        sb[:, j] = sc6[:, j] & 63
+        sb[:, j + 4] = m6[:, j] & 63
+    for j in range(4, 8):
+        sb[:, j + 4] = (sc6[:, j] & 15) | ((m6[:, j] & 15) << 4)
+        sb[:, j - 4] |= (sc6[:, j] >> 4) << 6
+        sb[:, j] |= (m6[:, j] >> 4) << 6
+    out[:, 4:16] = sb.astype(np.uint8)
+    for g in range(4):  # bytes 32g + l: low nibble element 64g + l, high nibble 64g + 32 + l
+        out[:, 16 + 32 * g:48 + 32 * g] = q[:, 2 * g, :] | (q[:, 2 * g + 1, :] << 4)
+    return out.ravel()
+
+
+def q4k_weight_normal(seed, k, n, sigma=0.02):
+    """[n rows][k] N(0, sigma) weight quantized to Q4_K (realistic magnitudes)."""
+    return quantize_q4k(normal(seed, k * n, sigma))
+
+
 def weight_bytes(dtype, k, n):
     from laguna_hip import Q4_K, Q8_0, F32
     if dtype == Q4_K:
@@ -130,10 +169,12 @@ def _weight(seed, dtype, k, n):
     raise ValueError(dtype)
 
 
-def dflash_model(seed, hp, n_layers, types=None, norm_sigma=0.0):
+def dflash_model(seed, hp, n_layers, types=None, norm_sigma=0.0, trained_scale=False):
     """Random-init draft model: (encoder dict, list of layer dicts), keys as the
     oracle's forward_block takes them.  Default types: Q4_K everywhere except
-    Q8_0 attn_output.  Norm weights are 1 + N(0, norm_sigma)."""
+    Q8_0 attn_output.  Norm weights are 1 + N(0, norm_sigma).  Q4_K weights are
+    random valid blocks (values up to a few units, far from zero-mean), or with
+    trained_scale N(0, 0.02) values quantized to Q4_K."""
     from laguna_hip import Q4_K, Q8_0
     types = {**{p: Q4_K for p in DFLASH_PROJ}, "attn_output": Q8_0, "fc": Q4_K, **(types or {})}
     shapes = dflash_shapes(hp)
@@ -142,8 +183,11 @@ def dflash_model(seed, hp, n_layers, types=None, norm_sigma=0.0):
     def norm(n):
         return (1.0 + normal(int(next(sub)), n, norm_sigma)).astype(np.float32) if norm_sigma else np.ones(n, np.float32)
 
+    def weight(s, dtype, k, n):
+        return q4k_weight_normal(s, k, n) if trained_scale and dtype == Q4_K else _weight(s, dtype, k, n)
+
     A = hp.n_aux * hp.n_embd
-    W = {"enc_aux_norm": norm(A), "fc": _weight(int(next(sub)), types["fc"], A, hp.n_embd), "fc_dtype": types["fc"],
+    W = {"enc_aux_norm": norm(A), "fc": weight(int(next(sub)), types["fc"], A, hp.n_embd), "fc_dtype": types["fc"],
          "enc_output_norm": norm(hp.n_embd), "output_norm": norm(hp.n_embd)}
     layers = []
     for _ in range(n_layers):
@@ -151,7 +195,7 @@ def dflash_model(seed, hp, n_layers, types=None, norm_sigma=0.0):
              "ffn_norm": norm(hp.n_embd)}
         for p in DFLASH_PROJ:
             k, n = shapes[p]
-            L[p] = _weight(int(next(sub)), types[p], k, n)
+            L[p] = weight(int(next(sub)), types[p], k, n)
             L[p + "_dtype"] = types[p]
         layers.append(L)
     return W, layers
@@ -167,3 +211,52 @@ def dflash_inputs(seed, hp, n_layers, m, ctx_len):
     k_ctx = [normal(int(s[4 + 2 * i]), ctx_len * kvd).reshape(ctx_len, kvd) for i in range(n_layers)]
     v_ctx = [normal(int(s[5 + 2 * i]), ctx_len * kvd).reshape(ctx_len, kvd) for i in range(n_layers)]
     return feat, tok, k_ctx, v_ctx
+
+
+# ---- dense target model (random init) -------------------------------------------------
+
+def target_model(seed, hp, types=None, gate_layers=None, n_q_heads=None, norm_sigma=0.1, output_dtype=None,
+                 emb_dtype=None):
+    """Random-init dense target (src/target.rs:30-43 tensors): (layers, extras).
+    layers: dicts keyed as the target oracle and TargetModel take them; attn_gate
+    only in gate_layers (default: every layer); n_q_heads per layer (default
+    hp.n_heads).  extras: output_norm, output (+ dtype), tok_embd (+ dtype).
+    Default types: Q4_K projections with a Q8_0 attn_output, Q4_K LM head, Q8_0
+    embeddings; every weight is N(0, 0.02) quantized to its type."""
+    from laguna_hip import Q4_K, Q8_0
+    types = {**{p: Q4_K for p in DFLASH_PROJ}, "attn_output": Q8_0, **(types or {})}
+    output_dtype = Q4_K if output_dtype is None else output_dtype
+    emb_dtype = Q8_0 if emb_dtype is None else emb_dtype
+    gate_layers = range(hp.n_layers) if gate_layers is None else gate_layers
+    sub = iter(splitmix64(seed, 8 + 16 * hp.n_layers))
+
+    def norm(n):
+        return (1.0 + normal(int(next(sub)), n, norm_sigma)).astype(np.float32)
+
+    def weight(s, dtype, k, n):  # N(0, 0.02) weights, as a trained model's are
+        if dtype == Q4_K:
+            return q4k_weight_normal(s, k, n)
+        return _weight(s, dtype, k, n)
+
+    E, HD, KVD = hp.n_embd, hp.head_dim, hp.n_kv * hp.head_dim
+    layers = []
+    for li in range(hp.n_layers):
+        H = hp.n_heads if n_q_heads is None else n_q_heads[li]
+        shapes = {"attn_q": (E, H * HD), "attn_k": (E, KVD), "attn_v": (E, KVD), "attn_gate": (E, H),
+                  "attn_output": (H * HD, E), "ffn_gate": (E, hp.n_ff), "ffn_up": (E, hp.n_ff),
+                  "ffn_down": (hp.n_ff, E)}
+        L = {"attn_norm": norm(E), "attn_q_norm": norm(HD), "attn_k_norm": norm(HD), "ffn_norm": norm(E),
+             "n_q_heads": H}
+        for p in DFLASH_PROJ:
+            k, n = shapes[p]
+            s = int(next(sub))
+            if p == "attn_gate" and li not in gate_layers:
+                L[p], L[p + "_dtype"] = None, None
+                continue
+            L[p] = weight(s, types[p], k, n)
+            L[p + "_dtype"] = types[p]
+        layers.append(L)
+    extras = {"output_norm": norm(E), "output": weight(int(next(sub)), output_dtype, E, hp.n_vocab),
+              "output_dtype": output_dtype, "tok_embd": weight(int(next(sub)), emb_dtype, E, hp.n_vocab),
+              "tok_embd_dtype": emb_dtype}
+    return layers, extras
