@@ -23,9 +23,12 @@ Pinning (tests/test_dflash_oracle.py): closed forms per op (constant vectors
 through RMSNorm, zero rotation at pos 0, norm preservation and an exact quarter
 turn of RoPE, one-key and equal-score attention, the softplus threshold), the
 reference's own constants (eps 1e-5 / 1e-6, theta 5e5, threshold 20, scale
-1/sqrt(head_dim)), and the composite against a loop-by-loop restatement at a tiny
-size.  No reference test or fixture covers these ops: beyond those checks their
-parity is unpinned.
+1/sqrt(head_dim)), and the composite against closed forms -- zero attention
+output and FFN down weights leave rmsnorm(token) * output_norm; zero attention
+norm weights make every score equal, so each token averages the context values
+over exactly the positions it may see, times softplus(0) -- and against a
+loop-by-loop restatement at a tiny size.  No reference test or fixture covers
+these ops: beyond those checks their parity is unpinned.
 """
 import numpy as np
 

@@ -243,3 +243,74 @@ def test_block_forward_one_token_is_the_reference_sequence(tiny):
         x = x + dfo.proj(f, L["ffn_down"], L["ffn_down_dtype"], CFG.n_ff, E)
     x = dfo.rmsnorm(x, W["output_norm"])
     np.testing.assert_allclose(y, x, rtol=1e-12, atol=1e-12)
+
+
+def _weights_f64(raw, dtype, k, n):
+    # the projection's dequantized weight [n][k], decoded by the C oracle alone
+    import oracle as orc
+    if dtype == lh.F32:
+        return np.asarray(raw, np.float32).reshape(n, k).astype(np.float64)
+    return orc.dequant(raw, dtype, k * n).reshape(n, k).astype(np.float64)
+
+
+def _rms(x, w, eps=1e-5):
+    x = np.asarray(x, np.float64)
+    return x * np.asarray(w, np.float64) / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+
+
+def test_block_forward_zero_branches_is_the_normed_token(tiny):
+    # attn_output = 0 and ffn_down = 0: every residual branch adds exactly zero, so the
+    # block output is rmsnorm(token) * output_norm whatever the rest of the model does
+    W, layers = tiny
+    M, C = 3, 5
+    feat, tok, kc, vc = synth.dflash_inputs(0x5EED0110, CFG, 2, M, C)
+    E, QD = CFG.n_embd, CFG.n_heads * CFG.head_dim
+    z = [dict(L, attn_output=np.zeros(QD * E, np.float32), attn_output_dtype=lh.F32,
+              ffn_down=np.zeros(CFG.n_ff * E, np.float32), ffn_down_dtype=lh.F32) for L in layers]
+    y = dfo.forward_block(feat, tok, W, z, kc, vc, C, CFG)
+    np.testing.assert_allclose(y, _rms(tok, W["output_norm"]), rtol=1e-14, atol=0)
+
+
+def test_block_forward_zero_attn_norm_is_uniform_causal_attention(tiny):
+    # attn_norm = 0 zeroes the normed rows, so every query, block key, block value and
+    # gate logit is 0: the scores are all equal, the gate is softplus(0) = ln 2, and
+    # token t (at position C + M + t) averages the values of the C + M + t + 1
+    # positions it may see, of which only the C context values are nonzero:
+    #     a_t[h] = ln 2 * sum_{p < C} v_ctx[p][kv(h)] / (C + M + t + 1),
+    #     kv(h) = h * n_kv / n_q.
+    # With ffn_down = 0 the layer adds only W_o a_t.  One layer, written out directly.
+    W, layers = tiny
+    M, C = 4, 6
+    E, H, KV, HD = CFG.n_embd, CFG.n_heads, CFG.n_kv, CFG.head_dim
+    feat, tok, kc, vc = synth.dflash_inputs(0x5EED0111, CFG, 1, M, C)
+    L = dict(layers[0], attn_norm=np.zeros(E, np.float32), ffn_down=np.zeros(CFG.n_ff * E, np.float32),
+             ffn_down_dtype=lh.F32)
+    y = dfo.forward_block(feat, tok, W, [L], kc, vc, C, CFG)
+    Wo = _weights_f64(L["attn_output"], L["attn_output_dtype"], H * HD, E)
+    vsum = np.asarray(vc[0], np.float64).reshape(C, KV, HD).sum(axis=0)
+    want = []
+    for t in range(M):
+        a = np.concatenate([vsum[h * KV // H] for h in range(H)]) * np.log(2.0) / (C + M + t + 1)
+        want.append(_rms(tok[t].astype(np.float64) + Wo @ a, W["output_norm"]))
+    np.testing.assert_allclose(y, np.array(want), rtol=1e-12, atol=1e-12 * np.max(np.abs(want)))
+
+
+def test_block_forward_constant_context_value(tiny):
+    # the same closed form with every context value row equal to c: the average over
+    # the visible positions is c * C / (C + M + t + 1), a check of the position count
+    # that does not depend on which context rows a query sees
+    W, layers = tiny
+    M, C = 2, 3
+    E, H, KV, HD = CFG.n_embd, CFG.n_heads, CFG.n_kv, CFG.head_dim
+    feat, tok, kc, _ = synth.dflash_inputs(0x5EED0112, CFG, 1, M, C)
+    c = synth.normal(0x5EED0113, KV * HD)
+    vc = [np.tile(c, (C, 1))]
+    L = dict(layers[0], attn_norm=np.zeros(E, np.float32), ffn_down=np.zeros(CFG.n_ff * E, np.float32),
+             ffn_down_dtype=lh.F32)
+    y = dfo.forward_block(feat, tok, W, [L], kc, vc, C, CFG)
+    Wo = _weights_f64(L["attn_output"], L["attn_output_dtype"], H * HD, E)
+    cr = np.asarray(c, np.float64).reshape(KV, HD)
+    for t in range(M):
+        a = np.concatenate([cr[h * KV // H] for h in range(H)]) * np.log(2.0) * C / (C + M + t + 1)
+        np.testing.assert_allclose(y[t], _rms(tok[t].astype(np.float64) + Wo @ a, W["output_norm"]), rtol=1e-12,
+                                   atol=1e-12)

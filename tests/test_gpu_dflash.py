@@ -5,14 +5,18 @@ Tolerances (all relative to the largest magnitude of the f64 result, ||y-yhat||_
 * norms, RoPE, gates: f32 arithmetic, 1e-5 (measured 1e-7);
 * attention on matrix cores: q, k, p and v enter as three bf16 parts each (all 24
   bits) with the six significant part products, 1e-5 (measured 8e-7);
-* the block forward: 1e-3 (measured 4e-7 .. 6e-5, 3.4e-5 for the full draft).
-  The random-init model (GGUF-random Q4_K blocks have a large common-mode weight)
-  drives some token rows into steep regions -- attention gates near -20, FFN
-  values of 1e3-1e4 -- where one-ulp changes inside exp move the output by 1e-3:
-  the m = 32 case has such rows (an all-f32 numpy evaluation of the same forward
-  differs from f64 there by 8e-5 in one rounding order, the GPU by 1e-4 .. 1e-3
-  as rounding orders change).  That case is held to 3e-3 and, on exactly its
-  data, every op of the chain is held to f32 grade (test_ops_f32_grade_*).
+* the block forward on weights of trained magnitude (N(0, 0.02) quantized): 3e-6
+  (measured 1.4e-7 .. 2.3e-7);
+* the block forward on GGUF-random Q4_K blocks, whose large common-mode weight
+  drives the hidden state far from trained-model ranges: about ten times each
+  case's measured error (4e-7 .. 8e-5, written per case), 1e-4 for the full draft
+  (measured 3.7e-5).  The m = 32 case has token rows in steep regions --
+  attention gates near -20, FFN values of 1e3-1e4 -- where one-ulp changes
+  inside exp move the output by 1e-3 (an all-f32 numpy evaluation of the same
+  forward differs from f64 there by 8e-5 in one rounding order, the GPU by
+  1e-4 .. 1e-3 as rounding orders change).  That case is held to 3e-3 and, on
+  exactly its data, every op of the chain is held to f32 grade
+  (test_ops_f32_grade_*).
 """
 import numpy as np
 import pytest
@@ -25,7 +29,8 @@ pytestmark = pytest.mark.gpu
 
 TOL_F32 = 1e-5
 TOL_ATTN = 1e-5
-TOL_FWD = 1e-3
+TOL_FWD = 1e-4  # the full draft on GGUF-random blocks (measured 3.7e-5)
+TOL_FWD_TRAINED = 3e-6  # measured 1.4e-7 .. 2.3e-7
 TOL_FWD_STEEP = 3e-3
 
 
@@ -141,8 +146,9 @@ SMALL = lh.DFlashConfig(n_embd=512, n_heads=4, n_kv=2, head_dim=128, rope_dim=12
 SMALL64 = lh.DFlashConfig(n_embd=256, n_heads=8, n_kv=2, head_dim=64, rope_dim=64, n_ff=512, n_aux=2, n_layers=2)
 
 
-def build(ctx, cfg, seed, m, ctx_len, norm_sigma=0.1, types=None):
-    W, layers = synth.dflash_model(seed, cfg, cfg.n_layers, types=types, norm_sigma=norm_sigma)
+def build(ctx, cfg, seed, m, ctx_len, norm_sigma=0.1, types=None, trained_scale=False):
+    W, layers = synth.dflash_model(seed, cfg, cfg.n_layers, types=types, norm_sigma=norm_sigma,
+                                   trained_scale=trained_scale)
     feat, tok, kc, vc = synth.dflash_inputs(seed + 1, cfg, cfg.n_layers, m, ctx_len)
     model = lh.DFlashModel(ctx, cfg, W, layers)
     model.set_context(kc, vc)
@@ -158,9 +164,11 @@ def test_encode(ctx):
     check("encode", model.encode(feat), dfo.encode(feat, W, cfg), 1e-4)
 
 
-@pytest.mark.parametrize("cfg,m,ctx_len,tol", [(SMALL, 1, 0, TOL_FWD), (SMALL, 7, 0, TOL_FWD),
-                                               (SMALL, 16, 100, TOL_FWD), (SMALL, 16, 64, TOL_FWD),
-                                               (SMALL, 32, 70, TOL_FWD_STEEP), (SMALL64, 5, 33, TOL_FWD)])
+# (config, m, context, tolerance): the measured error of each case, on GGUF-random
+# blocks, is 2.4e-6, 3.3e-6, 8.4e-5, 2.7e-5, 6.0e-4 and 4.1e-7
+@pytest.mark.parametrize("cfg,m,ctx_len,tol", [(SMALL, 1, 0, 3e-5), (SMALL, 7, 0, 3e-5),
+                                               (SMALL, 16, 100, 8e-4), (SMALL, 16, 64, 3e-4),
+                                               (SMALL, 32, 70, TOL_FWD_STEEP), (SMALL64, 5, 33, 1e-5)])
 def test_forward_block_small(ctx, cfg, m, ctx_len, tol):
     print(f"forward_block n_embd={cfg.n_embd} hd={cfg.head_dim} m={m} ctx={ctx_len}", flush=True)
     model, (W, layers, feat, tok, kc, vc) = build(ctx, cfg, 0x5EED0220 + m, m, ctx_len)
@@ -168,12 +176,21 @@ def test_forward_block_small(ctx, cfg, m, ctx_len, tol):
     check("forward_block", y, dfo.forward_block(feat, tok, W, layers, kc, vc, ctx_len, cfg), tol)
 
 
+@pytest.mark.parametrize("cfg,m,ctx_len", [(SMALL, 1, 0), (SMALL, 16, 100), (SMALL, 32, 70), (SMALL64, 5, 33)])
+def test_forward_block_trained_scale(ctx, cfg, m, ctx_len):
+    print(f"forward_block trained-scale weights n_embd={cfg.n_embd} m={m} ctx={ctx_len}", flush=True)
+    model, (W, layers, feat, tok, kc, vc) = build(ctx, cfg, 0x5EED0270 + m, m, ctx_len, trained_scale=True)
+    y = model.forward_block(feat, tok)
+    check("forward_block trained", y, dfo.forward_block(feat, tok, W, layers, kc, vc, ctx_len, cfg),
+          TOL_FWD_TRAINED)
+
+
 def test_forward_injected_decode_hidden(ctx):
     # the reference's entry point: one token, sequence [injected, token]
     print("forward_injected_decode_hidden (m=1, no context)", flush=True)
     model, (W, layers, feat, tok, kc, vc) = build(ctx, SMALL, 0x5EED0230, 1, 0)
     y = model.forward_injected_decode_hidden(feat[0], tok[0])
-    check("injected decode", y[None], dfo.forward_block(feat, tok, W, layers, kc, vc, 0, SMALL), TOL_FWD)
+    check("injected decode", y[None], dfo.forward_block(feat, tok, W, layers, kc, vc, 0, SMALL), 5e-5)  # 5.1e-6
 
 
 def test_forward_mixed_weight_types(ctx):
@@ -181,7 +198,7 @@ def test_forward_mixed_weight_types(ctx):
     types = {"attn_q": lh.Q8_0, "attn_k": lh.F32, "ffn_up": lh.Q8_0, "fc": lh.Q8_0}
     model, (W, layers, feat, tok, kc, vc) = build(ctx, SMALL, 0x5EED0240, 4, 20, types=types)
     check("forward mixed", model.forward_block(feat, tok),
-          dfo.forward_block(feat, tok, W, layers, kc, vc, 20, SMALL), TOL_FWD)
+          dfo.forward_block(feat, tok, W, layers, kc, vc, 20, SMALL), 1.5e-4)  # measured 1.5e-5
 
 
 def test_graph_replays_match_eager(ctx):
