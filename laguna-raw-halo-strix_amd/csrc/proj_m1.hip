@@ -4,12 +4,12 @@
 // (one invocation per output row, per-element byte decode, uncoalesced) with
 // gfx950 kernels.
 //
-// Q4_K (k % 256 == 0, k <= 16384, 16-byte aligned tensor), kernels chosen by
-// measurement:
+// Q4_K (k % 256 == 0, 16-byte aligned tensor), kernels chosen by measurement:
 //  * plain projections with k <= 4096: integer dot products of the raw nibbles
 //    against byte digits of the activations (k_q4k_m1_dig, described there).
 //  * plain projections with k > 4096: vector ALU (k_q4k_m1).  Lane p of a row
-//    team owns the 64-element group p of the row; a nibble masked in place is an
+//    team (up to 4 waves, 16384 elements per pass; longer rows take several passes)
+//    owns the 64-element group p of the pass; a nibble masked in place is an
 //    f16 subnormal (q * 2^-24, or q * 2^-20 for a high nibble), so one AND gives two
 //    operands of v_fma_mix_f32 against the f32 activations, and the block's scale
 //    and min enter once per 32-element sub-block:
@@ -24,7 +24,8 @@
 //    only its k slice); the slices of a row range are summed in slice order by
 //    the last workgroup to finish.
 //
-// Q8_0: vector ALU.  A "team" of TW = ceil(k/4096) waves covers one row: lane p of
+// Q8_0: vector ALU.  A "team" of TW = min(4, ceil(k/4096)) waves covers one row (in
+// passes of 16384 elements beyond that): lane p of
 // the team owns the 64-element group p of the row (two 34-byte blocks, 68 bytes,
 // dword aligned) and keeps the 64 activations of that group in registers; the
 // team's partial sums meet in a DPP/swizzle wavefront reduction (plus LDS across
@@ -49,7 +50,6 @@ using namespace lg;
 
 std::atomic<uint32_t> g_grid_cap{0};  // 0 = automatic
 
-constexpr uint32_t M1_MAX_K = 16384;  // 4 waves x 64 lanes x 64 elements
 constexpr int M1_RPW_MAX = 8;         // rows per team whose loads are in flight together
 
 // ------------------------------------------------------------------------------------------
@@ -217,51 +217,59 @@ __device__ __forceinline__ float q4_dot(const uint4 &hd, const uint4 &qa, const 
 
 // Rows row0 .. row0+RPW-1 of the team, loaded all at once (rows past n clamp to n-1
 // and are not stored).  Then the activations, then one row at a time as it lands.
+// k beyond one pass of the team (TW * 4096 elements) is covered in passes whose
+// partial sums accumulate per row.
 template <int TW, int TEAMS, int RPW, bool FUSE>
 __global__ __launch_bounds__(TW *TEAMS * 64) void k_q4k_m1(const float *__restrict__ x, const float *__restrict__ up,
                                                             const uint8_t *__restrict__ w, float *__restrict__ y,
                                                             uint32_t k, uint32_t n, uint64_t row_bytes) {
     constexpr int XPT = (16 * TW + TEAMS * TW - 1) / (TEAMS * TW);
+    constexpr uint32_t KPASS = TW * 64 * 64;  // elements one pass covers
     __shared__ __attribute__((aligned(16))) float xs[TW * 64 * 68];
     __shared__ float red[TW > 1 ? TEAMS * RPW * TW : 1];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t team = wave / TW, wt = wave % TW;
-    const uint32_t P = k >> 6;
     const uint32_t p0 = wt * 64 + lane;
-    const bool active = p0 < P;
-    const uint32_t p = active ? p0 : 0;  // idle lanes read group 0 and contribute 0
-    const Q4Lane L = q4_lane(p & 3u);
-    const uint64_t lane_off = (uint64_t)(p >> 2) * Q4K_BYTES;
+    const Q4Lane L = q4_lane(p0 & 3u);  // passes start at multiples of 256 elements: the same group parity
     const uint32_t qoff = 16 + 32 * L.g;
     const uint32_t row0 = (blockIdx.x * TEAMS + team) * RPW;
 
-    XFetch<XPT, FUSE> xf;
-    x_fetch<XPT, FUSE>(xf, x, up, k);
-    uint4 hd[RPW], qa[RPW], qb[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const uint32_t row = row0 + r < n ? row0 + r : n - 1;
-        const uint8_t *blk = w + (uint64_t)row * row_bytes + lane_off;
-        hd[r] = *reinterpret_cast<const uint4 *>(blk);
-        qa[r] = *reinterpret_cast<const uint4 *>(blk + qoff);
-        qb[r] = *reinterpret_cast<const uint4 *>(blk + qoff + 16);
-    }
-    float xr[64];
-    x_share<XPT, FUSE>(xf, k, wt, lane, xs, xr);
-    if (!active) {
-#pragma unroll
-        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
-    }
-    float X0 = 0.f, X1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
-
-    // Idle lanes contribute an explicit 0, not 0 * (a scale that may be inf or NaN).
     float acc[RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const float v = q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L);
-        acc[r] = active ? v : 0.0f;
+    for (int r = 0; r < RPW; r++) acc[r] = 0.0f;
+    for (uint32_t c0 = 0; c0 < k; c0 += KPASS) {  // uniform over the workgroup
+        const uint32_t kc = k - c0 < KPASS ? k - c0 : KPASS;
+        const bool active = p0 < (kc >> 6);
+        const uint32_t p = active ? p0 : 0;  // idle lanes read group 0 and contribute 0
+        const uint64_t lane_off = (uint64_t)(c0 / QK_K + (p >> 2)) * Q4K_BYTES;
+        XFetch<XPT, FUSE> xf;
+        x_fetch<XPT, FUSE>(xf, x + c0, FUSE ? up + c0 : up, kc);
+        uint4 hd[RPW], qa[RPW], qb[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const uint32_t row = row0 + r < n ? row0 + r : n - 1;
+            const uint8_t *blk = w + (uint64_t)row * row_bytes + lane_off;
+            hd[r] = *reinterpret_cast<const uint4 *>(blk);
+            qa[r] = *reinterpret_cast<const uint4 *>(blk + qoff);
+            qb[r] = *reinterpret_cast<const uint4 *>(blk + qoff + 16);
+        }
+        if (c0) __syncthreads();  // every wave has read the previous pass's activations
+        float xr[64];
+        x_share<XPT, FUSE>(xf, kc, wt, lane, xs, xr);
+        if (!active) {
+#pragma unroll
+            for (int i = 0; i < 64; i++) xr[i] = 0.0f;
+        }
+        float X0 = 0.f, X1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
+
+        // Idle lanes contribute an explicit 0, not 0 * (a scale that may be inf or NaN).
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const float v = q4_dot(hd[r], qa[r], qb[r], xr, X0, X1, L);
+            acc[r] += active ? v : 0.0f;
+        }
     }
     team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
 }
@@ -308,59 +316,67 @@ __global__ __launch_bounds__(TW *TEAMS * 64) void k_q80_m1(const float *__restri
                                                             float *__restrict__ y, uint32_t k, uint32_t n,
                                                             uint64_t row_bytes) {
     constexpr int XPT = (16 * TW + TEAMS * TW - 1) / (TEAMS * TW);
+    constexpr uint32_t KPASS = TW * 64 * 64;  // elements one pass of the team covers
     __shared__ __attribute__((aligned(16))) float xs[TW * 64 * 68];
     __shared__ __attribute__((aligned(16))) lg_u32x4 stage_all[TW * TEAMS][64 * Q8_LOADS];
     __shared__ float red[TW > 1 ? TEAMS * RPW * TW : 1];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t team = wave / TW, wt = wave % TW;
-    const uint32_t P = k >> 6;
     const uint32_t p0 = wt * 64 + lane;
-    const bool active = p0 < P;
-    // this wave's share of a row: groups wt*64 .. min(P, wt*64+64), a multiple of 4 groups
-    const uint32_t groups = P > wt * 64 ? (P - wt * 64 < 64 ? P - wt * 64 : 64) : 0;
-    const uint32_t seg16 = groups * 68 / 16;
     lg_u32x4 *stage = stage_all[wave];
     const uint32_t row0 = (blockIdx.x * TEAMS + team) * RPW;
-
-    XFetch<XPT, false> xf;
-    x_fetch<XPT, false>(xf, x, nullptr, k);
     constexpr int NL = (int)Q8_LOADS;
-    lg_u32x4 c[RPW * NL];  // native vectors: plain loads and stores, kept in registers
-#pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        const uint32_t row = row0 + r < n ? row0 + r : n - 1;
-        const lg_u32x4 *src =
-            reinterpret_cast<const lg_u32x4 *>(w + (uint64_t)row * row_bytes + (uint64_t)wt * Q8_SEG);
-#pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const uint32_t ch = lane + 64 * i;
-            c[r * NL + i] = src[ch < seg16 ? ch : 0];  // chunks past the share re-read chunk 0
-        }
-    }
-    float xr[64];
-    x_share<XPT, false>(xf, k, wt, lane, xs, xr);
-    if (!active) {
-#pragma unroll
-        for (int i = 0; i < 64; i++) xr[i] = 0.0f;
-    }
-    float X0 = 0.f, X1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
 
-    // Idle lanes read stage words nobody wrote: their partials are replaced by 0.
     float acc[RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
+    for (int r = 0; r < RPW; r++) acc[r] = 0.0f;
+    for (uint32_t c0 = 0; c0 < k; c0 += KPASS) {  // uniform over the workgroup
+        const uint32_t kc = k - c0 < KPASS ? k - c0 : KPASS;
+        const uint32_t P = kc >> 6;
+        const bool active = p0 < P;
+        // this wave's share of the pass: groups wt*64 .. min(P, wt*64+64), a multiple of 4 groups
+        const uint32_t groups = P > wt * 64 ? (P - wt * 64 < 64 ? P - wt * 64 : 64) : 0;
+        const uint32_t seg16 = groups * 68 / 16;
+        XFetch<XPT, false> xf;
+        x_fetch<XPT, false>(xf, x + c0, nullptr, kc);
+        lg_u32x4 c[RPW * NL];  // native vectors: plain loads and stores, kept in registers
 #pragma unroll
-        for (int i = 0; i < NL; i++) stage[lane + 64 * i] = c[r * NL + i];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const float v = q8_dot(reinterpret_cast<const uint32_t *>(stage) + 17 * lane, xr, X0, X1);
-        acc[r] = active ? v : 0.0f;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int r = 0; r < RPW; r++) {
+            const uint32_t row = row0 + r < n ? row0 + r : n - 1;
+            const lg_u32x4 *src = reinterpret_cast<const lg_u32x4 *>(w + (uint64_t)row * row_bytes +
+                                                                     (uint64_t)c0 / QK8_0 * Q80_BYTES +
+                                                                     (uint64_t)wt * Q8_SEG);
+#pragma unroll
+            for (int i = 0; i < NL; i++) {
+                const uint32_t ch = lane + 64 * i;
+                c[r * NL + i] = src[ch < seg16 ? ch : 0];  // chunks past the share re-read chunk 0
+            }
+        }
+        if (c0) __syncthreads();  // every wave has read the previous pass's activations
+        float xr[64];
+        x_share<XPT, false>(xf, kc, wt, lane, xs, xr);
+        if (!active) {
+#pragma unroll
+            for (int i = 0; i < 64; i++) xr[i] = 0.0f;
+        }
+        float X0 = 0.f, X1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) X0 += xr[i], X1 += xr[32 + i];
+
+        // Idle lanes read stage words nobody wrote: their partials are replaced by 0.
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+#pragma unroll
+            for (int i = 0; i < NL; i++) stage[lane + 64 * i] = c[r * NL + i];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const float v = q8_dot(reinterpret_cast<const uint32_t *>(stage) + 17 * lane, xr, X0, X1);
+            acc[r] += active ? v : 0.0f;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
     }
     team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
 }
@@ -981,6 +997,11 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     }
 }
 
+__global__ __launch_bounds__(256) void k_fill_zero(float *__restrict__ c, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) c[i] = 0.0f;
+}
+
 // ------------------------------------------------------------------------------------------
 // f32 weights: kernels/proj.comp (row_major = 0: w[i*k+j]; 1: w[j*n+i])
 
@@ -1197,9 +1218,9 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
     LG_REQUIRE(dtype == LG_Q4_K || dtype == LG_Q8_0 || dtype == LG_F32, "%s: unsupported weight dtype %d", name,
                dtype);
     hipStream_t s = (hipStream_t)stream;
-    if (k == 0) {  // empty sum: c = 0
+    if (k == 0) {  // empty sum: c = 0 (a fill kernel, which graph capture records safely)
         LG_EXTENT(c, (uint64_t)n * 4, name);
-        LG_HIP_TRY(hipMemsetAsync(c, 0, (uint64_t)n * 4, s));
+        hipLaunchKernelGGL(k_fill_zero, dim3((n + 255) / 256), dim3(256), 0, s, c, n);
         return after_launch(name, s);
     }
     const bool fuse = up != nullptr;
@@ -1211,7 +1232,7 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
     LG_EXTENT(w, tensor_bytes(dtype, elems), name);
 
     const uint8_t *wb = static_cast<const uint8_t *>(w);
-    const bool vec_ok = aligned16(x) && (!fuse || aligned16(up)) && k % QK_K == 0 && k <= M1_MAX_K;
+    const bool vec_ok = aligned16(x) && (!fuse || aligned16(up)) && k % QK_K == 0;
     if (dtype == LG_Q4_K && vec_ok && expert_offset % QK_K == 0) {
         const uint8_t *wbase = wb + (uint64_t)expert_offset / QK_K * Q4K_BYTES;
         if (aligned16(wbase))

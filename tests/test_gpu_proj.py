@@ -107,7 +107,8 @@ def test_q4k_exponent0_scales(ctx):
 
 @pytest.mark.parametrize("dtype", [lh.Q4_K, lh.Q8_0])
 @pytest.mark.parametrize("k,n", [(256, 1), (256, 7), (512, 33), (768, 5), (1024, 64), (2048, 9),
-                                 (2304, 11), (3072, 13), (4352, 3), (6144, 17), (16384, 5)])
+                                 (2304, 11), (3072, 13), (4352, 3), (6144, 17), (16384, 5),
+                                 (16640, 7), (20480, 64), (32768, 33)])  # past 16384: passes over k
 def test_small_and_odd_shapes(ctx, dtype, k, n):
     seed = 1000 + k + n
     print(f"proj small dtype={dtype} k={k} n={n}", flush=True)

@@ -45,7 +45,7 @@ def test_k_slices(ctx, split):
     parity(y1, y64, a, TOL)
 
 
-@pytest.mark.parametrize("k,n", [(256, 3), (512, 17), (4096, 4096), (12288, 64), (16384, 33)])
+@pytest.mark.parametrize("k,n", [(256, 3), (512, 17), (4096, 4096), (12288, 64), (16384, 33), (20480, 40)])
 def test_shapes(ctx, k, n):
     print(f"fused k={k} n={n}", flush=True)
     raw = synth.q4k_weight(210 + k, k, n)
