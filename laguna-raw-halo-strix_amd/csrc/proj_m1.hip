@@ -15,12 +15,14 @@
 //    and min enter once per 32-element sub-block:
 //        sum_j x_j ((d sc) q_j - dmin m) = d sc 2^24 S - dmin m X,
 //        S = sum x q 2^-24,  X = sum x (per lane, once).
-//  * the fused SiLU(gate)*up down projection: int8 matrix cores (k_q4k_m1_mfma).
-//    The activations become exact integers (three signed byte digits per element,
-//    one power-of-two scale per 256-element super-block) and the raw nibbles are
-//    the other operand, so a byte product costs no decode; each (row, sub-block)
-//    pair gets its scale and min once, in an f32 epilogue.  Work is split over
-//    workgroups by rows and by k (each workgroup computes SiLU for, and converts,
+//  * the fused SiLU(gate)*up down projection: int8 matrix cores, k_q4k_m1_wide (one
+//    workgroup per 16 rows holds all of k, k <= 16384; described there) or, beyond,
+//    k_q4k_m1_mfma.
+//    In both, the activations become exact integers (three signed byte digits per
+//    element, one power-of-two scale per 256-element super-block) and the raw nibbles
+//    are the other operand, so a byte product costs no decode; each (row, sub-block)
+//    pair gets its scale and min once, in an f32 epilogue.  k_q4k_m1_mfma splits work
+//    over workgroups by rows and by k (each workgroup computes SiLU for, and converts,
 //    only its k slice); the slices of a row range are summed in slice order by
 //    the last workgroup to finish.
 //
@@ -997,6 +999,234 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// Q4_K M = 1 on int8 matrix cores with k split over the waves of one workgroup
+// (k_q4k_m1_wide): the fused SiLU(gate)*up down projection.
+//
+// A workgroup owns RG groups of 16 rows and all of k: wave v takes super-blocks
+// SPC*v .. SPC*v+SPC-1, converts their activations (with FUSE, silu(gate)*up) into
+// its own LDS table of byte digits, and multiplies them by the raw nibbles of its 16
+// rows with v_mfma_i32_16x16x64_i8.  The waves' row sums meet in LDS once at the end,
+// so no partial sum leaves the workgroup and nothing waits on other workgroups.
+//
+// Digits.  Each 256-element super-block is scaled by 2^sh (max|x| 2^sh in
+// [2^20, 2^21)) and rounded to integers X, whose bytes XOR 0x80 are signed digits
+// t0, t1, t2 with X = t0 + 2^8 t1 + 2^16 t2.  The A operand's row 4g+d holds digit
+// d of the 64 elements of group g, in the k-block (lanes 16g..16g+15) where B holds
+// that group's nibbles, and zeros elsewhere; so C[4g+d][n] is digit d's dot product
+// with row n's group g, and lane n + 16g receives all three in registers 0..2:
+//     sum_j X_j q_j = C0 + 2^8 C1 + 2^16 C2   (per sub-block, exact in int32).
+// Two MFMAs per sub-block (low nibbles: bytes 0-15 and 16-31 of the group's 32) give
+// sub-block 2g, two more (high nibbles) sub-block 2g+1.  The f32 epilogue per lane:
+//     d 2^-sh (sc_2g S_2g + sc_2g+1 S_2g+1) - dmin (m_2g X_2g + m_2g+1 X_2g+1).
+// Super-blocks holding a non-finite value, a magnitude >= 2^21 or a nonzero magnitude
+// below 2^-60 cannot be scaled that way: if any does, the workgroup's rows take the
+// reference's per-element loop.
+constexpr uint32_t WIDE_TAB = 768;  // one super-block's digit table: 4 groups x 3 digits x 64 bytes
+
+__host__ __device__ constexpr uint32_t wide_wave_lds(int spc) { return 2 * spc * WIDE_TAB + spc * 8 * 4 + spc * 4; }
+inline uint32_t wide_lds_bytes(uint32_t waves, uint32_t rg, int spc) {
+    return waves * wide_wave_lds(spc) + waves * rg * 16 * 4 + waves * 4;
+}
+
+// xor-16 / xor-32 partners through the gfx950 lane swaps
+__device__ __forceinline__ uint32_t max_x16(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return p[0] > p[1] ? p[0] : p[1];
+}
+__device__ __forceinline__ uint32_t max_x32(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return p[0] > p[1] ? p[0] : p[1];
+}
+__device__ __forceinline__ float add_x16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float add_x32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int RG, int SPC, bool FUSE>
+__global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ x, const float *__restrict__ up,
+                                                      const uint8_t *__restrict__ w, float *__restrict__ y,
+                                                      uint32_t n, uint32_t nsb, uint64_t row_bytes) {
+    constexpr uint32_t WLDS = wide_wave_lds(SPC);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, KQ = blockDim.x >> 6;
+    const uint32_t nn = l & 15u, g = l >> 4;
+    const uint32_t row0 = blockIdx.x * (16u * RG);
+    const uint32_t sb0 = wave * SPC;
+    const uint32_t cnt = sb0 < nsb ? (nsb - sb0 < (uint32_t)SPC ? nsb - sb0 : (uint32_t)SPC) : 0u;
+    uint8_t *T = lds + wave * WLDS;        // digit tables
+    uint8_t *Z = T + SPC * WIDE_TAB;       // zeros: the A operand's rows outside their k-block
+    float *Xs = reinterpret_cast<float *>(Z + SPC * WIDE_TAB);  // sub-block sums of x
+    float *Fs = Xs + SPC * 8;                                   // 2^-sh per super-block
+    float *s_part = reinterpret_cast<float *>(lds + KQ * WLDS);
+    uint32_t *s_bad = reinterpret_cast<uint32_t *>(s_part + KQ * RG * 16);
+    // the super-block of step t (steps past this wave's share re-read a valid one; dropped)
+    uint32_t sbt[SPC];
+#pragma unroll
+    for (int t = 0; t < SPC; t++) sbt[t] = sb0 + t < nsb ? sb0 + t : nsb - 1u;
+
+    // activations first (loads complete in issue order), then every weight load
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *u4 = reinterpret_cast<const float4 *>(up);
+    float4 xv[SPC], uv[FUSE ? SPC : 1];
+#pragma unroll
+    for (int t = 0; t < SPC; t++) {
+        xv[t] = x4[sbt[t] * 64u + l];
+        if constexpr (FUSE) uv[t] = u4[sbt[t] * 64u + l];
+    }
+    uint4 hd[RG][SPC], q0[RG][SPC], q1[RG][SPC];  // header and the lane's 32 quant bytes of group g
+#pragma unroll
+    for (int r = 0; r < RG; r++) {
+        const uint32_t row = row0 + 16u * r + nn < n ? row0 + 16u * r + nn : n - 1u;
+        const uint8_t *base = w + (uint64_t)row * row_bytes;
+#pragma unroll
+        for (int t = 0; t < SPC; t++) {
+            const uint8_t *b = base + sbt[t] * Q4K_BYTES;
+            hd[r][t] = *reinterpret_cast<const uint4 *>(b);
+            q0[r][t] = *reinterpret_cast<const uint4 *>(b + 16 + 32 * g);
+            q1[r][t] = *reinterpret_cast<const uint4 *>(b + 32 + 32 * g);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (int)(SPC * WIDE_TAB / 1024); i++)
+        *reinterpret_cast<uint4 *>(Z + l * 16u + i * 1024u) = make_uint4(0, 0, 0, 0);
+
+    // digits: lane l converts elements 4l .. 4l+3 of each super-block
+    uint32_t bad = 0;
+#pragma unroll
+    for (int t = 0; t < SPC; t++) {
+        float4 v = xv[t];
+        if constexpr (FUSE) {
+            const float4 u = uv[t];
+            v = make_float4(silu_mul(v.x, u.x), silu_mul(v.y, u.y), silu_mul(v.z, u.z), silu_mul(v.w, u.w));
+        }
+        uint32_t mb = max(max(__float_as_uint(v.x) & 0x7FFFFFFFu, __float_as_uint(v.y) & 0x7FFFFFFFu),
+                          max(__float_as_uint(v.z) & 0x7FFFFFFFu, __float_as_uint(v.w) & 0x7FFFFFFFu));
+        mb = max(mb, dpp_u<0xB1>(mb));   // quad_perm 1,0,3,2
+        mb = max(mb, dpp_u<0x4E>(mb));   // quad_perm 2,3,0,1
+        mb = max(mb, dpp_u<0x124>(mb));  // row_ror 4
+        mb = max(mb, dpp_u<0x128>(mb));  // row_ror 8
+        mb = max_x16(mb);
+        mb = max_x32(mb);
+        const bool outside = mb >= 0x4A000000u || (mb != 0u && mb < 0x21800000u);  // >= 2^21 or NaN/inf; < 2^-60
+        bad |= outside && t < (int)cnt ? 1u : 0u;
+        const int E = (int)(mb >> 23) - 127;
+        const int sh = (mb == 0u || outside) ? 0 : 20 - E;
+        const float scale = __uint_as_float((uint32_t)(127 + sh) << 23);
+        const uint32_t U0 = __float_as_uint(__builtin_fmaf(v.x, scale, 12582912.0f)) - 0x4ABF7F80u;
+        const uint32_t U1 = __float_as_uint(__builtin_fmaf(v.y, scale, 12582912.0f)) - 0x4ABF7F80u;
+        const uint32_t U2 = __float_as_uint(__builtin_fmaf(v.z, scale, 12582912.0f)) - 0x4ABF7F80u;
+        const uint32_t U3 = __float_as_uint(__builtin_fmaf(v.w, scale, 12582912.0f)) - 0x4ABF7F80u;
+        const uint32_t lo01 = __builtin_amdgcn_perm(U1, U0, 0x05010400u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(U3, U2, 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(U1, U0, 0x0C0C0602u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(U3, U2, 0x0C0C0602u);
+        uint8_t *tp = T + t * WIDE_TAB + (l >> 4) * 192u + 4u * (l & 15u);
+        *reinterpret_cast<uint32_t *>(tp) = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+        *reinterpret_cast<uint32_t *>(tp + 64) = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+        *reinterpret_cast<uint32_t *>(tp + 128) = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+        float sum = (v.x + v.y) + (v.z + v.w);
+        sum += dpp_f<0xB1>(sum);
+        sum += dpp_f<0x4E>(sum);
+        sum += dpp_f<0x124>(sum);  // row_ror 4 brings lane i-4: lane 8j+4 holds lanes 8j .. 8j+7
+        if ((l & 7u) == 4u) Xs[t * 8 + (l >> 3)] = sum;
+        if (l == 0) Fs[t] = __uint_as_float((uint32_t)(127 - sh) << 23);
+    }
+    wave_lds_fence();
+
+    // lane roles for the A operand: row i = 4 slot + d, digits where slot == k-block g and d < 3
+    const uint32_t slotA = (l & 15u) >> 2, dA = l & 3u;
+    const uint8_t *abase = slotA == g && dA < 3u ? T + g * 192u + dA * 64u : Z;
+    const Q4Lane L = q4_lane(g);  // scale / min bit positions of sub-blocks 2g, 2g+1
+    const bool lo = g < 2;
+
+    float acc[RG];
+#pragma unroll
+    for (int r = 0; r < RG; r++) acc[r] = 0.0f;
+    const lg_i32x4 z4 = {0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < SPC; t++) {
+        const bool live = t < (int)cnt;
+        const lg_i32x4 A00 = *reinterpret_cast<const lg_i32x4 *>(abase + t * WIDE_TAB);
+        const lg_i32x4 A10 = *reinterpret_cast<const lg_i32x4 *>(abase + t * WIDE_TAB + 16);
+        const lg_i32x4 A01 = *reinterpret_cast<const lg_i32x4 *>(abase + t * WIDE_TAB + 32);
+        const lg_i32x4 A11 = *reinterpret_cast<const lg_i32x4 *>(abase + t * WIDE_TAB + 48);
+        const float2 X2 = *reinterpret_cast<const float2 *>(Xs + t * 8 + 2 * g);
+        const float F = Fs[t];
+#pragma unroll
+        for (int r = 0; r < RG; r++) {
+            const uint4 a = q0[r][t], b = q1[r][t];
+            const lg_i32x4 bl0 = {(int)(a.x & 0x0F0F0F0Fu), (int)(a.y & 0x0F0F0F0Fu), (int)(a.z & 0x0F0F0F0Fu),
+                                  (int)(a.w & 0x0F0F0F0Fu)};
+            const lg_i32x4 bl1 = {(int)(b.x & 0x0F0F0F0Fu), (int)(b.y & 0x0F0F0F0Fu), (int)(b.z & 0x0F0F0F0Fu),
+                                  (int)(b.w & 0x0F0F0F0Fu)};
+            const lg_i32x4 bh0 = {(int)((a.x >> 4) & 0x0F0F0F0Fu), (int)((a.y >> 4) & 0x0F0F0F0Fu),
+                                  (int)((a.z >> 4) & 0x0F0F0F0Fu), (int)((a.w >> 4) & 0x0F0F0F0Fu)};
+            const lg_i32x4 bh1 = {(int)((b.x >> 4) & 0x0F0F0F0Fu), (int)((b.y >> 4) & 0x0F0F0F0Fu),
+                                  (int)((b.z >> 4) & 0x0F0F0F0Fu), (int)((b.w >> 4) & 0x0F0F0F0Fu)};
+            lg_i32x4 cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A00, bl0, z4, 0, 0, 0);
+            cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(A10, bl1, cl, 0, 0, 0);
+            lg_i32x4 ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(A01, bh0, z4, 0, 0, 0);
+            ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(A11, bh1, ch, 0, 0, 0);
+            const uint4 h = hd[r][t];
+            const float Se = (float)(cl[0] + (cl[1] << 8) + (cl[2] << 16));
+            const float So = (float)(ch[0] + (ch[1] << 8) + (ch[2] << 16));
+            const float d = mq_half(h.x & 0xFFFFu) * F, dm = mq_half(h.x >> 16);
+            const uint32_t srcA = lo ? h.y : h.w, srcM = lo ? h.z : h.w;
+            const float sce = (float)(__builtin_amdgcn_ubfe(srcA, L.sa[0], 4) | (__builtin_amdgcn_ubfe(h.y, L.sb[0], 2) << 4));
+            const float sco = (float)(__builtin_amdgcn_ubfe(srcA, L.sa[1], 4) | (__builtin_amdgcn_ubfe(h.y, L.sb[1], 2) << 4));
+            const float me = (float)(__builtin_amdgcn_ubfe(srcM, L.ma[0], 4) | (__builtin_amdgcn_ubfe(h.z, L.mb[0], 2) << 4));
+            const float mo = (float)(__builtin_amdgcn_ubfe(srcM, L.ma[1], 4) | (__builtin_amdgcn_ubfe(h.z, L.mb[1], 2) << 4));
+            const float ts = __builtin_fmaf(sco, So, sce * Se);
+            const float tm = __builtin_fmaf(mo, X2.y, me * X2.x);
+            const float v = __builtin_fmaf(-dm, tm, d * ts);
+            acc[r] += live ? v : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RG; r++) {
+        acc[r] = add_x32(add_x16(acc[r]));  // the 4 groups of row nn
+        if (g == 0) s_part[wave * (RG * 16) + 16 * r + nn] = acc[r];
+    }
+    if (l == 0) s_bad[wave] = bad;
+    __syncthreads();
+    uint32_t any_bad = 0;
+    for (uint32_t i = 0; i < KQ; i++) any_bad |= s_bad[i];
+    if (!any_bad) {
+        if (threadIdx.x < RG * 16u && row0 + threadIdx.x < n) {
+            float sum = 0.0f;
+            for (uint32_t i = 0; i < KQ; i++) sum += s_part[i * (RG * 16) + threadIdx.x];
+            y[row0 + threadIdx.x] = sum;
+        }
+        return;
+    }
+    // the reference's per-element loop (kernels/proj_q4k.comp:60-75, activation.comp:21-28)
+    for (uint32_t rr = wave; rr < RG * 16u; rr += KQ) {
+        const uint32_t row = row0 + rr;
+        if (row >= n) break;
+        float a = 0.0f;
+        for (uint32_t j = l; j < nsb * QK_K; j += 64u) {
+            float xj = x[j];
+            if constexpr (FUSE) xj = silu_mul(xj, up[j]);
+            a = __builtin_fmaf(xj, q4k_elem(w, (uint64_t)row * nsb * QK_K + j), a);
+        }
+        a = wave_sum(a);
+        if (l == 0) y[row] = a;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_fill_zero(float *__restrict__ c, uint32_t n) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) c[i] = 0.0f;
@@ -1135,6 +1365,35 @@ int launch_q4k_mfma(const float *x, const float *up, const uint8_t *w, float *y,
     return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
 }
 
+// k_q4k_m1_wide: one workgroup per 16 rows, ceil(k / 1024) waves of 4 super-blocks
+// each (k <= 16384), its LDS allowed past the 64 KiB default once per device.
+constexpr int WIDE_SPC = 4;
+constexpr uint32_t WIDE_MAX_SB = 16 * WIDE_SPC;
+
+std::mutex g_wide_mu;
+bool g_wide_attr[64][2] = {};
+
+template <bool FUSE>
+int launch_q4k_wide(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n,
+                    hipStream_t s) {
+    int dev = 0;
+    LG_HIP_TRY(hipGetDevice(&dev));
+    LG_REQUIRE(dev >= 0 && dev < 64, "proj_q4k_m1: device %d", dev);
+    {
+        std::lock_guard<std::mutex> lk(g_wide_mu);
+        if (!g_wide_attr[dev][FUSE]) {
+            LG_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_q4k_m1_wide<1, WIDE_SPC, FUSE>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)wide_lds_bytes(16, 1, WIDE_SPC)));
+            g_wide_attr[dev][FUSE] = true;
+        }
+    }
+    const uint32_t nsb = k / QK_K, waves = (nsb + WIDE_SPC - 1) / WIDE_SPC;
+    hipLaunchKernelGGL((k_q4k_m1_wide<1, WIDE_SPC, FUSE>), dim3((n + 15) / 16), dim3(waves * 64),
+                       wide_lds_bytes(waves, 1, WIDE_SPC), s, x, up, w, y, n, nsb, (uint64_t)nsb * Q4K_BYTES);
+    return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
+}
+
 template <int TW, int TEAMS, int RPW, bool FUSE>
 void launch_q4k_r(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n,
                   hipStream_t s) {
@@ -1235,10 +1494,14 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
     const bool vec_ok = aligned16(x) && (!fuse || aligned16(up)) && k % QK_K == 0;
     if (dtype == LG_Q4_K && vec_ok && expert_offset % QK_K == 0) {
         const uint8_t *wbase = wb + (uint64_t)expert_offset / QK_K * Q4K_BYTES;
-        if (aligned16(wbase))
-            // Measured on MI355X: the matrix-core kernel wins where the activation work is
-        // heavy (the fused SiLU); the vector kernels win on the plain projections.
-        return fuse ? launch_q4k_mfma<true>(x, up, wbase, c, k, n, s) : launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
+        if (aligned16(wbase)) {
+            // Measured on MI355X: the vector kernels win on the plain projections; the fused
+            // SiLU's activation work favours int8 matrix cores, with all of k in one
+            // workgroup up to 16384 and split over workgroups beyond.
+            if (!fuse) return launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
+            return k / QK_K <= WIDE_MAX_SB ? launch_q4k_wide<true>(x, up, wbase, c, k, n, s)
+                                           : launch_q4k_mfma<true>(x, up, wbase, c, k, n, s);
+        }
     }
     if (dtype == LG_Q8_0 && vec_ok && !fuse && aligned16(wb)) return launch_q80(x, wb, c, k, n, s);
     if (dtype == LG_F32 && !fuse) {
