@@ -7,7 +7,8 @@
 // Q4_K (k % 256 == 0, 16-byte aligned tensor), kernels chosen by measurement:
 //  * plain projections with k <= 4096: integer dot products of the raw nibbles
 //    against byte digits of the activations (k_q4k_m1_dig, described there).
-//  * plain projections with k > 4096: vector ALU (k_q4k_m1).  Lane p of a row
+//  * plain projections with 4096 < k <= 16384: k_q4k_m1_wide, as the fused path below.
+//  * plain projections with k > 16384: vector ALU (k_q4k_m1).  Lane p of a row
 //    team (up to 4 waves, 16384 elements per pass; longer rows take several passes)
 //    owns the 64-element group p of the pass; a nibble masked in place is an
 //    f16 subnormal (q * 2^-24, or q * 2^-20 for a high nibble), so one AND gives two
@@ -1495,12 +1496,16 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
     if (dtype == LG_Q4_K && vec_ok && expert_offset % QK_K == 0) {
         const uint8_t *wbase = wb + (uint64_t)expert_offset / QK_K * Q4K_BYTES;
         if (aligned16(wbase)) {
-            // Measured on MI355X: the vector kernels win on the plain projections; the fused
-            // SiLU's activation work favours int8 matrix cores, with all of k in one
-            // workgroup up to 16384 and split over workgroups beyond.
-            if (!fuse) return launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
-            return k / QK_K <= WIDE_MAX_SB ? launch_q4k_wide<true>(x, up, wbase, c, k, n, s)
-                                           : launch_q4k_mfma<true>(x, up, wbase, c, k, n, s);
+            // Measured on MI355X (4096 -> 14336 / 14336 -> 4096): k <= 4096 plain, the
+            // integer dot kernel (8.8 us; k_q4k_m1_wide 9.8); up to 16384, all of k in one
+            // workgroup on int8 matrix cores (plain 10.5 us against 13.8 for the vector
+            // kernel; fused 11.4-11.8 against 13.9 split over workgroups); beyond, the
+            // vector kernel in passes (plain) or the split matrix-core kernel (fused).
+            const bool wide = k / QK_K <= WIDE_MAX_SB;
+            if (!fuse) return k > 4096 && wide ? launch_q4k_wide<false>(x, nullptr, wbase, c, k, n, s)
+                                               : launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
+            return wide ? launch_q4k_wide<true>(x, up, wbase, c, k, n, s)
+                        : launch_q4k_mfma<true>(x, up, wbase, c, k, n, s);
         }
     }
     if (dtype == LG_Q8_0 && vec_ok && !fuse && aligned16(wb)) return launch_q80(x, wb, c, k, n, s);

@@ -61,11 +61,12 @@ def assert_same_non_finite(y, y64):
     assert np.array_equal(np.sign(y[inf]), np.sign(y64[inf]))
 
 
-@pytest.mark.parametrize("k,n", [(4096, 300), (1024, 37)])
+@pytest.mark.parametrize("k,n", [(4096, 300), (1024, 37), (12288, 40)])
 def test_q4k_activations_outside_the_digit_range(ctx, k, n):
-    # Q4_K with k <= 4096 converts x to byte digits per 64-element group; values it
-    # cannot scale (non-finite, >= 2^21, nonzero below 2^-60) send the call to the
-    # reference's per-element loop, whose results the f64 accumulation matches.
+    # Q4_K up to k = 16384 converts x to byte digits (per 64-element group up to 4096,
+    # per super-block beyond); values it cannot scale (non-finite, >= 2^21, nonzero
+    # below 2^-60) send the call to the reference's per-element loop, whose results
+    # the f64 accumulation matches.
     raw = synth.q4k_weight(300 + k, k, n)
     x = synth.normal(301 + k, k)
     for idx, val in [(5, np.inf), (k - 3, -np.inf), (k // 3, np.nan)]:
