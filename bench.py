@@ -317,7 +317,7 @@ class Read(Workload):
 HEAD_KERNEL = "k_q4k_m1_dig"
 WORKLOADS = {
     "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003, kernel=HEAD_KERNEL),
-    "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001, kernel="k_q80_m1"),
+    "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001, kernel="k_q80_m1_dig"),
     "q4k_down_silu": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, fused=True, kernel="k_q4k_m1_wide"),
     "q4k_m1_k14336": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, kernel="k_q4k_m1_wide"),
     "q4k_m1_k20480": lambda: MatvecM1(lh.Q4_K, 20480, 4096, 0x5EED000C, kernel="k_q4k_m1"),

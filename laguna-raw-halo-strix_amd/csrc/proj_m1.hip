@@ -27,7 +27,8 @@
 //    only its k slice); the slices of a row range are summed in slice order by
 //    the last workgroup to finish.
 //
-// Q8_0: vector ALU.  A "team" of TW = min(4, ceil(k/4096)) waves covers one row (in
+// Q8_0 with k <= 4096: integer dot products against activation digits (k_q80_m1_dig,
+// described there).  Q8_0 with k > 4096: vector ALU.  A "team" of TW = min(4, ceil(k/4096)) waves covers one row (in
 // passes of 16384 elements beyond that): lane p of
 // the team owns the 64-element group p of the row (two 34-byte blocks, 68 bytes,
 // dword aligned) and keeps the 64 activations of that group in registers; the
@@ -828,6 +829,79 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void k_q4k_m1_mfma(const float *__re
 }
 
 // ------------------------------------------------------------------------------------------
+// The activation digits shared by the k <= 4096 integer-dot kernels.  A workgroup of
+// 256 threads converts x once: thread t takes elements 16t .. 16t+15 (group t/4,
+// quarter t%4; threads past k/16 read element 0 and fill table entries that only idle
+// lanes read) into the LDS table dg_tab (per group: digit planes 0, 1, 2 x 16 dwords)
+// and dg_xf (per group: the sums of elements 0-31 and 32-63, and 2^-sh).
+struct DigLds {
+    uint32_t tab[64 * 48];
+    float xf[64 * 4];
+    uint32_t bad;
+};
+
+__device__ __forceinline__ void dig_load_x(const float *__restrict__ x, uint32_t k, float4 (&xv)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t e4 = 4 * threadIdx.x + j;
+        xv[j] = reinterpret_cast<const float4 *>(x)[e4 < k / 4 ? e4 : 0];
+    }
+}
+
+// After a barrier that follows dg.bad = 0; flags dg.bad when some live group cannot be
+// scaled (non-finite, >= 2^21, nonzero below 2^-60).  A barrier must follow before
+// dig_read.
+__device__ __forceinline__ void dig_convert(const float4 (&xv)[4], uint32_t k, DigLds &dg) {
+    const uint32_t tid = threadIdx.x;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[4 * j] = xv[j].x, v[4 * j + 1] = xv[j].y, v[4 * j + 2] = xv[j].z, v[4 * j + 3] = xv[j].w;
+    uint32_t mb = 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) mb = max(mb, __float_as_uint(v[j]) & 0x7FFFFFFFu);
+    // the group's maximum over its four threads (a quad)
+    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+    const bool outside = mb >= 0x4A000000u || (mb != 0u && mb < 0x21800000u);  // >= 2^21 or NaN/inf; < 2^-60
+    const int E = (int)(mb >> 23) - 127;
+    const int sh = (mb == 0u || outside) ? 0 : 20 - E;
+    const float scale = __uint_as_float((uint32_t)(127 + sh) << 23);
+    uint32_t U[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) U[j] = __float_as_uint(__builtin_fmaf(v[j], scale, 12582912.0f)) - 0x4ABF7F80u;
+    uint32_t *dgp = dg.tab + (tid >> 2) * 48 + 4 * (tid & 3u);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {  // elements 4q .. 4q+3 of this thread's 16: one dword per digit plane
+        const uint32_t lo01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x05010400u);
+        const uint32_t lo23 = __builtin_amdgcn_perm(U[4 * q + 3], U[4 * q + 2], 0x05010400u);
+        const uint32_t hi01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x0C0C0602u);
+        const uint32_t hi23 = __builtin_amdgcn_perm(U[4 * q + 3], U[4 * q + 2], 0x0C0C0602u);
+        dgp[q] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+        dgp[16 + q] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+        dgp[32 + q] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) sum += v[j];
+    sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+    if ((tid & 3u) == 0) dg.xf[(tid >> 2) * 4 + 0] = sum;  // elements 0-31 of the group
+    if ((tid & 3u) == 2) dg.xf[(tid >> 2) * 4 + 1] = sum;  // elements 32-63
+    if ((tid & 3u) == 0) dg.xf[(tid >> 2) * 4 + 2] = __uint_as_float((uint32_t)(127 - sh) << 23);
+    if (tid < k / 16 && outside) dg.bad = 1u;
+}
+
+// Group p's 48 digit dwords and its X0, X1, 2^-sh into registers.
+__device__ __forceinline__ void dig_read(const DigLds &dg, uint32_t p, uint32_t (&D)[48], float &X0, float &X1,
+                                         float &F) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(dg.tab + p * 48);
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+        const uint4 u = src[i];
+        D[4 * i] = u.x, D[4 * i + 1] = u.y, D[4 * i + 2] = u.z, D[4 * i + 3] = u.w;
+    }
+    X0 = dg.xf[p * 4], X1 = dg.xf[p * 4 + 1], F = dg.xf[p * 4 + 2];
+}
+
 // Q4_K with k <= 4096, not fused: integer dot products (v_dot4_i32_i8) of the raw
 // nibbles against three signed byte digits of the activations.
 //
@@ -853,9 +927,7 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
                                                             float *__restrict__ y, uint32_t k, uint32_t n,
                                                             uint64_t row_bytes) {
     static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
-    __shared__ __attribute__((aligned(16))) uint32_t s_dig[64 * 48];  // group p: digit planes 0, 1, 2 x 16 dwords
-    __shared__ float s_xf[64 * 4];                                       // group p: X0, X1, 2^-sh
-    __shared__ uint32_t s_bad;
+    __shared__ __attribute__((aligned(16))) DigLds dg;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, team = tid >> 6;
     const uint32_t P = k >> 6;
     const bool active = lane < P;
@@ -864,14 +936,8 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     const uint32_t lane_off = (p >> 2) * Q4K_BYTES;
     const uint32_t stride = gridDim.x * TEAMS * R;
 
-    // thread t converts elements 16t .. 16t+15 (group t/4, quarter t%4); threads past
-    // k/16 read element 0 and fill table entries that only idle lanes read
     float4 xv[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t e4 = 4 * tid + j;
-        xv[j] = reinterpret_cast<const float4 *>(x)[e4 < k / 4 ? e4 : 0];
-    }
+    dig_load_x(x, k, xv);
     // the first rows' weights are in flight while x is converted
     uint32_t r0 = (blockIdx.x * TEAMS + team) * R;
     uint4 hd[2][R], qa[2][R], qb[2][R];
@@ -886,58 +952,14 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
         }
     };
     load(0, r0);
-    if (tid == 0) s_bad = 0u;
+    if (tid == 0) dg.bad = 0u;
     __syncthreads();
-    {
-        float v[16];
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            v[4 * j] = xv[j].x, v[4 * j + 1] = xv[j].y, v[4 * j + 2] = xv[j].z, v[4 * j + 3] = xv[j].w;
-        uint32_t mb = 0;
-#pragma unroll
-        for (int j = 0; j < 16; j++) mb = max(mb, __float_as_uint(v[j]) & 0x7FFFFFFFu);
-        // the group's maximum over its four threads (a quad)
-        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
-        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
-        const bool outside = mb >= 0x4A000000u || (mb != 0u && mb < 0x21800000u);  // >= 2^21 or NaN/inf; < 2^-60
-        const int E = (int)(mb >> 23) - 127;
-        const int sh = (mb == 0u || outside) ? 0 : 20 - E;
-        const float scale = __uint_as_float((uint32_t)(127 + sh) << 23);
-        uint32_t U[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) U[j] = __float_as_uint(__builtin_fmaf(v[j], scale, 12582912.0f)) - 0x4ABF7F80u;
-        uint32_t *dg = s_dig + (tid >> 2) * 48 + 4 * (tid & 3u);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {  // elements 4q .. 4q+3 of this thread's 16: one dword per digit plane
-            const uint32_t lo01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x05010400u);
-            const uint32_t lo23 = __builtin_amdgcn_perm(U[4 * q + 3], U[4 * q + 2], 0x05010400u);
-            const uint32_t hi01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x0C0C0602u);
-            const uint32_t hi23 = __builtin_amdgcn_perm(U[4 * q + 3], U[4 * q + 2], 0x0C0C0602u);
-            dg[q] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
-            dg[16 + q] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
-            dg[32 + q] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
-        }
-        float sum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; j++) sum += v[j];
-        sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
-        if ((tid & 3u) == 0) s_xf[(tid >> 2) * 4 + 0] = sum;  // elements 0-31 of the group (sub-block 2g)
-        if ((tid & 3u) == 2) s_xf[(tid >> 2) * 4 + 1] = sum;  // elements 32-63 (sub-block 2g+1)
-        if ((tid & 3u) == 0) s_xf[(tid >> 2) * 4 + 2] = __uint_as_float((uint32_t)(127 - sh) << 23);
-        if (tid < k / 16 && outside) s_bad = 1u;
-    }
+    dig_convert(xv, k, dg);
     __syncthreads();
     uint32_t D[48];
-    {
-        const uint4 *src = reinterpret_cast<const uint4 *>(s_dig + p * 48);
-#pragma unroll
-        for (int i = 0; i < 12; i++) {
-            const uint4 u = src[i];
-            D[4 * i] = u.x, D[4 * i + 1] = u.y, D[4 * i + 2] = u.z, D[4 * i + 3] = u.w;
-        }
-    }
-    const float X0 = s_xf[p * 4], X1 = s_xf[p * 4 + 1], F = s_xf[p * 4 + 2];
-    if (s_bad) {  // the reference's per-element loop (kernels/proj_q4k.comp:60-75)
+    float X0, X1, F;
+    dig_read(dg, p, D, X0, X1, F);
+    if (dg.bad) {  // the reference's per-element loop (kernels/proj_q4k.comp:60-75)
         for (uint32_t rr = blockIdx.x * TEAMS + team; rr < n; rr += gridDim.x * TEAMS) {
             float a = 0.0f;
             for (uint32_t j = lane; j < k; j += 64) a = __builtin_fmaf(x[j], q4k_elem(w, (uint64_t)rr * k + j), a);
@@ -979,6 +1001,117 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
             float v = dotrow(hd[b][r], qa[b][r], qb[b][r]);
             v = wave_sum(active ? v : 0.0f);
             if (lane == 0 && rr + r < n) y[rr + r] = v;
+        }
+    };
+    for (;;) {  // every wave leaves once its next rows start at or past n
+        const uint32_t r1 = r0 + stride;
+        if (r1 >= n) {
+            reduce(0, r0);
+            break;
+        }
+        load(1, r1);
+        reduce(0, r0);
+        const uint32_t r2 = r1 + stride;
+        if (r2 >= n) {
+            reduce(1, r1);
+            break;
+        }
+        load(0, r2);
+        reduce(1, r1);
+        r0 = r2;
+    }
+}
+
+// Q8_0 with k <= 4096: the same digits against the raw int8 quants.  Lane p owns
+// group p of a row (blocks 2p, 2p+1: 68 bytes at offset 68p); each wave stages a row
+// through its own LDS region with coalesced 16-byte loads (as k_q80_m1) and every lane
+// reads back its 17 dwords.  Per block, three v_dot4_i32_i8 sums C0, C1, C2 of the quants
+// against the digit planes give sum_j X_j q_j = C0 + 2^8 C1 + 2^16 C2 (each C exact in
+// int32; combined in f32, as |sum| may pass 2^31), and the row's term is
+// d 2^-sh (C0 + 2^8 C1 + 2^16 C2).  Rows stride over the grid R at a time, the next
+// rows' loads in flight while the current rows are reduced.
+template <int TEAMS, int R>
+__global__ __launch_bounds__(TEAMS * 64) void k_q80_m1_dig(const float *__restrict__ x, const uint8_t *__restrict__ w,
+                                                            float *__restrict__ y, uint32_t k, uint32_t n,
+                                                            uint64_t row_bytes) {
+    static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
+    constexpr int NL = (int)Q8_LOADS;
+    __shared__ __attribute__((aligned(16))) DigLds dg;
+    __shared__ __attribute__((aligned(16))) lg_u32x4 stage_all[TEAMS][64 * NL];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, team = tid >> 6;
+    const uint32_t P = k >> 6;
+    const bool active = lane < P;
+    const uint32_t p = active ? lane : 0u;  // idle lanes read group 0 and contribute 0
+    const uint32_t seg16 = P * 68 / 16;     // a row's 16-byte chunks (P is a multiple of 4)
+    const uint32_t stride = gridDim.x * TEAMS * R;
+    lg_u32x4 *stage = stage_all[team];
+
+    float4 xv[4];
+    dig_load_x(x, k, xv);
+    uint32_t r0 = (blockIdx.x * TEAMS + team) * R;
+    lg_u32x4 c[2][R][NL];
+    auto load = [&](int b, uint32_t rr) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t row = min(rr + r, n - 1u);  // rows past n re-read row n-1 and are not stored
+            const lg_u32x4 *src = reinterpret_cast<const lg_u32x4 *>(w + (uint64_t)row * row_bytes);
+#pragma unroll
+            for (int i = 0; i < NL; i++) {
+                const uint32_t ch = lane + 64 * i;
+                c[b][r][i] = src[ch < seg16 ? ch : 0];  // chunks past the row re-read chunk 0
+            }
+        }
+    };
+    load(0, r0);
+    if (tid == 0) dg.bad = 0u;
+    __syncthreads();
+    dig_convert(xv, k, dg);
+    __syncthreads();
+    uint32_t D[48];
+    float X0, X1, F;
+    dig_read(dg, p, D, X0, X1, F);
+    if (dg.bad) {  // the reference's per-element loop (kernels/proj_q8_0.comp:47-66)
+        for (uint32_t rr = blockIdx.x * TEAMS + team; rr < n; rr += gridDim.x * TEAMS) {
+            float a = 0.0f;
+            for (uint32_t j = lane; j < k; j += 64) a = __builtin_fmaf(x[j], q80_elem(w, (uint64_t)rr * k + j), a);
+            a = wave_sum(a);
+            if (lane == 0) y[rr] = a;
+        }
+        return;
+    }
+    // Idle lanes read stage words nobody wrote: their partials are replaced by 0.
+    auto dotrow = [&](const uint32_t *v) -> float {
+        int c0 = 0, c1 = 0, c2 = 0, e0 = 0, e1 = 0, e2 = 0;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            // block 0's quants start 2 bytes into the lane's 68: realign; block 1's at byte 36
+            const int a = (int)__builtin_amdgcn_alignbit(v[t + 1], v[t], 16), b = (int)v[9 + t];
+            c0 = __builtin_amdgcn_sdot4(a, (int)D[t], c0, false);
+            c1 = __builtin_amdgcn_sdot4(a, (int)D[16 + t], c1, false);
+            c2 = __builtin_amdgcn_sdot4(a, (int)D[32 + t], c2, false);
+            e0 = __builtin_amdgcn_sdot4(b, (int)D[8 + t], e0, false);
+            e1 = __builtin_amdgcn_sdot4(b, (int)D[24 + t], e1, false);
+            e2 = __builtin_amdgcn_sdot4(b, (int)D[40 + t], e2, false);
+        }
+        const float S0 = __builtin_fmaf(65536.0f, (float)c2, __builtin_fmaf(256.0f, (float)c1, (float)c0));
+        const float S1 = __builtin_fmaf(65536.0f, (float)e2, __builtin_fmaf(256.0f, (float)e1, (float)e0));
+        const float d0 = mq_half(v[0] & 0xFFFFu), d1 = mq_half(v[8] >> 16);
+        return F * __builtin_fmaf(d1, S1, d0 * S0);
+    };
+    auto reduce = [&](int b, uint32_t rr) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+#pragma unroll
+            for (int i = 0; i < NL; i++) stage[lane + 64 * i] = c[b][r][i];
+            wave_lds_fence();
+            uint32_t v[17];
+            const uint32_t *sp = reinterpret_cast<const uint32_t *>(stage) + 17 * p;
+#pragma unroll
+            for (int i = 0; i < 17; i++) v[i] = sp[i];
+            wave_lds_fence();
+            float a = dotrow(v);
+            a = wave_sum(active ? a : 0.0f);
+            if (lane == 0 && rr + r < n) y[rr + r] = a;
         }
     };
     for (;;) {  // every wave leaves once its next rows start at or past n
@@ -1463,7 +1596,16 @@ int launch_q80_t(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_
 
 int launch_q80(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
     const uint32_t P = k / 64;
-    if (P <= 64) return launch_q80_t<1, 8>(x, w, y, k, n, s);
+    if (P <= 64) {
+        constexpr int TEAMS = 4, R = 2;
+        uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
+        const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed);
+        const uint32_t cap = gc ? gc : 256;  // one per CU: measured best for 4096 rows (5.62 us, 512: 5.73)
+        grid = grid < cap ? grid : cap;
+        hipLaunchKernelGGL((k_q80_m1_dig<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
+                           (uint64_t)k / QK8_0 * Q80_BYTES);
+        return after_launch("proj_q8_0_m1", s);
+    }
     if (P <= 128) return launch_q80_t<2, 4>(x, w, y, k, n, s);
     if (P <= 192) return launch_q80_t<3, 2>(x, w, y, k, n, s);
     return launch_q80_t<4, 2>(x, w, y, k, n, s);

@@ -61,20 +61,21 @@ def assert_same_non_finite(y, y64):
     assert np.array_equal(np.sign(y[inf]), np.sign(y64[inf]))
 
 
-@pytest.mark.parametrize("k,n", [(4096, 300), (1024, 37), (12288, 40)])
-def test_q4k_activations_outside_the_digit_range(ctx, k, n):
-    # Q4_K up to k = 16384 converts x to byte digits (per 64-element group up to 4096,
-    # per super-block beyond); values it cannot scale (non-finite, >= 2^21, nonzero
-    # below 2^-60) send the call to the reference's per-element loop, whose results
-    # the f64 accumulation matches.
-    raw = synth.q4k_weight(300 + k, k, n)
+@pytest.mark.parametrize("dtype,k,n", [(lh.Q4_K, 4096, 300), (lh.Q4_K, 1024, 37), (lh.Q4_K, 12288, 40),
+                                       (lh.Q8_0, 4096, 300), (lh.Q8_0, 1024, 37)])
+def test_activations_outside_the_digit_range(ctx, dtype, k, n):
+    # Q4_K up to k = 16384 and Q8_0 up to 4096 convert x to byte digits (per
+    # 64-element group up to 4096, per super-block beyond); values they cannot scale
+    # (non-finite, >= 2^21, nonzero below 2^-60) send the call to the reference's
+    # per-element loop, whose results the f64 accumulation matches.
+    raw = weight(dtype, 300 + k, k, n)
     x = synth.normal(301 + k, k)
     for idx, val in [(5, np.inf), (k - 3, -np.inf), (k // 3, np.nan)]:
-        print(f"proj q4k k={k} x[{idx}]={val}", flush=True)
+        print(f"proj dtype={dtype} k={k} x[{idx}]={val}", flush=True)
         xs = x.copy()
         xs[idx] = val
-        y64, _ = orc.proj_quant_f64(xs, raw, orc.Q4_K, k, n)
-        assert_same_non_finite(run_proj(ctx, lh.Q4_K, raw, xs, k, n), y64)
+        y64, _ = orc.proj_quant_f64(xs, raw, dtype, k, n)
+        assert_same_non_finite(run_proj(ctx, dtype, raw, xs, k, n), y64)
     cases = {
         "huge": lambda v: np.where(np.arange(k) == 77, np.float32(3e6), v),       # one value >= 2^21
         "tiny": lambda v: (v * 1e-20).astype(np.float32),                           # all below 2^-60
@@ -83,10 +84,10 @@ def test_q4k_activations_outside_the_digit_range(ctx, k, n):
         "mixed_scales": lambda v: (v * np.exp2(np.arange(k) // 64 % 40 - 30.0)).astype(np.float32),
     }
     for name, f in cases.items():
-        print(f"proj q4k k={k} {name} activations", flush=True)
+        print(f"proj dtype={dtype} k={k} {name} activations", flush=True)
         xs = f(x).astype(np.float32)
-        y64, a = orc.proj_quant_f64(xs, raw, orc.Q4_K, k, n)
-        parity(run_proj(ctx, lh.Q4_K, raw, xs, k, n), y64, a, TOL)
+        y64, a = orc.proj_quant_f64(xs, raw, dtype, k, n)
+        parity(run_proj(ctx, dtype, raw, xs, k, n), y64, a, TOL)
 
 
 def test_q4k_exponent0_scales(ctx):
