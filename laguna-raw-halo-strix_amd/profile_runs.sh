@@ -31,8 +31,9 @@ run() {  # run NAME ARGS...: one rocprofv3 invocation, stop on failure
 }
 
 if [ "$WHAT" = all ] || [ "$WHAT" = traces ]; then
-    for W in ${TRACES:-q4k_m1 q8_0_m1 q4k_down_silu q4k_m16_f32 q4k_m16_f32_tiled q8_0_m16_f32_tiled \
-             lm_head_verify_m16 dflash_block_eager ceil_read_33.1MB ceil_empty}; do
+    for W in ${TRACES:-q4k_m1 q8_0_m1 q4k_down_silu q4k_m1_k14336 q4k_m1_k20480 q4k_lm_head_m1 q4k_m16_f32 \
+             q4k_m16_f32_tiled q8_0_m16_f32_tiled lm_head_verify_m16 dflash_block_eager ceil_read_33.1MB \
+             ceil_read_17.8MB ceil_empty}; do
         ARGS=(--kernel-trace --stats --output-format csv -d "$OUT/tr_$W" -o run -- $BENCH --workload $W --no-extra --no-cpu)
         run "tr_$W" "${ARGS[@]}"
         $PS trace --dir "$OUT/tr_$W" --out "$SUM/kernel_trace_$W.txt" \
@@ -41,7 +42,7 @@ if [ "$WHAT" = all ] || [ "$WHAT" = traces ]; then
 fi
 
 # workload, kernel name, weights per launch
-COUNTED="q4k_m1:k_q4k_m1_rows:58720256 q4k_m16_f32_tiled:k_q4k_mm:58720256 q4k_down_silu:k_q4k_m1:58720256"
+COUNTED="q4k_m1:k_q4k_m1_dig:58720256 q8_0_m1:k_q80_m1_dig:16777216 q4k_m16_f32_tiled:k_q4k_mm:58720256 q4k_down_silu:k_q4k_m1_wide:58720256"
 if [ "$WHAT" = all ] || [ "$WHAT" = counters ]; then
     for E in $COUNTED; do
         IFS=: read -r W K NW <<< "$E"
@@ -55,7 +56,7 @@ if [ "$WHAT" = all ] || [ "$WHAT" = counters ]; then
     done
 fi
 
-TRAFFIC="q4k_m1:k_q4k_m1_rows q8_0_m1:k_q80_m1 q4k_down_silu:k_q4k_m1 q4k_m16_f32_tiled:k_q4k_mm"
+TRAFFIC="q4k_m1:k_q4k_m1_dig q8_0_m1:k_q80_m1_dig q4k_down_silu:k_q4k_m1_wide q4k_m16_f32_tiled:k_q4k_mm"
 if [ "$WHAT" = all ] || [ "$WHAT" = traffic ]; then
     for E in $TRAFFIC; do
         IFS=: read -r W K <<< "$E"
