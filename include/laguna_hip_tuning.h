@@ -23,6 +23,10 @@ int lg_set_m1_grid_cap(uint32_t cap);
 /* Number of k slices of the Q4_K M = 1 matrix-core kernel (the fused SiLU down
  * projection). */
 int lg_set_m1_split(uint32_t slices);
+/* Kernel family of the Q4_K M = 1 projections: 1 = vector ALU / integer dot
+ * products, 2 = int8 matrix cores (k <= 16384; other k keep family 1).  Any other
+ * value is LG_EINVAL. */
+int lg_set_m1_kernel(uint32_t kind);
 /* Small-M products (lg_dispatch_proj_quant_batch, the draft forward): ch chunks of
  * 256 elements per k slice (1, 2; 4 for Q4_K with m <= 16) and rt 16-row tiles per
  * wavefront (1, 2, 4; clamped to the kernel's register budget).  A captured

@@ -224,15 +224,27 @@ __device__ __forceinline__ uint4 ld_stream16(const void *p) {
 template <int I>
 __device__ __forceinline__ float ubyte_f(uint32_t u) { return (float)((u >> (8 * I)) & 0xFFu); }
 
+// v plus the v of lane i ^ 16 (lane_add_x16) or i ^ 32 (lane_add_x32), through the
+// gfx950 row swaps v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).
+// With both operands v, the swap leaves one operand holding the even (lower) rows and
+// the other the odd (upper) ones, so their sum is v_i + v_(i^16) in every lane: the
+// same float as __shfl_xor(v, 16) + v (addition is commutative).
+__device__ __forceinline__ float lane_add_x16(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float lane_add_x32(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 // Lanes 0-15 of each row combine with DPP (xor 1, xor 2 via quad_perm, then
-// row_ror 4 and 8), the four rows with two cross-row swizzles.
+// row_ror 4 and 8), the four rows with the two row swaps.
 __device__ __forceinline__ float wave_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)); // row_ror 4
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)); // row_ror 8
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    return lane_add_x32(lane_add_x16(v));
 }

@@ -1192,12 +1192,16 @@ __device__ __forceinline__ float dpp_f(float v) {
 template <int RG, int SPC, bool FUSE>
 __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ x, const float *__restrict__ up,
                                                       const uint8_t *__restrict__ w, float *__restrict__ y,
-                                                      uint32_t n, uint32_t nsb, uint64_t row_bytes) {
+                                                      uint32_t n, uint32_t nsb, uint64_t row_bytes, uint32_t rpw) {
     constexpr uint32_t WLDS = wide_wave_lds(SPC);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, KQ = blockDim.x >> 6;
     const uint32_t nn = l & 15u, g = l >> 4;
-    const uint32_t row0 = blockIdx.x * (16u * RG);
+    // rows [row0, rend) of this workgroup (rpw <= 16 RG; the grid keeps row0 < n), as
+    // nrg groups of 16; a partial last group repeats row rend-1 in its idle columns
+    const uint32_t row0 = blockIdx.x * rpw;
+    const uint32_t rend = row0 + rpw < n ? row0 + rpw : n;
+    const uint32_t nrg = (rend - row0 + 15u) >> 4;
     const uint32_t sb0 = wave * SPC;
     const uint32_t cnt = sb0 < nsb ? (nsb - sb0 < (uint32_t)SPC ? nsb - sb0 : (uint32_t)SPC) : 0u;
     uint8_t *T = lds + wave * WLDS;        // digit tables
@@ -1223,7 +1227,8 @@ __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ 
     uint4 hd[RG][SPC], q0[RG][SPC], q1[RG][SPC];  // header and the lane's 32 quant bytes of group g
 #pragma unroll
     for (int r = 0; r < RG; r++) {
-        const uint32_t row = row0 + 16u * r + nn < n ? row0 + 16u * r + nn : n - 1u;
+        if (RG > 1 && r >= (int)nrg) break;
+        const uint32_t row = row0 + 16u * r + nn < rend ? row0 + 16u * r + nn : rend - 1u;
         const uint8_t *base = w + (uint64_t)row * row_bytes;
 #pragma unroll
         for (int t = 0; t < SPC; t++) {
@@ -1234,8 +1239,9 @@ __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ 
         }
     }
 #pragma unroll
-    for (int i = 0; i < (int)(SPC * WIDE_TAB / 1024); i++)
-        *reinterpret_cast<uint4 *>(Z + l * 16u + i * 1024u) = make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < (int)((SPC * WIDE_TAB + 1023) / 1024); i++)
+        if (l * 16u + i * 1024u < SPC * WIDE_TAB)
+            *reinterpret_cast<uint4 *>(Z + l * 16u + i * 1024u) = make_uint4(0, 0, 0, 0);
 
     // digits: lane l converts elements 4l .. 4l+3 of each super-block
     uint32_t bad = 0;
@@ -1301,6 +1307,7 @@ __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ 
         const float F = Fs[t];
 #pragma unroll
         for (int r = 0; r < RG; r++) {
+            if (RG > 1 && r >= (int)nrg) break;
             const uint4 a = q0[r][t], b = q1[r][t];
             const lg_i32x4 bl0 = {(int)(a.x & 0x0F0F0F0Fu), (int)(a.y & 0x0F0F0F0Fu), (int)(a.z & 0x0F0F0F0Fu),
                                   (int)(a.w & 0x0F0F0F0Fu)};
@@ -1331,6 +1338,7 @@ __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ 
     }
 #pragma unroll
     for (int r = 0; r < RG; r++) {
+        if (RG > 1 && r >= (int)nrg) break;
         acc[r] = add_x32(add_x16(acc[r]));  // the 4 groups of row nn
         if (g == 0) s_part[wave * (RG * 16) + 16 * r + nn] = acc[r];
     }
@@ -1339,7 +1347,7 @@ __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ 
     uint32_t any_bad = 0;
     for (uint32_t i = 0; i < KQ; i++) any_bad |= s_bad[i];
     if (!any_bad) {
-        if (threadIdx.x < RG * 16u && row0 + threadIdx.x < n) {
+        if (row0 + threadIdx.x < rend) {
             float sum = 0.0f;
             for (uint32_t i = 0; i < KQ; i++) sum += s_part[i * (RG * 16) + threadIdx.x];
             y[row0 + threadIdx.x] = sum;
@@ -1349,7 +1357,7 @@ __global__ __launch_bounds__(1024) void k_q4k_m1_wide(const float *__restrict__ 
     // the reference's per-element loop (kernels/proj_q4k.comp:60-75, activation.comp:21-28)
     for (uint32_t rr = wave; rr < RG * 16u; rr += KQ) {
         const uint32_t row = row0 + rr;
-        if (row >= n) break;
+        if (row >= rend) break;
         float a = 0.0f;
         for (uint32_t j = l; j < nsb * QK_K; j += 64u) {
             float xj = x[j];
@@ -1499,10 +1507,19 @@ int launch_q4k_mfma(const float *x, const float *up, const uint8_t *w, float *y,
     return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
 }
 
-// k_q4k_m1_wide: one workgroup per 16 rows, ceil(k / 1024) waves of 4 super-blocks
-// each (k <= 16384), its LDS allowed past the 64 KiB default once per device.
+// k_q4k_m1_wide launch shapes (k <= 16384):
+//  * k <= 4096: one super-block per wave (k / 256 waves) and up to four groups of 16
+//    rows per workgroup: ceil(n / G) rows per workgroup (G = the CU count, or the grid
+//    cap) clamped to 16 .. 64, each wave holding its rows' loads in flight at once.
+//    Selected by lg_set_m1_kernel(2) only: on 4096 -> 14336 its 16-row loads stream
+//    slower than the integer-dot kernel's whole-row loads.
+//  * above: four super-blocks per wave (ceil(k / 1024) waves), 16 rows per workgroup,
+//    its LDS allowed past the 64 KiB default once per device.
 constexpr int WIDE_SPC = 4;
 constexpr uint32_t WIDE_MAX_SB = 16 * WIDE_SPC;
+constexpr int WIDE_RG1 = 4;  // row groups per workgroup at one super-block per wave
+
+std::atomic<uint32_t> g_m1_kernel{0};  // 0 = automatic, 1 = vector ALU / integer dot, 2 = matrix cores
 
 std::mutex g_wide_mu;
 bool g_wide_attr[64][2] = {};
@@ -1510,6 +1527,19 @@ bool g_wide_attr[64][2] = {};
 template <bool FUSE>
 int launch_q4k_wide(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n,
                     hipStream_t s) {
+    const uint32_t nsb = k / QK_K;
+    const uint64_t rb = (uint64_t)nsb * Q4K_BYTES;
+    if (nsb <= 16) {
+        uint32_t G = (uint32_t)device_cus();
+        const uint32_t cap = g_grid_cap.load(std::memory_order_relaxed);
+        if (cap && cap < G) G = cap;
+        uint64_t rpw = ((uint64_t)n + G - 1) / G;
+        rpw = rpw < 16 ? 16 : rpw > 16u * WIDE_RG1 ? 16u * WIDE_RG1 : rpw;
+        const uint32_t grid = (uint32_t)(((uint64_t)n + rpw - 1) / rpw);
+        hipLaunchKernelGGL((k_q4k_m1_wide<WIDE_RG1, 1, FUSE>), dim3(grid), dim3(nsb * 64),
+                           wide_lds_bytes(nsb, WIDE_RG1, 1), s, x, up, w, y, n, nsb, rb, (uint32_t)rpw);
+        return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
+    }
     int dev = 0;
     LG_HIP_TRY(hipGetDevice(&dev));
     LG_REQUIRE(dev >= 0 && dev < 64, "proj_q4k_m1: device %d", dev);
@@ -1522,9 +1552,9 @@ int launch_q4k_wide(const float *x, const float *up, const uint8_t *w, float *y,
             g_wide_attr[dev][FUSE] = true;
         }
     }
-    const uint32_t nsb = k / QK_K, waves = (nsb + WIDE_SPC - 1) / WIDE_SPC;
+    const uint32_t waves = (nsb + WIDE_SPC - 1) / WIDE_SPC;
     hipLaunchKernelGGL((k_q4k_m1_wide<1, WIDE_SPC, FUSE>), dim3((n + 15) / 16), dim3(waves * 64),
-                       wide_lds_bytes(waves, 1, WIDE_SPC), s, x, up, w, y, n, nsb, (uint64_t)nsb * Q4K_BYTES);
+                       wide_lds_bytes(waves, 1, WIDE_SPC), s, x, up, w, y, n, nsb, rb, 16u);
     return after_launch(FUSE ? "proj_q4k_m1_silu" : "proj_q4k_m1", s);
 }
 
@@ -1644,8 +1674,13 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
             // kernel; fused 11.4-11.8 against 13.9 split over workgroups); beyond, the
             // vector kernel in passes (plain) or the split matrix-core kernel (fused).
             const bool wide = k / QK_K <= WIDE_MAX_SB;
-            if (!fuse) return k > 4096 && wide ? launch_q4k_wide<false>(x, nullptr, wbase, c, k, n, s)
-                                               : launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
+            const uint32_t kind = g_m1_kernel.load(std::memory_order_relaxed);
+            if (!fuse) {
+                const bool mc = kind == 2 ? wide : kind == 1 ? false : wide && k > 4096;
+                return mc ? launch_q4k_wide<false>(x, nullptr, wbase, c, k, n, s)
+                          : launch_q4k<false>(x, nullptr, wbase, c, k, n, s);
+            }
+            if (kind == 1) return launch_q4k<true>(x, up, wbase, c, k, n, s);
             return wide ? launch_q4k_wide<true>(x, up, wbase, c, k, n, s)
                         : launch_q4k_mfma<true>(x, up, wbase, c, k, n, s);
         }
@@ -1743,6 +1778,16 @@ int lg_set_m1_grid_cap(uint32_t cap) {
 // repeatable for a fixed one.
 int lg_set_m1_split(uint32_t slices) {
     g_m1_split.store(slices, std::memory_order_relaxed);
+    return LG_OK;
+}
+
+// Kernel family of the Q4_K M=1 projections (0 = automatic, 1 = vector ALU /
+// integer dot products, 2 = int8 matrix cores where k <= 16384).  A tuning hook
+// like the two above.
+int lg_set_m1_kernel(uint32_t kind) {
+    clear_error();
+    LG_REQUIRE(kind <= 2, "lg_set_m1_kernel: kind %u (0, 1 or 2)", kind);
+    g_m1_kernel.store(kind, std::memory_order_relaxed);
     return LG_OK;
 }
 

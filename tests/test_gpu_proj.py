@@ -284,3 +284,55 @@ def test_grid_cap_launch_shapes(ctx, cap):
     y64, a = orc.proj_quant_f64(x, raw, orc.Q4_K, k, n)
     parity(y0, y64, a, TOL)
     parity(y1, y64, a, TOL)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+@pytest.mark.parametrize("k,n", [(4096, 14336), (4096, 16500), (4096, 777), (4096, 57), (4096, 16), (4096, 1),
+                                 (1024, 37), (256, 3), (3072, 100), (14336, 100), (12288, 40)])
+def test_q4k_kernel_families(ctx, kind, k, n):
+    # Family 1 (vector ALU / integer dot products) and family 2 (int8 matrix cores
+    # over row ranges of up to 64 rows per workgroup, partial 16-row groups
+    # included) both meet parity at every shape; each is bit-for-bit repeatable.
+    seed = 5000 + k + n
+    print(f"proj q4k kernel family {kind} k={k} n={n}", flush=True)
+    raw = synth.q4k_weight(seed, k, n)
+    x = synth.normal(seed + 1, k)
+    lh.check(lh.lib().lg_set_m1_kernel(kind))
+    try:
+        y1 = run_proj(ctx, lh.Q4_K, raw, x, k, n)
+        y2 = run_proj(ctx, lh.Q4_K, raw, x, k, n)
+    finally:
+        lh.check(lh.lib().lg_set_m1_kernel(0))
+    assert np.array_equal(y1, y2)
+    y64, a = orc.proj_quant_f64(x, raw, lh.Q4_K, k, n)
+    parity(y1, y64, a, TOL)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_q4k_kernel_families_outside_digit_range(ctx, kind):
+    k, n = 4096, 300
+    raw = synth.q4k_weight(5100, k, n)
+    x = synth.normal(5101, k)
+    lh.check(lh.lib().lg_set_m1_kernel(kind))
+    try:
+        for idx, val in [(5, np.inf), (k - 3, -np.inf), (k // 3, np.nan)]:
+            print(f"proj q4k family {kind} x[{idx}]={val}", flush=True)
+            xs = x.copy()
+            xs[idx] = val
+            y64, _ = orc.proj_quant_f64(xs, raw, lh.Q4_K, k, n)
+            assert_same_non_finite(run_proj(ctx, lh.Q4_K, raw, xs, k, n), y64)
+        for name, xs in [("tiny", (x * 1e-20).astype(np.float32)),
+                         ("wide", np.where(np.arange(k) % 256 == 9, np.float32(30.0), x * np.float32(1e-3))),
+                         ("huge", np.where(np.arange(k) == 77, np.float32(3e6), x))]:
+            print(f"proj q4k family {kind} {name} activations", flush=True)
+            xs = xs.astype(np.float32)
+            y64, a = orc.proj_quant_f64(xs, raw, lh.Q4_K, k, n)
+            parity(run_proj(ctx, lh.Q4_K, raw, xs, k, n), y64, a, TOL)
+    finally:
+        lh.check(lh.lib().lg_set_m1_kernel(0))
+
+
+def test_m1_kernel_hook_rejects_unknown_family(ctx):
+    with pytest.raises(lh.LagunaError) as e:
+        lh.check(lh.lib().lg_set_m1_kernel(3))
+    assert e.value.status == lh.EINVAL
