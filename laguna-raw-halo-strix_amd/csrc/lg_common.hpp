@@ -31,6 +31,8 @@ bool blocking();
 
 // Check a launch and honour blocking mode (no wait while the stream is being captured).
 int after_launch(const char *what, hipStream_t s);
+// Compute units of the current device.
+int device_cus();
 
 // While one lives, after_launch on this thread does not wait in blocking mode: a
 // multi-launch entry point waits once, at its end.
@@ -128,11 +130,14 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
 // With `up` (f32 activations only), x is replaced by silu(x) * up (SiLU FFN input).
 // With `glu`, the two jobs are an FFN's gate and up products (equal n, f32 x, no
 // residuals): job 0's output receives silu(gate) * up and job 1's is scratch.
+// skip_rows: leading activation rows whose outputs the caller does not need; whole
+// 16-row token tiles below it are neither computed nor stored (c keeps what it held).
 struct BatchJob {
     const void *w;
     float *c;
     const float *res;
     uint32_t n;
+    uint32_t skip_rows = 0;
 };
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype);
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jobs, uint32_t njobs, uint32_t k,

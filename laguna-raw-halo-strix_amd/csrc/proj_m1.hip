@@ -1421,20 +1421,6 @@ __global__ __launch_bounds__(256) void k_activation(const float *__restrict__ g,
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-std::mutex g_cu_mu;
-
-int device_cus() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    std::lock_guard<std::mutex> lk(g_cu_mu);
-    if (!cus[dev]) {
-        int c = 0;
-        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-        cus[dev] = c;
-    }
-    return cus[dev];
-}
 
 // Rows per team: enough that the grid covers the CUs once (or the tuning cap on
 // workgroups), at most M1_RPW_MAX; larger n simply launches more workgroups.

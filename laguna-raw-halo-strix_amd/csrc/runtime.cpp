@@ -27,6 +27,21 @@ int fail(int status, const char *fmt, ...) {
 
 void clear_error() { g_err.clear(); }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cus() {
+    static std::mutex mu;
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!cus[dev]) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
 // Registry of live lg_buf_alloc allocations: base -> size.
 static std::mutex g_mu;
 static std::map<uintptr_t, uint64_t> g_allocs;

@@ -38,6 +38,8 @@ def test_static_scratch_equals_workspace_entry_point(ctx):
 
 
 def test_static_scratch_rejects_oversize(ctx):
-    k, n, m = 4096, 151936, 16  # the vocab-sized LM head at m = 16 needs about 78 MB of partial sums
-    st = lh.lib().lg_dispatch_proj_quant_batch_static(None, lh.F32, None, None, k, n, m, lh.Q4_K, None)
+    # a vocab-sized Q8_0 product at m = 16 is split over 16 k slices: about 155 MB of
+    # partial sums, past the 16 MiB scratch
+    k, n, m = 4096, 151936, 16
+    st = lh.lib().lg_dispatch_proj_quant_batch_static(None, lh.F32, None, None, k, n, m, lh.Q8_0, None)
     assert st == lh.EINVAL and b"scratch" in lh.lib().lg_last_error()
