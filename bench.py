@@ -33,9 +33,9 @@ Also reported under "extra":
 
 `cpu_baseline`: the oracle (the C restatement of the reference's CPU and shader
 arithmetic) on the host cores: Q8_0 dequant_to_f32 of the 4096x4096 tensor, the
-f32 matvec in proj.comp order on 4096x4096 f32 weights, and the fused Q4_K matvec
-in proj_q4k.comp order on the headline workload, each on one thread and on the
-process's CPU share.
+f32 matvec in proj.comp order on 4096x4096 f32 weights, the fused Q8_0 matvec in
+proj_q8_0.comp order on 4096x4096, and the fused Q4_K matvec in proj_q4k.comp
+order on the headline workload, each on one thread and on the process's CPU share.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-extra] [--no-cpu]
 """
@@ -451,7 +451,14 @@ def cpu_baseline(budget_s=2.0):
         legs[f"proj_f32_4096x4096_t{t}"] = {"GBps": round(bps / 1e9, 4), "threads": t, "calls": reps,
                                             "seconds": round(secs, 2)}
     del wf
-    # 3. the fused Q4_K matvec in kernels/proj_q4k.comp order on the headline workload
+    # 3a. the fused Q8_0 matvec in kernels/proj_q8_0.comp order (4096 x 4096)
+    x8 = synth.normal(0x5EED0002, 4096)
+    for t in (1, nthr):
+        bps, reps, secs = _rate(lambda: orc.proj_q8_0(x8, q8, 4096, 4096, threads=t), q8.nbytes + 4 * 4096 + 4 * 4096,
+                                budget_s)
+        legs[f"proj_q8_0_4096x4096_t{t}"] = {"GBps": round(bps / 1e9, 4), "threads": t, "calls": reps,
+                                             "seconds": round(secs, 2)}
+    # 3b. the fused Q4_K matvec in kernels/proj_q4k.comp order on the headline workload
     k, n = 4096, 14336
     q4 = synth.q4k_weight(0x5EED0003, k, n)
     x = synth.normal(0x5EED0004, k)
@@ -464,8 +471,9 @@ def cpu_baseline(budget_s=2.0):
     return {"value": head["GBps"], "unit": "GB/s", "cores": nthr, "kind": "port",
             "cpu_model": cpu_model(), "cpu_count": os.cpu_count(), "legs": legs,
             "sample": f"oracle (C, -O2, no FMA contraction) on the host: Q8_0 dequant_to_f32 of 4096x4096, f32 "
-                      f"proj.comp-order matvec 4096x4096, fused Q4_K proj_q4k.comp-order matvec 4096->14336 (the "
-                      f"value); whole calls repeated for about {budget_s:.0f} s each on 1 and {nthr} threads"}
+                      f"proj.comp-order matvec 4096x4096, fused Q8_0 proj_q8_0.comp-order matvec 4096x4096, fused "
+                      f"Q4_K proj_q4k.comp-order matvec 4096->14336 (the value); whole calls repeated for about "
+                      f"{budget_s:.0f} s each on 1 and {nthr} threads"}
 
 
 CAL_BYTES = 64 << 20  # lg_buf_copy size that hardware traffic counters are calibrated against
