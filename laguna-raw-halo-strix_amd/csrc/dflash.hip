@@ -96,6 +96,96 @@ __global__ __launch_bounds__(256) void k_rmsnorm4(const float *x, const float *_
                                                v[i].w * wv[i].w * rms);
 }
 
+// The block forward's norms folded into its projections (the products apply the
+// norm's weight and 1/rms around them; csrc/proj_batch.hip).  What stays outside:
+//
+// The encoder's output norm and, for a run of layers, each layer's attention norm of
+// its result (the injected rows are the same in every layer), in one launch:
+//   xe = x w / rms(x),   out_j = xe run.w[j] / rms(xe)
+// with the arithmetic of k_rmsnorm4, so the rows equal the two norms run apart.
+constexpr uint32_t NORM_RUN = 8;
+struct NormRun {
+    const float *w[NORM_RUN];
+    float *out[NORM_RUN];
+    uint32_t count;
+};
+
+// Rows of n floats, n a multiple of 4 up to 1024 V4: thread i holds float4s i,
+// i + 256, ... of the row (zeros past its end).
+template <int V4>
+__device__ __forceinline__ void load_row4(const float *__restrict__ r, uint32_t n, float4 (&v)[V4]) {
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const uint32_t e = i * 256 + threadIdx.x;
+        v[i] = e < n / 4 ? reinterpret_cast<const float4 *>(r)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+template <int V4>
+__device__ __forceinline__ float sum_sq4(const float4 (&v)[V4], float *red) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V4; i++)
+        s = __builtin_fmaf(v[i].x, v[i].x, __builtin_fmaf(v[i].y, v[i].y,
+            __builtin_fmaf(v[i].z, v[i].z, __builtin_fmaf(v[i].w, v[i].w, s))));
+    return block_sum<256>(s, red);
+}
+
+__device__ __forceinline__ float4 mul4(float4 a, float4 b, float c) {
+    return make_float4(a.x * b.x * c, a.y * b.y * c, a.z * b.z * c, a.w * b.w * c);
+}
+
+template <int V4>
+__global__ __launch_bounds__(256) void k_rmsnorm4_fan(const float *__restrict__ x, const float *__restrict__ w,
+                                                      float *__restrict__ xe, NormRun run, uint32_t n, float eps) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * n;
+    float4 v[V4], wv[V4];
+    load_row4<V4>(x + base, n, v);
+    load_row4<V4>(w, n, wv);
+    const float rms = 1.0f / sqrtf(sum_sq4<V4>(v, red) / (float)n + eps);
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const uint32_t e = i * 256 + threadIdx.x;
+        v[i] = mul4(v[i], wv[i], rms);
+        if (e < n / 4) reinterpret_cast<float4 *>(xe + base)[e] = v[i];
+    }
+    const float rms2 = 1.0f / sqrtf(sum_sq4<V4>(v, red) / (float)n + eps);
+    for (uint32_t j = 0; j < run.count; j++) {
+        load_row4<V4>(run.w[j], n, wv);
+#pragma unroll
+        for (int i = 0; i < V4; i++) {
+            const uint32_t e = i * 256 + threadIdx.x;
+            if (e < n / 4) reinterpret_cast<float4 *>(run.out[j] + base)[e] = mul4(v[i], wv[i], rms2);
+        }
+    }
+}
+
+// The block's token rows entering layer 0: x = tokens, y = tokens * w (layer 0's
+// attention-norm weight, its 1/rms left to the products), and per row the sum of
+// tokens^2 in slot 0 of `cols` slots (the others zero): the layout the products'
+// norm epilogue writes.
+template <int V4>
+__global__ __launch_bounds__(256) void k_rows_in(const float *__restrict__ tok, float *__restrict__ x,
+                                                 float *__restrict__ y, const float *__restrict__ w,
+                                                 float *__restrict__ ss, uint32_t cols, uint32_t n) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * n;
+    float4 v[V4], wv[V4];
+    load_row4<V4>(tok + base, n, v);
+    load_row4<V4>(w, n, wv);
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const uint32_t e = i * 256 + threadIdx.x;
+        if (e < n / 4) {
+            reinterpret_cast<float4 *>(x + base)[e] = v[i];
+            reinterpret_cast<float4 *>(y + base)[e] = mul4(v[i], wv[i], 1.0f);
+        }
+    }
+    const float s = sum_sq4<V4>(v, red);
+    for (uint32_t p = threadIdx.x; p < cols; p += 256) ss[(uint64_t)blockIdx.x * cols + p] = p == 0 ? s : 0.0f;
+}
+
 // ------------------------------------------------------------------------------------------
 // QK-norm + NeoX RoPE (kernels/qk_norm_rope.comp:23-67): one wavefront per (row, head).
 
@@ -111,11 +201,17 @@ struct QkJob {
 // The forward's attention gate of the tokens, when its weights are raw Q4_K blocks:
 // out[r][h] = sum_j x[r][j] W[h][j] (src/dflash.rs:942-944), one wavefront per
 // (row, head), lane p taking the 64-element groups p, p + 64, ... of the row.
+// With ss (the folded attention norm: x arrives with the norm's weight applied),
+// row r's result is multiplied by (sum_{p < cols} ss[r * cols + p] / k + eps)^-1/2,
+// cols <= 64.
 struct GateJob {
     const float *x;
     const uint8_t *w;
     float *out;
     uint32_t n_heads, k, units, blocks;
+    const float *ss;
+    uint32_t cols;
+    float eps;
 };
 
 __device__ __forceinline__ void gate_dot(const GateJob &g, uint32_t unit, uint32_t lane) {
@@ -154,6 +250,10 @@ __device__ __forceinline__ void gate_dot(const GateJob &g, uint32_t unit, uint32
         acc += (d * (float)sc0) * slo - (dmin * (float)m0) * xlo + (d * (float)sc1) * shi - (dmin * (float)m1) * xhi;
     }
     acc = wave_sum(acc);
+    if (g.ss) {
+        const float p = lane < g.cols ? g.ss[(uint64_t)row * g.cols + lane] : 0.0f;
+        acc *= 1.0f / sqrtf(wave_sum(p) / (float)g.k + g.eps);
+    }
     if (lane == 0) g.out[(uint64_t)row * g.n_heads + head] = acc;
 }
 
@@ -680,6 +780,29 @@ int run_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t
     return after_launch("rmsnorm", s);
 }
 
+// Rows of n floats, n a multiple of 4 up to 8192 (the folded norms' kernels).
+bool fan_width_ok(uint32_t n) { return n && n % 4 == 0 && n <= 8192; }
+
+int run_norm_fan(const float *x, const float *w, float *xe, const NormRun &run, uint32_t n, uint32_t rows, float eps,
+                 hipStream_t s) {
+    const dim3 grid(rows);
+    if (n <= 1024) hipLaunchKernelGGL(k_rmsnorm4_fan<1>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    else if (n <= 2048) hipLaunchKernelGGL(k_rmsnorm4_fan<2>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    else if (n <= 4096) hipLaunchKernelGGL(k_rmsnorm4_fan<4>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    else hipLaunchKernelGGL(k_rmsnorm4_fan<8>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    return after_launch("encoder and attention norms", s);
+}
+
+int run_rows_in(const float *tok, float *x, float *y, const float *w, float *ss, uint32_t cols, uint32_t n,
+                uint32_t rows, hipStream_t s) {
+    const dim3 grid(rows);
+    if (n <= 1024) hipLaunchKernelGGL(k_rows_in<1>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
+    else if (n <= 2048) hipLaunchKernelGGL(k_rows_in<2>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
+    else if (n <= 4096) hipLaunchKernelGGL(k_rows_in<4>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
+    else hipLaunchKernelGGL(k_rows_in<8>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
+    return after_launch("token rows in", s);
+}
+
 QkJob qk_job(const float *x, const float *w, float *out, uint32_t n_heads, uint32_t pos, uint32_t rows) {
     const uint32_t units = rows * n_heads;
     return {x, w, out, n_heads, pos, units, (units + 3) / 4};
@@ -741,8 +864,11 @@ constexpr uint64_t FREQ_BYTES = 1024;  // rope_dim <= head_dim <= 256: at most 1
 // attention partials and the small-M product workspace.  The eager entry points
 // share one per device (grown on demand); a graph owns its own, since a captured
 // graph keeps the addresses it was recorded with.
+// ny, ssa, ssb: the folded norms (forward_folded): per layer the [2m][E] attention
+// input (injected rows normalised, token rows with the norm's weight applied), and
+// the token rows' sums of squares ahead of the attention and FFN norms.
 struct FwdLayout {
-    float *xe, *nxe, *kk, *vv, *q, *att, *gate, *o, *h, *g, *u, *feat_n, *part, *freq;
+    float *xe, *nxe, *kk, *vv, *q, *att, *gate, *o, *h, *g, *u, *feat_n, *part, *ny, *ssa, *ssb, *freq;
     void *pws;
     uint64_t pws_bytes, total;
 };
@@ -751,10 +877,13 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
     const uint64_t E = hp.n_embd, QD = (uint64_t)hp.n_heads * hp.head_dim, KVD = (uint64_t)hp.n_kv_heads * hp.head_dim;
     const uint64_t FF = hp.n_ff, A = (uint64_t)hp.n_aux * hp.n_embd;
     const uint32_t S = ctx_len + 2 * m;
+    const uint64_t ss_floats = (uint64_t)m * ((E + 63) / 64);  // at most one partial per 64 rows
     const uint64_t floats[] = {2 * m * E, 2 * m * E, 2 * m * KVD, 2 * m * KVD,  2 * m * QD, m * QD,
                                2 * (uint64_t)m * hp.n_heads,      m * E,        m * E,  m * FF, m * FF, m * A,
-                               attn_partial_floats(S, hp.n_kv_heads)};
-    float **dst[] = {&L.xe, &L.nxe, &L.kk, &L.vv, &L.q, &L.att, &L.gate, &L.o, &L.h, &L.g, &L.u, &L.feat_n, &L.part};
+                               attn_partial_floats(S, hp.n_kv_heads), (uint64_t)hp.n_layers * 2 * m * E,
+                               ss_floats, ss_floats};
+    float **dst[] = {&L.xe, &L.nxe, &L.kk, &L.vv, &L.q, &L.att, &L.gate, &L.o, &L.h, &L.g, &L.u, &L.feat_n, &L.part,
+                     &L.ny, &L.ssa, &L.ssb};
     // The RoPE table and the small-M product workspace (whose arrival counters come
     // first) sit at fixed offsets whatever (m, ctx_len) are: an uploaded table stays
     // valid, and the counters stay zero, across calls that lay the rest out differently.
@@ -896,10 +1025,46 @@ int encode(const lg_dflash_model *md, const FwdLayout &W, const float *features,
     return run_rmsnorm(W.o, md->enc_output_norm, out, E, m, 1, E, hp.rms_eps, s);
 }
 
+int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *features, const float *tokens,
+                   uint32_t m, uint32_t ctx_len, float *out, hipStream_t s);
+
+// Whether every norm but the output norm can fold into the products around it: all
+// eight projections of every layer on the matrix-core path, rows of a width the fan
+// kernels take, and per-token partial-sum counts within what the consumers load.
+std::atomic<uint32_t> g_fold_norms{1};  // lg_set_draft_norms
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool norms_foldable(const lg_dflash_model *md, const float *tokens, uint32_t m) {
+    const lg_dflash_hparams &hp = md->hp;
+    const uint32_t E = hp.n_embd, QD = hp.n_heads * hp.head_dim, FF = hp.n_ff;
+    if (!g_fold_norms.load(std::memory_order_relaxed) || !fan_width_ok(E) || !aligned16(tokens) ||
+        !aligned16(md->enc_output_norm))
+        return false;
+    for (uint32_t li = 0; li < hp.n_layers; li++) {
+        const lg_dflash_layer &L = md->layers[li];
+        const bool ok = proj_batch_mfma_ok(L.attn_q_type, E, L.attn_q) && proj_batch_mfma_ok(L.attn_k_type, E, L.attn_k) &&
+                        proj_batch_mfma_ok(L.attn_v_type, E, L.attn_v) &&
+                        proj_batch_mfma_ok(L.attn_gate_type, E, L.attn_gate) &&
+                        proj_batch_mfma_ok(L.attn_output_type, QD, L.attn_output) &&
+                        proj_batch_mfma_ok(L.ffn_gate_type, E, L.ffn_gate) &&
+                        proj_batch_mfma_ok(L.ffn_up_type, E, L.ffn_up) &&
+                        proj_batch_mfma_ok(L.ffn_down_type, FF, L.ffn_down) && aligned16(L.attn_norm);
+        if (!ok) return false;
+        // the attention norm's sums come from the previous layer's down projection (the
+        // gate job's wave reads at most 64), the FFN norm's from o_proj
+        const uint32_t ca = li ? proj_batch_norm_cols(md->layers[li - 1].ffn_down_type, FF, E, m) : 1u;
+        const uint32_t cb = proj_batch_norm_cols(L.attn_output_type, QD, E, m);
+        if (ca > proj_batch_rs_cols_max(2 * m) || ca > 64 || cb > proj_batch_rs_cols_max(m)) return false;
+    }
+    return true;
+}
+
 // Block generalisation of DFlashModel::forward_injected_decode_hidden
 // (src/dflash.rs:877-976): m tokens over ctx_len cached positions.
 int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features, const float *tokens, uint32_t m,
             uint32_t ctx_len, float *out, hipStream_t s) {
+    if (norms_foldable(md, tokens, m)) return forward_folded(md, W, features, tokens, m, ctx_len, out, s);
     const lg_dflash_hparams &hp = md->hp;
     const uint32_t E = hp.n_embd, H = hp.n_heads, KV = hp.n_kv_heads, HD = hp.head_dim, FF = hp.n_ff;
     const uint32_t QD = H * HD, KVD = KV * HD;
@@ -965,6 +1130,106 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
             // x += ffn_down(silu(gate) * up), the activation computed while staging the product's input
             LG_TRY(proj_batch_multi(W.g, LG_F32, W.u, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
         }
+    }
+    if (md->output_norm) return run_rmsnorm(x, md->output_norm, out, E, m, 1, E, hp.rms_eps, s);
+    hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, x, out, mE);
+    return after_launch("copy hidden", s);
+}
+
+// The same forward with the attention and FFN norms folded into the products around
+// them (rmsnorm(x) W^T = (x w) W^T / rms(x)): the product that writes the residual
+// stream x also writes x w for the next norm and the sums of x^2 per workgroup column;
+// the next product takes x w and scales its results by 1/rms.  The encoder's output
+// norm and every layer's attention norm of the (fixed) injected rows run in one launch.
+int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *features, const float *tokens,
+                   uint32_t m, uint32_t ctx_len, float *out, hipStream_t s) {
+    const lg_dflash_hparams &hp = md->hp;
+    const uint32_t E = hp.n_embd, H = hp.n_heads, KV = hp.n_kv_heads, HD = hp.head_dim, FF = hp.n_ff;
+    const uint32_t QD = H * HD, KVD = KV * HD, A = hp.n_aux * hp.n_embd;
+    const uint64_t mE = (uint64_t)m * E, ly = 2 * mE;  // W.ny: one [2m][E] attention input per layer
+    const float eps = hp.rms_eps;
+    // encoder (src/dflash.rs:157-234), then layer l's attention norm of its rows into
+    // rows 0..m-1 of W.ny + l ly (src/dflash.rs:917-923)
+    LG_TRY(run_rmsnorm(features, md->enc_aux_norm, W.feat_n, E, m, hp.n_aux, A, eps, s));
+    LG_TRY(proj(W, W.feat_n, md->fc, md->fc_type, W.o, A, E, m, s));
+    for (uint32_t l0 = 0; l0 < hp.n_layers; l0 += NORM_RUN) {
+        NormRun run{};
+        run.count = hp.n_layers - l0 < NORM_RUN ? hp.n_layers - l0 : NORM_RUN;
+        for (uint32_t j = 0; j < run.count; j++) {
+            run.w[j] = md->layers[l0 + j].attn_norm;
+            run.out[j] = W.ny + (l0 + j) * ly;
+        }
+        LG_TRY(run_norm_fan(W.o, md->enc_output_norm, W.xe, run, E, m, eps, s));
+    }
+    float *x = W.xe + mE;  // the tokens' residual stream
+    LG_TRY(run_rows_in(tokens, x, W.ny + mE, md->layers[0].attn_norm, W.ssa, 1, E, m, s));
+    uint32_t cols_a = 1;  // partial sums per token row in W.ssa
+    for (uint32_t li = 0; li < hp.n_layers; li++) {
+        const lg_dflash_layer &L = md->layers[li];
+        const float *Y = W.ny + li * ly, *ny = Y + mE;
+        const RowScale ra{W.ssa, cols_a, m, eps};  // over Y's 2m rows: the token rows scaled
+        const RowScale rt{W.ssa, cols_a, 0, eps};  // over the token rows alone
+        // K, V of [injected; tokens], Q and the gate of the tokens (src/dflash.rs:924-944),
+        // grouped as in forward()
+        float *q = W.q, *gate = W.gate;
+        GateJob gj{};
+        const bool kvq = L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type;
+        if (kvq && L.attn_gate_type == LG_Q4_K) {
+            const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                    {L.attn_q, W.q, nullptr, QD}};
+            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
+                                    &ra));
+            q = W.q + (uint64_t)m * QD;
+            gate = W.gate + (uint64_t)m * H;
+            gj = {ny, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4, W.ssa, cols_a,
+                  eps};
+        } else if (kvq && L.attn_k_type == L.attn_gate_type) {
+            const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                    {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
+            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
+                                    &ra));
+            q = W.q + (uint64_t)m * QD;
+            gate = W.gate + (uint64_t)m * H;
+        } else {
+            const BatchJob k1{L.attn_k, W.kk, nullptr, KVD}, v1{L.attn_v, W.vv, nullptr, KVD};
+            const BatchJob q1{L.attn_q, W.q, nullptr, QD}, g1{L.attn_gate, W.gate, nullptr, H};
+            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, &k1, 1, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
+                                    &ra));
+            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, &v1, 1, E, 2 * m, L.attn_v_type, W.pws, W.pws_bytes, s, false,
+                                    &ra));
+            LG_TRY(proj_batch_multi(ny, LG_F32, nullptr, &q1, 1, E, m, L.attn_q_type, W.pws, W.pws_bytes, s, false, &rt));
+            LG_TRY(proj_batch_multi(ny, LG_F32, nullptr, &g1, 1, E, m, L.attn_gate_type, W.pws, W.pws_bytes, s, false,
+                                    &rt));
+        }
+        LG_TRY(run_qk_norm_rope(qk_job(W.kk, L.attn_k_norm, W.kk, KV, ctx_len, 2 * m),
+                                qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim, hp.qk_eps, s,
+                                gj));
+        LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
+                             W.att, W.part, s, gate));
+        // x += o_proj, writing x ffn_norm and the sums of x^2 for the FFN norm (src/dflash.rs:960-962)
+        const uint32_t cols_b = proj_batch_norm_cols(L.attn_output_type, QD, E, m);
+        const BatchJob oj{L.attn_output, x, x, E, W.h, L.ffn_norm, W.ssb};
+        LG_TRY(proj_batch_multi(W.att, LG_F32, nullptr, &oj, 1, QD, m, L.attn_output_type, W.pws, W.pws_bytes, s));
+        const RowScale rb{W.ssb, cols_b, 0, eps};
+        // SwiGLU FFN (src/dflash.rs:962-968); x += ffn_down, writing the next layer's
+        // attention input rows and sums of x^2
+        const bool next = li + 1 < hp.n_layers;
+        const BatchJob dj{L.ffn_down, x, x, E, next ? W.ny + (li + 1) * ly + mE : nullptr,
+                          next ? md->layers[li + 1].attn_norm : nullptr, next ? W.ssa : nullptr};
+        if (L.ffn_gate_type == L.ffn_up_type) {
+            const BatchJob jb[2] = {{L.ffn_gate, W.g, nullptr, FF}, {L.ffn_up, W.u, nullptr, FF}};
+            LG_TRY(proj_batch_multi(W.h, LG_F32, nullptr, jb, 2, E, m, L.ffn_gate_type, W.pws, W.pws_bytes, s, true,
+                                    &rb));
+            LG_TRY(proj_batch_multi(W.g, LG_F32, nullptr, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
+        } else {
+            const BatchJob g1{L.ffn_gate, W.g, nullptr, FF}, u1{L.ffn_up, W.u, nullptr, FF};
+            LG_TRY(proj_batch_multi(W.h, LG_F32, nullptr, &g1, 1, E, m, L.ffn_gate_type, W.pws, W.pws_bytes, s, false,
+                                    &rb));
+            LG_TRY(proj_batch_multi(W.h, LG_F32, nullptr, &u1, 1, E, m, L.ffn_up_type, W.pws, W.pws_bytes, s, false,
+                                    &rb));
+            LG_TRY(proj_batch_multi(W.g, LG_F32, W.u, &dj, 1, FF, m, L.ffn_down_type, W.pws, W.pws_bytes, s));
+        }
+        if (next) cols_a = proj_batch_norm_cols(L.ffn_down_type, FF, E, m);
     }
     if (md->output_norm) return run_rmsnorm(x, md->output_norm, out, E, m, 1, E, hp.rms_eps, s);
     hipLaunchKernelGGL(k_copy, dim3(blocks_for(mE)), dim3(256), 0, s, x, out, mE);
@@ -1260,3 +1525,11 @@ int lg_dflash_graph_destroy(void *graph) {
 }
 
 }  // extern "C"
+
+// The draft forward's attention and FFN norms folded into the products around them
+// (1, the default, where the model allows it) or run as their own launches (0): a
+// switch for A/B measurement; both meet the same parity bound.
+extern "C" int lg_set_draft_norms(uint32_t folded) {
+    g_fold_norms.store(folded ? 1u : 0u, std::memory_order_relaxed);
+    return LG_OK;
+}

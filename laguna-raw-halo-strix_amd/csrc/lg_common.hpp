@@ -130,18 +130,38 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
 // With `up` (f32 activations only), x is replaced by silu(x) * up (SiLU FFN input).
 // With `glu`, the two jobs are an FFN's gate and up products (equal n, f32 x, no
 // residuals): job 0's output receives silu(gate) * up and job 1's is scratch.
-// skip_rows: leading activation rows whose outputs the caller does not need; whole
-// 16-row token tiles below it are neither computed nor stored (c keeps what it held).
+//
+// An RMSNorm between two products runs inside them (m <= 32, Q4_K / Q8_0 weights on
+// the matrix-core path, f32 activations, not with `up`):
+//  * job fields y, yw, ss (not glu): also y = c * yw[row] (c the job's output, e.g. the
+//    residual stream with res = c) and ss[t * cols + g] = sum of c[t][row]^2 over the
+//    rows of workgroup column g, cols = proj_batch_norm_cols(w_dtype, k, n, m);
+//  * RowScale on the consuming call (x = such a y): the results of activation rows
+//    t >= tok0 are multiplied by (sum_g ss[(t - tok0) * cols + g] / k + eps)^-1/2, the
+//    norm's 1/rms (rows below tok0 arrive normalised).  cols <= proj_batch_rs_cols_max(m).
 struct BatchJob {
     const void *w;
     float *c;
     const float *res;
     uint32_t n;
-    uint32_t skip_rows = 0;
+    float *y = nullptr;
+    const float *yw = nullptr;
+    float *ss = nullptr;
+};
+struct RowScale {
+    const float *ss = nullptr;
+    uint32_t cols = 0, tok0 = 0;
+    float eps = 0.0f;
 };
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype);
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jobs, uint32_t njobs, uint32_t k,
-                     uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s, bool glu = false);
+                     uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s, bool glu = false,
+                     const RowScale *rs = nullptr);
+uint32_t proj_batch_norm_cols(int w_dtype, uint32_t k, uint32_t n, uint32_t m);
+uint32_t proj_batch_rs_cols_max(uint32_t m);
+// Whether products with these weights (f32 activations, 16-byte aligned) take the
+// matrix-core path, which the folded norm needs.
+bool proj_batch_mfma_ok(int w_dtype, uint32_t k, const void *w);
 
 // ---- launchers of the draft's glue kernels, used by the target forward (one row each;
 // in place allowed where the kernels allow it: rmsnorm, qk_norm_rope, gate_attn, add)
@@ -243,13 +263,17 @@ __device__ __forceinline__ float lane_add_x32(float v) {
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// Sum over the 64 lanes of a wavefront; every lane receives the total.
-// Lanes 0-15 of each row combine with DPP (xor 1, xor 2 via quad_perm, then
-// row_ror 4 and 8), the four rows with the two row swaps.
-__device__ __forceinline__ float wave_sum(float v) {
+// Sum over each 16-lane row: DPP xor 1, xor 2 (quad_perm), then row_ror 4 and 8.
+// Every lane receives its row's sum (lanes of different quads may associate the
+// terms differently).
+__device__ __forceinline__ float row16_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)); // row_ror 4
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)); // row_ror 8
-    return lane_add_x32(lane_add_x16(v));
+    return v;
 }
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total: the rows
+// by DPP, then the four rows with the two row swaps.
+__device__ __forceinline__ float wave_sum(float v) { return lane_add_x32(lane_add_x16(row16_sum(v))); }

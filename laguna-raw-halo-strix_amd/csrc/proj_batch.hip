@@ -98,18 +98,36 @@ __device__ __forceinline__ void q8_codes(uint32_t v, uint32_t &p02, uint32_t &p1
 // j owns workgroup columns g0 .. g0 + ceil(n / (64 RT)) - 1 and writes out[m][n]
 // (plus res, when given), using `part` for its slice partial sums.  Arrival
 // counters are indexed by the global workgroup column.
+//
+// RMSNorm folded into the products (kernels/rmsnorm.comp:23-34), for the draft's
+// residual stream:
+//  * a producing job (ss != null, not GLU) also writes y = out * yw[row] (the next
+//    norm's weight applied) and, per token, the sum of out^2 over each workgroup
+//    column's rows: ss[token * columns + column];
+//  * a consuming launch (NORM kernels) takes such a y as its activations and scales
+//    the results of tokens t >= rs_tok0 by (sum_p rs_ss[(t - rs_tok0) * rs_cols + p]
+//    / k + rs_eps)^-1/2, so W (x w / rms) = (W (x w)) / rms replaces the norm launch.
+//    The workgroup that finishes a column computes the scales, with the slices'
+//    partial sums in flight.
 constexpr int MM_JOBS = 4;
+constexpr uint32_t MM_SS_LOADS = 4;  // partial sums a consuming lane loads (per-token capacity 4 * 16 / TT)
 struct MmJob {
     const uint8_t *w;
     float *out;
     const float *res;
     float *part;
+    float *y;
+    const float *yw;
+    float *ss;
     uint32_t n, g0;
 };
 struct MmJobs {
     MmJob j[MM_JOBS];
     uint32_t count;
     uint32_t tiled;  // Q4_K weights in LG_Q4_K_T16 tiles
+    const float *rs_ss;
+    uint32_t rs_cols, rs_tok0;
+    float rs_eps;
 };
 // GLU launches pair two products of n rows each (gate: job 0, up: job 1): every
 // workgroup column covers the same 32*RT rows of both, wavefronts 0-1 the gate
@@ -144,7 +162,6 @@ struct Frags {
     float4 r[PER][2];                                    // f32 activations (FUSE: gate)
     float4 ru[FUSE ? PER : 1][2];                        // FUSE: up
     uint4 h[PER];                                        // bf16 activations
-
     __device__ __forceinline__ static void unit(int i, uint32_t &t, uint32_t &jj, uint32_t &kg, uint32_t &tl) {
         const uint32_t u = i * 256 + threadIdx.x;
         tl = u & 15u;
@@ -238,11 +255,52 @@ struct Frags {
     }
 };
 
+// NORM: token threadIdx.x / LT of the launch (LT = 16 / TT lanes per token) takes its
+// partial sums p = sub, sub + LT, ... (branch-free: slots past the columns and tokens
+// without a scale read a valid slot, dropped in rs_store).
+template <int TT>
+__device__ __forceinline__ void ss_load(float (&ssv)[MM_SS_LOADS], const MmJobs &jobs, uint32_t m) {
+    constexpr uint32_t LT = 16 / TT;
+    const uint32_t tok = threadIdx.x / LT, sub = threadIdx.x % LT, cols = jobs.rs_cols, tok0 = jobs.rs_tok0;
+    const uint32_t rows = m > tok0 ? m - tok0 : 1u;
+    const uint32_t r = tok >= tok0 && tok - tok0 < rows ? tok - tok0 : 0u;
+#pragma unroll
+    for (uint32_t j = 0; j < MM_SS_LOADS; j++) {
+        const uint32_t p = sub + LT * j;
+        ssv[j] = jobs.rs_ss[(uint64_t)r * cols + (p < cols ? p : cols - 1)];
+    }
+}
+
+// NORM: rsl[t] = (sum of token t's partials / k + eps)^-1/2, or 1 for tokens below
+// tok0 (and past m).  The lanes of a token add their slots in slot order, then meet
+// in DPP steps within their 16-lane row: xor 1, xor 2 (quad_perm), the half-row
+// mirror (lane i and 7 - i of each 8) and, for 16 lanes per token, the row mirror
+// (i and 15 - i).  Every lane of the token ends with the sum.
+template <int TT>
+__device__ __forceinline__ void rs_store(const float (&ssv)[MM_SS_LOADS], float *rsl, const MmJobs &jobs, uint32_t m,
+                                         uint32_t k) {
+    constexpr uint32_t LT = 16 / TT;
+    const uint32_t tok = threadIdx.x / LT, sub = threadIdx.x % LT, tok0 = jobs.rs_tok0;
+    float s = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < MM_SS_LOADS; j++) s += sub + LT * j < jobs.rs_cols ? ssv[j] : 0.0f;
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    if constexpr (LT == 16)
+        s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x140, 0xF, 0xF, false));  // row_mirror
+    if (sub == 0) rsl[tok] = tok >= tok0 && tok < m ? 1.0f / sqrtf(s / (float)k + jobs.rs_eps) : 1.0f;
+}
+
 // The workgroup's results: the output itself (one slice), or its slice's partial
-// sums and, in the last workgroup of the row group to finish, their ordered sum.
-template <int TT, int RT, bool GLU>
+// sums and, in the last workgroup of the row group to finish, their ordered sum;
+// scaled per token by rsl (NORM), and with y and the column's sums of squares when
+// ssout is given (not GLU).
+template <int TT, int RT, bool GLU, bool NORM>
 __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out, const float *res, float *part,
-                                       uint32_t *cnt, uint32_t rt0, uint32_t m, uint32_t n, float *xch) {
+                                       uint32_t *cnt, uint32_t rt0, uint32_t m, uint32_t n, float *xch,
+                                       const MmJobs &jobs, uint32_t k, float *y, const float *yw, float *ssout,
+                                       uint32_t bx) {
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
     const uint32_t S = gridDim.y, s = blockIdx.y;
     const uint64_t mn = (uint64_t)m * n;
@@ -265,6 +323,10 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
         __shared__ uint32_t last;
         if (!arrive_last(&cnt[blockIdx.x], S, &last)) return;
     }
+    // NORM: the partial sums of squares behind the token scales, loaded with the
+    // slices' partial sums (only the workgroup that finishes a column reads them)
+    float ssv[MM_SS_LOADS];
+    if constexpr (NORM) ss_load<TT>(ssv, jobs, m);
     // Slices are added in slice order (the sum does not depend on arrival order);
     // the loads of G slices for all RT row tiles are in flight together.
     constexpr uint32_t G = RT * TT >= 16 ? 1u : 16u / (RT * TT);
@@ -303,6 +365,17 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 #pragma unroll
                     for (int r = 0; r < 4; r++) v[i][t][r] += q0 + g < S ? pv[g][i][t][r] : 0.0f;
     }
+    if constexpr (NORM) {
+        __shared__ float rsl[TT * 16];
+        rs_store<TT>(ssv, rsl, jobs, m, k);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) v[i][t][r] *= rsl[t * 16 + 4 * kg + r];
+    }
     if constexpr (GLU) {
         // wavefronts 2-3 pass their up sums through LDS (`xch`, free once every
         // wavefront is past its products) to wavefronts 0-1, which hold the gate sums
@@ -327,10 +400,16 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
                 for (int r = 0; r < 4; r++)
                     v[i][t][r] = silu_mul(v[i][t][r], xch[((wave * RT + i) * TT + t) * 256 + r * 64 + l]);
     }
+    float sq[TT][4];  // ssout: this lane's sum of out^2 over its rows, per token
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sq[t][r] = 0.0f;
 #pragma unroll
     for (int i = 0; i < RT; i++) {
         const uint32_t row = (rt0 + i) * 16 + (l & 15u);
         if (row >= n) continue;
+        const float wy = !GLU && ssout ? yw[row] : 0.0f;
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
@@ -338,9 +417,32 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
                 const uint32_t tok = t * 16 + 4 * kg + r;
                 if (tok < m) {
                     const uint64_t o = (uint64_t)tok * n + row;
-                    out[o] = res ? res[o] + v[i][t][r] : v[i][t][r];
+                    const float ov = res ? res[o] + v[i][t][r] : v[i][t][r];
+                    out[o] = ov;
+                    if (!GLU && ssout) {
+                        y[o] = ov * wy;
+                        sq[t][r] = __builtin_fmaf(ov, ov, sq[t][r]);
+                    }
                 }
             }
+    }
+    if constexpr (!GLU) {
+        if (ssout) {  // uniform: every wavefront of the workgroup is here
+            // the wavefront's 16 rows per tile (the lanes of a k-group) in a DPP
+            // reduction, then the four wavefronts in wavefront order
+            __shared__ float ssl[4][TT * 16];
+            const uint32_t wave = threadIdx.x >> 6;
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float rsum = row16_sum(sq[t][r]);
+                    if ((l & 15u) == 0) ssl[wave][t * 16 + 4 * kg + r] = rsum;
+                }
+            __syncthreads();
+            const uint32_t tk = threadIdx.x, cols = (n + 64 * RT - 1) / (64 * RT);
+            if (tk < TT * 16 && tk < m) ssout[(uint64_t)tk * cols + bx] = (ssl[0][tk] + ssl[1][tk]) + (ssl[2][tk] + ssl[3][tk]);
+        }
     }
 }
 
@@ -349,7 +451,7 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 // every weight load of the slice (branch-free: rows past n and blocks past k read
 // row n-1 / the last block and are never used), the fragment build while the
 // weights are in flight, then the products.
-template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU>
+template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM>
 __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
     MM_JOB_SELECT;
@@ -457,11 +559,12 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
         }
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
-    finish<TT, RT, GLU>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf));
+    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
+                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx);
 }
 
 // Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
-template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU>
+template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM>
 __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
     MM_JOB_SELECT;
@@ -552,7 +655,8 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
         }
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
-    finish<TT, RT, GLU>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf));
+    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
+                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx);
 }
 
 // Fallback for shapes outside the MFMA path (f32 weights, k not a multiple of the
@@ -638,10 +742,11 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     return {ch, slices, tiles, rt};
 }
 
-template <int TT, int PARTS, int CH, bool FUSE, bool GLU>
+template <int TT, int PARTS, int CH, bool FUSE, bool GLU, bool NORM>
 void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt,
                uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
-#define LG_MM(K, R) hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE, GLU>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
+#define LG_MM(K, R) \
+    hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE, GLU, NORM>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
     // mm_shape keeps rt * ch within each kernel's register budget
     if (dtype == LG_Q4_K) {
         if constexpr (4 * CH <= 8)
@@ -671,18 +776,18 @@ void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up
 #undef LG_MM
 }
 
-template <int PARTS, bool FUSE, bool GLU = false>
+template <int PARTS, bool FUSE, bool GLU = false, bool NORM = false>
 int launch_mm(int dtype, const MmShape &sh, uint32_t groups, const void *x, const float *up, const MmJobs &jobs,
               uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
     const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
     if (sh.tiles == 1) {
-        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<1, PARTS, 1, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<1, PARTS, 1, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     } else {
-        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<2, PARTS, 1, FUSE, GLU>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<2, PARTS, 1, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     }
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
 }
@@ -718,13 +823,39 @@ uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, in
     return proj_batch_multi_ws_bytes(k, &n, 1, m, w_dtype);
 }
 
+uint32_t proj_batch_norm_cols(int w_dtype, uint32_t k, uint32_t n, uint32_t m) {
+    if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
+    if (w_dtype == LG_Q8_0_T16) w_dtype = LG_Q8_0;
+    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32);
+    return (n + 64 * sh.rt - 1) / (64 * sh.rt);
+}
+
+uint32_t proj_batch_rs_cols_max(uint32_t m) { return MM_SS_LOADS * (m > 16 ? 8u : 16u); }
+
+bool proj_batch_mfma_ok(int w_dtype, uint32_t k, const void *w) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(w);
+    if (w_dtype == LG_Q4_K_T16 || w_dtype == LG_Q8_0_T16) return k && k % QK_K == 0 && (a & 15u) == 0;
+    if (w_dtype == LG_Q4_K) return k && k % QK_K == 0 && (a & 15u) == 0;
+    if (w_dtype == LG_Q8_0) return k && k % QK8_0 == 0 && (a & 1u) == 0;
+    return false;
+}
+
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jb, uint32_t njobs, uint32_t k,
-                     uint32_t m, int w_dtype, void *ws_given, uint64_t ws_bytes, hipStream_t s, bool glu) {
+                     uint32_t m, int w_dtype, void *ws_given, uint64_t ws_bytes, hipStream_t s, bool glu,
+                     const RowScale *rs) {
     const char *name = "lg_dispatch_proj_quant_batch";
     LG_REQUIRE(njobs >= 1 && njobs <= (uint32_t)MM_JOBS, "%s: %u jobs (1..%d)", name, njobs, MM_JOBS);
     LG_REQUIRE(!glu || (njobs == 2 && jb[0].n == jb[1].n && !up && x_dtype == LG_F32 && !jb[0].res && !jb[1].res),
                "%s: a gate/up pair takes two products of equal n over f32 activations, without residuals", name);
     if (m == 0) return LG_OK;
+    const bool norm = rs && rs->ss && rs->tok0 < m;
+    bool epi = false;
+    for (uint32_t j = 0; j < njobs; j++) epi = epi || jb[j].ss;
+    LG_REQUIRE(!norm || (x_dtype == LG_F32 && !up && rs->cols >= 1 && rs->cols <= proj_batch_rs_cols_max(m)),
+               "%s: a folded RMSNorm takes f32 activations without up and 1..%u partial sums per row (got %u)", name,
+               proj_batch_rs_cols_max(m), norm ? rs->cols : 0u);
+    LG_REQUIRE(!epi || (njobs == 1 && !glu && m <= 32 && x_dtype == LG_F32 && jb[0].y && jb[0].yw),
+               "%s: the RMSNorm epilogue takes one job over at most 32 f32 rows, with y and yw", name);
     LG_REQUIRE(m <= 64, "%s: m=%u exceeds 64", name, m);
     LG_REQUIRE(x, "%s: null activations", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
@@ -751,10 +882,16 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         LG_REQUIRE(b.w && b.c, "%s: null pointer in job %u", name, j);
         LG_EXTENT(b.c, (uint64_t)m * b.n * 4, name);
         if (b.res) LG_EXTENT(b.res, (uint64_t)m * b.n * 4, name);
+        if (b.ss) {
+            LG_EXTENT(b.y, (uint64_t)m * b.n * 4, name);
+            LG_EXTENT(b.yw, (uint64_t)b.n * 4, name);
+            LG_EXTENT(b.ss, (uint64_t)m * proj_batch_norm_cols(w_dtype, k, b.n, m) * 4, name);
+        }
         if (k) LG_EXTENT(b.w, tiled ? tiled_bytes(w_dtype, k, b.n) : tensor_bytes(w_dtype, (uint64_t)b.n * k), name);
         LG_REQUIRE(!tiled || (reinterpret_cast<uintptr_t>(b.w) & 15u) == 0, "%s: unaligned tiled weights", name);
     }
     if (ntot == 0) return LG_OK;
+    if (norm) LG_EXTENT(rs->ss, (uint64_t)(m - rs->tok0) * rs->cols * 4, name);
     if (tiled) w_dtype = w_dtype == LG_Q4_K_T16 ? LG_Q4_K : LG_Q8_0;  // the same kernels, reading tiles
     const uint32_t blk = w_dtype == LG_Q4_K ? QK_K : QK8_0;
     bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
@@ -762,6 +899,8 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     for (uint32_t j = 0; j < njobs; j++)
         fast = fast && (w_dtype != LG_Q4_K || (reinterpret_cast<uintptr_t>(jb[j].w) & 15u) == 0) &&
                (reinterpret_cast<uintptr_t>(jb[j].w) & 1u) == 0;
+    LG_REQUIRE(fast || !(norm || epi), "%s: a folded RMSNorm needs the matrix-core path (k a multiple of the block, "
+               "aligned operands)", name);
     if (!fast) {
         for (uint32_t j = 0; j < njobs; j++) {
             if (jb[j].n == 0) continue;
@@ -794,7 +933,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         for (uint32_t j = 0; j < njobs; j++) {
             const uint64_t off = (uint64_t)16 * t0 * jb[j].n;
             jobs.j[j] = {static_cast<const uint8_t *>(jb[j].w), jb[j].c + off, jb[j].res ? jb[j].res + off : nullptr,
-                         reinterpret_cast<float *>(pb), jb[j].n, groups};
+                         reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups};
             if (pb) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
             groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
         }
@@ -804,12 +943,22 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         }
         jobs.count = njobs;
         jobs.tiled = tiled ? 1u : 0u;
+        // the folded norm's scaled rows in this pair of tiles (rows 16 t0 .. 16 t0 + ml - 1)
+        const bool pnorm = norm && 16 * t0 + ml > rs->tok0;
+        if (pnorm) {
+            jobs.rs_tok0 = rs->tok0 > 16 * t0 ? rs->tok0 - 16 * t0 : 0u;
+            jobs.rs_ss = rs->ss + (uint64_t)(16 * t0 > rs->tok0 ? 16 * t0 - rs->tok0 : 0u) * rs->cols;
+            jobs.rs_cols = rs->cols;
+            jobs.rs_eps = rs->eps;
+        }
         LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
         const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
         const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
         if (x_dtype == LG_BF16) LG_TRY((launch_mm<1, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else if (up) LG_TRY((launch_mm<3, true>(w_dtype, sh, groups, xt, ut, jobs, cnt, ml, k, s)));
+        else if (glu && pnorm) LG_TRY((launch_mm<3, false, true, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else if (glu) LG_TRY((launch_mm<3, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
+        else if (pnorm) LG_TRY((launch_mm<3, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else LG_TRY((launch_mm<3, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
     }
     return LG_OK;

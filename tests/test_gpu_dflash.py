@@ -226,6 +226,26 @@ def test_graph_replays_match_eager(ctx):
     stream.destroy()
 
 
+@pytest.mark.parametrize("cfg,m,ctx_len,tol", [(SMALL, 1, 0, 3e-5), (SMALL, 16, 100, 8e-4),
+                                               (SMALL, 32, 70, TOL_FWD_STEEP), (SMALL64, 5, 33, 1e-5)])
+def test_forward_folded_norms_and_separate_norms(ctx, cfg, m, ctx_len, tol):
+    # The attention and FFN RMSNorms folded into the projections (the default: the
+    # product writing the residual stream also writes x * w and sums of x^2, the next
+    # product scales by 1/rms) and run as their own launches: both within the case's
+    # bound of the oracle, each bit-for-bit repeatable.
+    print(f"forward folded vs separate norms n_embd={cfg.n_embd} m={m} ctx={ctx_len}", flush=True)
+    model, (W, layers, feat, tok, kc, vc) = build(ctx, cfg, 0x5EED0220 + m, m, ctx_len)  # the cases above
+    want = dfo.forward_block(feat, tok, W, layers, kc, vc, ctx_len, cfg)
+    try:
+        for folded in (1, 0):
+            lh.check(lh.lib().lg_set_draft_norms(folded))
+            y = model.forward_block(feat, tok)
+            np.testing.assert_array_equal(y, model.forward_block(feat, tok))
+            check(f"forward folded={folded}", y, want, tol)
+    finally:
+        lh.check(lh.lib().lg_set_draft_norms(1))
+
+
 @pytest.fixture(scope="module")
 def draft_full():
     cfg = lh.DFlashConfig()
@@ -260,7 +280,14 @@ def test_forward_block_draft_full_size(ctx, draft_full):
     y = model.forward_block(feat, tok)
     y2 = model.forward_block(feat, tok)
     np.testing.assert_array_equal(y, y2)  # deterministic
-    check("forward full", y, dfo.forward_block(feat, tok, W, layers, kc, vc, 2048, cfg), TOL_FWD)
+    want = dfo.forward_block(feat, tok, W, layers, kc, vc, 2048, cfg)
+    check("forward full", y, want, TOL_FWD)
+    # the same with the attention and FFN norms as their own launches
+    lh.check(lh.lib().lg_set_draft_norms(0))
+    try:
+        check("forward full, separate norms", model.forward_block(feat, tok), want, TOL_FWD)
+    finally:
+        lh.check(lh.lib().lg_set_draft_norms(1))
     model.free()
 
 
