@@ -97,17 +97,24 @@ __global__ __launch_bounds__(256) void k_rmsnorm4(const float *x, const float *_
 }
 
 // The block forward's norms folded into its projections (the products apply the
-// norm's weight and 1/rms around them; csrc/proj_batch.hip).  What stays outside:
-//
-// The encoder's output norm and, for a run of layers, each layer's attention norm of
-// its result (the injected rows are the same in every layer), in one launch:
-//   xe = x w / rms(x),   out_j = xe run.w[j] / rms(xe)
-// with the arithmetic of k_rmsnorm4, so the rows equal the two norms run apart.
+// norm's weight and 1/rms around them; csrc/proj_batch.hip).  What stays outside
+// runs in one launch at the start of the block, workgroup (row, j):
+//  * j < run.count: the encoder's output norm of row `row` and layer run.w[j]'s
+//    attention norm of it (the injected rows are the same in every layer):
+//      xe = x w / rms(x) (stored by j = 0),   out_j = xe run.w[j] / rms(xe),
+//    with the arithmetic of k_rmsnorm4, so the rows equal the two norms run apart;
+//  * j = run.count (when tok is given): token row `row` entering layer 0:
+//    xt = tok, yt = tok * wt (layer 0's attention-norm weight, its 1/rms left to the
+//    products), and the sum of tok^2 in slot 0 of the row's `cols` slots of ss (the
+//    others zero): the layout the products' norm epilogue writes.
 constexpr uint32_t NORM_RUN = 8;
 struct NormRun {
     const float *w[NORM_RUN];
     float *out[NORM_RUN];
     uint32_t count;
+    const float *tok, *wt;
+    float *xt, *yt, *ss;
+    uint32_t cols;
 };
 
 // Rows of n floats, n a multiple of 4 up to 1024 V4: thread i holds float4s i,
@@ -118,6 +125,15 @@ __device__ __forceinline__ void load_row4(const float *__restrict__ r, uint32_t 
     for (int i = 0; i < V4; i++) {
         const uint32_t e = i * 256 + threadIdx.x;
         v[i] = e < n / 4 ? reinterpret_cast<const float4 *>(r)[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+template <int V4>
+__device__ __forceinline__ void store_row4(float *__restrict__ r, uint32_t n, const float4 (&v)[V4]) {
+#pragma unroll
+    for (int i = 0; i < V4; i++) {
+        const uint32_t e = i * 256 + threadIdx.x;
+        if (e < n / 4) reinterpret_cast<float4 *>(r)[e] = v[i];
     }
 }
 
@@ -136,54 +152,35 @@ __device__ __forceinline__ float4 mul4(float4 a, float4 b, float c) {
 }
 
 template <int V4>
-__global__ __launch_bounds__(256) void k_rmsnorm4_fan(const float *__restrict__ x, const float *__restrict__ w,
-                                                      float *__restrict__ xe, NormRun run, uint32_t n, float eps) {
+__global__ __launch_bounds__(256) void k_norms_in(const float *__restrict__ x, const float *__restrict__ w,
+                                                  float *__restrict__ xe, NormRun run, uint32_t n, float eps) {
     __shared__ float red[4];
     const uint64_t base = (uint64_t)blockIdx.x * n;
+    const uint32_t j = blockIdx.y;
     float4 v[V4], wv[V4];
+    if (j == run.count) {  // a token row
+        load_row4<V4>(run.tok + base, n, v);
+        load_row4<V4>(run.wt, n, wv);
+        store_row4<V4>(run.xt + base, n, v);
+#pragma unroll
+        for (int i = 0; i < V4; i++) wv[i] = mul4(v[i], wv[i], 1.0f);
+        store_row4<V4>(run.yt + base, n, wv);
+        const float s = sum_sq4<V4>(v, red);
+        for (uint32_t p = threadIdx.x; p < run.cols; p += 256)
+            run.ss[(uint64_t)blockIdx.x * run.cols + p] = p == 0 ? s : 0.0f;
+        return;
+    }
     load_row4<V4>(x + base, n, v);
     load_row4<V4>(w, n, wv);
     const float rms = 1.0f / sqrtf(sum_sq4<V4>(v, red) / (float)n + eps);
 #pragma unroll
-    for (int i = 0; i < V4; i++) {
-        const uint32_t e = i * 256 + threadIdx.x;
-        v[i] = mul4(v[i], wv[i], rms);
-        if (e < n / 4) reinterpret_cast<float4 *>(xe + base)[e] = v[i];
-    }
+    for (int i = 0; i < V4; i++) v[i] = mul4(v[i], wv[i], rms);
+    if (j == 0) store_row4<V4>(xe + base, n, v);
     const float rms2 = 1.0f / sqrtf(sum_sq4<V4>(v, red) / (float)n + eps);
-    for (uint32_t j = 0; j < run.count; j++) {
-        load_row4<V4>(run.w[j], n, wv);
+    load_row4<V4>(run.w[j], n, wv);
 #pragma unroll
-        for (int i = 0; i < V4; i++) {
-            const uint32_t e = i * 256 + threadIdx.x;
-            if (e < n / 4) reinterpret_cast<float4 *>(run.out[j] + base)[e] = mul4(v[i], wv[i], rms2);
-        }
-    }
-}
-
-// The block's token rows entering layer 0: x = tokens, y = tokens * w (layer 0's
-// attention-norm weight, its 1/rms left to the products), and per row the sum of
-// tokens^2 in slot 0 of `cols` slots (the others zero): the layout the products'
-// norm epilogue writes.
-template <int V4>
-__global__ __launch_bounds__(256) void k_rows_in(const float *__restrict__ tok, float *__restrict__ x,
-                                                 float *__restrict__ y, const float *__restrict__ w,
-                                                 float *__restrict__ ss, uint32_t cols, uint32_t n) {
-    __shared__ float red[4];
-    const uint64_t base = (uint64_t)blockIdx.x * n;
-    float4 v[V4], wv[V4];
-    load_row4<V4>(tok + base, n, v);
-    load_row4<V4>(w, n, wv);
-#pragma unroll
-    for (int i = 0; i < V4; i++) {
-        const uint32_t e = i * 256 + threadIdx.x;
-        if (e < n / 4) {
-            reinterpret_cast<float4 *>(x + base)[e] = v[i];
-            reinterpret_cast<float4 *>(y + base)[e] = mul4(v[i], wv[i], 1.0f);
-        }
-    }
-    const float s = sum_sq4<V4>(v, red);
-    for (uint32_t p = threadIdx.x; p < cols; p += 256) ss[(uint64_t)blockIdx.x * cols + p] = p == 0 ? s : 0.0f;
+    for (int i = 0; i < V4; i++) wv[i] = mul4(v[i], wv[i], rms2);
+    store_row4<V4>(run.out[j] + base, n, wv);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -783,24 +780,14 @@ int run_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t
 // Rows of n floats, n a multiple of 4 up to 8192 (the folded norms' kernels).
 bool fan_width_ok(uint32_t n) { return n && n % 4 == 0 && n <= 8192; }
 
-int run_norm_fan(const float *x, const float *w, float *xe, const NormRun &run, uint32_t n, uint32_t rows, float eps,
+int run_norms_in(const float *x, const float *w, float *xe, const NormRun &run, uint32_t n, uint32_t rows, float eps,
                  hipStream_t s) {
-    const dim3 grid(rows);
-    if (n <= 1024) hipLaunchKernelGGL(k_rmsnorm4_fan<1>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
-    else if (n <= 2048) hipLaunchKernelGGL(k_rmsnorm4_fan<2>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
-    else if (n <= 4096) hipLaunchKernelGGL(k_rmsnorm4_fan<4>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
-    else hipLaunchKernelGGL(k_rmsnorm4_fan<8>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
-    return after_launch("encoder and attention norms", s);
-}
-
-int run_rows_in(const float *tok, float *x, float *y, const float *w, float *ss, uint32_t cols, uint32_t n,
-                uint32_t rows, hipStream_t s) {
-    const dim3 grid(rows);
-    if (n <= 1024) hipLaunchKernelGGL(k_rows_in<1>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
-    else if (n <= 2048) hipLaunchKernelGGL(k_rows_in<2>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
-    else if (n <= 4096) hipLaunchKernelGGL(k_rows_in<4>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
-    else hipLaunchKernelGGL(k_rows_in<8>, grid, dim3(256), 0, s, tok, x, y, w, ss, cols, n);
-    return after_launch("token rows in", s);
+    const dim3 grid(rows, run.count + (run.tok ? 1 : 0));
+    if (n <= 1024) hipLaunchKernelGGL(k_norms_in<1>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    else if (n <= 2048) hipLaunchKernelGGL(k_norms_in<2>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    else if (n <= 4096) hipLaunchKernelGGL(k_norms_in<4>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    else hipLaunchKernelGGL(k_norms_in<8>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
+    return after_launch("encoder, attention and token-row norms", s);
 }
 
 QkJob qk_job(const float *x, const float *w, float *out, uint32_t n_heads, uint32_t pos, uint32_t rows) {
@@ -1152,6 +1139,9 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
     // rows 0..m-1 of W.ny + l ly (src/dflash.rs:917-923)
     LG_TRY(run_rmsnorm(features, md->enc_aux_norm, W.feat_n, E, m, hp.n_aux, A, eps, s));
     LG_TRY(proj(W, W.feat_n, md->fc, md->fc_type, W.o, A, E, m, s));
+    // and the token rows entering layer 0: x = tokens, with layer 0's x attn_norm and
+    // sums of squares
+    float *x = W.xe + mE;  // the tokens' residual stream
     for (uint32_t l0 = 0; l0 < hp.n_layers; l0 += NORM_RUN) {
         NormRun run{};
         run.count = hp.n_layers - l0 < NORM_RUN ? hp.n_layers - l0 : NORM_RUN;
@@ -1159,10 +1149,16 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
             run.w[j] = md->layers[l0 + j].attn_norm;
             run.out[j] = W.ny + (l0 + j) * ly;
         }
-        LG_TRY(run_norm_fan(W.o, md->enc_output_norm, W.xe, run, E, m, eps, s));
+        if (l0 == 0) {
+            run.tok = tokens;
+            run.wt = md->layers[0].attn_norm;
+            run.xt = x;
+            run.yt = W.ny + mE;
+            run.ss = W.ssa;
+            run.cols = 1;
+        }
+        LG_TRY(run_norms_in(W.o, md->enc_output_norm, W.xe, run, E, m, eps, s));
     }
-    float *x = W.xe + mE;  // the tokens' residual stream
-    LG_TRY(run_rows_in(tokens, x, W.ny + mE, md->layers[0].attn_norm, W.ssa, 1, E, m, s));
     uint32_t cols_a = 1;  // partial sums per token row in W.ssa
     for (uint32_t li = 0; li < hp.n_layers; li++) {
         const lg_dflash_layer &L = md->layers[li];
