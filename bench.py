@@ -26,6 +26,10 @@ Also reported under "extra":
   context (HIP graph replay and eager), in us per block, draft tokens/s and
   GB/s of algorithmic bytes (every weight, the context K/V, inputs and outputs
   once per block);
+* the target side of the verify loop: one token through a 6-layer dense target
+  of the draft's shape over a 2048-position K/V cache, with three captured
+  states and the vocab-sized LM head (GB/s of every weight and the cache read
+  once);
 * ceilings: an empty kernel, and a plain streaming read (lg_bench_read) of
   17.8, 33.0 and 350 MB buffers through the same kind of rotating pool; the
   headline's roofline carries its fraction of both 8 TB/s and the measured read
@@ -128,6 +132,18 @@ def _pool(ctx, raw, tiled=None):
             b = t
         pool.append(b)
     return pool, copies * raw.nbytes
+
+
+_DRAFT = {}
+
+
+def draft_model(seed, cfg):
+    """The random-init draft (synth.dflash_model), generated once per process: the
+    draft-block workloads and the target workload share its layers."""
+    key = (seed, cfg.n_layers)
+    if key not in _DRAFT:
+        _DRAFT[key] = synth.dflash_model(seed, cfg, cfg.n_layers)
+    return _DRAFT[key]
 
 
 class Workload:
@@ -251,7 +267,7 @@ class DFlashBlock(Workload):
 
     def setup(self, ctx, stream=None):
         cfg, m = self.cfg, self.m
-        W, layers = synth.dflash_model(self.seed, cfg, cfg.n_layers)
+        W, layers = draft_model(self.seed, cfg)
         feat, tok, kc, vc = synth.dflash_inputs(self.seed + 1, cfg, cfg.n_layers, m, self.ctx_len)
         nbytes = lambda a: np.asarray(a).nbytes
         wbytes = sum(nbytes(W[n]) for n in ("enc_aux_norm", "fc", "enc_output_norm", "output_norm"))
@@ -314,6 +330,74 @@ class Read(Workload):
         lh.check(lh.lib().lg_bench_read(w.ptr, self.bytes_per_call, stream))
 
 
+class TargetToken(Workload):
+    """Target-side verify step: one token through a dense target with the device K/V
+    cache holding `ctx_len` positions (src/target.rs:298-578), the hidden states
+    captured after layers 1, 3 and 5 (the draft's three features), then the Q4_K LM
+    head over the vocabulary (src/target.rs:580-605).  Six layers of the draft's shape
+    (hidden 4096, 32 Q / 8 KV heads of 128, FFN 14336, an attention gate), weights of
+    trained magnitude: zero-mean Q4_K blocks (synth.centered_q4k, standard deviation
+    0.02) with a ggml-quantized N(0, 0.02) Q8_0 attn_output, so the residual stream
+    stays finite as in a real model; the six layers hold device copies of one set of
+    values.  The cache holds N(0, 1) keys and values.  Every
+    call appends position ctx_len (the cache length is reset before each), so each
+    reads all weights once (1.2 GB, past the Infinity Cache)."""
+
+    graph_mode = False  # the cache length is host state the call advances
+
+    def __init__(self, ctx_len=2048, n_vocab=151936, seed=0x5EED000A):
+        self.ctx_len, self.n_vocab, self.seed = ctx_len, n_vocab, seed
+        self.name = f"dense target forward, 1 token over a {ctx_len}-position K/V cache, 6 layers + LM head {n_vocab}"
+        self.kernel = None
+
+    def setup(self, ctx):
+        dc = lh.DFlashConfig()
+        cfg = lh.TargetConfig(n_embd=dc.n_embd, n_heads=dc.n_heads, n_kv=dc.n_kv, head_dim=dc.head_dim,
+                              n_ff=dc.n_ff, n_layers=dc.n_layers, n_vocab=self.n_vocab, rope_dim=dc.rope_dim)
+        E, HD, KVD, FF, H = cfg.n_embd, cfg.head_dim, cfg.n_kv * cfg.head_dim, cfg.n_ff, cfg.n_heads
+        shapes = {"attn_q": (E, H * HD), "attn_k": (E, KVD), "attn_v": (E, KVD), "attn_gate": (E, H),
+                  "attn_output": (H * HD, E), "ffn_gate": (E, FF), "ffn_up": (E, FF), "ffn_down": (FF, E)}
+        seeds = iter(synth.splitmix64(self.seed, 12))
+        L = {n: np.ones(HD if n in ("attn_q_norm", "attn_k_norm") else E, np.float32) for n in lh.TARGET_NORMS}
+        for p, (k, n) in shapes.items():
+            sd = int(next(seeds))
+            if p == "attn_output":
+                L[p], L[p + "_dtype"] = synth.q8_0_weight(sd, k, n), lh.Q8_0
+            else:
+                L[p], L[p + "_dtype"] = synth.centered_q4k(sd, k * n // 256), lh.Q4_K
+        # every layer uploads its own device copy of the same host arrays: the calls
+        # read 6 distinct sets of weights (generating one set keeps the set-up short)
+        layers = [dict(L) for _ in range(cfg.n_layers)]
+        out = synth.centered_q4k(int(next(seeds)), cfg.n_embd * cfg.n_vocab // 256)
+        onorm = np.ones(cfg.n_embd, np.float32)
+        nbytes = lambda a: np.asarray(a).nbytes
+        wbytes = sum(nbytes(L[n]) for L in layers for n in lh.TARGET_NORMS + lh.TARGET_PROJ) + out.nbytes
+        kvd = cfg.n_kv * cfg.head_dim
+        kvbytes = 2 * cfg.n_layers * (self.ctx_len + 1) * kvd * 4
+        self.bytes_per_call = wbytes + kvbytes + onorm.nbytes + 4 * (cfg.n_embd * 5 + cfg.n_vocab)
+        self.model = lh.TargetModel(ctx, cfg, layers, output_norm=onorm, output=out, output_dtype=lh.Q4_K)
+        del layers, out
+        self.cache = lh.TargetKvCache(self.model, self.ctx_len + 1)
+        n = cfg.n_layers * (self.ctx_len + 1) * kvd
+        self.cache.k.upload(synth.normal(self.seed + 8, n))
+        self.cache.v.upload(synth.normal(self.seed + 9, n))
+        self.x = lh.upload_f32(ctx, synth.normal(self.seed + 10, cfg.n_embd))
+        self.capture = [1, 3, 5]
+        self.cb = lh.GpuBuffer(ctx, 4 * len(self.capture) * cfg.n_embd)
+        self.lb = lh.GpuBuffer(ctx, 4 * cfg.n_vocab)
+        self.pool_bytes = self.bytes_per_call
+
+    def step(self, i, stream):
+        self.cache._c.len = self.ctx_len
+        self.model.forward_token_device(self.x, self.capture, self.cb, self.lb, cache=self.cache, stream=stream)
+
+    def teardown(self):
+        self.model.free()
+        self.cache.free()
+        for b in (self.x, self.cb, self.lb):
+            b.free()
+
+
 HEAD_KERNEL = "k_q4k_m1_dig"
 WORKLOADS = {
     "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003, kernel=HEAD_KERNEL),
@@ -333,6 +417,7 @@ WORKLOADS = {
     "lm_head_verify_m16": lambda: VerifyBlock(4096, 151936, 0x5EED000B),
     "dflash_block": lambda: DFlashBlock(),
     "dflash_block_eager": lambda: DFlashBlock(graph=False),
+    "target_token": lambda: TargetToken(),
     "ceil_empty": lambda: Empty(256),
     "ceil_read_17.8MB": lambda: Read(17858560),
     "ceil_read_33.1MB": lambda: Read(33103872),
@@ -340,7 +425,7 @@ WORKLOADS = {
 }
 EXTRA = ["q8_0_m1", "q4k_down_silu", "q4k_m1_k14336", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
          "q8_0_m16_f32", "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16",
-         "dflash_block", "dflash_block_eager", "ceil_empty", "ceil_read_17.8MB", "ceil_read_33.1MB",
+         "dflash_block", "dflash_block_eager", "target_token", "ceil_empty", "ceil_read_17.8MB", "ceil_read_33.1MB",
          "ceil_read_350MB"]
 
 

@@ -33,13 +33,16 @@ int lg_set_m1_kernel(uint32_t kind);
  * draft-forward graph keeps the workspace it was sized with: set this before
  * lg_dflash_graph_create. */
 int lg_set_batch_shape(uint32_t ch, uint32_t rt);
-/* The draft forward's attention and FFN RMSNorms: 1 (the default) folds them into
- * the projections around them wherever the model allows it (every projection on the
- * matrix-core path, n_embd a multiple of 4 up to 8192, 16-byte aligned norm weights
- * and tokens); 0 runs each as its own launch.  Unlike the hooks above, 0 is not the
- * automatic choice.  Set it before lg_dflash_graph_create: a captured graph keeps the
- * launches it recorded. */
-int lg_set_draft_norms(uint32_t folded);
+/* The forwards' RMSNorms: 1 (the default) folds them into the projections around
+ * them wherever the model allows it, 0 runs each as its own launch.  The draft
+ * forward folds its attention and FFN norms when every projection is on the
+ * matrix-core path (n_embd a multiple of 4 up to 8192, 16-byte aligned norm weights
+ * and tokens); the target forward folds each layer's residual adds and norms into
+ * its Q4_K input projections when they are on the M = 1 integer-dot path (n_embd a
+ * multiple of 256 up to 4096, 16-byte aligned operands).  Unlike the hooks above, 0
+ * is not the automatic choice.  Set it before lg_dflash_graph_create: a captured
+ * graph keeps the launches it recorded. */
+int lg_set_fold_norms(uint32_t folded);
 
 /* ---- ceiling kernels: what one launch, and one read of a buffer, cost. */
 

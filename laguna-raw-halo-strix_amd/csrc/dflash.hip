@@ -570,6 +570,105 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 
 __device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g : logf(1.0f + expf(g)); }  // src/dflash.rs:957
 
+// The chunk partials of k_attn_chunk for a few queries (rows * G <= ADQ: one token's
+// query heads), straight from memory in f32: no bf16 parts, no LDS tiles.  One
+// workgroup per (64-position chunk, kv head); wave w takes positions 16w .. 16w+15.
+//   scores: lane (p, quarter) dots the 32 dims 32 quarter .. of K row p with every
+//           query (held in LDS), the four quarters meet in two lane swaps;
+//   softmax: wave w takes queries w, w + 4 over the chunk's 64 scores;
+//   P V: each wave adds its 16 positions for every query (lane = dims 2l, 2l+1), and
+//        the four waves' sums meet in LDS in wave order.
+// Every K and V load of the chunk is issued at the start.  Partials as k_attn_chunk
+// writes them (unnormalised O, and the chunk's max and sum of each query).
+constexpr uint32_t ADQ = 8;
+
+__global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q, const float *__restrict__ k0,
+                                                     const float *__restrict__ v0, uint32_t n0,
+                                                     const float *__restrict__ k1, const float *__restrict__ v1,
+                                                     uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv,
+                                                     uint32_t qpos0, int causal, float scale, uint32_t nch,
+                                                     float *__restrict__ part_o, float *__restrict__ part_ml) {
+    __shared__ float4 lq[ADQ][AHD / 4];
+    __shared__ float lp[ADQ][ACH];
+    __shared__ float lo[4][ADQ][AHD];
+    const uint32_t h = blockIdx.y, c = blockIdx.x;
+    const uint32_t G = n_q / n_kv, nq = rows * G;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t kvld = n_kv * AHD;
+    auto kv_row = [&](const float *a0, const float *a1, uint32_t p) {  // position p of the sequence (p < S)
+        return p < n0 ? a0 + (uint64_t)p * kvld : a1 + (uint64_t)(p - n0) * kvld;
+    };
+    // K: position 16 wave + (lane & 15), dims 32 (lane >> 4) ..; V: position 16 wave + j, dims 2 lane ..
+    const uint32_t pk = c * ACH + 16 * wave + (lane & 15u), qd = lane >> 4;
+    float4 kr[8];
+    {
+        const float *kp = kv_row(k0, k1, pk < S ? pk : S - 1) + h * AHD + 32 * qd;
+#pragma unroll
+        for (int i = 0; i < 8; i++) kr[i] = reinterpret_cast<const float4 *>(kp)[i];
+    }
+    float2 vr[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t p = c * ACH + 16 * wave + j;
+        vr[j] = reinterpret_cast<const float2 *>(kv_row(v0, v1, p < S ? p : S - 1) + h * AHD)[lane];
+    }
+    for (uint32_t e = tid; e < nq * (AHD / 4); e += 256) {
+        const uint32_t qi = e / (AHD / 4), t = qi / G, hq = h * G + qi % G;
+        lq[qi][e % (AHD / 4)] = reinterpret_cast<const float4 *>(q + (uint64_t)t * n_q * AHD + hq * AHD)[e % (AHD / 4)];
+    }
+    __syncthreads();
+    // scores of position pk for every query
+    for (uint32_t qi = 0; qi < nq; qi++) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 qv = lq[qi][8 * qd + i];
+            d = __builtin_fmaf(kr[i].x, qv.x, __builtin_fmaf(kr[i].y, qv.y,
+                __builtin_fmaf(kr[i].z, qv.z, __builtin_fmaf(kr[i].w, qv.w, d))));
+        }
+        d = lane_add_x32(lane_add_x16(d));  // the four quarters
+        const uint32_t qpos = qpos0 + qi / G;
+        const bool ok = pk < S && (!causal || pk <= qpos);
+        if (qd == 0) lp[qi][16 * wave + (lane & 15u)] = ok ? d * scale : -INFINITY;
+    }
+    __syncthreads();
+    // softmax over the chunk: wave w, queries w and w + 4
+    for (uint32_t qi = wave; qi < nq; qi += 4) {
+        const float sv = lp[qi][lane];
+        float m = sv;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float mu = m == -INFINITY ? 0.0f : m;  // a fully masked chunk has P = 0
+        const float pv = expf(sv - mu);
+        lp[qi][lane] = pv;
+        const float l = wave_sum(pv);
+        if (lane == 0) {
+            const uint64_t pi = ((uint64_t)h * nch + c) * AQ + qi;
+            part_ml[2 * pi] = m;
+            part_ml[2 * pi + 1] = l;
+        }
+    }
+    __syncthreads();
+    // P V over this wave's 16 positions, every query
+    for (uint32_t qi = 0; qi < nq; qi++) {
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float pw = lp[qi][16 * wave + j];
+            o0 = __builtin_fmaf(pw, vr[j].x, o0);
+            o1 = __builtin_fmaf(pw, vr[j].y, o1);
+        }
+        lo[wave][qi][2 * lane] = o0;
+        lo[wave][qi][2 * lane + 1] = o1;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < nq * AHD; e += 256) {
+        const uint32_t qi = e / AHD, d = e % AHD;
+        const uint64_t pi = ((uint64_t)h * nch + c) * AQ + qi;
+        part_o[pi * AHD + d] = ((lo[0][qi][d] + lo[1][qi][d]) + lo[2][qi][d]) + lo[3][qi][d];
+    }
+}
+
 // The block's own positions (the `tail`, at most ATAIL, after the n0 context
 // positions that the chunk kernel covers) are attended here, in f32: wave w takes
 // tail positions 16w .. 16w+15 and forms a partial like a chunk's.
@@ -579,15 +678,16 @@ constexpr uint32_t ATAIL = 64;
 // query: wave w takes the w-th quarter of the chunks (their partials loaded CB at a
 // time, all in flight together), then its part of the tail; the quarters meet in
 // LDS, added in wave order.  With `gate` ([rows][n_q]), the result of head hq of
-// row t is then multiplied by softplus(gate[t][hq]) (the forward's attention gate,
-// src/dflash.rs:956-959).
+// row t is then multiplied by softplus(gate[t][hq]) (gmode 1: the draft forward's
+// attention gate, src/dflash.rs:956-959; gmode 2: kernels/gate_attn.comp:27, the
+// target's, log(1 + exp(g)) with no threshold).
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
                                                       const float *__restrict__ part_ml, float *__restrict__ out,
                                                       uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch,
                                                       const float *__restrict__ gate, const float *__restrict__ q,
                                                       const float *__restrict__ k1, const float *__restrict__ v1,
                                                       uint32_t T, uint32_t n0, uint32_t qpos0, int causal,
-                                                      float scale) {
+                                                      float scale, int gmode) {
     constexpr uint32_t CB = 8, TW = ATAIL / 4;
     __shared__ float sm[4], sl[4], so[4][AHD];
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -680,7 +780,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     if (gate) {
-        const float g = softplus_gate(gate[(uint64_t)t * n_q + hq]);
+        const float gv = gate[(uint64_t)t * n_q + hq];
+        const float g = gmode == 2 ? logf(1.0f + expf(gv)) : softplus_gate(gv);
         o[lane] = (o0 * inv) * g;
         o[64 + lane] = (o1 * inv) * g;
     } else {
@@ -805,6 +906,8 @@ int run_qk_norm_rope(const QkJob &a, const QkJob &b, const float *freq, uint32_t
     return after_launch("qk_norm_rope", s);
 }
 
+bool aligned16_ptr(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
     const uint32_t nch = (S + ACH - 1) / ACH;
     return (size_t)n_kv * nch * AQ * (AHD + 2);
@@ -814,7 +917,7 @@ size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
 // With `gate` ([rows][n_q]) each head's result is multiplied by softplus of its gate.
 int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0, const float *k1, const float *v1,
                   uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t qpos0, int causal,
-                  float *out, float *part, hipStream_t s, const float *gate = nullptr) {
+                  float *out, float *part, hipStream_t s, const float *gate = nullptr, int gmode = 1) {
     const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
     const uint32_t G = n_q / n_kv;
     if (part && hd == AHD && rows * G <= AQ) {
@@ -824,13 +927,18 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
         const uint32_t T = k1 && S > n0 && S - n0 <= ATAIL ? S - n0 : 0;
         const uint32_t Sc = T ? n0 : S, nch = (Sc + ACH - 1) / ACH;
         float *part_ml = part + (size_t)n_kv * nch * AQ * AHD;
-        if (nch) {
+        if (nch && rows * G <= ADQ && aligned16_ptr(q) && aligned16_ptr(k0) && aligned16_ptr(v0) &&
+            (!k1 || (aligned16_ptr(k1) && aligned16_ptr(v1)))) {
+            hipLaunchKernelGGL(k_attn_decode, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, Sc,
+                               rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
+            LG_TRY(after_launch("attn_decode", s));
+        } else if (nch) {
             hipLaunchKernelGGL(k_attn_chunk, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, Sc,
                                rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
             LG_TRY(after_launch("attn_chunk", s));
         }
         hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, part, part_ml, out, rows, n_q,
-                           n_kv, nch, gate, q, k1, v1, T, n0, qpos0, causal, scale);
+                           n_kv, nch, gate, q, k1, v1, T, n0, qpos0, causal, scale, gmode);
         return after_launch("attn_combine", s);
     }
     hipLaunchKernelGGL(k_attn_simple, dim3((rows * n_q + 3) / 4), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S, rows,
@@ -838,7 +946,7 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
     LG_TRY(after_launch("attn_simple", s));
     if (!gate) return LG_OK;
     const uint64_t total = (uint64_t)rows * n_q * hd;
-    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, out, gate, out, n_q, hd, total, 1);
+    hipLaunchKernelGGL(k_gate_mul, dim3(blocks_for(total)), dim3(256), 0, s, out, gate, out, n_q, hd, total, gmode);
     return after_launch("softplus_gate_mul", s);
 }
 
@@ -1018,7 +1126,7 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
 // Whether every norm but the output norm can fold into the products around it: all
 // eight projections of every layer on the matrix-core path, rows of a width the fan
 // kernels take, and per-token partial-sum counts within what the consumers load.
-std::atomic<uint32_t> g_fold_norms{1};  // lg_set_draft_norms
+std::atomic<uint32_t> g_fold_norms{1};  // lg_set_fold_norms
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -1271,11 +1379,19 @@ int glue_qk_norm_rope(const float *x, const float *w, float *out, uint32_t n_hea
     return run_qk_norm_rope(qk_job(x, w, out, n_heads, pos, 1), QkJob{}, freq, head_dim, rope_dim, eps, s);
 }
 
+int glue_qk_norm_rope2(const float *q, const float *wq, float *q_out, uint32_t n_q, const float *k, const float *wk,
+                       float *k_out, uint32_t n_kv, uint32_t head_dim, uint32_t rope_dim, uint32_t pos,
+                       const float *freq, float eps, hipStream_t s) {
+    return run_qk_norm_rope(qk_job(q, wq, q_out, n_q, pos, 1), qk_job(k, wk, k_out, n_kv, pos, 1), freq, head_dim,
+                            rope_dim, eps, s);
+}
+
 uint64_t glue_attn_partial_bytes(uint32_t seq_len, uint32_t n_kv) { return attn_partial_floats(seq_len, n_kv) * 4; }
 
 int glue_attention(const float *q, const float *k, const float *v, uint32_t seq_len, uint32_t q_pos, uint32_t n_q,
-                   uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s) {
-    return run_attention(q, k, v, seq_len, nullptr, nullptr, seq_len, 1, n_q, n_kv, head_dim, q_pos, 1, out, part, s);
+                   uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s, const float *gate) {
+    return run_attention(q, k, v, seq_len, nullptr, nullptr, seq_len, 1, n_q, n_kv, head_dim, q_pos, 1, out, part, s,
+                         gate, 2);
 }
 
 int glue_gate_attn(const float *attn, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
@@ -1522,10 +1638,14 @@ int lg_dflash_graph_destroy(void *graph) {
 
 }  // extern "C"
 
-// The draft forward's attention and FFN norms folded into the products around them
-// (1, the default, where the model allows it) or run as their own launches (0): a
-// switch for A/B measurement; both meet the same parity bound.
-extern "C" int lg_set_draft_norms(uint32_t folded) {
+namespace lg {
+bool fold_norms() { return g_fold_norms.load(std::memory_order_relaxed) != 0; }
+}  // namespace lg
+
+// The forwards' RMSNorms (and the target's residual adds) folded into the products
+// around them (1, the default, where the model allows it) or run as their own
+// launches (0): a switch for A/B measurement; both meet the same parity bound.
+extern "C" int lg_set_fold_norms(uint32_t folded) {
     g_fold_norms.store(folded ? 1u : 0u, std::memory_order_relaxed);
     return LG_OK;
 }

@@ -163,16 +163,44 @@ uint32_t proj_batch_rs_cols_max(uint32_t m);
 // matrix-core path, which the folded norm needs.
 bool proj_batch_mfma_ok(int w_dtype, uint32_t k, const void *w);
 
+// A dense layer's input on the M = 1 integer-dot path: the activations are
+// RMSNorm(x + xadd) (xadd, nw may be null: no add, no norm) and up to four Q4_K
+// products over them run as one launch, job j writing y[j][0..n[j]).  The first
+// workgroup also writes x + xadd to xout and xcap, and the normed activations to
+// nxout (each may be null); xout must not alias x or xadd.  k <= 4096, a multiple of
+// 256; 16-byte aligned operands (proj_m1_in_ok says whether the call qualifies).
+struct M1In {
+    const void *w[4] = {};
+    int type[4] = {};
+    float *y[4] = {};
+    uint32_t n[4] = {};
+    uint32_t count = 0;
+    const float *xadd = nullptr, *nw = nullptr;
+    float eps = 0.0f;
+    float *xout = nullptr, *xcap = nullptr, *nxout = nullptr;
+};
+bool proj_m1_in_ok(uint32_t k, const float *x, const M1In &in);
+// lg_set_fold_norms: whether the forwards fold their norms into the products.
+bool fold_norms();
+int proj_m1_in(const float *x, const M1In &in, uint32_t k, hipStream_t s);
+
 // ---- launchers of the draft's glue kernels, used by the target forward (one row each;
 // in place allowed where the kernels allow it: rmsnorm, qk_norm_rope, gate_attn, add)
 int glue_rmsnorm(const float *x, const float *w, float *out, uint32_t n, uint32_t rows, float eps, hipStream_t s);
 int glue_qk_norm_rope(const float *x, const float *w, float *out, uint32_t n_heads, uint32_t head_dim,
                       uint32_t rope_dim, uint32_t pos, const float *freq, float eps, hipStream_t s);
+// Q (n_q heads) and K (n_kv heads) of one row in one launch.
+int glue_qk_norm_rope2(const float *q, const float *wq, float *q_out, uint32_t n_q, const float *k, const float *wk,
+                       float *k_out, uint32_t n_kv, uint32_t head_dim, uint32_t rope_dim, uint32_t pos,
+                       const float *freq, float eps, hipStream_t s);
 // Causal attention of one query row at q_pos over seq_len keys/values; `part` holds
-// glue_attn_partial_bytes(seq_len, n_kv) bytes (or is null: the plain kernel).
+// glue_attn_partial_bytes(seq_len, n_kv) bytes (or is null: the plain kernel).  With
+// `gate` ([n_q]) each head's result is multiplied by log(1 + exp(gate[h]))
+// (kernels/gate_attn.comp).
 uint64_t glue_attn_partial_bytes(uint32_t seq_len, uint32_t n_kv);
 int glue_attention(const float *q, const float *k, const float *v, uint32_t seq_len, uint32_t q_pos, uint32_t n_q,
-                   uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s);
+                   uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s,
+                   const float *gate = nullptr);
 int glue_gate_attn(const float *attn, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
                    hipStream_t s);
 int glue_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);

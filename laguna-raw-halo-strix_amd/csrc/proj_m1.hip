@@ -922,12 +922,36 @@ __device__ __forceinline__ void dig_read(const DigLds &dg, uint32_t p, uint32_t 
 // x once into an LDS table of 48 digit dwords per group, each lane keeps its group's
 // 48 dwords in registers, and the waves stride over rows R at a time with the next
 // rows' loads in flight while the current rows are reduced.
-template <int TEAMS, int R>
-__global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restrict__ x, const uint8_t *__restrict__ w,
-                                                            float *__restrict__ y, uint32_t k, uint32_t n,
-                                                            uint64_t row_bytes) {
+//
+// IN (a layer's input, k_q4k_m1_dig_in): the activations are the RMSNorm of x + xadd
+// (src/target.rs:426-437, 526-532: the residual add, then the norm), each workgroup
+// computing the norm's sum of squares from its own staged copy, and up to four
+// products over them run as one launch (virtual rows off[j] .. off[j+1]-1 are job j's
+// rows; jobs past the count start at n).  Workgroup 0 also writes x + xadd (the
+// residual stream) and the normed activations where asked.  Job j's weights and
+// outputs are addressed as offsets from job 0's (wofs bytes, yofs elements), each
+// pointer a kernel argument of its own: a pointer read from a structure, or selected
+// among several, has no known address space, and its loads become flat loads whose
+// waits also wait for the LDS traffic.
+struct DigIn {
+    const float *xadd;  // null: the activations are x
+    const float *nw;    // null: no norm
+    float *xout, *xcap;  // x + xadd, written by workgroup 0 (each may be null)
+    float *nxout;        // the normed activations, written by workgroup 0 (may be null)
+    const uint8_t *w0;
+    float *y0;
+    int64_t wofs[4], yofs[4];
+    uint32_t off[4];
+    float eps;
+};
+
+template <int TEAMS, int R, bool IN>
+__device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, const uint8_t *__restrict__ w,
+                                                float *__restrict__ y, uint32_t k, uint32_t n, uint64_t row_bytes,
+                                                const DigIn &in) {
     static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
     __shared__ __attribute__((aligned(16))) DigLds dg;
+    __shared__ float ssq[IN ? TEAMS : 1];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, team = tid >> 6;
     const uint32_t P = k >> 6;
     const bool active = lane < P;
@@ -936,24 +960,88 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     const uint32_t lane_off = (p >> 2) * Q4K_BYTES;
     const uint32_t stride = gridDim.x * TEAMS * R;
 
-    float4 xv[4];
+    float4 xv[4], av[4], nwv[4];
     dig_load_x(x, k, xv);
-    // the first rows' weights are in flight while x is converted
-    uint32_t r0 = (blockIdx.x * TEAMS + team) * R;
+    if constexpr (IN) {
+        if (in.xadd) dig_load_x(in.xadd, k, av);
+        if (in.nw) dig_load_x(in.nw, k, nwv);
+    }
+    // IN: the job of virtual row `row` (jobs past the count start at n), selected
+    // among values held in scalar registers: a dynamically indexed read of the
+    // argument block would put a scalar load before every row's weight loads
+    auto job = [&](uint32_t row, const uint8_t *&wj, float *&yj, uint32_t &lr) {
+        int64_t wo = 0, yo = 0;
+        lr = row;
+#pragma unroll
+        for (int i = 1; i < 4; i++)
+            if (row >= in.off[i]) wo = in.wofs[i], yo = in.yofs[i], lr = row - in.off[i];
+        wj = in.w0 + wo;
+        yj = in.y0 + yo;
+    };
+    // the first rows' weights are in flight while x is converted.  The wave's rows are
+    // held in scalar registers (they are uniform over the wave): row addresses (and,
+    // IN, each row's job) cost scalar instructions (8.68 -> 8.47 us on 4096 -> 14336)
+    uint32_t r0 = __builtin_amdgcn_readfirstlane((blockIdx.x * TEAMS + team) * R);
     uint4 hd[2][R], qa[2][R], qb[2][R];
     auto load = [&](int b, uint32_t rr) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t row = min(rr + r, n - 1u);  // rows past n re-read row n-1 and are not stored
-            const uint8_t *blk = w + (uint64_t)row * row_bytes + lane_off;
+            const uint8_t *blk;
+            if constexpr (IN) {
+                const uint8_t *wj;
+                float *yj;
+                uint32_t lr;
+                job(row, wj, yj, lr);
+                blk = wj + (uint64_t)lr * row_bytes + lane_off;
+            } else {
+                blk = w + (uint64_t)row * row_bytes + lane_off;
+            }
             hd[b][r] = *reinterpret_cast<const uint4 *>(blk);
             qa[b][r] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * L.g);
             qb[b][r] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * L.g);
         }
     };
     load(0, r0);
+    float rs = 1.0f;  // IN: the norm's 1 / rms
+    if constexpr (IN) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (in.xadd)
+                xv[j] = make_float4(xv[j].x + av[j].x, xv[j].y + av[j].y, xv[j].z + av[j].z, xv[j].w + av[j].w);
+            const bool live = 4 * tid + j < k / 4;
+            if (live && blockIdx.x == 0) {
+                if (in.xout) reinterpret_cast<float4 *>(in.xout)[4 * tid + j] = xv[j];
+                if (in.xcap) reinterpret_cast<float4 *>(in.xcap)[4 * tid + j] = xv[j];
+            }
+            if (live)
+                sq = __builtin_fmaf(xv[j].x, xv[j].x, __builtin_fmaf(xv[j].y, xv[j].y,
+                     __builtin_fmaf(xv[j].z, xv[j].z, __builtin_fmaf(xv[j].w, xv[j].w, sq))));
+        }
+        if (in.nw) {
+            sq = wave_sum(sq);
+            if (lane == 0) ssq[team] = sq;
+        }
+    }
     if (tid == 0) dg.bad = 0u;
     __syncthreads();
+    if constexpr (IN) {
+        if (in.nw) {  // kernels/rmsnorm.comp:23-34: x w / sqrt(mean(x^2) + eps)
+            float t = 0.0f;
+#pragma unroll
+            for (int i = 0; i < TEAMS; i++) t += ssq[i];
+            rs = 1.0f / sqrtf(t / (float)k + in.eps);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                xv[j] = make_float4(xv[j].x * nwv[j].x * rs, xv[j].y * nwv[j].y * rs, xv[j].z * nwv[j].z * rs,
+                                    xv[j].w * nwv[j].w * rs);
+        }
+        if (in.nxout && blockIdx.x == 0)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (4 * tid + j < k / 4) reinterpret_cast<float4 *>(in.nxout)[4 * tid + j] = xv[j];
+    }
     dig_convert(xv, k, dg);
     __syncthreads();
     uint32_t D[48];
@@ -962,9 +1050,23 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     if (dg.bad) {  // the reference's per-element loop (kernels/proj_q4k.comp:60-75)
         for (uint32_t rr = blockIdx.x * TEAMS + team; rr < n; rr += gridDim.x * TEAMS) {
             float a = 0.0f;
-            for (uint32_t j = lane; j < k; j += 64) a = __builtin_fmaf(x[j], q4k_elem(w, (uint64_t)rr * k + j), a);
-            a = wave_sum(a);
-            if (lane == 0) y[rr] = a;
+            if constexpr (IN) {
+                const uint8_t *wj;
+                float *yj;
+                uint32_t lr;
+                job(rr, wj, yj, lr);
+                for (uint32_t j = lane; j < k; j += 64) {
+                    float xj = in.xadd ? x[j] + in.xadd[j] : x[j];
+                    if (in.nw) xj = xj * in.nw[j] * rs;
+                    a = __builtin_fmaf(xj, q4k_elem(wj, (uint64_t)lr * k + j), a);
+                }
+                a = wave_sum(a);
+                if (lane == 0) yj[lr] = a;
+            } else {
+                for (uint32_t j = lane; j < k; j += 64) a = __builtin_fmaf(x[j], q4k_elem(w, (uint64_t)rr * k + j), a);
+                a = wave_sum(a);
+                if (lane == 0) y[rr] = a;
+            }
         }
         return;
     }
@@ -1000,7 +1102,17 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
         for (int r = 0; r < R; r++) {
             float v = dotrow(hd[b][r], qa[b][r], qb[b][r]);
             v = wave_sum(active ? v : 0.0f);
-            if (lane == 0 && rr + r < n) y[rr + r] = v;
+            if (lane == 0 && rr + r < n) {
+                if constexpr (IN) {
+                    const uint8_t *wj;
+                    float *yj;
+                    uint32_t lr;
+                    job(rr + r, wj, yj, lr);
+                    yj[lr] = v;
+                } else {
+                    y[rr + r] = v;
+                }
+            }
         }
     };
     for (;;) {  // every wave leaves once its next rows start at or past n
@@ -1020,6 +1132,24 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
         reduce(1, r1);
         r0 = r2;
     }
+}
+
+template <int TEAMS, int R>
+__global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restrict__ x, const uint8_t *__restrict__ w,
+                                                            float *__restrict__ y, uint32_t k, uint32_t n,
+                                                            uint64_t row_bytes) {
+    q4k_m1_dig_body<TEAMS, R, false>(x, w, y, k, n, row_bytes, DigIn{});
+}
+
+template <int TEAMS, int R>
+__global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig_in(
+    const float *__restrict__ x, const float *xadd, const float *__restrict__ nw, float *xout, float *xcap,
+    float *nxout, const uint8_t *__restrict__ w0, float *y0, int64_t wo1, int64_t wo2, int64_t wo3, int64_t yo1,
+    int64_t yo2, int64_t yo3, uint32_t off1, uint32_t off2, uint32_t off3, uint32_t n, float eps, uint32_t k,
+    uint64_t row_bytes) {
+    const DigIn in{xadd, nw, xout, xcap, nxout, w0, y0, {0, wo1, wo2, wo3}, {0, yo1, yo2, yo3}, {0u, off1, off2, off3},
+                   eps};
+    q4k_m1_dig_body<TEAMS, R, true>(x, nullptr, nullptr, k, n, row_bytes, in);
 }
 
 // Q8_0 with k <= 4096: the same digits against the raw int8 quants.  Lane p owns
@@ -1687,6 +1817,52 @@ int proj_quant(const float *x, const float *up, const void *w, float *c, uint32_
 }
 
 }  // namespace
+
+namespace lg {
+
+bool proj_m1_in_ok(uint32_t k, const float *x, const M1In &in) {
+    auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (k == 0 || k > 4096 || k % QK_K || in.count < 1 || in.count > 4 || !a16(x) || !a16(in.xadd) || !a16(in.nw) ||
+        !a16(in.xout) || !a16(in.xcap) || !a16(in.nxout))
+        return false;
+    for (uint32_t j = 0; j < in.count; j++)
+        if (in.type[j] != LG_Q4_K || !in.w[j] || !in.y[j] || !a16(in.w[j])) return false;
+    return true;
+}
+
+int proj_m1_in(const float *x, const M1In &in, uint32_t k, hipStream_t s) {
+    const char *name = "proj_q4k_m1_in";
+    LG_REQUIRE(proj_m1_in_ok(k, x, in), "%s: k=%u or its operands are outside the integer-dot path", name, k);
+    const uint8_t *w[4] = {};
+    float *y[4] = {};
+    uint32_t off[4] = {}, n = 0;
+    for (uint32_t j = 0; j < in.count; j++) {
+        w[j] = static_cast<const uint8_t *>(in.w[j]);
+        y[j] = in.y[j];
+        off[j] = n;
+        n += in.n[j];
+    }
+    for (uint32_t j = in.count; j < 4; j++) off[j] = n;  // past the count: never selected
+    if (n == 0) return LG_OK;
+    constexpr int TEAMS = 4, R = 2;
+    uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
+    const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed);
+    const uint32_t cap = gc ? gc : 512;
+    grid = grid < cap ? grid : cap;
+    int64_t wo[4] = {}, yo[4] = {};
+    for (uint32_t j = 1; j < in.count; j++) {  // byte and element offsets from job 0's
+        wo[j] = (int64_t)(reinterpret_cast<uintptr_t>(w[j]) - reinterpret_cast<uintptr_t>(w[0]));
+        yo[j] = (int64_t)(reinterpret_cast<uintptr_t>(y[j]) - reinterpret_cast<uintptr_t>(y[0])) / 4;
+        LG_REQUIRE(((reinterpret_cast<uintptr_t>(y[j]) - reinterpret_cast<uintptr_t>(y[0])) & 3u) == 0,
+                   "%s: output %u is not float-aligned with output 0", name, j);
+    }
+    hipLaunchKernelGGL((k_q4k_m1_dig_in<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, in.xadd, in.nw, in.xout,
+                       in.xcap, in.nxout, w[0], y[0], wo[1], wo[2], wo[3], yo[1], yo[2], yo[3], off[1], off[2], off[3],
+                       n, in.eps, k, (uint64_t)k / QK_K * Q4K_BYTES);
+    return after_launch(name, s);
+}
+
+}  // namespace lg
 
 extern "C" {
 

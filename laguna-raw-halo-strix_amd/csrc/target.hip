@@ -22,7 +22,7 @@ using namespace lg;
 constexpr uint32_t TABLE_FLOATS = 128;  // rope_dim <= head_dim <= 256
 
 struct TgtLayout {
-    float *x, *nx, *q, *k, *v, *att, *gate, *g, *u, *o, *freq, *freq_swa, *part;
+    float *x, *nx, *q, *k, *v, *att, *gate, *g, *u, *o, *freq, *freq_swa, *part, *x2;
     uint64_t total;
 };
 
@@ -37,12 +37,13 @@ uint64_t layout(const lg_target_model *md, uint32_t seq_len, uint8_t *base, TgtL
     const uint64_t E = hp.n_embd, H = max_q_dim(md), QD = H * hp.head_dim, KVD = (uint64_t)hp.n_kv_heads * hp.head_dim;
     const uint64_t FF = hp.n_ff;
     const uint64_t floats[] = {E, E, QD, KVD, KVD, QD, H, FF, FF, E, TABLE_FLOATS, TABLE_FLOATS,
-                               glue_attn_partial_bytes(seq_len, hp.n_kv_heads) / 4};
-    float **dst[] = {&L.x, &L.nx, &L.q, &L.k, &L.v, &L.att, &L.gate, &L.g, &L.u, &L.o, &L.freq, &L.freq_swa, &L.part};
+                               glue_attn_partial_bytes(seq_len, hp.n_kv_heads) / 4, E};
+    float **dst[] = {&L.x, &L.nx, &L.q, &L.k, &L.v, &L.att, &L.gate, &L.g, &L.u, &L.o, &L.freq, &L.freq_swa, &L.part,
+                     &L.x2};
     // the two RoPE tables first, at fixed offsets whatever seq_len is, so that an
     // uploaded table stays valid across calls
     uint64_t off = 0;
-    const int order[] = {10, 11, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 12};
+    const int order[] = {10, 11, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 13, 12};
     for (int i : order) {
         *dst[i] = reinterpret_cast<float *>(base + off);
         off += (floats[i] * 4 + 255) & ~(uint64_t)255;
@@ -133,27 +134,48 @@ int proj(const float *x, const void *w, int type, float *c, uint32_t k, uint32_t
     return lg_dispatch_proj_quant(x, w, c, k, n, type, s);
 }
 
-// TargetModel::forward_token_impl (src/target.rs:314-578) for a dense model.
-int forward(const lg_target_model *md, const TgtLayout &W, const float *input, const int32_t *slot, float *captured,
-            float *logits, float *hidden, lg_target_kv_cache *cache, hipStream_t s) {
+bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool q4k16(int type, const void *w) { return type == LG_Q4_K && a16(w); }
+
+// Whether the forward can build each layer's inputs inside its products
+// (forward_in): every attention and FFN input projection Q4_K on the M = 1
+// integer-dot path, 16-byte aligned activations, norms and outputs.
+bool inputs_foldable(const lg_target_model *md, const float *input, const float *captured, const float *hidden) {
+    const lg_target_hparams &hp = md->hp;
+    if (!fold_norms() || hp.n_embd > 4096 || hp.n_embd % QK_K || !a16(input) || !a16(captured) || !a16(hidden) ||
+        !a16(md->output_norm))
+        return false;
+    for (uint32_t l = 0; l < hp.n_layers; l++) {
+        const lg_target_layer &L = md->layers[l];
+        if (!q4k16(L.attn_q_type, L.attn_q) || !q4k16(L.attn_k_type, L.attn_k) || !q4k16(L.attn_v_type, L.attn_v) ||
+            (L.attn_gate && !q4k16(L.attn_gate_type, L.attn_gate)) || !q4k16(L.ffn_gate_type, L.ffn_gate) ||
+            !q4k16(L.ffn_up_type, L.ffn_up) || !a16(L.attn_norm) || !a16(L.ffn_norm))
+            return false;
+    }
+    return true;
+}
+
+// TargetModel::forward_token_impl with each layer's inputs built inside the M = 1
+// products that take them: the residual add (src/target.rs:526-532, 553-555) and the
+// RMSNorm (:426-437, :533-537) run in the launch of Q, K, V and the gate together,
+// and in the launch of the FFN's gate and up together (proj_m1_in), whose first
+// workgroup also writes the residual stream, alternating between two buffers.  The
+// LM head takes the last add and the output norm the same way when it is Q4_K.
+int forward_in(const lg_target_model *md, const TgtLayout &W, const float *input, const int32_t *slot,
+               float *captured, float *logits, float *hidden, lg_target_kv_cache *cache, hipStream_t s) {
     const lg_target_hparams &hp = md->hp;
     const uint32_t E = hp.n_embd, KV = hp.n_kv_heads, HD = hp.head_dim, FF = hp.n_ff, KVD = KV * HD;
     const uint32_t pos = cache ? cache->len : 0;
-    LG_TRY(glue_copy(input, W.x, E, s));
+    const float *cur = input;  // the residual stream, before the pending add
+    const float *add = nullptr;
+    float *bufs[2] = {W.x, W.x2};
+    uint32_t nb = 0;
     for (uint32_t li = 0; li < hp.n_layers; li++) {
         const lg_target_layer &L = md->layers[li];
         const uint32_t H = L.n_q_heads, QD = H * HD;
-        if (slot[li] >= 0) LG_TRY(glue_copy(W.x, captured + (uint64_t)slot[li] * E, E, s));
-        LG_TRY(glue_rmsnorm(W.x, L.attn_norm, W.nx, E, 1, hp.rms_eps, s));
-        LG_TRY(proj(W.nx, L.attn_q, L.attn_q_type, W.q, E, QD, s));
-        LG_TRY(proj(W.nx, L.attn_k, L.attn_k_type, W.k, E, KVD, s));
-        LG_TRY(proj(W.nx, L.attn_v, L.attn_v_type, W.v, E, KVD, s));
-        // src/target.rs:438-461: SWA layers (index % 4 != 0) rotate with the SWA table
-        const bool swa = hp.swa && li % 4 != 0;
+        const bool swa = hp.swa && li % 4 != 0;  // src/target.rs:438-461
         const float *freq = swa ? W.freq_swa : W.freq;
         const uint32_t rd = swa ? hp.rope_dim_swa : hp.rope_dim;
-        LG_TRY(glue_qk_norm_rope(W.q, L.attn_q_norm, W.q, H, HD, rd, pos, freq, hp.qk_eps, s));
-        // the normed, roped key goes straight to its cache slot; the value is cached as projected
         float *kdst = W.k, *vdst = W.v;
         const float *kseq = W.k, *vseq = W.v;
         uint32_t seq = 1;
@@ -164,15 +186,105 @@ int forward(const lg_target_model *md, const TgtLayout &W, const float *input, c
             kseq = cache->k + (uint64_t)li * cache->capacity * KVD;
             vseq = cache->v + (uint64_t)li * cache->capacity * KVD;
             seq = pos + 1;
-            LG_TRY(glue_copy(W.v, vdst, KVD, s));
         }
-        LG_TRY(glue_qk_norm_rope(W.k, L.attn_k_norm, kdst, KV, HD, rd, pos, freq, hp.qk_eps, s));
+        // the state entering the layer (captured here), normed: Q, K, V and the gate
+        M1In a;
+        a.w[0] = L.attn_q, a.type[0] = L.attn_q_type, a.y[0] = W.q, a.n[0] = QD;
+        a.w[1] = L.attn_k, a.type[1] = L.attn_k_type, a.y[1] = W.k, a.n[1] = KVD;
+        a.w[2] = L.attn_v, a.type[2] = L.attn_v_type, a.y[2] = vdst, a.n[2] = KVD;
+        a.count = 3;
+        if (L.attn_gate) {
+            a.w[3] = L.attn_gate, a.type[3] = L.attn_gate_type, a.y[3] = W.gate, a.n[3] = H;
+            a.count = 4;
+        }
+        a.xadd = add, a.nw = L.attn_norm, a.eps = hp.rms_eps;
+        a.xout = add ? bufs[nb] : nullptr;
+        a.xcap = slot[li] >= 0 ? captured + (uint64_t)slot[li] * E : nullptr;
+        LG_TRY(proj_m1_in(cur, a, E, s));
+        if (add) {
+            cur = bufs[nb];
+            nb ^= 1u;
+            add = nullptr;
+        }
+        LG_TRY(glue_qk_norm_rope2(W.q, L.attn_q_norm, W.q, H, W.k, L.attn_k_norm, kdst, KV, HD, rd, pos, freq,
+                                  hp.qk_eps, s));
+        LG_TRY(glue_attention(W.q, kseq, vseq, seq, seq - 1, H, KV, HD, W.att, W.part, s,
+                              L.attn_gate ? W.gate : nullptr));
+        LG_TRY(proj(W.att, L.attn_output, L.attn_output_type, W.o, QD, E, s));
+        // x + o_proj, normed: the FFN's gate and up
+        M1In f;
+        f.w[0] = L.ffn_gate, f.type[0] = L.ffn_gate_type, f.y[0] = W.g, f.n[0] = FF;
+        f.w[1] = L.ffn_up, f.type[1] = L.ffn_up_type, f.y[1] = W.u, f.n[1] = FF;
+        f.count = 2;
+        f.xadd = W.o, f.nw = L.ffn_norm, f.eps = hp.rms_eps, f.xout = bufs[nb];
+        LG_TRY(proj_m1_in(cur, f, E, s));
+        cur = bufs[nb];
+        nb ^= 1u;
+        if (L.ffn_down_type == LG_Q4_K) {  // silu(gate) * up inside the down projection
+            LG_TRY(lg_dispatch_silu_mul_proj_quant(W.g, W.u, L.ffn_down, W.o, FF, E, LG_Q4_K, s));
+        } else {
+            LG_TRY(lg_dispatch_activation(W.g, W.u, W.g, FF, s));
+            LG_TRY(proj(W.g, L.ffn_down, L.ffn_down_type, W.o, FF, E, s));
+        }
+        add = W.o;
+    }
+    float *fcap = slot[hp.n_layers] >= 0 ? captured + (uint64_t)slot[hp.n_layers] * E : nullptr;
+    if (md->output && q4k16(md->output_type, md->output)) {  // src/target.rs:558-577 in one launch
+        M1In o;
+        o.w[0] = md->output, o.type[0] = md->output_type, o.y[0] = logits, o.n[0] = hp.n_vocab;
+        o.count = 1;
+        o.xadd = add, o.nw = md->output_norm, o.eps = hp.rms_eps, o.xcap = fcap, o.nxout = hidden;
+        return proj_m1_in(cur, o, E, s);
+    }
+    LG_TRY(glue_add(cur, add, W.x, E, s));
+    if (fcap) LG_TRY(glue_copy(W.x, fcap, E, s));
+    if (md->output_norm) LG_TRY(glue_rmsnorm(W.x, md->output_norm, W.x, E, 1, hp.rms_eps, s));
+    if (hidden) LG_TRY(glue_copy(W.x, hidden, E, s));
+    if (md->output) return proj(W.x, md->output, md->output_type, logits, E, hp.n_vocab, s);
+    return glue_copy(W.x, logits, E, s);
+}
+
+// TargetModel::forward_token_impl (src/target.rs:314-578) for a dense model.
+int forward(const lg_target_model *md, const TgtLayout &W, const float *input, const int32_t *slot, float *captured,
+            float *logits, float *hidden, lg_target_kv_cache *cache, hipStream_t s) {
+    const lg_target_hparams &hp = md->hp;
+    const uint32_t E = hp.n_embd, KV = hp.n_kv_heads, HD = hp.head_dim, FF = hp.n_ff, KVD = KV * HD;
+    const uint32_t pos = cache ? cache->len : 0;
+    if (inputs_foldable(md, input, captured, hidden))
+        return forward_in(md, W, input, slot, captured, logits, hidden, cache, s);
+    LG_TRY(glue_copy(input, W.x, E, s));
+    for (uint32_t li = 0; li < hp.n_layers; li++) {
+        const lg_target_layer &L = md->layers[li];
+        const uint32_t H = L.n_q_heads, QD = H * HD;
+        if (slot[li] >= 0) LG_TRY(glue_copy(W.x, captured + (uint64_t)slot[li] * E, E, s));
+        LG_TRY(glue_rmsnorm(W.x, L.attn_norm, W.nx, E, 1, hp.rms_eps, s));
+        // src/target.rs:438-461: SWA layers (index % 4 != 0) rotate with the SWA table
+        const bool swa = hp.swa && li % 4 != 0;
+        const float *freq = swa ? W.freq_swa : W.freq;
+        const uint32_t rd = swa ? hp.rope_dim_swa : hp.rope_dim;
+        // the normed, roped key goes straight to its cache slot, and so does the value
+        // as projected
+        float *kdst = W.k, *vdst = W.v;
+        const float *kseq = W.k, *vseq = W.v;
+        uint32_t seq = 1;
+        if (cache) {
+            const uint64_t slot_off = ((uint64_t)li * cache->capacity + pos) * KVD;
+            kdst = cache->k + slot_off;
+            vdst = cache->v + slot_off;
+            kseq = cache->k + (uint64_t)li * cache->capacity * KVD;
+            vseq = cache->v + (uint64_t)li * cache->capacity * KVD;
+            seq = pos + 1;
+        }
+        LG_TRY(proj(W.nx, L.attn_q, L.attn_q_type, W.q, E, QD, s));
+        LG_TRY(proj(W.nx, L.attn_k, L.attn_k_type, W.k, E, KVD, s));
+        LG_TRY(proj(W.nx, L.attn_v, L.attn_v_type, vdst, E, KVD, s));
+        // src/target.rs:496-507: the gate, applied to each head inside the attention
+        if (L.attn_gate) LG_TRY(proj(W.nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, s));
+        LG_TRY(glue_qk_norm_rope2(W.q, L.attn_q_norm, W.q, H, W.k, L.attn_k_norm, kdst, KV, HD, rd, pos, freq,
+                                  hp.qk_eps, s));
         // src/target.rs:466-494: one position (no cache: the token itself) or the cached sequence
-        LG_TRY(glue_attention(W.q, kseq, vseq, seq, seq - 1, H, KV, HD, W.att, W.part, s));
-        if (L.attn_gate) {  // src/target.rs:496-507
-            LG_TRY(proj(W.nx, L.attn_gate, L.attn_gate_type, W.gate, E, H, s));
-            LG_TRY(glue_gate_attn(W.att, W.gate, W.att, H, HD, s));
-        }
+        LG_TRY(glue_attention(W.q, kseq, vseq, seq, seq - 1, H, KV, HD, W.att, W.part, s,
+                              L.attn_gate ? W.gate : nullptr));
         LG_TRY(proj(W.att, L.attn_output, L.attn_output_type, W.o, QD, E, s));
         LG_TRY(glue_add(W.x, W.o, W.x, E, s));
         LG_TRY(glue_rmsnorm(W.x, L.ffn_norm, W.nx, E, 1, hp.rms_eps, s));

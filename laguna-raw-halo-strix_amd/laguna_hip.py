@@ -102,7 +102,7 @@ SIGNATURES = {
     "lg_set_m1_grid_cap": (_i, [_u32]),
     "lg_set_m1_split": (_i, [_u32]),
     "lg_set_m1_kernel": (_i, [_u32]),
-    "lg_set_draft_norms": (_i, [_u32]),
+    "lg_set_fold_norms": (_i, [_u32]),
     "lg_set_batch_shape": (_i, [_u32, _u32]),
     # ceiling kernels for measurement (no counterpart in the reference)
     "lg_bench_empty": (_i, [_u32, _vp]),

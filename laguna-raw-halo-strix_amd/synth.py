@@ -85,6 +85,23 @@ def random_q4k(seed, n_blocks, dlo=1e-4, dhi=4e-3):
     return out.ravel()
 
 
+def centered_q4k(seed, n_blocks, sigma=0.02):
+    """n_blocks Q4_K super-blocks of zero-mean weights with standard deviation near
+    sigma, fast (numpy's PCG64, not SplitMix64: bulk data for benchmarks): random
+    nibbles q, every sub-block's scale 2 and min 15 (so w =
+    d (2q - 15), zero-mean over q in 0..15, standard deviation 9.2 d), and d = dmin
+    drawn per block uniform in [0.75, 1.25] sigma / 9.2."""
+    rng = np.random.Generator(np.random.PCG64(seed))  # bulk bytes at memory speed
+    out = rng.bit_generator.random_raw(n_blocks * Q4_K_BYTES // 8).view(np.uint8).reshape(n_blocks, Q4_K_BYTES)
+    d = ((0.75 + 0.5 * rng.random(n_blocks)) * sigma / 9.2).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+    out[:, 2:4] = d.view(np.uint8).reshape(n_blocks, 2)
+    # 6-bit (scale, min) pairs of the 8 sub-blocks: bytes 4-7 the scales of 0-3,
+    # 8-11 the mins of 0-3, 12-15 the low nibbles of 4-7's scale and min
+    out[:, 4:16] = np.array([2] * 4 + [15] * 4 + [2 | (15 << 4)] * 4, np.uint8)
+    return out.ravel()
+
+
 def q8_0_weight(seed, k, n, sigma=0.02):
     """[n rows][k] weight, GGUF layout (k contiguous per output row), as Q8_0 bytes."""
     return quantize_q8_0(normal(seed, k * n, sigma))

@@ -102,6 +102,13 @@ ATTN_CASES = [
     (8, 8, 128, 7, 200, 150, 1),       # no grouping
     (4, 1, 128, 16, 97, 80, 1),        # G = 4, one kv head
     (4, 2, 128, 16, 150, 120, 1),      # G = 2
+    # rows*G <= 8 (one token's heads): the f32 decode partials
+    (32, 8, 128, 1, 2049, 2048, 1),    # the target's token over a 2048-position cache
+    (32, 8, 128, 1, 4100, 4099, 1),
+    (32, 8, 128, 2, 700, 690, 1),      # two rows of four heads
+    (16, 2, 128, 1, 130, 129, 1),      # G = 8
+    (32, 8, 128, 1, 100, 50, 0),       # non-causal, ragged chunk
+    (32, 8, 128, 3, 66, 40, 1),        # G = 4, rows 3: 12 queries, the matrix-core chunks
     (32, 8, 128, 32, 300, 250, 1),     # rows*G = 128 > 64: wavefront path
     (4, 2, 64, 3, 50, 40, 1),          # head_dim 64: wavefront path
     (2, 2, 256, 2, 33, 31, 1),
@@ -238,12 +245,12 @@ def test_forward_folded_norms_and_separate_norms(ctx, cfg, m, ctx_len, tol):
     want = dfo.forward_block(feat, tok, W, layers, kc, vc, ctx_len, cfg)
     try:
         for folded in (1, 0):
-            lh.check(lh.lib().lg_set_draft_norms(folded))
+            lh.check(lh.lib().lg_set_fold_norms(folded))
             y = model.forward_block(feat, tok)
             np.testing.assert_array_equal(y, model.forward_block(feat, tok))
             check(f"forward folded={folded}", y, want, tol)
     finally:
-        lh.check(lh.lib().lg_set_draft_norms(1))
+        lh.check(lh.lib().lg_set_fold_norms(1))
 
 
 @pytest.fixture(scope="module")
@@ -283,11 +290,11 @@ def test_forward_block_draft_full_size(ctx, draft_full):
     want = dfo.forward_block(feat, tok, W, layers, kc, vc, 2048, cfg)
     check("forward full", y, want, TOL_FWD)
     # the same with the attention and FFN norms as their own launches
-    lh.check(lh.lib().lg_set_draft_norms(0))
+    lh.check(lh.lib().lg_set_fold_norms(0))
     try:
         check("forward full, separate norms", model.forward_block(feat, tok), want, TOL_FWD)
     finally:
-        lh.check(lh.lib().lg_set_draft_norms(1))
+        lh.check(lh.lib().lg_set_fold_norms(1))
     model.free()
 
 

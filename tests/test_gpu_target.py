@@ -93,6 +93,45 @@ def test_forward_token_cached(ctx, swa):
     model.free()
 
 
+@pytest.mark.parametrize("cached", [False, True])
+def test_forward_token_folded_inputs_and_separate(ctx, cached):
+    # Each layer's residual adds and RMSNorms inside its Q4_K input projections (the
+    # default: Q, K, V and the gate in one launch, the FFN's gate and up in another, the
+    # LM head taking the last add and the output norm) and as their own launches (the
+    # switch off): both within TOL of the oracle for the logits and every captured
+    # state (each layer's input and the final state), and the normed final hidden of
+    # the two within TOL of each other.
+    cfg, hp = cfgs()
+    print(f"target forward, folded inputs against separate launches, cached={cached}", flush=True)
+    model, layers, ex = build(ctx, 0x7A20, cfg, gate_layers=[0, 3], n_q_heads=[4, 2, 4, 4])
+    idx = [0, 1, 2, 3, NL]
+    steps = 3 if cached else 1
+    hidden = {}
+    try:
+        for folded in (1, 0):
+            lh.check(lh.lib().lg_set_fold_norms(folded))
+            cache = lh.TargetKvCache(model, steps) if cached else None
+            ocache = tgo.KvCache(NL) if cached else None
+            hb, cb, lb = lh.GpuBuffer(ctx, 4 * E), lh.GpuBuffer(ctx, 4 * len(idx) * E), lh.GpuBuffer(ctx, 4 * V)
+            for t in range(steps):
+                x = synth.normal(0x7A21 + t, E)
+                xb = lh.upload_f32(ctx, x)
+                nc = model.forward_token_device(xb, idx, cb, lb, hidden=hb, cache=cache)
+                assert nc == len(idx)
+                got = (lb.read_f32(V).copy(), list(cb.read_f32(nc * E).reshape(nc, E).copy()))
+                want = tgo.forward_token(x, layers, hp, ex["output_norm"], ex["output"], ex["output_dtype"], idx,
+                                         ocache)
+                check_step(f"folded={folded} position {t}", got, want)
+                hidden[(folded, t)] = hb.read_f32(E).copy()
+            if cache is not None:
+                assert cache.len == steps
+                cache.free()
+    finally:
+        lh.check(lh.lib().lg_set_fold_norms(1))
+    for t in range(steps):
+        assert rel(hidden[(1, t)], hidden[(0, t)]) <= TOL
+
+
 def test_cache_full_is_an_error_and_leaves_len(ctx):
     cfg, _ = cfgs(n_layers=1)
     model, _, _ = build(ctx, 0x7A06, cfg)
