@@ -669,6 +669,135 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q
     }
 }
 
+// One token's attention over a cache (the dense target, src/target.rs:443-507):
+// QK-norm + NeoX RoPE of the token's query heads as each workgroup stages them, and of
+// its key (row S-1 of the K sequence, normed in place by the workgroup whose chunk
+// holds it, so the cache keeps it normed), then the chunk partials of k_attn_decode
+// for k_attn_combine.  The norms follow k_qk_norm_rope (one head per wavefront, lane d
+// holding dims d and d + 64).  Combining the chunks in the last workgroup of each kv
+// head to finish (an arrival counter) instead of a second launch measured slower
+// (440 against 413 us per target token): its loads of every chunk's partials sit on
+// the critical path.
+struct TokAttn {
+    const float *q;            // [n_q][128], as projected
+    const float *qn_w, *kn_w;  // QK-norm weights [128]
+    const float *freq;         // RoPE table (64 entries) when rope_dim is 128
+    uint32_t rope, pos;        // rope_dim is 128 (1) or 0; the token's position
+    float eps, scale;
+    float *k;                  // [S][n_kv][128]: rows below S-1 normed and roped, row S-1 as projected
+    const float *v;            // [S][n_kv][128]
+    uint32_t S, n_q, n_kv, nch;
+    float *part_o, *part_ml;   // per (kv head, chunk, query): as k_attn_chunk writes them
+};
+
+// The head at h (128 floats, lane d: dims d and d + 64) normed and rotated at `pos`.
+__device__ __forceinline__ void head_norm_rope(float &a, float &b, const float *__restrict__ w, const TokAttn &t,
+                                               uint32_t lane) {
+    float s = __builtin_fmaf(a, a, 0.0f);
+    s = __builtin_fmaf(b, b, s);
+    const float rms = 1.0f / sqrtf(wave_sum(s) / (float)AHD + t.eps);
+    const float n0 = a * w[lane] * rms, n1 = b * w[64 + lane] * rms;
+    if (!t.rope) {
+        a = n0, b = n1;
+        return;
+    }
+    const float ang = t.freq[lane] * (float)t.pos;
+    const float c = cosf(ang), sn = sinf(ang);
+    a = n0 * c - n1 * sn;
+    b = n1 * c + n0 * sn;
+}
+
+__global__ __launch_bounds__(256) void k_attn_token(TokAttn t) {
+    __shared__ float lq[ADQ][AHD];
+    __shared__ float lkn[AHD];
+    __shared__ float lp[ADQ][ACH];
+    __shared__ float lo[4][ADQ][AHD];
+    const uint32_t h = blockIdx.y, c = blockIdx.x;
+    const uint32_t G = t.n_q / t.n_kv, nq = G;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t kvld = t.n_kv * AHD, S = t.S, self = S - 1;
+    const bool owner = self / ACH == c;  // this chunk holds the token's own key
+    const uint32_t pk = c * ACH + 16 * wave + (lane & 15u), qd = lane >> 4;
+    float4 kr[8];
+    {
+        const float *kp = t.k + (uint64_t)(pk < S ? pk : S - 1) * kvld + h * AHD + 32 * qd;
+#pragma unroll
+        for (int i = 0; i < 8; i++) kr[i] = reinterpret_cast<const float4 *>(kp)[i];
+    }
+    float2 vr[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const uint32_t p = c * ACH + 16 * wave + j;
+        vr[j] = reinterpret_cast<const float2 *>(t.v + (uint64_t)(p < S ? p : S - 1) * kvld + h * AHD)[lane];
+    }
+    // the query heads of this kv head, and (owner) the token's key, normed and rotated
+    for (uint32_t qi = wave; qi < nq; qi += 4) {
+        const float *qp = t.q + (uint64_t)(h * G + qi) * AHD;
+        float a = qp[lane], b = qp[64 + lane];
+        head_norm_rope(a, b, t.qn_w, t, lane);
+        lq[qi][lane] = a;
+        lq[qi][64 + lane] = b;
+    }
+    if (owner && wave == 3) {
+        float *kp = t.k + (uint64_t)self * kvld + h * AHD;
+        float a = kp[lane], b = kp[64 + lane];
+        head_norm_rope(a, b, t.kn_w, t, lane);
+        lkn[lane] = a;
+        lkn[64 + lane] = b;
+        kp[lane] = a;  // the cache keeps the normed key (no other workgroup reads this row)
+        kp[64 + lane] = b;
+    }
+    __syncthreads();
+    if (owner && pk == self)
+#pragma unroll
+        for (int i = 0; i < 8; i++) kr[i] = reinterpret_cast<const float4 *>(lkn)[8 * qd + i];
+    // scores of position pk for every query (causal: every position up to the token's)
+    for (uint32_t qi = 0; qi < nq; qi++) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 qv = reinterpret_cast<const float4 *>(lq[qi])[8 * qd + i];
+            d = __builtin_fmaf(kr[i].x, qv.x, __builtin_fmaf(kr[i].y, qv.y,
+                __builtin_fmaf(kr[i].z, qv.z, __builtin_fmaf(kr[i].w, qv.w, d))));
+        }
+        d = lane_add_x32(lane_add_x16(d));
+        if (qd == 0) lp[qi][16 * wave + (lane & 15u)] = pk < S ? d * t.scale : -INFINITY;
+    }
+    __syncthreads();
+    const uint64_t pbase = ((uint64_t)h * t.nch + c) * AQ;
+    for (uint32_t qi = wave; qi < nq; qi += 4) {
+        const float sv = lp[qi][lane];
+        float m = sv;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float mu = m == -INFINITY ? 0.0f : m;
+        const float pv = expf(sv - mu);
+        lp[qi][lane] = pv;
+        const float l = wave_sum(pv);
+        if (lane == 0) {
+            t.part_ml[2 * (pbase + qi)] = m;
+            t.part_ml[2 * (pbase + qi) + 1] = l;
+        }
+    }
+    __syncthreads();
+    for (uint32_t qi = 0; qi < nq; qi++) {
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float pw = lp[qi][16 * wave + j];
+            o0 = __builtin_fmaf(pw, vr[j].x, o0);
+            o1 = __builtin_fmaf(pw, vr[j].y, o1);
+        }
+        lo[wave][qi][2 * lane] = o0;
+        lo[wave][qi][2 * lane + 1] = o1;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < nq * AHD; e += 256) {
+        const uint32_t qi = e / AHD, d = e % AHD;
+        t.part_o[(pbase + qi) * AHD + d] = ((lo[0][qi][d] + lo[1][qi][d]) + lo[2][qi][d]) + lo[3][qi][d];
+    }
+}
+
 // The block's own positions (the `tail`, at most ATAIL, after the n0 context
 // positions that the chunk kernel covers) are attended here, in f32: wave w takes
 // tail positions 16w .. 16w+15 and forms a partial like a chunk's.
@@ -1392,6 +1521,30 @@ int glue_attention(const float *q, const float *k, const float *v, uint32_t seq_
                    uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s, const float *gate) {
     return run_attention(q, k, v, seq_len, nullptr, nullptr, seq_len, 1, n_q, n_kv, head_dim, q_pos, 1, out, part, s,
                          gate, 2);
+}
+
+bool glue_attention_token_ok(uint32_t head_dim, uint32_t n_q, uint32_t n_kv, uint32_t rope_dim) {
+    return head_dim == AHD && n_kv && n_q % n_kv == 0 && n_q / n_kv <= ADQ && (rope_dim == 0 || rope_dim == AHD);
+}
+
+int glue_attention_token(const float *q, const float *qn_w, const float *kn_w, const float *freq, uint32_t rope_dim,
+                         uint32_t pos, float eps, float *k, const float *v, uint32_t seq_len, uint32_t n_q,
+                         uint32_t n_kv, uint32_t head_dim, const float *gate, float *out, float *part, hipStream_t s) {
+    LG_REQUIRE(glue_attention_token_ok(head_dim, n_q, n_kv, rope_dim) && seq_len && part &&
+                   aligned16_ptr(k) && aligned16_ptr(v),
+               "attention_token: shape (head_dim %u, %u / %u heads, rope_dim %u) or operands outside the kernel",
+               head_dim, n_q, n_kv, rope_dim);
+    TokAttn t{};
+    t.q = q, t.qn_w = qn_w, t.kn_w = kn_w, t.freq = freq, t.rope = rope_dim ? 1u : 0u, t.pos = pos, t.eps = eps;
+    t.scale = 1.0f / sqrtf((float)head_dim);  // src/dflash.rs:1173
+    t.k = k, t.v = v, t.S = seq_len, t.n_q = n_q, t.n_kv = n_kv, t.nch = (seq_len + ACH - 1) / ACH;
+    t.part_o = part;
+    t.part_ml = part + (size_t)n_kv * t.nch * AQ * AHD;
+    hipLaunchKernelGGL(k_attn_token, dim3(t.nch, n_kv), dim3(256), 0, s, t);
+    LG_TRY(after_launch("attention_token", s));
+    hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, t.part_o, t.part_ml, out, 1u, n_q, n_kv,
+                       t.nch, gate, q, nullptr, nullptr, 0u, 0u, 0u, 1, t.scale, 2);
+    return after_launch("attn_combine", s);
 }
 
 int glue_gate_attn(const float *attn, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,

@@ -201,6 +201,14 @@ uint64_t glue_attn_partial_bytes(uint32_t seq_len, uint32_t n_kv);
 int glue_attention(const float *q, const float *k, const float *v, uint32_t seq_len, uint32_t q_pos, uint32_t n_q,
                    uint32_t n_kv, uint32_t head_dim, float *out, float *part, hipStream_t s,
                    const float *gate = nullptr);
+// One token's attention step over seq_len keys/values: QK-norm + NeoX RoPE at `pos`
+// of the query heads and of key row seq_len - 1 (normed in place in k), the
+// attention, and the gate log(1 + exp(gate[h])) when gate is given.  `part` as for
+// glue_attention.
+bool glue_attention_token_ok(uint32_t head_dim, uint32_t n_q, uint32_t n_kv, uint32_t rope_dim);
+int glue_attention_token(const float *q, const float *qn_w, const float *kn_w, const float *freq, uint32_t rope_dim,
+                         uint32_t pos, float eps, float *k, const float *v, uint32_t seq_len, uint32_t n_q,
+                         uint32_t n_kv, uint32_t head_dim, const float *gate, float *out, float *part, hipStream_t s);
 int glue_gate_attn(const float *attn, const float *gate, float *out, uint32_t n_heads, uint32_t head_dim,
                    hipStream_t s);
 int glue_add(const float *a, const float *b, float *out, uint64_t n, hipStream_t s);

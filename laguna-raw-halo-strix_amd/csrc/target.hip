@@ -190,7 +190,10 @@ int forward_in(const lg_target_model *md, const TgtLayout &W, const float *input
         // the state entering the layer (captured here), normed: Q, K, V and the gate
         M1In a;
         a.w[0] = L.attn_q, a.type[0] = L.attn_q_type, a.y[0] = W.q, a.n[0] = QD;
-        a.w[1] = L.attn_k, a.type[1] = L.attn_k_type, a.y[1] = W.k, a.n[1] = KVD;
+        // with the one-token attention the key goes straight to its slot and is normed there
+        const bool tok = glue_attention_token_ok(HD, H, KV, rd) && (reinterpret_cast<uintptr_t>(kseq) & 15u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(vseq) & 15u) == 0;
+        a.w[1] = L.attn_k, a.type[1] = L.attn_k_type, a.y[1] = tok ? kdst : W.k, a.n[1] = KVD;
         a.w[2] = L.attn_v, a.type[2] = L.attn_v_type, a.y[2] = vdst, a.n[2] = KVD;
         a.count = 3;
         if (L.attn_gate) {
@@ -206,10 +209,16 @@ int forward_in(const lg_target_model *md, const TgtLayout &W, const float *input
             nb ^= 1u;
             add = nullptr;
         }
-        LG_TRY(glue_qk_norm_rope2(W.q, L.attn_q_norm, W.q, H, W.k, L.attn_k_norm, kdst, KV, HD, rd, pos, freq,
-                                  hp.qk_eps, s));
-        LG_TRY(glue_attention(W.q, kseq, vseq, seq, seq - 1, H, KV, HD, W.att, W.part, s,
-                              L.attn_gate ? W.gate : nullptr));
+        if (tok) {
+            LG_TRY(glue_attention_token(W.q, L.attn_q_norm, L.attn_k_norm, freq, rd, pos, hp.qk_eps,
+                                        kdst - (uint64_t)(seq - 1) * KVD, vseq, seq, H, KV, HD,
+                                        L.attn_gate ? W.gate : nullptr, W.att, W.part, s));
+        } else {
+            LG_TRY(glue_qk_norm_rope2(W.q, L.attn_q_norm, W.q, H, W.k, L.attn_k_norm, kdst, KV, HD, rd, pos, freq,
+                                      hp.qk_eps, s));
+            LG_TRY(glue_attention(W.q, kseq, vseq, seq, seq - 1, H, KV, HD, W.att, W.part, s,
+                                  L.attn_gate ? W.gate : nullptr));
+        }
         LG_TRY(proj(W.att, L.attn_output, L.attn_output_type, W.o, QD, E, s));
         // x + o_proj, normed: the FFN's gate and up
         M1In f;
