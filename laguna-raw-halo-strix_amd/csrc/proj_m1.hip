@@ -945,7 +945,7 @@ struct DigIn {
     float eps;
 };
 
-template <int TEAMS, int R, bool IN>
+template <int TEAMS, int R, bool IN, int NJ = 1>
 __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, const uint8_t *__restrict__ w,
                                                 float *__restrict__ y, uint32_t k, uint32_t n, uint64_t row_bytes,
                                                 const DigIn &in) {
@@ -971,10 +971,13 @@ __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, con
     // argument block would put a scalar load before every row's weight loads
     auto job = [&](uint32_t row, const uint8_t *&wj, float *&yj, uint32_t &lr) {
         int64_t wo = 0, yo = 0;
+        row = __builtin_amdgcn_readfirstlane(row);  // uniform over the wave: scalar selection
         lr = row;
+        if constexpr (NJ > 1) {
 #pragma unroll
-        for (int i = 1; i < 4; i++)
-            if (row >= in.off[i]) wo = in.wofs[i], yo = in.yofs[i], lr = row - in.off[i];
+            for (int i = 1; i < NJ; i++)
+                if (row >= in.off[i]) wo = in.wofs[i], yo = in.yofs[i], lr = row - in.off[i];
+        }
         wj = in.w0 + wo;
         yj = in.y0 + yo;
     };
@@ -1141,7 +1144,7 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     q4k_m1_dig_body<TEAMS, R, false>(x, w, y, k, n, row_bytes, DigIn{});
 }
 
-template <int TEAMS, int R>
+template <int TEAMS, int R, int NJ>
 __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig_in(
     const float *__restrict__ x, const float *xadd, const float *__restrict__ nw, float *xout, float *xcap,
     float *nxout, const uint8_t *__restrict__ w0, float *y0, int64_t wo1, int64_t wo2, int64_t wo3, int64_t yo1,
@@ -1149,7 +1152,7 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig_in(
     uint64_t row_bytes) {
     const DigIn in{xadd, nw, xout, xcap, nxout, w0, y0, {0, wo1, wo2, wo3}, {0, yo1, yo2, yo3}, {0u, off1, off2, off3},
                    eps};
-    q4k_m1_dig_body<TEAMS, R, true>(x, nullptr, nullptr, k, n, row_bytes, in);
+    q4k_m1_dig_body<TEAMS, R, true, NJ>(x, nullptr, nullptr, k, n, row_bytes, in);
 }
 
 // Q8_0 with k <= 4096: the same digits against the raw int8 quants.  Lane p owns
@@ -1856,9 +1859,14 @@ int proj_m1_in(const float *x, const M1In &in, uint32_t k, hipStream_t s) {
         LG_REQUIRE(((reinterpret_cast<uintptr_t>(y[j]) - reinterpret_cast<uintptr_t>(y[0])) & 3u) == 0,
                    "%s: output %u is not float-aligned with output 0", name, j);
     }
-    hipLaunchKernelGGL((k_q4k_m1_dig_in<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, in.xadd, in.nw, in.xout,
-                       in.xcap, in.nxout, w[0], y[0], wo[1], wo[2], wo[3], yo[1], yo[2], yo[3], off[1], off[2], off[3],
-                       n, in.eps, k, (uint64_t)k / QK_K * Q4K_BYTES);
+#define LG_DIG_IN(NJ)                                                                                        \
+    hipLaunchKernelGGL((k_q4k_m1_dig_in<TEAMS, R, NJ>), dim3(grid), dim3(TEAMS * 64), 0, s, x, in.xadd, in.nw, in.xout, \
+                       in.xcap, in.nxout, w[0], y[0], wo[1], wo[2], wo[3], yo[1], yo[2], yo[3], off[1], off[2], off[3], \
+                       n, in.eps, k, (uint64_t)k / QK_K * Q4K_BYTES)
+    if (in.count == 1) LG_DIG_IN(1);
+    else if (in.count == 2) LG_DIG_IN(2);
+    else LG_DIG_IN(4);
+#undef LG_DIG_IN
     return after_launch(name, s);
 }
 
