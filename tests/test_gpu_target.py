@@ -132,6 +132,34 @@ def test_forward_token_folded_inputs_and_separate(ctx, cached):
         assert rel(hidden[(1, t)], hidden[(0, t)]) <= TOL
 
 
+def test_forward_token_folded_inputs_element_fallback(ctx):
+    # Norm weights of 1e-30 over a whole 64-element group make that group's normed
+    # activations (its maximum included) fall below 2^-60, which the integer-dot digits
+    # cannot scale: the layer-input launches (and the LM head, through output_norm) take
+    # the per-element loop of the reference's shader, with the residual add and the norm
+    # applied per element.  Both paths meet TOL.
+    cfg, hp = cfgs(n_layers=2)
+    print("target forward, folded inputs on the per-element path", flush=True)
+    layers, ex = synth.target_model(0x7A30, cfg)
+    for L in layers:
+        for nm in ("attn_norm", "ffn_norm"):
+            L[nm] = L[nm].copy()
+            L[nm][64:128] = 1e-30
+    ex["output_norm"] = ex["output_norm"].copy()
+    ex["output_norm"][128:192] = 1e-30
+    model = lh.TargetModel(ctx, cfg, layers, output_norm=ex["output_norm"], output=ex["output"],
+                           output_dtype=ex["output_dtype"])
+    x = synth.normal(0x7A31, E)
+    want = tgo.forward_token(x, layers, hp, ex["output_norm"], ex["output"], ex["output_dtype"], [0, 1, 2])
+    try:
+        for folded in (1, 0):
+            lh.check(lh.lib().lg_set_fold_norms(folded))
+            check_step(f"tiny norm weights, folded={folded}", model.forward_token(x, [0, 1, 2]), want)
+    finally:
+        lh.check(lh.lib().lg_set_fold_norms(1))
+    model.free()
+
+
 def test_cache_full_is_an_error_and_leaves_len(ctx):
     cfg, _ = cfgs(n_layers=1)
     model, _, _ = build(ctx, 0x7A06, cfg)
