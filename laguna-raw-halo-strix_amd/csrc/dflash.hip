@@ -690,24 +690,25 @@ struct TokAttn {
     float *part_o, *part_ml;   // per (kv head, chunk, query): as k_attn_chunk writes them
 };
 
-// The head at h (128 floats, lane d: dims d and d + 64) normed and rotated at `pos`.
-__device__ __forceinline__ void head_norm_rope(float &a, float &b, const float *__restrict__ w, const TokAttn &t,
-                                               uint32_t lane) {
+// A head (128 floats, lane d: dims d and d + 64) normed with weights (w0, w1) and
+// rotated at `pos` by the lane's frequency fr.
+__device__ __forceinline__ void head_norm_rope(float &a, float &b, float w0, float w1, float fr, const TokAttn &t) {
     float s = __builtin_fmaf(a, a, 0.0f);
     s = __builtin_fmaf(b, b, s);
     const float rms = 1.0f / sqrtf(wave_sum(s) / (float)AHD + t.eps);
-    const float n0 = a * w[lane] * rms, n1 = b * w[64 + lane] * rms;
+    const float n0 = a * w0 * rms, n1 = b * w1 * rms;
     if (!t.rope) {
         a = n0, b = n1;
         return;
     }
-    const float ang = t.freq[lane] * (float)t.pos;
+    const float ang = fr * (float)t.pos;
     const float c = cosf(ang), sn = sinf(ang);
     a = n0 * c - n1 * sn;
     b = n1 * c + n0 * sn;
 }
 
 __global__ __launch_bounds__(256) void k_attn_token(TokAttn t) {
+    constexpr uint32_t QW = ADQ / 4;  // query heads per wavefront
     __shared__ float lq[ADQ][AHD];
     __shared__ float lkn[AHD];
     __shared__ float lp[ADQ][ACH];
@@ -717,7 +718,28 @@ __global__ __launch_bounds__(256) void k_attn_token(TokAttn t) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t kvld = t.n_kv * AHD, S = t.S, self = S - 1;
     const bool owner = self / ACH == c;  // this chunk holds the token's own key
+    const bool kown = owner && wave == 3;
     const uint32_t pk = c * ACH + 16 * wave + (lane & 15u), qd = lane >> 4;
+    // The wave's query heads (qi = wave, wave + 4), the norm weights, the lane's
+    // rotation frequency and (kown) the token's key are loaded ahead of the cache
+    // rows: loads complete in issue order, so the norms then wait only for these.
+    float qa[QW], qb[QW];
+#pragma unroll
+    for (uint32_t r = 0; r < QW; r++) {
+        const uint32_t qi = wave + 4 * r < nq ? wave + 4 * r : 0;  // branch-free: unused heads read head 0
+        const float *qp = t.q + (uint64_t)(h * G + qi) * AHD;
+        qa[r] = qp[lane];
+        qb[r] = qp[64 + lane];
+    }
+    const float wq0 = t.qn_w[lane], wq1 = t.qn_w[64 + lane];
+    const float fr = t.rope ? t.freq[lane] : 0.0f;
+    float ka = 0.0f, kb = 0.0f, wk0 = 0.0f, wk1 = 0.0f;
+    float *kself = t.k + (uint64_t)self * kvld + h * AHD;
+    if (kown) {
+        ka = kself[lane], kb = kself[64 + lane];
+        wk0 = t.kn_w[lane], wk1 = t.kn_w[64 + lane];
+    }
+    asm volatile("" ::: "memory");  // keep these loads issued before the cache rows
     float4 kr[8];
     {
         const float *kp = t.k + (uint64_t)(pk < S ? pk : S - 1) * kvld + h * AHD + 32 * qd;
@@ -731,21 +753,21 @@ __global__ __launch_bounds__(256) void k_attn_token(TokAttn t) {
         vr[j] = reinterpret_cast<const float2 *>(t.v + (uint64_t)(p < S ? p : S - 1) * kvld + h * AHD)[lane];
     }
     // the query heads of this kv head, and (owner) the token's key, normed and rotated
-    for (uint32_t qi = wave; qi < nq; qi += 4) {
-        const float *qp = t.q + (uint64_t)(h * G + qi) * AHD;
-        float a = qp[lane], b = qp[64 + lane];
-        head_norm_rope(a, b, t.qn_w, t, lane);
+#pragma unroll
+    for (uint32_t r = 0; r < QW; r++) {
+        const uint32_t qi = wave + 4 * r;
+        if (qi >= nq) break;  // uniform over the wave
+        float a = qa[r], b = qb[r];
+        head_norm_rope(a, b, wq0, wq1, fr, t);
         lq[qi][lane] = a;
         lq[qi][64 + lane] = b;
     }
-    if (owner && wave == 3) {
-        float *kp = t.k + (uint64_t)self * kvld + h * AHD;
-        float a = kp[lane], b = kp[64 + lane];
-        head_norm_rope(a, b, t.kn_w, t, lane);
-        lkn[lane] = a;
-        lkn[64 + lane] = b;
-        kp[lane] = a;  // the cache keeps the normed key (no other workgroup reads this row)
-        kp[64 + lane] = b;
+    if (kown) {
+        head_norm_rope(ka, kb, wk0, wk1, fr, t);
+        lkn[lane] = ka;
+        lkn[64 + lane] = kb;
+        kself[lane] = ka;  // the cache keeps the normed key (no other workgroup reads this row)
+        kself[64 + lane] = kb;
     }
     __syncthreads();
     if (owner && pk == self)

@@ -178,6 +178,7 @@ struct M1In {
     const float *xadd = nullptr, *nw = nullptr;
     float eps = 0.0f;
     float *xout = nullptr, *xcap = nullptr, *nxout = nullptr;
+    bool glu = false;  // two jobs of equal n (gate, up): y[0] = silu(gate) * up, y[1] unused
 };
 bool proj_m1_in_ok(uint32_t k, const float *x, const M1In &in);
 // lg_set_fold_norms: whether the forwards fold their norms into the products.

@@ -933,6 +933,10 @@ __device__ __forceinline__ void dig_read(const DigLds &dg, uint32_t p, uint32_t 
 // pointer a kernel argument of its own: a pointer read from a structure, or selected
 // among several, has no known address space, and its loads become flat loads whose
 // waits also wait for the LDS traffic.
+//
+// GLU (IN, two jobs of equal size: an FFN's gate and up): virtual row 2r is gate row
+// r and 2r + 1 is up row r, so a wave's two rows are one pair, and it writes
+// silu(gate) * up (kernels/activation.comp:21-28) as row r of job 0's output.
 struct DigIn {
     const float *xadd;  // null: the activations are x
     const float *nw;    // null: no norm
@@ -945,11 +949,12 @@ struct DigIn {
     float eps;
 };
 
-template <int TEAMS, int R, bool IN, int NJ = 1>
+template <int TEAMS, int R, bool IN, int NJ = 1, bool GLU = false>
 __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, const uint8_t *__restrict__ w,
                                                 float *__restrict__ y, uint32_t k, uint32_t n, uint64_t row_bytes,
                                                 const DigIn &in) {
     static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
+    static_assert(!GLU || (IN && NJ == 2 && R == 2), "GLU pairs the two rows of a wave");
     __shared__ __attribute__((aligned(16))) DigLds dg;
     __shared__ float ssq[IN ? TEAMS : 1];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, team = tid >> 6;
@@ -973,6 +978,12 @@ __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, con
         int64_t wo = 0, yo = 0;
         row = __builtin_amdgcn_readfirstlane(row);  // uniform over the wave: scalar selection
         lr = row;
+        if constexpr (GLU) {
+            wj = in.w0 + ((row & 1u) ? in.wofs[1] : 0);
+            yj = in.y0;
+            lr = row >> 1;
+            return;
+        }
         if constexpr (NJ > 1) {
 #pragma unroll
             for (int i = 1; i < NJ; i++)
@@ -1051,6 +1062,26 @@ __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, con
     float X0, X1, F;
     dig_read(dg, p, D, X0, X1, F);
     if (dg.bad) {  // the reference's per-element loop (kernels/proj_q4k.comp:60-75)
+        if constexpr (GLU) {  // pair r: gate row r and up row r, then silu(gate) * up
+            for (uint32_t pr = blockIdx.x * TEAMS + team; pr < n / 2; pr += gridDim.x * TEAMS) {
+                float a[2] = {0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const uint8_t *wj;
+                    float *yj;
+                    uint32_t lr;
+                    job(2 * pr + u, wj, yj, lr);
+                    for (uint32_t j = lane; j < k; j += 64) {
+                        float xj = in.xadd ? x[j] + in.xadd[j] : x[j];
+                        if (in.nw) xj = xj * in.nw[j] * rs;
+                        a[u] = __builtin_fmaf(xj, q4k_elem(wj, (uint64_t)lr * k + j), a[u]);
+                    }
+                    a[u] = wave_sum(a[u]);
+                }
+                if (lane == 0) in.y0[pr] = silu_mul(a[0], a[1]);
+            }
+            return;
+        }
         for (uint32_t rr = blockIdx.x * TEAMS + team; rr < n; rr += gridDim.x * TEAMS) {
             float a = 0.0f;
             if constexpr (IN) {
@@ -1101,6 +1132,12 @@ __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, con
     };
     // Idle lanes contribute an explicit 0, not 0 * (a scale that may be inf or NaN).
     auto reduce = [&](int b, uint32_t rr) {
+        if constexpr (GLU) {  // rows rr (gate) and rr + 1 (up) of pair rr / 2
+            const float g = wave_sum(active ? dotrow(hd[b][0], qa[b][0], qb[b][0]) : 0.0f);
+            const float u = wave_sum(active ? dotrow(hd[b][1], qa[b][1], qb[b][1]) : 0.0f);
+            if (lane == 0 && rr < n) in.y0[rr >> 1] = silu_mul(g, u);
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float v = dotrow(hd[b][r], qa[b][r], qb[b][r]);
@@ -1144,7 +1181,7 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig(const float *__restri
     q4k_m1_dig_body<TEAMS, R, false>(x, w, y, k, n, row_bytes, DigIn{});
 }
 
-template <int TEAMS, int R, int NJ>
+template <int TEAMS, int R, int NJ, bool GLU = false>
 __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig_in(
     const float *__restrict__ x, const float *xadd, const float *__restrict__ nw, float *xout, float *xcap,
     float *nxout, const uint8_t *__restrict__ w0, float *y0, int64_t wo1, int64_t wo2, int64_t wo3, int64_t yo1,
@@ -1152,7 +1189,7 @@ __global__ __launch_bounds__(TEAMS * 64) void k_q4k_m1_dig_in(
     uint64_t row_bytes) {
     const DigIn in{xadd, nw, xout, xcap, nxout, w0, y0, {0, wo1, wo2, wo3}, {0, yo1, yo2, yo3}, {0u, off1, off2, off3},
                    eps};
-    q4k_m1_dig_body<TEAMS, R, true, NJ>(x, nullptr, nullptr, k, n, row_bytes, in);
+    q4k_m1_dig_body<TEAMS, R, true, NJ, GLU>(x, nullptr, nullptr, k, n, row_bytes, in);
 }
 
 // Q8_0 with k <= 4096: the same digits against the raw int8 quants.  Lane p owns
@@ -1830,7 +1867,7 @@ bool proj_m1_in_ok(uint32_t k, const float *x, const M1In &in) {
         return false;
     for (uint32_t j = 0; j < in.count; j++)
         if (in.type[j] != LG_Q4_K || !in.w[j] || !in.y[j] || !a16(in.w[j])) return false;
-    return true;
+    return !in.glu || (in.count == 2 && in.n[0] == in.n[1]);
 }
 
 int proj_m1_in(const float *x, const M1In &in, uint32_t k, hipStream_t s) {
@@ -1859,13 +1896,14 @@ int proj_m1_in(const float *x, const M1In &in, uint32_t k, hipStream_t s) {
         LG_REQUIRE(((reinterpret_cast<uintptr_t>(y[j]) - reinterpret_cast<uintptr_t>(y[0])) & 3u) == 0,
                    "%s: output %u is not float-aligned with output 0", name, j);
     }
-#define LG_DIG_IN(NJ)                                                                                        \
-    hipLaunchKernelGGL((k_q4k_m1_dig_in<TEAMS, R, NJ>), dim3(grid), dim3(TEAMS * 64), 0, s, x, in.xadd, in.nw, in.xout, \
+#define LG_DIG_IN(NJ, GLU)                                                                                   \
+    hipLaunchKernelGGL((k_q4k_m1_dig_in<TEAMS, R, NJ, GLU>), dim3(grid), dim3(TEAMS * 64), 0, s, x, in.xadd, in.nw, in.xout, \
                        in.xcap, in.nxout, w[0], y[0], wo[1], wo[2], wo[3], yo[1], yo[2], yo[3], off[1], off[2], off[3], \
                        n, in.eps, k, (uint64_t)k / QK_K * Q4K_BYTES)
-    if (in.count == 1) LG_DIG_IN(1);
-    else if (in.count == 2) LG_DIG_IN(2);
-    else LG_DIG_IN(4);
+    if (in.count == 1) LG_DIG_IN(1, false);
+    else if (in.glu) LG_DIG_IN(2, true);
+    else if (in.count == 2) LG_DIG_IN(2, false);
+    else LG_DIG_IN(4, false);
 #undef LG_DIG_IN
     return after_launch(name, s);
 }

@@ -220,21 +220,18 @@ int forward_in(const lg_target_model *md, const TgtLayout &W, const float *input
                                   L.attn_gate ? W.gate : nullptr));
         }
         LG_TRY(proj(W.att, L.attn_output, L.attn_output_type, W.o, QD, E, s));
-        // x + o_proj, normed: the FFN's gate and up
+        // x + o_proj, normed: the FFN's gate and up, each pair of rows written as
+        // silu(gate) * up (src/target.rs:530-545), then the down projection of that
         M1In f;
         f.w[0] = L.ffn_gate, f.type[0] = L.ffn_gate_type, f.y[0] = W.g, f.n[0] = FF;
         f.w[1] = L.ffn_up, f.type[1] = L.ffn_up_type, f.y[1] = W.u, f.n[1] = FF;
         f.count = 2;
+        f.glu = true;
         f.xadd = W.o, f.nw = L.ffn_norm, f.eps = hp.rms_eps, f.xout = bufs[nb];
         LG_TRY(proj_m1_in(cur, f, E, s));
         cur = bufs[nb];
         nb ^= 1u;
-        if (L.ffn_down_type == LG_Q4_K) {  // silu(gate) * up inside the down projection
-            LG_TRY(lg_dispatch_silu_mul_proj_quant(W.g, W.u, L.ffn_down, W.o, FF, E, LG_Q4_K, s));
-        } else {
-            LG_TRY(lg_dispatch_activation(W.g, W.u, W.g, FF, s));
-            LG_TRY(proj(W.g, L.ffn_down, L.ffn_down_type, W.o, FF, E, s));
-        }
+        LG_TRY(proj(W.g, L.ffn_down, L.ffn_down_type, W.o, FF, E, s));
         add = W.o;
     }
     float *fcap = slot[hp.n_layers] >= 0 ? captured + (uint64_t)slot[hp.n_layers] * E : nullptr;
