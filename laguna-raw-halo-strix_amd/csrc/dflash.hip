@@ -115,6 +115,9 @@ struct NormRun {
     const float *tok, *wt;
     float *xt, *yt, *ss;
     uint32_t cols;
+    float *rope;        // with freq (64 entries): the rotation table of positions pos0 + p,
+    const float *freq;  // p < 2 * rows: rope[p][i] = cos (i < 64) or sin (i >= 64) of
+    uint32_t pos0;      // freq[i % 64] * (pos0 + p), as k_qk_norm_rope computes them
 };
 
 // Rows of n floats, n a multiple of 4 up to 1024 V4: thread i holds float4s i,
@@ -158,6 +161,12 @@ __global__ __launch_bounds__(256) void k_norms_in(const float *__restrict__ x, c
     const uint64_t base = (uint64_t)blockIdx.x * n;
     const uint32_t j = blockIdx.y;
     float4 v[V4], wv[V4];
+    if (run.rope && j == run.count + (run.tok ? 1u : 0u)) {  // two positions of the rotation table
+        const uint32_t p = 2 * blockIdx.x + (threadIdx.x >> 7), i = threadIdx.x & 127u;
+        const float ang = run.freq[i & 63u] * (float)(run.pos0 + p);
+        run.rope[(uint64_t)p * 128 + i] = i < 64 ? cosf(ang) : sinf(ang);
+        return;
+    }
     if (j == run.count) {  // a token row
         load_row4<V4>(run.tok + base, n, v);
         load_row4<V4>(run.wt, n, wv);
@@ -211,8 +220,9 @@ struct GateJob {
     float eps;
 };
 
-__device__ __forceinline__ void gate_dot(const GateJob &g, uint32_t unit, uint32_t lane) {
-    if (unit >= g.units) return;
+// Unit (row, head) = (unit / n_heads, unit % n_heads), unit < units: every lane
+// receives the result.
+__device__ __forceinline__ float gate_value(const GateJob &g, uint32_t unit, uint32_t lane) {
     const uint32_t row = unit / g.n_heads, head = unit % g.n_heads;
     const float *xr = g.x + (uint64_t)row * g.k;
     const uint8_t *wr = g.w + (uint64_t)head * (g.k / QK_K) * Q4K_BYTES;
@@ -251,7 +261,13 @@ __device__ __forceinline__ void gate_dot(const GateJob &g, uint32_t unit, uint32
         const float p = lane < g.cols ? g.ss[(uint64_t)row * g.cols + lane] : 0.0f;
         acc *= 1.0f / sqrtf(wave_sum(p) / (float)g.k + g.eps);
     }
-    if (lane == 0) g.out[(uint64_t)row * g.n_heads + head] = acc;
+    return acc;
+}
+
+__device__ __forceinline__ void gate_dot(const GateJob &g, uint32_t unit, uint32_t lane) {
+    if (unit >= g.units) return;
+    const float acc = gate_value(g, unit, lane);
+    if (lane == 0) g.out[unit] = acc;
 }
 
 // Job a takes workgroups 0 .. a.blocks-1, job b the next b.blocks (the forward's K
@@ -831,16 +847,18 @@ constexpr uint32_t ATAIL = 64;
 // LDS, added in wave order.  With `gate` ([rows][n_q]), the result of head hq of
 // row t is then multiplied by softplus(gate[t][hq]) (gmode 1: the draft forward's
 // attention gate, src/dflash.rs:956-959; gmode 2: kernels/gate_attn.comp:27, the
-// target's, log(1 + exp(g)) with no threshold).
+// target's, log(1 + exp(g)) with no threshold).  With gj.units > 0 the gate is
+// computed here instead (the draft's Q4_K gate, unit t * n_q + hq), by wave 3,
+// which has no share of the tail while the tail fits waves 0-2.
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
                                                       const float *__restrict__ part_ml, float *__restrict__ out,
                                                       uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch,
                                                       const float *__restrict__ gate, const float *__restrict__ q,
                                                       const float *__restrict__ k1, const float *__restrict__ v1,
                                                       uint32_t T, uint32_t n0, uint32_t qpos0, int causal,
-                                                      float scale, int gmode) {
+                                                      float scale, int gmode, GateJob gj) {
     constexpr uint32_t CB = 8, TW = ATAIL / 4;
-    __shared__ float sm[4], sl[4], so[4][AHD];
+    __shared__ float sm[4], sl[4], so[4][AHD], sg;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t gq = blockIdx.x;  // over n_kv * AQ
     const uint32_t G = n_q / n_kv;
@@ -848,6 +866,10 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup
     const uint64_t q0 = (uint64_t)h * nch * AQ + qi;  // partial index of chunk c: q0 + c * AQ
     const uint32_t per = (nch + 3) / 4, cb0 = wave * per, cb1 = cb0 + per < nch ? cb0 + per : nch;
+    if (gj.units && wave == 3) {  // uniform over the wave
+        const float gv = gate_value(gj, (qi / G) * n_q + h * G + qi % G, lane);
+        if (lane == 0) sg = gv;
+    }
     // this wave's tail partial (tm, tl, t0, t1): scores made uniform over the wave
     float tm = -INFINITY, tl = 0.0f, t0 = 0.0f, t1 = 0.0f;
     if (T > wave * TW) {
@@ -930,8 +952,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     const uint32_t t = qi / G, hq = h * G + qi % G;
     float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    if (gate) {
-        const float gv = gate[(uint64_t)t * n_q + hq];
+    if (gate || gj.units) {
+        const float gv = gj.units ? sg : gate[(uint64_t)t * n_q + hq];
         const float g = gmode == 2 ? logf(1.0f + expf(gv)) : softplus_gate(gv);
         o[lane] = (o0 * inv) * g;
         o[64 + lane] = (o1 * inv) * g;
@@ -1034,7 +1056,7 @@ bool fan_width_ok(uint32_t n) { return n && n % 4 == 0 && n <= 8192; }
 
 int run_norms_in(const float *x, const float *w, float *xe, const NormRun &run, uint32_t n, uint32_t rows, float eps,
                  hipStream_t s) {
-    const dim3 grid(rows, run.count + (run.tok ? 1 : 0));
+    const dim3 grid(rows, run.count + (run.tok ? 1 : 0) + (run.rope ? 1 : 0));
     if (n <= 1024) hipLaunchKernelGGL(k_norms_in<1>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
     else if (n <= 2048) hipLaunchKernelGGL(k_norms_in<2>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
     else if (n <= 4096) hipLaunchKernelGGL(k_norms_in<4>, grid, dim3(256), 0, s, x, w, xe, run, n, eps);
@@ -1068,7 +1090,8 @@ size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
 // With `gate` ([rows][n_q]) each head's result is multiplied by softplus of its gate.
 int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0, const float *k1, const float *v1,
                   uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t qpos0, int causal,
-                  float *out, float *part, hipStream_t s, const float *gate = nullptr, int gmode = 1) {
+                  float *out, float *part, hipStream_t s, const float *gate = nullptr, int gmode = 1,
+                  const GateJob *gj = nullptr) {
     const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
     const uint32_t G = n_q / n_kv;
     if (part && hd == AHD && rows * G <= AQ) {
@@ -1089,8 +1112,12 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
             LG_TRY(after_launch("attn_chunk", s));
         }
         hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, part, part_ml, out, rows, n_q,
-                           n_kv, nch, gate, q, k1, v1, T, n0, qpos0, causal, scale, gmode);
+                           n_kv, nch, gate, q, k1, v1, T, n0, qpos0, causal, scale, gmode, gj ? *gj : GateJob{});
         return after_launch("attn_combine", s);
+    }
+    if (gj) {  // the gate by itself, ahead of the attention that it scales
+        LG_TRY(run_qk_norm_rope(QkJob{}, QkJob{}, nullptr, hd, 0, 0.0f, s, *gj));
+        gate = gj->out;
     }
     hipLaunchKernelGGL(k_attn_simple, dim3((rows * n_q + 3) / 4), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S, rows,
                        n_q, n_kv, hd, qpos0, causal, scale, out);
@@ -1114,7 +1141,7 @@ constexpr uint64_t FREQ_BYTES = 1024;  // rope_dim <= head_dim <= 256: at most 1
 // input (injected rows normalised, token rows with the norm's weight applied), and
 // the token rows' sums of squares ahead of the attention and FFN norms.
 struct FwdLayout {
-    float *xe, *nxe, *kk, *vv, *q, *att, *gate, *o, *h, *g, *u, *feat_n, *part, *ny, *ssa, *ssb, *freq;
+    float *xe, *nxe, *kk, *vv, *q, *att, *gate, *o, *h, *g, *u, *feat_n, *part, *ny, *ssa, *ssb, *rope, *freq;
     void *pws;
     uint64_t pws_bytes, total;
 };
@@ -1127,9 +1154,9 @@ uint64_t layout(const lg_dflash_hparams &hp, uint32_t m, uint32_t ctx_len, uint8
     const uint64_t floats[] = {2 * m * E, 2 * m * E, 2 * m * KVD, 2 * m * KVD,  2 * m * QD, m * QD,
                                2 * (uint64_t)m * hp.n_heads,      m * E,        m * E,  m * FF, m * FF, m * A,
                                attn_partial_floats(S, hp.n_kv_heads), (uint64_t)hp.n_layers * 2 * m * E,
-                               ss_floats, ss_floats};
+                               ss_floats, ss_floats, 2 * (uint64_t)m * 128};
     float **dst[] = {&L.xe, &L.nxe, &L.kk, &L.vv, &L.q, &L.att, &L.gate, &L.o, &L.h, &L.g, &L.u, &L.feat_n, &L.part,
-                     &L.ny, &L.ssa, &L.ssb};
+                     &L.ny, &L.ssa, &L.ssb, &L.rope};
     // The RoPE table and the small-M product workspace (whose arrival counters come
     // first) sit at fixed offsets whatever (m, ctx_len) are: an uploaded table stays
     // valid, and the counters stay zero, across calls that lay the rest out differently.
@@ -1401,6 +1428,11 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
     // and the token rows entering layer 0: x = tokens, with layer 0's x attn_norm and
     // sums of squares
     float *x = W.xe + mE;  // the tokens' residual stream
+    // QK-norm and RoPE inside the K/V/Q launch (whole heads per workgroup column), the
+    // gate inside the attention's combine: for heads of 128 rotated in full, at most 32
+    // rows per launch and a Q4_K gate; the rotation table of the 2m positions is built
+    // with the first norms
+    const bool qkf = HD == AHD && hp.rope_dim == AHD && 2 * m <= 32;
     for (uint32_t l0 = 0; l0 < hp.n_layers; l0 += NORM_RUN) {
         NormRun run{};
         run.count = hp.n_layers - l0 < NORM_RUN ? hp.n_layers - l0 : NORM_RUN;
@@ -1415,6 +1447,11 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
             run.yt = W.ny + mE;
             run.ss = W.ssa;
             run.cols = 1;
+            if (qkf) {
+                run.rope = W.rope;
+                run.freq = W.freq;
+                run.pos0 = ctx_len;
+            }
         }
         LG_TRY(run_norms_in(W.o, md->enc_output_norm, W.xe, run, E, m, eps, s));
     }
@@ -1429,38 +1466,54 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
         float *q = W.q, *gate = W.gate;
         GateJob gj{};
         const bool kvq = L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type;
-        if (kvq && L.attn_gate_type == LG_Q4_K) {
-            const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                    {L.attn_q, W.q, nullptr, QD}};
+        if (qkf && kvq && L.attn_gate_type == LG_Q4_K) {
+            BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                              {L.attn_q, W.q, nullptr, QD}};
+            jb[0].qkw = L.attn_k_norm;
+            jb[2].qkw = L.attn_q_norm;
+            const QkRope qk{W.rope, hp.qk_eps};
             LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
-                                    &ra));
+                                    &ra, &qk));
             q = W.q + (uint64_t)m * QD;
-            gate = W.gate + (uint64_t)m * H;
-            gj = {ny, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4, W.ssa, cols_a,
-                  eps};
-        } else if (kvq && L.attn_k_type == L.attn_gate_type) {
-            const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                    {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
-            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
-                                    &ra));
-            q = W.q + (uint64_t)m * QD;
-            gate = W.gate + (uint64_t)m * H;
+            gj = {ny, static_cast<const uint8_t *>(L.attn_gate), W.gate + (uint64_t)m * H, H, E, m * H, (m * H + 3) / 4,
+                  W.ssa, cols_a, eps};
+            LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m,
+                                 1, W.att, W.part, s, nullptr, 1, &gj));
         } else {
-            const BatchJob k1{L.attn_k, W.kk, nullptr, KVD}, v1{L.attn_v, W.vv, nullptr, KVD};
-            const BatchJob q1{L.attn_q, W.q, nullptr, QD}, g1{L.attn_gate, W.gate, nullptr, H};
-            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, &k1, 1, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
-                                    &ra));
-            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, &v1, 1, E, 2 * m, L.attn_v_type, W.pws, W.pws_bytes, s, false,
-                                    &ra));
-            LG_TRY(proj_batch_multi(ny, LG_F32, nullptr, &q1, 1, E, m, L.attn_q_type, W.pws, W.pws_bytes, s, false, &rt));
-            LG_TRY(proj_batch_multi(ny, LG_F32, nullptr, &g1, 1, E, m, L.attn_gate_type, W.pws, W.pws_bytes, s, false,
-                                    &rt));
+            if (kvq && L.attn_gate_type == LG_Q4_K) {
+                const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                        {L.attn_q, W.q, nullptr, QD}};
+                LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
+                                        false, &ra));
+                q = W.q + (uint64_t)m * QD;
+                gate = W.gate + (uint64_t)m * H;
+                gj = {ny, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4,
+                      W.ssa, cols_a, eps};
+            } else if (kvq && L.attn_k_type == L.attn_gate_type) {
+                const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                        {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
+                LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
+                                        false, &ra));
+                q = W.q + (uint64_t)m * QD;
+                gate = W.gate + (uint64_t)m * H;
+            } else {
+                const BatchJob k1{L.attn_k, W.kk, nullptr, KVD}, v1{L.attn_v, W.vv, nullptr, KVD};
+                const BatchJob q1{L.attn_q, W.q, nullptr, QD}, g1{L.attn_gate, W.gate, nullptr, H};
+                LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, &k1, 1, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
+                                        false, &ra));
+                LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, &v1, 1, E, 2 * m, L.attn_v_type, W.pws, W.pws_bytes, s,
+                                        false, &ra));
+                LG_TRY(proj_batch_multi(ny, LG_F32, nullptr, &q1, 1, E, m, L.attn_q_type, W.pws, W.pws_bytes, s,
+                                        false, &rt));
+                LG_TRY(proj_batch_multi(ny, LG_F32, nullptr, &g1, 1, E, m, L.attn_gate_type, W.pws, W.pws_bytes, s,
+                                        false, &rt));
+            }
+            LG_TRY(run_qk_norm_rope(qk_job(W.kk, L.attn_k_norm, W.kk, KV, ctx_len, 2 * m),
+                                    qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim,
+                                    hp.qk_eps, s, gj));
+            LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m,
+                                 1, W.att, W.part, s, gate));
         }
-        LG_TRY(run_qk_norm_rope(qk_job(W.kk, L.attn_k_norm, W.kk, KV, ctx_len, 2 * m),
-                                qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim, hp.qk_eps, s,
-                                gj));
-        LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
-                             W.att, W.part, s, gate));
         // x += o_proj, writing x ffn_norm and the sums of x^2 for the FFN norm (src/dflash.rs:960-962)
         const uint32_t cols_b = proj_batch_norm_cols(L.attn_output_type, QD, E, m);
         const BatchJob oj{L.attn_output, x, x, E, W.h, L.ffn_norm, W.ssb};
@@ -1565,7 +1618,7 @@ int glue_attention_token(const float *q, const float *qn_w, const float *kn_w, c
     hipLaunchKernelGGL(k_attn_token, dim3(t.nch, n_kv), dim3(256), 0, s, t);
     LG_TRY(after_launch("attention_token", s));
     hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, t.part_o, t.part_ml, out, 1u, n_q, n_kv,
-                       t.nch, gate, q, nullptr, nullptr, 0u, 0u, 0u, 1, t.scale, 2);
+                       t.nch, gate, q, nullptr, nullptr, 0u, 0u, 0u, 1, t.scale, 2, GateJob{});
     return after_launch("attn_combine", s);
 }
 

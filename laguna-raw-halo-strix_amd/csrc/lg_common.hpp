@@ -139,6 +139,10 @@ int proj_batch(const void *x, int x_dtype, const void *w, float *c, uint32_t k, 
 //  * RowScale on the consuming call (x = such a y): the results of activation rows
 //    t >= tok0 are multiplied by (sum_g ss[(t - tok0) * cols + g] / k + eps)^-1/2, the
 //    norm's 1/rms (rows below tok0 arrive normalised).  cols <= proj_batch_rs_cols_max(m).
+//  * job field qkw with a QkRope on the call: the job's rows are heads of 128, and
+//    each head of each activation row t is written QK-normed with weights qkw and
+//    rotated (NeoX, all 128 dims) at row t's angles: table[t][0..63] the cosines and
+//    table[t][64..127] the sines of freq[i] * position(t) (the whole call's m rows).
 struct BatchJob {
     const void *w;
     float *c;
@@ -147,16 +151,21 @@ struct BatchJob {
     float *y = nullptr;
     const float *yw = nullptr;
     float *ss = nullptr;
+    const float *qkw = nullptr;
 };
 struct RowScale {
     const float *ss = nullptr;
     uint32_t cols = 0, tok0 = 0;
     float eps = 0.0f;
 };
+struct QkRope {
+    const float *table = nullptr;
+    float eps = 0.0f;
+};
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype);
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jobs, uint32_t njobs, uint32_t k,
                      uint32_t m, int w_dtype, void *ws, uint64_t ws_bytes, hipStream_t s, bool glu = false,
-                     const RowScale *rs = nullptr);
+                     const RowScale *rs = nullptr, const QkRope *qk = nullptr);
 uint32_t proj_batch_norm_cols(int w_dtype, uint32_t k, uint32_t n, uint32_t m);
 uint32_t proj_batch_rs_cols_max(uint32_t m);
 // Whether products with these weights (f32 activations, 16-byte aligned) take the

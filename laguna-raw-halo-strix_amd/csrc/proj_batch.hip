@@ -120,6 +120,7 @@ struct MmJob {
     const float *yw;
     float *ss;
     uint32_t n, g0;
+    const float *qkw;  // QK-norm weights (heads of 128 rows, RT = 2), or null
 };
 struct MmJobs {
     MmJob j[MM_JOBS];
@@ -128,6 +129,8 @@ struct MmJobs {
     const float *rs_ss;
     uint32_t rs_cols, rs_tok0;
     float rs_eps;
+    const float *rope;  // the QK jobs' rotation table: [token][cos 64 | sin 64]
+    float qk_eps;
 };
 // GLU launches pair two products of n rows each (gate: job 0, up: job 1): every
 // workgroup column covers the same 32*RT rows of both, wavefronts 0-1 the gate
@@ -296,11 +299,63 @@ __device__ __forceinline__ void rs_store(const float (&ssv)[MM_SS_LOADS], float 
 // sums and, in the last workgroup of the row group to finish, their ordered sum;
 // scaled per token by rsl (NORM), and with y and the column's sums of squares when
 // ssout is given (not GLU).
+// QK-norm and NeoX RoPE of whole heads (kernels/qk_norm_rope.comp:23-67,
+// src/dflash.rs:898-904) in the workgroup that finishes a column: with RT = 2 a
+// column is 128 rows, one head, and wavefront w holds dims 32 w + 16 i + (lane & 15)
+// (tile i).  Per token, the head's sum of squares meets in LDS in wavefront order,
+// and the rotation partner of dim d (d + 64 or d - 64) is read through LDS from
+// wavefront w ^ 2.  rope: per token, the cosines then the sines of its 64 angles.
+template <int TT>
+__device__ __forceinline__ void qk_head(float (&v)[2][TT][4], const float *__restrict__ w,
+                                        const float *__restrict__ rope, float eps, uint32_t m, float *xch) {
+    __shared__ float ssq[4][TT * 16];
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4, wave = threadIdx.x >> 6;
+    float wd[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) wd[i] = w[32 * wave + 16 * i + (l & 15u)];
+    __syncthreads();  // every wavefront is past its products: xch (the fragment LDS) is free
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float q = row16_sum(__builtin_fmaf(v[1][t][r], v[1][t][r], v[0][t][r] * v[0][t][r]));
+            if ((l & 15u) == 0) ssq[wave][t * 16 + 4 * kg + r] = q;
+        }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t tok = t * 16 + 4 * kg + r;
+            const float tot = ((ssq[0][tok] + ssq[1][tok]) + ssq[2][tok]) + ssq[3][tok];
+            const float rms = 1.0f / sqrtf(tot / 128.0f + eps);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                v[i][t][r] = v[i][t][r] * wd[i] * rms;
+                xch[((wave * 2 + i) * TT + t) * 256 + r * 64 + l] = v[i][t][r];
+            }
+        }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t tok = t * 16 + 4 * kg + r, tc = tok < m ? tok : m - 1;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const float p = xch[(((wave ^ 2u) * 2 + i) * TT + t) * 256 + r * 64 + l];
+                const uint32_t dm = 32 * (wave & 1u) + 16 * i + (l & 15u);
+                const float c = rope[(uint64_t)tc * 128 + dm], sn = rope[(uint64_t)tc * 128 + 64 + dm];
+                v[i][t][r] = wave < 2 ? v[i][t][r] * c - p * sn : v[i][t][r] * c + p * sn;
+            }
+        }
+}
+
 template <int TT, int RT, bool GLU, bool NORM>
 __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out, const float *res, float *part,
                                        uint32_t *cnt, uint32_t rt0, uint32_t m, uint32_t n, float *xch,
                                        const MmJobs &jobs, uint32_t k, float *y, const float *yw, float *ssout,
-                                       uint32_t bx) {
+                                       uint32_t bx, const float *qkw) {
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
     const uint32_t S = gridDim.y, s = blockIdx.y;
     const uint64_t mn = (uint64_t)m * n;
@@ -376,6 +431,8 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 #pragma unroll
                 for (int r = 0; r < 4; r++) v[i][t][r] *= rsl[t * 16 + 4 * kg + r];
     }
+    if constexpr (!GLU && RT == 2)
+        if (qkw) qk_head<TT>(v, qkw, jobs.rope, jobs.qk_eps, m, xch);  // uniform over the workgroup
     if constexpr (GLU) {
         // wavefronts 2-3 pass their up sums through LDS (`xch`, free once every
         // wavefront is past its products) to wavefronts 0-1, which hold the gate sums
@@ -559,8 +616,9 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
         }
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
+    static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lf), "the head exchange fits in the fragment LDS");
     finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
-                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx);
+                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
 
 // Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
@@ -655,8 +713,9 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
         }
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
+    static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lf), "the head exchange fits in the fragment LDS");
     finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
-                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx);
+                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
 
 // Fallback for shapes outside the MFMA path (f32 weights, k not a multiple of the
@@ -842,7 +901,7 @@ bool proj_batch_mfma_ok(int w_dtype, uint32_t k, const void *w) {
 
 int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob *jb, uint32_t njobs, uint32_t k,
                      uint32_t m, int w_dtype, void *ws_given, uint64_t ws_bytes, hipStream_t s, bool glu,
-                     const RowScale *rs) {
+                     const RowScale *rs, const QkRope *qk) {
     const char *name = "lg_dispatch_proj_quant_batch";
     LG_REQUIRE(njobs >= 1 && njobs <= (uint32_t)MM_JOBS, "%s: %u jobs (1..%d)", name, njobs, MM_JOBS);
     LG_REQUIRE(!glu || (njobs == 2 && jb[0].n == jb[1].n && !up && x_dtype == LG_F32 && !jb[0].res && !jb[1].res),
@@ -858,6 +917,15 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
                "%s: the RMSNorm epilogue takes one job over at most 32 f32 rows, with y and yw", name);
     LG_REQUIRE(m <= 64, "%s: m=%u exceeds 64", name, m);
     LG_REQUIRE(x, "%s: null activations", name);
+    bool qkn = false;  // QK-normed jobs: whole heads of 128 rows per workgroup column (RT = 2)
+    for (uint32_t j = 0; j < njobs; j++) {
+        if (!jb[j].qkw) continue;
+        qkn = true;
+        LG_REQUIRE(qk && qk->table && jb[j].n % 128 == 0 && !jb[j].res && !jb[j].ss,
+                   "%s: a QK-normed job takes the rotation table and heads of 128 rows, without residual or epilogue",
+                   name);
+    }
+    LG_REQUIRE(!qkn || (!glu && !up && m <= 32), "%s: QK-normed jobs take plain products over at most 32 rows", name);
     LG_REQUIRE(x_dtype == LG_F32 || x_dtype == LG_BF16, "%s: activation dtype %d (want F32 or BF16)", name, x_dtype);
     LG_REQUIRE(!up || x_dtype == LG_F32, "%s: the fused SiLU(gate)*up takes f32 activations", name);
     LG_REQUIRE(w_dtype == LG_Q4_K || w_dtype == LG_Q8_0 || w_dtype == LG_F32 || w_dtype == LG_Q4_K_T16 ||
@@ -899,8 +967,8 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     for (uint32_t j = 0; j < njobs; j++)
         fast = fast && (w_dtype != LG_Q4_K || (reinterpret_cast<uintptr_t>(jb[j].w) & 15u) == 0) &&
                (reinterpret_cast<uintptr_t>(jb[j].w) & 1u) == 0;
-    LG_REQUIRE(fast || !(norm || epi), "%s: a folded RMSNorm needs the matrix-core path (k a multiple of the block, "
-               "aligned operands)", name);
+    LG_REQUIRE(fast || !(norm || epi || qkn), "%s: a folded RMSNorm or QK-norm needs the matrix-core path (k a "
+               "multiple of the block, aligned operands)", name);
     if (!fast) {
         for (uint32_t j = 0; j < njobs; j++) {
             if (jb[j].n == 0) continue;
@@ -924,7 +992,8 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     const uint64_t xsz = x_dtype == LG_F32 ? 4 : 2;
     for (uint32_t t0 = 0; t0 < tiles; t0 += 2) {  // pairs of 16-token tiles
         const uint32_t ml = m - 16 * t0 < 32 ? m - 16 * t0 : 32;
-        const MmShape sh = mm_shape(w_dtype, k, (uint32_t)ntot, ml);
+        MmShape sh = mm_shape(w_dtype, k, (uint32_t)ntot, ml);
+        if (qkn) sh.rt = 2;  // within every budget: mm_shape keeps ch <= 4 (Q4_K) and <= 2 (Q8_0)
         uint32_t *cnt = static_cast<uint32_t *>(ws);
         uint8_t *pb = ws ? static_cast<uint8_t *>(ws) + CNT_BYTES : nullptr;
         if (sh.slices > 1) LG_REQUIRE(ws, "%s: no workspace for %u slices", name, sh.slices);
@@ -933,7 +1002,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         for (uint32_t j = 0; j < njobs; j++) {
             const uint64_t off = (uint64_t)16 * t0 * jb[j].n;
             jobs.j[j] = {static_cast<const uint8_t *>(jb[j].w), jb[j].c + off, jb[j].res ? jb[j].res + off : nullptr,
-                         reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups};
+                         reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups, jb[j].qkw};
             if (pb) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
             groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
         }
@@ -943,6 +1012,10 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         }
         jobs.count = njobs;
         jobs.tiled = tiled ? 1u : 0u;
+        if (qkn) {
+            jobs.rope = qk->table + (uint64_t)16 * t0 * 128;
+            jobs.qk_eps = qk->eps;
+        }
         // the folded norm's scaled rows in this pair of tiles (rows 16 t0 .. 16 t0 + ml - 1)
         const bool pnorm = norm && 16 * t0 + ml > rs->tok0;
         if (pnorm) {
