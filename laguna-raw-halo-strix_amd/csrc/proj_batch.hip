@@ -27,7 +27,10 @@
 // the workgroup writes the result; otherwise each writes its slice's partial sums
 // and the last workgroup of a row group to finish (a per-row-group arrival counter,
 // reset by that workgroup) adds the slices in slice order: the result does not
-// depend on which workgroup finishes last.
+// depend on which workgroup finishes last.  A single plain product of many rounds of
+// workgroups (a vocab-sized head) instead has its slices only store their partial
+// sums, and a second launch (k_mm_sum) adds them in the same order, so no workgroup
+// waits for its arrival.
 #include <mutex>
 #include <vector>
 
@@ -503,12 +506,88 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
     }
 }
 
+// A split-k workgroup of a wide launch: slice blockIdx.y's partial sums of the
+// wavefront's rows, part[slice][token][row], with plain stores; the launch after it
+// (k_mm_sum) adds the slices, so the workgroup leaves as soon as they are issued.
+template <int TT, int RT>
+__device__ __forceinline__ void store_slice(const float (&acc)[RT][TT][4], float *part, uint32_t rt0, uint32_t m,
+                                            uint32_t n) {
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
+    float *ps = part + (uint64_t)blockIdx.y * m * n;
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t tok = t * 16 + 4 * kg + r;
+                if (row < n && tok < m) ps[(uint64_t)tok * n + row] = acc[i][t][r];
+            }
+    }
+}
+
+// The finishing launch of a wide split-k product (one plain product: no residual, no
+// epilogue).  Workgroup (c, t) covers rows 64c .. 64c+63 and tokens 16t .. 16t+15:
+// thread (token threadIdx.x / 16, quad threadIdx.x % 16) adds rows 4 quad .. 4 quad + 3
+// of the S slices in slice order, with the loads of SUM_MAXS slices in flight at once.
+// V4: rows in float4 (n % 4 == 0 and a 16-byte aligned output).
+constexpr uint32_t SUM_ROWS = 64, SUM_MAXS = 16;
+// Launches of at least this many workgroups (about four rounds of the resident ones)
+// finish in k_mm_sum: there every workgroup's wait for its arrival would be paid in
+// each round.  Smaller ones finish in the kernel, where the last workgroups' reads of
+// the partial sums overlap other columns' products (a separate finishing launch cost
+// those 5-6 us per product on the draft's shapes).
+constexpr uint64_t WIDE_MIN_WGS = 4096;
+template <bool V4>
+__global__ __launch_bounds__(256) void k_mm_sum(const float *__restrict__ part, float *__restrict__ out, uint32_t m,
+                                                uint32_t n, uint32_t S) {
+    const uint32_t tl = threadIdx.x >> 4, qd = threadIdx.x & 15u;
+    const uint32_t tok = 16 * blockIdx.y + tl, row0 = blockIdx.x * SUM_ROWS + 4 * qd;
+    const uint64_t mn = (uint64_t)m * n;
+    const uint32_t tc = tok < m ? tok : m - 1;  // branch-free loads: rows and tokens past the end are clamped
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t q0 = 0; q0 < S; q0 += SUM_MAXS) {
+        float4 pv[SUM_MAXS];
+#pragma unroll
+        for (uint32_t g = 0; g < SUM_MAXS; g++) {
+            const uint32_t q = q0 + g < S ? q0 + g : S - 1;
+            const float *src = part + q * mn + (uint64_t)tc * n;
+            if constexpr (V4) {
+                pv[g] = *reinterpret_cast<const float4 *>(src + (row0 < n ? row0 : n - 4));
+            } else {
+                float e4[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) e4[e] = src[row0 + e < n ? row0 + e : n - 1];
+                pv[g] = make_float4(e4[0], e4[1], e4[2], e4[3]);
+            }
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < SUM_MAXS; g++)
+            if (q0 + g < S) {
+                v[0] += pv[g].x;
+                v[1] += pv[g].y;
+                v[2] += pv[g].z;
+                v[3] += pv[g].w;
+            }
+    }
+    if (tok >= m) return;
+    const uint64_t o = (uint64_t)tok * n + row0;
+    if (V4 && row0 < n) {
+        *reinterpret_cast<float4 *>(out + o) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (row0 + e < n) out[o + e] = v[e];
+    }
+}
+
 // Q4_K.  Wavefront w owns row tiles (4*blockIdx.x + w)*RT .. +RT-1; each activation
 // fragment read from LDS serves all RT tiles.  Order of work: the activation loads,
 // every weight load of the slice (branch-free: rows past n and blocks past k read
 // row n-1 / the last block and are never used), the fragment build while the
 // weights are in flight, then the products.
-template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM>
+template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM, bool WIDE = false>
 __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
     MM_JOB_SELECT;
@@ -617,12 +696,16 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
     static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lf), "the head exchange fits in the fragment LDS");
+    if constexpr (WIDE) {  // the slices' sums are added by k_mm_sum
+        store_slice<TT, RT>(acc, part, rt0, m, n);
+        return;
+    }
     finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
                               jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
 
 // Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
-template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM>
+template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM, bool WIDE = false>
 __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
     MM_JOB_SELECT;
@@ -714,6 +797,10 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
     static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lf), "the head exchange fits in the fragment LDS");
+    if constexpr (WIDE) {  // the slices' sums are added by k_mm_sum
+        store_slice<TT, RT>(acc, part, rt0, m, n);
+        return;
+    }
     finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
                               jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
@@ -801,11 +888,11 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
     return {ch, slices, tiles, rt};
 }
 
-template <int TT, int PARTS, int CH, bool FUSE, bool GLU, bool NORM>
+template <int TT, int PARTS, int CH, bool FUSE, bool GLU, bool NORM, bool WIDE>
 void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt,
                uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
 #define LG_MM(K, R) \
-    hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE, GLU, NORM>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
+    hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE, GLU, NORM, WIDE>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
     // mm_shape keeps rt * ch within each kernel's register budget
     if (dtype == LG_Q4_K) {
         if constexpr (4 * CH <= 8)
@@ -835,18 +922,18 @@ void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up
 #undef LG_MM
 }
 
-template <int PARTS, bool FUSE, bool GLU = false, bool NORM = false>
+template <int PARTS, bool FUSE, bool GLU = false, bool NORM = false, bool WIDE = false>
 int launch_mm(int dtype, const MmShape &sh, uint32_t groups, const void *x, const float *up, const MmJobs &jobs,
               uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
     const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
     if (sh.tiles == 1) {
-        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<1, PARTS, 1, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<1, PARTS, 1, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     } else {
-        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<2, PARTS, 1, FUSE, GLU, NORM>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        else launch_rt<2, PARTS, 1, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
     }
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
 }
@@ -1024,15 +1111,31 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
             jobs.rs_cols = rs->cols;
             jobs.rs_eps = rs->eps;
         }
+        // one plain product split over k in many rounds of workgroups: the slices only
+        // store their partial sums and k_mm_sum adds them
+        const bool wide = njobs == 1 && !qkn && !glu && !up && !pnorm && !jb[0].res && !jb[0].ss && sh.slices > 1 &&
+                          (uint64_t)groups * sh.slices >= WIDE_MIN_WGS;
         LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
         const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
         const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
-        if (x_dtype == LG_BF16) LG_TRY((launch_mm<1, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
+        if (wide && x_dtype == LG_BF16)
+            LG_TRY((launch_mm<1, false, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
+        else if (wide) LG_TRY((launch_mm<3, false, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
+        else if (x_dtype == LG_BF16) LG_TRY((launch_mm<1, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else if (up) LG_TRY((launch_mm<3, true>(w_dtype, sh, groups, xt, ut, jobs, cnt, ml, k, s)));
         else if (glu && pnorm) LG_TRY((launch_mm<3, false, true, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else if (glu) LG_TRY((launch_mm<3, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else if (pnorm) LG_TRY((launch_mm<3, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
         else LG_TRY((launch_mm<3, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
+        if (wide) {
+            const MmJob &j0 = jobs.j[0];
+            const dim3 sg((j0.n + SUM_ROWS - 1) / SUM_ROWS, (ml + 15) / 16);
+            if (j0.n % 4 == 0 && (reinterpret_cast<uintptr_t>(j0.out) & 15u) == 0)
+                hipLaunchKernelGGL(k_mm_sum<true>, sg, dim3(256), 0, s, j0.part, j0.out, ml, j0.n, sh.slices);
+            else
+                hipLaunchKernelGGL(k_mm_sum<false>, sg, dim3(256), 0, s, j0.part, j0.out, ml, j0.n, sh.slices);
+            LG_TRY(after_launch(name, s));
+        }
     }
     return LG_OK;
 }
