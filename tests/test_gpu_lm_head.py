@@ -50,3 +50,23 @@ def test_lm_head_verify_block(ctx, head, x_dtype):
     c = cb.read_f32(m * VOCAB).reshape(m, VOCAB)
     y64, a = orc.proj_quant_f64(np.ascontiguousarray(x), raw, lh.Q4_K, K, VOCAB)
     parity(c, y64, a, 1e-4)
+
+
+@pytest.mark.parametrize("m,n", [(20, VOCAB), (16, VOCAB - 2), (32, VOCAB)])
+def test_lm_head_block_finishing_launch(ctx, head, m, n):
+    # Vocab-sized blocks are split over k into more than 4,096 workgroups, so their
+    # slices only store partial sums and a second launch adds them: 20 and 32 rows
+    # are two token tiles (the second partial at m = 20), n = VOCAB - 2 is not a
+    # multiple of 4 (element-wise loads and stores).  Every row against f64, and two
+    # calls bit for bit.
+    raw, wb = head
+    print(f"lm head Q4_K {K}->{n} M={m} (finishing launch)", flush=True)
+    x = synth.normal(0x5EED0323 + m, m * K).reshape(m, K)
+    xb = lh.upload_f32(ctx, x.ravel())
+    cb = lh.GpuBuffer(ctx, 4 * m * n)
+    lh.dispatch_proj_quant_batch(ctx, xb, lh.F32, wb, cb, K, n, m, lh.Q4_K)
+    c = cb.read_f32(m * n).reshape(m, n)
+    lh.dispatch_proj_quant_batch(ctx, xb, lh.F32, wb, cb, K, n, m, lh.Q4_K)
+    assert np.array_equal(cb.read_f32(m * n).reshape(m, n).view(np.uint32), c.view(np.uint32))
+    y64, a = orc.proj_quant_f64(x, raw[: n * (raw.size // VOCAB)], lh.Q4_K, K, n)  # the first n rows
+    parity(c, y64, a, 1e-4)
