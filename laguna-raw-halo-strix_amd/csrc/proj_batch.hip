@@ -715,6 +715,10 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
     const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
     const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
     const uint32_t nsb = k / 32, sb0 = blockIdx.y * SB;
+    // raw rows can be staged through the fragment LDS when the wavefronts' rows fit (not
+    // for a gate/up pair, whose halves read different weights: the staging's barrier
+    // must be reached by the whole workgroup on one condition)
+    constexpr bool STAGE = !GLU && 64u * RT * SB * Q80_BYTES <= sizeof(lf);
     Frags<TT, PARTS, CH, FUSE> fr;
     fr.load(x, up, m, k, sb0);
     uint32_t dq[RT][SB], v0[RT][SB], v1[RT][SB];
@@ -738,6 +742,43 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
                 }
             }
         }
+    } else if (STAGE && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 && row_bytes % 16 == 0) {  // uniform
+        // Raw rows staged through the fragment LDS (free until the fragments are built):
+        // each wavefront reads its 16 RT rows' SB*34 bytes of the slice with 16-byte loads
+        // (RP pieces per row), then every lane picks its blocks' scale and quants out of
+        // LDS as 16-bit words.  Pieces past the end of a row re-read its last piece.
+        constexpr uint32_t RP = SB * Q80_BYTES / 16, NP = 16 * RT * RP, NL = (NP + 63) / 64;
+        uint4 *st = lf + wave * NP;
+        const uint64_t c0 = (uint64_t)sb0 * Q80_BYTES;
+        uint4 pc[NL];
+#pragma unroll
+        for (uint32_t i = 0; i < NL; i++) {
+            const uint32_t e = l + 64 * i < NP ? l + 64 * i : NP - 1;
+            const uint32_t r = e / RP, row = rt0 * 16 + r;
+            const uint64_t o = c0 + 16 * (e % RP);
+            pc[i] = *reinterpret_cast<const uint4 *>(w + (uint64_t)(row < n ? row : n - 1) * row_bytes +
+                                                     (o + 16 <= row_bytes ? o : row_bytes - 16));
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < NL; i++)
+            if (l + 64 * i < NP) st[l + 64 * i] = pc[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint16_t *sw = reinterpret_cast<const uint16_t *>(st);
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const uint16_t *sr = sw + (i * 16 + (l & 15u)) * RP * 8;
+#pragma unroll
+            for (int j = 0; j < SB; j++) {
+                const uint16_t *blk = sr + j * (Q80_BYTES / 2);
+                const uint16_t *q = blk + 1 + 4 * kg;
+                dq[i][j] = blk[0];
+                v0[i][j] = q[0] | ((uint32_t)q[1] << 16);
+                v1[i][j] = q[2] | ((uint32_t)q[3] << 16);
+            }
+        }
+        __syncthreads();  // every wavefront has its weights: the LDS is free for the fragments
     } else {
 #pragma unroll
         for (int i = 0; i < RT; i++) {
