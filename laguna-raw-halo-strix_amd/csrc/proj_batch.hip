@@ -704,7 +704,8 @@ __global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, cons
                               jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
 
-// Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned), read as 16-bit words.
+// Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned).  Raw rows are staged through
+// LDS with 16-byte loads where they fit (see STAGE), else read as 16-bit words.
 template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM, bool WIDE = false>
 __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
                                                 uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {

@@ -31,7 +31,7 @@ run() {  # run NAME ARGS...: one rocprofv3 invocation, stop on failure
 }
 
 if [ "$WHAT" = all ] || [ "$WHAT" = traces ]; then
-    for W in ${TRACES:-q4k_m1 q8_0_m1 q4k_down_silu q4k_m1_k14336 q4k_m1_k20480 q4k_lm_head_m1 q4k_m16_f32 \
+    for W in ${TRACES:-q4k_m1 q8_0_m1 q4k_down_silu q4k_m1_k14336 q4k_m1_k20480 q4k_lm_head_m1 q4k_m16_f32 q8_0_m16_f32 \
              q4k_m16_f32_tiled q8_0_m16_f32_tiled q4k_lm_head_m16 lm_head_verify_m16 dflash_block_eager target_token ceil_read_33.1MB \
              ceil_read_17.8MB ceil_empty}; do
         ARGS=(--kernel-trace --stats --output-format csv -d "$OUT/tr_$W" -o run -- $BENCH --workload $W --no-extra --no-cpu)
