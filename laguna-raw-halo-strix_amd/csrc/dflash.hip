@@ -414,23 +414,19 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 #pragma unroll
     for (int rd = 0; rd < KVR; rd++) {
         const uint32_t e = tid + 256u * rd;
-        uint32_t pk, dk, pv, dv;
+        uint32_t pk, dk;
         kblk(e, pk, dk);
-        vblk(e, pv, dv);
 #pragma unroll
         for (int i = 0; i < 4; i++) {  // branch-free: positions past S read position S-1 (zeroed below)
             const uint32_t p = c * ACH + 4 * pk + i, pc = p < S ? p : S - 1;
             const bool s0 = pc < n0;
             kq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + (uint64_t)(s0 ? pc : pc - n0) * kvld +
                                                           h * AHD + dk);
-            const uint32_t pw = c * ACH + 4 * pv + i, pwc = pw < S ? pw : S - 1;
-            const bool sv = pwc < n0;
-            vq[rd][i] = *reinterpret_cast<const float4 *>((sv ? v0 : v1) + (uint64_t)(sv ? pwc : pwc - n0) * kvld +
-                                                          h * AHD + dv);
         }
     }
-    // this lane's query row (A operand fragments for the 4 k-steps): loads issued
-    // first, with the chunk's K/V loads, so all of them are in flight together
+    // this lane's query row (A operand fragments for the 4 k-steps), then the V rows:
+    // every load is in flight together, and loads complete in issue order, so the
+    // K split waits only for K and Q, and V arrives under the scores and softmax
     const uint32_t qr = 16 * wave + l16;
     const bool qlive = qr < nq;  // branch-free: query rows past nq read row 0, zeroed
     float4 qx[AHD / 32][2];
@@ -446,18 +442,28 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
 #pragma unroll
     for (int rd = 0; rd < KVR; rd++) {
         const uint32_t e = tid + 256u * rd;
-        uint32_t pk, dk, pv, dv;
-        kblk(e, pk, dk);
+        uint32_t pv, dv;
         vblk(e, pv, dv);
-        float fk[4][4], fv[4][4];  // [position][dim]
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const bool okk = c * ACH + 4 * pk + i < S, okv = c * ACH + 4 * pv + i < S;
-            const float4 kv = kq[rd][i], vv = vq[rd][i];
+            const uint32_t pw = c * ACH + 4 * pv + i, pwc = pw < S ? pw : S - 1;
+            const bool sv = pwc < n0;
+            vq[rd][i] = *reinterpret_cast<const float4 *>((sv ? v0 : v1) + (uint64_t)(sv ? pwc : pwc - n0) * kvld +
+                                                          h * AHD + dv);
+        }
+    }
+#pragma unroll
+    for (int rd = 0; rd < KVR; rd++) {
+        const uint32_t e = tid + 256u * rd;
+        uint32_t pk, dk;
+        kblk(e, pk, dk);
+        float fk[4][4];  // [position][dim]
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool okk = c * ACH + 4 * pk + i < S;
+            const float4 kv = kq[rd][i];
             fk[i][0] = okk ? kv.x : 0.f, fk[i][1] = okk ? kv.y : 0.f, fk[i][2] = okk ? kv.z : 0.f;
             fk[i][3] = okk ? kv.w : 0.f;
-            fv[i][0] = okv ? vv.x : 0.f, fv[i][1] = okv ? vv.y : 0.f, fv[i][2] = okv ? vv.z : 0.f;
-            fv[i][3] = okv ? vv.w : 0.f;
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {  // K: position 4pk+i, dims dk..dk+3
@@ -468,16 +474,6 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
             *reinterpret_cast<uint2 *>(L.k[0] + o) = make_uint2(a[0], a[1]);
             *reinterpret_cast<uint2 *>(L.k[1] + o) = make_uint2(b[0], b[1]);
             *reinterpret_cast<uint2 *>(L.k[2] + o) = make_uint2(cc[0], cc[1]);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {  // V^T: dim dv+j, positions 4pv..4pv+3
-            uint32_t a[2], b[2], cc[2];
-            split3x2(fv[0][j], fv[1][j], a[0], b[0], cc[0]);
-            split3x2(fv[2][j], fv[3][j], a[1], b[1], cc[1]);
-            const uint32_t o = (dv + j) * VSTR + 4 * pv;
-            *reinterpret_cast<uint2 *>(L.v[0] + o) = make_uint2(a[0], a[1]);
-            *reinterpret_cast<uint2 *>(L.v[1] + o) = make_uint2(b[0], b[1]);
-            *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
         }
     }
     bf16x8 qa[AHD / 32][NP];
@@ -551,9 +547,32 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
                 L.p[pp][idx + PSTR] = (uint16_t)(w[pp] >> 16);
             }
         }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // V^T to LDS (dim dv+j, positions 4pv..4pv+3), now that the scores are done
+#pragma unroll
+    for (int rd = 0; rd < KVR; rd++) {
+        const uint32_t e = tid + 256u * rd;
+        uint32_t pv, dv;
+        vblk(e, pv, dv);
+        float fv[4][4];  // [position][dim]
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool okv = c * ACH + 4 * pv + i < S;
+            const float4 vv = vq[rd][i];
+            fv[i][0] = okv ? vv.x : 0.f, fv[i][1] = okv ? vv.y : 0.f, fv[i][2] = okv ? vv.z : 0.f;
+            fv[i][3] = okv ? vv.w : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t a[2], b[2], cc[2];
+            split3x2(fv[0][j], fv[1][j], a[0], b[0], cc[0]);
+            split3x2(fv[2][j], fv[3][j], a[1], b[1], cc[1]);
+            const uint32_t o = (dv + j) * VSTR + 4 * pv;
+            *reinterpret_cast<uint2 *>(L.v[0] + o) = make_uint2(a[0], a[1]);
+            *reinterpret_cast<uint2 *>(L.v[1] + o) = make_uint2(b[0], b[1]);
+            *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
+        }
+    }
+    __syncthreads();  // V^T and every wave's P rows are in LDS
 
     // O = P V for this wave's 16 query rows and the 8 dimension tiles
     f32x4 Od[8];
