@@ -30,9 +30,11 @@ Also reported under "extra":
   of the draft's shape over a 2048-position K/V cache, with three captured
   states and the vocab-sized LM head (GB/s of every weight and the cache read
   once);
-* ceilings: an empty kernel, and a plain streaming read (lg_bench_read) of
-  17.8, 33.0 and 350 MB buffers through the same kind of rotating pool; the
-  headline's roofline carries its fraction of both 8 TB/s and the measured read
+* ceilings: an empty kernel, and the fastest plain streaming read
+  (lg_bench_read_shape) of 17.9, 33.1 and 350.7 MB buffers through the same kind
+  of rotating pool, over a sweep of read shapes (threads per workgroup, loads in
+  flight per thread, one-shot or persistent grid, plain or nontemporal loads);
+  the headline's roofline carries its fraction of both 8 TB/s and the best read
   of its own byte count.
 
 `cpu_baseline`: the oracle (the C restatement of the reference's CPU and shader
@@ -312,9 +314,16 @@ class Empty(Workload):
 
 
 class Read(Workload):
-    def __init__(self, nbytes):
-        self.bytes_per_call = nbytes
-        self.name = f"streaming read of {nbytes / 1e6:.1f} MB (one-shot, 32 KiB per workgroup)"
+    """A plain streaming read of `nbytes` through a rotating pool; `shape` =
+    (threads per workgroup, 16-byte loads per thread per chunk, workgroups per CU of
+    a persistent grid or 0 for one-shot, nontemporal loads), as lg_bench_read_shape."""
+
+    def __init__(self, nbytes, shape=(256, 8, 0, 0)):
+        self.bytes_per_call, self.shape = nbytes, tuple(shape)
+        t, l, pc, nt = self.shape
+        grid = f"persistent {pc}/CU" if pc else "one-shot"
+        self.name = (f"streaming read of {nbytes / 1e6:.1f} MB ({t} threads x {l} loads = {t * l * 16 // 1024} KiB "
+                     f"per chunk, {grid}{', nontemporal' if nt else ''})")
         self.kernel = "k_read"
 
     def setup(self, ctx):
@@ -327,7 +336,45 @@ class Read(Workload):
 
     def step(self, i, stream):
         w = self.pool[i % len(self.pool)]
-        lh.check(lh.lib().lg_bench_read(w.ptr, self.bytes_per_call, stream))
+        lh.check(lh.lib().lg_bench_read_shape(w.ptr, self.bytes_per_call, *self.shape, stream))
+
+
+READ_SHAPES = [(t, l, pc, nt) for t in (256, 512, 1024) for l in (2, 4, 8, 16) for pc in (0, 1, 2)
+               for nt in (0, 1) if not (pc and t * l > 8192)]
+READ_SIZES = {"17.8MB": 17858560, "33.1MB": 33103872, "350MB": 350684672}
+
+
+def ceiling_sweep(ctx, hip, reps=5, launches=MIN_LAUNCHES):
+    """The fastest plain read of each byte count over READ_SHAPES: per size, one
+    rotating pool, every shape timed as the workloads are (median of `reps` x
+    `launches` back-to-back calls, HIP events on the stream)."""
+    out = {}
+    for tag, nbytes in READ_SIZES.items():
+        wl = Read(nbytes)
+        wl.setup(ctx)
+        stream = lh.Stream()
+        s = stream.ptr
+        res = []
+        for shape in READ_SHAPES:
+            wl.shape = shape
+            for i in range(3):
+                wl.step(i, s)
+            stream.sync()
+            t = [1000.0 * hip.time_ms(s, lambda: [wl.step(r * launches + i, s) for i in range(launches)]) / launches
+                 for r in range(reps)]
+            res.append((statistics.median(t), shape))
+        wl.teardown()
+        stream.destroy()
+        res.sort()
+        us, best = res[0]
+        base = next(u for u, sh in res if sh == (256, 8, 0, 0))
+        out[tag] = {"bytes": nbytes, "best_us": round(us, 3), "best_GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "best_shape": {"threads": best[0], "loads": best[1], "per_cu": best[2], "nontemporal": best[3]},
+                    "default_shape_us": round(base, 3), "shapes_tried": len(res),
+                    "top5": [[round(u, 3), list(sh)] for u, sh in res[:5]]}
+        print(f"# ceiling sweep {tag}: best {us:.3f} us {best} (default shape {base:.3f} us)", file=sys.stderr,
+              flush=True)
+    return out
 
 
 class TargetToken(Workload):
@@ -425,8 +472,7 @@ WORKLOADS = {
 }
 EXTRA = ["q8_0_m1", "q4k_down_silu", "q4k_m1_k14336", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
          "q8_0_m16_f32", "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16",
-         "dflash_block", "dflash_block_eager", "target_token", "ceil_empty", "ceil_read_17.8MB", "ceil_read_33.1MB",
-         "ceil_read_350MB"]
+         "dflash_block", "dflash_block_eager", "target_token", "ceil_empty"]
 
 
 def time_workload(ctx, hip, wl, steps, warmup, launches=None):
@@ -633,10 +679,12 @@ def main():
                 "kernel": wl.kernel}
     else:  # a workload that moves no data (the empty kernel)
         roof = {"bound": "launch", "us_per_call": head["us_per_call"], "kernel": wl.kernel}
-    ceil = extra.get("ceil_read_33.1MB") if args.workload == "q4k_m1" else None
+    sweep = None if args.no_extra else ceiling_sweep(ctx, hip)
+    ceil = sweep.get("33.1MB") if sweep and args.workload == "q4k_m1" else None
     if ceil:
-        roof.update({"ceiling_read_GBps": ceil["GBps"], "frac_of_ceiling_read": round(head["GBps"] / ceil["GBps"], 4),
-                     "ceiling_read_us": ceil["us_per_call"]})
+        roof.update({"ceiling_read_GBps": ceil["best_GBps"], "frac_of_ceiling_read": round(head["GBps"] /
+                                                                                              ceil["best_GBps"], 4),
+                     "ceiling_read_us": ceil["best_us"], "ceiling_read_shape": ceil["best_shape"]})
     if "ceil_empty" in extra:
         roof["empty_launch_us"] = extra["ceil_empty"]["us_per_call"]
         roof["empty_launch_us_graph"] = extra["ceil_empty"].get("us_per_call_graph")
@@ -660,6 +708,7 @@ def main():
         "graph_us_per_call": head.get("us_per_call_graph"),
         "roofline": roof,
         "extra": extra,
+        "ceiling_sweep": sweep,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

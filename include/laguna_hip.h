@@ -176,15 +176,24 @@ int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, floa
 /* lg_dispatch_proj_quant_batch without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments and results, bit for bit; the partial sums and arrival counters live
- * in a fixed 16 MiB + 64 KiB device array that every GPU the library runs on holds
- * until the process ends (set up by lg_init, or by the first call on a device).
- * Shapes whose workspace would exceed it (about m * n * 32 bytes for k = 4096,
- * m <= 32) are LG_EINVAL.  Calls on one GPU share the array: calls that overlap in
- * time on one GPU, on any stream, race. */
+ * arguments and results, bit for bit; the activation fragment records, partial
+ * sums and arrival counters live in a fixed 16 MiB + 64 KiB device array that
+ * every GPU the library runs on holds until the process ends (set up by lg_init,
+ * or by the first call on a device).  Shapes whose workspace
+ * (lg_proj_quant_batch_ws_bytes) exceeds it are LG_EINVAL.  Calls on one GPU share
+ * the array: calls that overlap in time on one GPU, on any stream, race. */
 int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, const void *w, float *c,
                                         uint32_t k, uint32_t n, uint32_t m, int w_dtype,
                                         void *stream);
+
+/* Device workspace bytes lg_dispatch_proj_quant_batch needs for this shape on the
+ * current device (0: the shape takes the element-wise path, which needs none).  No
+ * counterpart in the reference.  It is about (m / 16 rounded up) * (k / 256) * 17 KiB
+ * of fragment records, plus 64 KiB of arrival counters, plus the split-k partial
+ * sums: slices * min(m, 32) * n * 4 bytes when the product splits k over slices.
+ * lg_dispatch_proj_quant_batch_static accepts a shape when this is at most
+ * 16 MiB + 64 KiB. */
+uint64_t lg_proj_quant_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int w_dtype);
 
 /* Q4_K and Q8_0 weights repacked for the small-M products (no counterpart in the
  * reference, which reads GGUF blocks in place; for callers that load a model once

@@ -52,6 +52,14 @@ int lg_bench_empty(uint32_t workgroups, void *stream);
  * aligned) once: each workgroup streams a contiguous 32 KiB run, every load issued
  * up front. */
 int lg_bench_read(const void *buf, uint64_t bytes, void *stream);
+/* The same read in other shapes, for finding the fastest read of a byte count:
+ * `threads` per workgroup (256, 512, 1024), `loads` 16-byte loads per thread issued
+ * at once per chunk (2, 4, 8, 16), a one-shot grid of one chunk per workgroup
+ * (per_cu = 0) or a persistent grid of per_cu (1..8) workgroups per compute unit
+ * looping over the chunks, and plain or nontemporal loads.  lg_bench_read is
+ * (256, 8, 0, 0). */
+int lg_bench_read_shape(const void *buf, uint64_t bytes, uint32_t threads, uint32_t loads, uint32_t per_cu,
+                        uint32_t nontemporal, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,5 @@
 // Ceiling kernels for measurement (no counterpart in the reference): an empty
-// kernel and a plain streaming read.  Timed next to the projections, they give what
+// kernel and plain streaming reads.  Timed next to the projections, they give what
 // one launch and one read of the same bytes cost on this device, so that each
 // projection's time can be read against both.
 #include "lg_common.hpp"
@@ -14,23 +14,51 @@ namespace {
 
 __global__ __launch_bounds__(256) void k_empty() {}
 
-// Every thread issues its READ_L 16-byte loads at once; workgroup b reads the
-// contiguous READ_L * 4 KiB starting at b * READ_L * 4 KiB (the last one re-reads the
-// final 16 bytes for its indices past the end).
-constexpr int READ_L = 8;
-
-__global__ __launch_bounds__(256) void k_read(const uint4 *__restrict__ p, uint64_t n16) {
-    const uint64_t base = (uint64_t)blockIdx.x * READ_L * 256 + threadIdx.x;
-    uint4 v[READ_L];
-#pragma unroll
-    for (int i = 0; i < READ_L; i++) {
-        const uint64_t j = base + (uint64_t)i * 256;
-        v[i] = p[j < n16 ? j : n16 - 1];
-    }
+// A streaming read of n16 16-byte words in chunks of T * L words: every thread issues
+// its L loads of a chunk at once, thread t of the chunk reading words t, t + T, ...
+// One-shot (PERSIST false): workgroup b reads chunk b.  Persistent: the grid holds a
+// fixed number of workgroups per compute unit and workgroup b reads chunks b,
+// b + gridDim.x, ...  NT reads with the nontemporal (streaming) hint.  Indices past
+// the end re-read the last word.
+template <int T, int L, bool NT, bool PERSIST>
+__global__ __launch_bounds__(T) void k_read(const uint4 *__restrict__ p, uint64_t n16) {
+    const uint64_t per = (uint64_t)T * L, nch = (n16 + per - 1) / per;
     uint32_t s = 0;
+    for (uint64_t c = blockIdx.x; c < nch; c += PERSIST ? gridDim.x : nch) {
+        const uint64_t base = c * per + threadIdx.x;
+        uint4 v[L];
 #pragma unroll
-    for (int i = 0; i < READ_L; i++) s ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+        for (int i = 0; i < L; i++) {
+            const uint64_t j = base + (uint64_t)i * T;
+            const uint4 *q = p + (j < n16 ? j : n16 - 1);
+            v[i] = NT ? ld_stream16(q) : *q;
+        }
+#pragma unroll
+        for (int i = 0; i < L; i++) s ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
     if (s == 0x9E3779B9u) lg_bench_sink = s;
+}
+
+template <int T, int L, bool NT>
+void launch_read(const uint4 *p, uint64_t n16, uint32_t per_cu, hipStream_t s) {
+    const uint64_t nch = (n16 + (uint64_t)T * L - 1) / ((uint64_t)T * L);
+    if (per_cu) {
+        const uint64_t g = (uint64_t)per_cu * device_cus();
+        hipLaunchKernelGGL((k_read<T, L, NT, true>), dim3((uint32_t)(g < nch ? g : nch)), dim3(T), 0, s, p, n16);
+    } else {
+        hipLaunchKernelGGL((k_read<T, L, NT, false>), dim3((uint32_t)nch), dim3(T), 0, s, p, n16);
+    }
+}
+
+template <int T, bool NT>
+int read_l(const uint4 *p, uint64_t n16, uint32_t loads, uint32_t per_cu, hipStream_t s) {
+    switch (loads) {
+    case 2: launch_read<T, 2, NT>(p, n16, per_cu, s); return LG_OK;
+    case 4: launch_read<T, 4, NT>(p, n16, per_cu, s); return LG_OK;
+    case 8: launch_read<T, 8, NT>(p, n16, per_cu, s); return LG_OK;
+    case 16: launch_read<T, 16, NT>(p, n16, per_cu, s); return LG_OK;
+    default: return fail(LG_EINVAL, "lg_bench_read_shape: %u loads per thread (2, 4, 8 or 16)", loads);
+    }
 }
 
 }  // namespace
@@ -43,16 +71,30 @@ extern "C" int lg_bench_empty(uint32_t workgroups, void *stream) {
     return after_launch("lg_bench_empty", s);
 }
 
-extern "C" int lg_bench_read(const void *buf, uint64_t bytes, void *stream) {
+extern "C" int lg_bench_read_shape(const void *buf, uint64_t bytes, uint32_t threads, uint32_t loads,
+                                   uint32_t per_cu, uint32_t nontemporal, void *stream) {
     clear_error();
-    LG_REQUIRE(buf, "lg_bench_read: null buffer");
+    const char *name = "lg_bench_read_shape";
+    LG_REQUIRE(buf, "%s: null buffer", name);
     LG_REQUIRE(bytes >= 16 && bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(buf) & 15u) == 0,
-               "lg_bench_read: %llu bytes (a positive multiple of 16, 16-byte aligned)", (unsigned long long)bytes);
-    LG_EXTENT(buf, bytes, "lg_bench_read");
-    const uint64_t n16 = bytes / 16, per = (uint64_t)READ_L * 256;
-    const uint64_t wgs = (n16 + per - 1) / per;
-    LG_REQUIRE(wgs <= 0x7FFFFFFFu, "lg_bench_read: %llu bytes is too large", (unsigned long long)bytes);
+               "%s: %llu bytes (a positive multiple of 16, 16-byte aligned)", name, (unsigned long long)bytes);
+    LG_REQUIRE(per_cu <= 8, "%s: %u workgroups per compute unit (0 = one-shot grid, else 1..8)", name, per_cu);
+    LG_EXTENT(buf, bytes, name);
+    const uint64_t n16 = bytes / 16;
+    LG_REQUIRE(n16 / threads / 2 <= 0x7FFFFFFFu, "%s: %llu bytes is too large", name, (unsigned long long)bytes);
+    const uint4 *p = static_cast<const uint4 *>(buf);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_read, dim3((uint32_t)wgs), dim3(256), 0, s, static_cast<const uint4 *>(buf), n16);
-    return after_launch("lg_bench_read", s);
+    int st;
+    switch (threads) {
+    case 256: st = nontemporal ? read_l<256, true>(p, n16, loads, per_cu, s) : read_l<256, false>(p, n16, loads, per_cu, s); break;
+    case 512: st = nontemporal ? read_l<512, true>(p, n16, loads, per_cu, s) : read_l<512, false>(p, n16, loads, per_cu, s); break;
+    case 1024: st = nontemporal ? read_l<1024, true>(p, n16, loads, per_cu, s) : read_l<1024, false>(p, n16, loads, per_cu, s); break;
+    default: return fail(LG_EINVAL, "%s: %u threads per workgroup (256, 512 or 1024)", name, threads);
+    }
+    LG_TRY(st);
+    return after_launch(name, s);
+}
+
+extern "C" int lg_bench_read(const void *buf, uint64_t bytes, void *stream) {
+    return lg_bench_read_shape(buf, bytes, 256, 8, 0, 0, stream);
 }

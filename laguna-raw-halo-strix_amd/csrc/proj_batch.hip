@@ -1,36 +1,40 @@
 // Small-M products (block verify, m <= 64 activation rows): lg_dispatch_proj_quant_batch.
-// Replaces kernels/matmul.comp (never dispatched by the reference) with bf16 MFMA
-// tiles on gfx950 (v_mfma_f32_16x16x32_bf16: D[16x16] += A[16x32] * B[32x16]).
+// Replaces kernels/matmul.comp (never dispatched by the reference) with f16 MFMA
+// tiles on gfx950 (v_mfma_f32_16x16x32_f16: D[16x16] += A[16x32] * B[32x16]), in two
+// launches per call.
 //
-//   A = activations: 16 rows (tokens) x 32 k (one 32-element sub-block).  f32
-//       activations are split exactly into three bf16 parts x = x0 + x1 + x2 (each
-//       the nearest bf16 of what the previous parts leave: together all 24
-//       significant bits, so the products are f32-grade); bf16 activations are one
-//       part.  Each workgroup builds the fragments of its slice of k straight from
-//       the activations, with the per-sub-block sums X, in LDS.
-//   B = weight codes of 16 output rows x the same 32 k, built in registers from
-//       the raw blocks:  Q4_K nibble q -> bf16 1 + q/16 (one shift and one and-or
-//       per pair);  Q8_0 int8 q -> bf16 of q + 128 (exact: 8 significant bits).
-//   Epilogue per sub-block j of output row i (D = sum_k x_k B_k):
-//       Q4_K:  sum x w = 16 d sc (D - X) - dmin m X
-//       Q8_0:  sum x w = d (D - 128 X)
+//   k_mm_prep builds the A operands once per call, for every 16-token tile and
+//       256-element chunk of k (a "fragment record"): each token's chunk is scaled by
+//       a power of two 2^e that puts its largest magnitude in [2^14, 2^15), and every
+//       scaled value v is split into two f16 parts, hi = f16(v) and lo = f16(v - hi)
+//       (22 significant bits, down to the f16 subnormal step 2^-24 of the scaled
+//       chunk), laid out as the MFMA's lane fragments; with them the sums X of each
+//       32-element sub-block of the scaled values, and 2^-e.
+//   k_q4k_mf / k_q80_mf stream the weights: B = weight codes of 16 output rows x 32 k
+//       built in registers from the raw blocks as f16 subnormals (gfx950's MFMA keeps
+//       f16 denormals), so the code of a nibble is the nibble itself:
+//         Q4_K  low nibble q -> q 2^-24 (one and per pair), high nibble -> 16 q 2^-24;
+//         Q8_0  int8 q -> (q + 128) 2^-24 (xor, and per pair).
+//       Per sub-block j of output row i (D_j = sum_k A_k B_k, over both parts):
+//         Q4_K  sum x w = 2^24 d sc_j D_j (2^20 for high nibbles) - dmin m_j X_j
+//         Q8_0  sum x w = 2^24 d_j D_j - 128 d_j X_j
+//       the X terms as f32 matrix products (k = the chunk's 8 sub-blocks), and the
+//       chunk's sum scaled by 2^-e per token.
 //
 // Operand lane layout (16x16x32): lane l supplies row l%16 of A / column l%16 of B
-// at k-group l/16 (8 consecutive bf16); D row 4*(l/16)+r, column l%16 lands in
+// at k-group l/16 (8 consecutive values); D row 4*(l/16)+r, column l%16 lands in
 // lane l, register r.  Inside a k-group the order of the 8 values only has to
 // agree between A and B; both use byte order {0,2,1,3,4,6,5,7}, which is the
-// order the nibble-pair encoding produces.
+// order the masks produce.
 //
-// Work split (split-K): workgroup (blockIdx.x, blockIdx.y) = 64*RT output rows (RT
-// 16-row tiles per wavefront) x slice blockIdx.y of k (CH chunks of 256 elements:
-// one Q4_K super-block or eight Q8_0 blocks per row and chunk).  With one slice
-// the workgroup writes the result; otherwise each writes its slice's partial sums
-// and the last workgroup of a row group to finish (a per-row-group arrival counter,
-// reset by that workgroup) adds the slices in slice order: the result does not
-// depend on which workgroup finishes last.  A single plain product of many rounds of
-// workgroups (a vocab-sized head) instead has its slices only store their partial
-// sums, and a second launch (k_mm_sum) adds them in the same order, so no workgroup
-// waits for its arrival.
+// Work split: workgroup (blockIdx.x, blockIdx.y) = 64*RT output rows (RT 16-row
+// tiles per wavefront, four wavefronts) x slice blockIdx.y of k: `ch` chunks walked
+// in order, the next chunk's weights and fragment record in flight while the
+// current one is multiplied (the record double-buffered in LDS, one barrier per
+// chunk).  With one slice the workgroup writes the result; otherwise each writes
+// its slice's partial sums and the last workgroup of a row group to finish (a
+// per-row-group arrival counter, reset by that workgroup) adds the slices in slice
+// order: the result does not depend on which workgroup finishes last.
 #include <mutex>
 #include <vector>
 
@@ -40,62 +44,38 @@ namespace {
 
 using namespace lg;
 
-typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32): a low, b high.
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+// ref_half (the reference's binary16 decoder, src/dflash.rs:314-329) through the
+// hardware conversion: IEEE for normals, zeros and inf; an exponent-0 code with a
+// nonzero mantissa decodes as 2^-14 (1 + m/1024) = IEEE's m 2^-24 plus 2^-14, with
+// the code's sign.  (A NaN code stays a NaN; its payload is not kept.)
+__device__ __forceinline__ float ref_half_hw(uint32_t h) {
+    const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    const uint32_t t = h & 0x7FFFu;
+    const float q = __uint_as_float(((h & 0x8000u) << 16) | 0x38800000u);  // +-2^-14
+    return t - 1u < 0x3FFu ? f + q : f;
 }
 
-// a[j] = 16 d sc_j for the 8 sub-blocks (the code term's scales).
-__device__ __forceinline__ void q4k_scales_a(uint32_t s0, uint32_t s2, float d16, float (&a)[8]) {
-    const uint32_t sl = s0 & 0x3F3F3F3Fu, sh = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-    const float scf[8] = {ubyte_f<0>(sl), ubyte_f<1>(sl), ubyte_f<2>(sl), ubyte_f<3>(sl),
-                          ubyte_f<0>(sh), ubyte_f<1>(sh), ubyte_f<2>(sh), ubyte_f<3>(sh)};
-#pragma unroll
-    for (int j = 0; j < 8; j++) a[j] = d16 * scf[j];
+__device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(f16x8, make_uint4(a, b, c, d));
 }
 
-// The X coefficients -(16 d sc_j + dmin m_j) of sub-blocks j = g and g + 4 (g < 4, a
-// lane's k-group): the B operand of the f32 product that adds the min terms.
-__device__ __forceinline__ void q4k_min_coef(uint32_t s0, uint32_t s1, uint32_t s2, float d16, float dmin,
-                                             uint32_t g, float &c_lo, float &c_hi) {
-    const uint32_t b0 = s0 >> (8 * g), b1 = s1 >> (8 * g), b2 = s2 >> (8 * g);
-    const uint32_t sc_lo = b0 & 63u, m_lo = b1 & 63u;
-    const uint32_t sc_hi = (b2 & 15u) | (((b0 >> 6) & 3u) << 4), m_hi = ((b2 >> 4) & 15u) | (((b1 >> 6) & 3u) << 4);
-    c_lo = -__builtin_fmaf(dmin, (float)m_lo, d16 * (float)sc_lo);
-    c_hi = -__builtin_fmaf(dmin, (float)m_hi, d16 * (float)sc_hi);
-}
+// Fragment record of one (16-token tile, 256-element chunk), FR_U4 16-byte words:
+//   [0, 1024)     word (j*2 + p)*64 + l: part p (0 = hi, 1 = lo) of sub-block j's A
+//                 operand, lane l: token l%16, elements 32j + 8(l/16) + {0,2,1,3,4,6,5,7}
+//   [1024, 1056)  float2 per lane l: (X[l%16][l/16], X[l%16][l/16 + 4]), X the sums of
+//                 the scaled values over each sub-block
+//   [1056, 1060)  the 16 tokens' 2^-e
+constexpr uint32_t FR_X = 1024, FR_S = 1056, FR_U4 = 1088;
+constexpr uint32_t FR_BYTES = FR_U4 * 16;
 
-__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    uint4 u = make_uint4(a, b, c, d);
-    return __builtin_bit_cast(bf16x8, u);
-}
-
-// Q4_K nibble pairs -> bf16 (1 + q/16) pairs, byte order {0,2,1,3} per dword.
-__device__ __forceinline__ void q4_codes(uint32_t v0, uint32_t v1, bf16x8 &lo, bf16x8 &hi) {
-    uint32_t M = 0x00780078u, C = 0x3F803F80u;
-    asm volatile("" : "+v"(M), "+v"(C));  // VGPR operands: one v_and_or_b32 per pair
-    lo = as_bf16x8(((v0 << 3) & M) | C, ((v0 >> 5) & M) | C, ((v1 << 3) & M) | C, ((v1 >> 5) & M) | C);
-    hi = as_bf16x8(((v0 >> 1) & M) | C, ((v0 >> 9) & M) | C, ((v1 >> 1) & M) | C, ((v1 >> 9) & M) | C);
-}
-
-// int8 bytes -> bf16 of (q + 128), byte order {0,2,1,3} per dword.
-__device__ __forceinline__ void q8_codes(uint32_t v, uint32_t &p02, uint32_t &p13) {
-    const uint32_t u = v ^ 0x80808080u;
-    const uint32_t f0 = __float_as_uint(ubyte_f<0>(u));
-    const uint32_t f1 = __float_as_uint(ubyte_f<1>(u));
-    const uint32_t f2 = __float_as_uint(ubyte_f<2>(u));
-    const uint32_t f3 = __float_as_uint(ubyte_f<3>(u));
-    p02 = (f0 >> 16) | (f2 & 0xFFFF0000u);
-    p13 = (f1 >> 16) | (f3 & 0xFFFF0000u);
-}
+// 2^-24 scaled codes: Q4_K nibbles in place (low nibbles of bytes 0 and 2 / 1 and 3
+// of a dword: `& LO4`, high nibbles `& HI4`), Q8_0 bytes biased to unsigned.
+constexpr uint32_t LO4 = 0x000F000Fu, HI4 = 0x00F000F0u, LO8 = 0x00FF00FFu;
 
 // A launch runs up to MM_JOBS products that share the activations x (and k): job
 // j owns workgroup columns g0 .. g0 + ceil(n / (64 RT)) - 1 and writes out[m][n]
@@ -140,7 +120,7 @@ struct MmJobs {
 // rows and 2-3 the up rows, and writes only silu(gate) * up, to job 0's output.
 #define MM_JOB_SELECT                                                                     \
     uint32_t J_ = 0;                                                                      \
-    if constexpr (GLU) J_ = threadIdx.x >> 7;                                             \
+    if constexpr (GLU) J_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);             \
     else _Pragma("unroll") for (int j_ = 1; j_ < MM_JOBS; j_++) if ((uint32_t)j_ < jobs.count && \
                                                               blockIdx.x >= jobs.j[j_].g0) J_ = j_; \
     const uint8_t *w = jobs.j[J_].w;                                                      \
@@ -154,112 +134,94 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * (1.0f / (1.0f + expf(-g))) * u;
 }
 
-// The activation fragments of a slice, built in LDS by the whole workgroup.
-//   lf[((t*SB + jj)*PARTS + p)*64 + lane] : part p of the A operand of token tile t,
-//                                          sub-block jj of the slice
-//   lx[(t*SB + jj)*16 + token]            : X, the sum of the 32 activations
-// A unit is (token tile t, sub-block jj, k-group kg, token tl): 8 activations.
-// load() issues the global loads (branch-free: tokens past m and sub-blocks past k
-// read a valid element and are zeroed at store()), store() splits and writes.
-template <int TT, int PARTS, int CH, bool FUSE = false>
-struct Frags {
-    static constexpr int SB = 8 * CH;
-    static constexpr int PER = TT * 16 * SB * 4 / 256;  // units per thread
-    float4 r[PER][2];                                    // f32 activations (FUSE: gate)
-    float4 ru[FUSE ? PER : 1][2];                        // FUSE: up
-    uint4 h[PER];                                        // bf16 activations
-    __device__ __forceinline__ static void unit(int i, uint32_t &t, uint32_t &jj, uint32_t &kg, uint32_t &tl) {
-        const uint32_t u = i * 256 + threadIdx.x;
-        tl = u & 15u;
-        kg = (u >> 4) & 3u;
-        jj = (u >> 6) % SB;
-        t = u / (64 * SB);
-    }
+// ---- fragment records (k_mm_prep)
+//
+// Workgroup (c, tq) builds chunk c of the records of tokens 4 tq .. 4 tq + 3: wavefront
+// w takes token 4 tq + w (tokens past m are zero), lane q its elements 4q .. 4q + 3 of
+// the chunk, which are half of k-group (q % 8) / 2 of sub-block q / 8.  The chunk's
+// largest magnitude meets in a wavefront reduction, each sub-block's sum in DPP steps
+// over its 8 lanes.  XT: 0 = f32 activations, 1 = bf16; FUSE: the activations are
+// silu(x) * up (f32).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));   // quad_perm 1,0,3,2
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));   // quad_perm 2,3,0,1
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));  // row_ror 4
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));  // row_ror 8
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
-    __device__ __forceinline__ void load(const void *__restrict__ x, const float *__restrict__ up, uint32_t m,
-                                         uint32_t k, uint32_t sb0) {
-        const uint32_t nsb = k / 32;
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            uint32_t t, jj, kg, tl;
-            unit(i, t, jj, kg, tl);
-            const uint32_t tok = t * 16 + tl < m ? t * 16 + tl : m - 1;
-            const uint32_t sb = sb0 + jj < nsb ? sb0 + jj : nsb - 1;
-            const uint64_t e = (uint64_t)tok * k + 32 * sb + 8 * kg;
-            if constexpr (PARTS == 1) {
-                h[i] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + e);
-            } else {
-                const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e);
-                r[i][0] = p[0];
-                r[i][1] = p[1];
-                if constexpr (FUSE) {
-                    const float4 *pu = reinterpret_cast<const float4 *>(up + e);
-                    ru[i][0] = pu[0];
-                    ru[i][1] = pu[1];
-                }
-            }
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+
+template <int XT, bool FUSE>
+__global__ __launch_bounds__(256) void k_mm_prep(const void *__restrict__ x, const float *__restrict__ up,
+                                                 uint4 *__restrict__ fr, uint32_t m, uint32_t k) {
+    const uint32_t c = blockIdx.x, nb = k / QK_K;
+    const uint32_t w = threadIdx.x >> 6, q = threadIdx.x & 63u, t = blockIdx.y * 4 + w, tok = t & 15u;
+    const bool live = t < m;
+    const uint64_t e0 = (uint64_t)(live ? t : m - 1) * k + (uint64_t)QK_K * c + 4 * q;
+    float v[4];
+    if constexpr (XT == 1) {
+        const uint2 h = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + e0);
+        v[0] = bf16_to_f32(h.x & 0xFFFFu);
+        v[1] = __uint_as_float(h.x & 0xFFFF0000u);
+        v[2] = bf16_to_f32(h.y & 0xFFFFu);
+        v[3] = __uint_as_float(h.y & 0xFFFF0000u);
+    } else {
+        const float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e0);
+        v[0] = f.x;
+        v[1] = f.y;
+        v[2] = f.z;
+        v[3] = f.w;
+        if constexpr (FUSE) {  // kernels/activation.comp:21-28
+            const float4 u = *reinterpret_cast<const float4 *>(up + e0);
+            v[0] = silu_mul(v[0], u.x);
+            v[1] = silu_mul(v[1], u.y);
+            v[2] = silu_mul(v[2], u.z);
+            v[3] = silu_mul(v[3], u.w);
         }
     }
-
-    __device__ __forceinline__ void store(uint4 *lf, float *lx, uint32_t m, uint32_t k, uint32_t sb0) const {
-        const uint32_t nsb = k / 32;
+    float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < PER; i++) {
-            uint32_t t, jj, kg, tl;
-            unit(i, t, jj, kg, tl);
-            const bool valid = t * 16 + tl < m && sb0 + jj < nsb;
-            float sum;
-            uint32_t wd[PARTS][4];  // fragment slots 0..7 hold activations 0,2,1,3,4,6,5,7
-            if constexpr (PARTS == 1) {
-                const uint32_t raw[4] = {h[i].x, h[i].y, h[i].z, h[i].w};  // activations 0..7, two per word
-                // slot pairs (0,1), (2,3), (4,5), (6,7) hold activations (0,2), (1,3), (4,6), (5,7)
-                const uint32_t w0 = (raw[0] & 0xFFFFu) | (raw[1] << 16), w1 = (raw[0] >> 16) | (raw[1] & 0xFFFF0000u);
-                const uint32_t w2 = (raw[2] & 0xFFFFu) | (raw[3] << 16), w3 = (raw[2] >> 16) | (raw[3] & 0xFFFF0000u);
-                wd[0][0] = valid ? w0 : 0u;
-                wd[0][1] = valid ? w1 : 0u;
-                wd[0][2] = valid ? w2 : 0u;
-                wd[0][3] = valid ? w3 : 0u;
-                float v[8];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    v[2 * q] = __uint_as_float(wd[0][q] << 16);
-                    v[2 * q + 1] = __uint_as_float(wd[0][q] & 0xFFFF0000u);
-                }
-                sum = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-            } else {
-                float f[8] = {r[i][0].x, r[i][0].y, r[i][0].z, r[i][0].w, r[i][1].x, r[i][1].y, r[i][1].z, r[i][1].w};
-                if constexpr (FUSE) {  // kernels/activation.comp:21-28
-                    const float u[8] = {ru[i][0].x, ru[i][0].y, ru[i][0].z, ru[i][0].w,
-                                        ru[i][1].x, ru[i][1].y, ru[i][1].z, ru[i][1].w};
-#pragma unroll
-                    for (int q = 0; q < 8; q++) f[q] = silu_mul(f[q], u[q]);
-                }
-#pragma unroll
-                for (int q = 0; q < 8; q++) f[q] = valid ? f[q] : 0.0f;
-                sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
-                // pairs in slot order: (0,2) (1,3) (4,6) (5,7); each part is the nearest
-                // bf16 of what the earlier parts leave (exact residuals)
-                float lo[4] = {f[0], f[1], f[4], f[5]}, hi[4] = {f[2], f[3], f[6], f[7]};
-#pragma unroll
-                for (int p = 0; p < PARTS; p++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        wd[p][q] = pk_bf16(lo[q], hi[q]);
-                        if (p + 1 < PARTS) {
-                            lo[q] -= __uint_as_float(wd[p][q] << 16);
-                            hi[q] -= __uint_as_float(wd[p][q] & 0xFFFF0000u);
-                        }
-                    }
-            }
-#pragma unroll
-            for (int p = 0; p < PARTS; p++)
-                lf[((t * SB + jj) * PARTS + p) * 64 + kg * 16 + tl] = make_uint4(wd[p][0], wd[p][1], wd[p][2], wd[p][3]);
-            sum += __shfl_xor(sum, 16);  // the 4 k-groups of this token and sub-block
-            sum += __shfl_xor(sum, 32);
-            if (kg == 0) lx[(t * SB + jj) * 16 + tl] = sum;
-        }
+    for (int i = 0; i < 4; i++) {
+        v[i] = live ? v[i] : 0.0f;
+        amax = fmaxf(amax, fabsf(v[i]));
     }
-};
+    amax = wave_max(amax);
+    // 2^e puts the chunk's largest magnitude in [2^14, 2^15); a zero or non-finite
+    // chunk keeps e = 0 (non-finite values then reach the products as f16 inf / NaN)
+    int e = 0;
+    if (amax > 0.0f && amax <= 3.4028234664e38f) {
+        e = 15 - __builtin_amdgcn_frexp_expf(amax);
+        e = e < -126 ? -126 : (e > 126 ? 126 : e);
+    }
+    float hi[4], lo[4], s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float wv = __builtin_ldexpf(v[i], e);
+        hi[i] = (float)(_Float16)wv;
+        lo[i] = wv - hi[i];  // exact: hi is the f16 nearest wv
+        s += wv;
+    }
+    // the sub-block's sum over its 8 lanes: quads, then the half-row mirror (lane i and
+    // 7 - i of each 8), the same float in all 8
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x141, 0xF, 0xF, false));
+    uint4 *rec = fr + ((uint64_t)(t >> 4) * nb + c) * FR_U4;
+    const uint32_t j = q >> 3, kg = (q & 7u) >> 1, half = q & 1u, lane = kg * 16 + tok;
+    uint2 *wa = reinterpret_cast<uint2 *>(rec + (j * 2) * 64 + lane) + half;
+    wa[0] = make_uint2(pk_f16(hi[0], hi[2]), pk_f16(hi[1], hi[3]));
+    wa[128] = make_uint2(pk_f16(lo[0], lo[2]), pk_f16(lo[1], lo[3]));  // part 1: 64 words on
+    float *rf = reinterpret_cast<float *>(rec);
+    if ((q & 7u) == 0) rf[4 * FR_X + ((j & 3u) * 16 + tok) * 2 + (j >> 2)] = s;
+    if (q == 0) rf[4 * FR_S + tok] = __builtin_ldexpf(1.0f, -e);
+}
 
 // NORM: token threadIdx.x / LT of the launch (LT = 16 / TT lanes per token) takes its
 // partial sums p = sub, sub + LT, ... (branch-free: slots past the columns and tokens
@@ -506,299 +468,303 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
     }
 }
 
-// A split-k workgroup of a wide launch: slice blockIdx.y's partial sums of the
-// wavefront's rows, part[slice][token][row], with plain stores; the launch after it
-// (k_mm_sum) adds the slices, so the workgroup leaves as soon as they are issued.
-template <int TT, int RT>
-__device__ __forceinline__ void store_slice(const float (&acc)[RT][TT][4], float *part, uint32_t rt0, uint32_t m,
-                                            uint32_t n) {
+// ---- products over fragment records
+//
+// The weights of one chunk (256 elements of k) for a wavefront's RT row tiles: lane l
+// holds row l%16's pieces of k-group l/16.
+//   Q4_K: the super-block header (16 bytes) and, for each 64-element group g, the 8
+//         quant bytes 32g + 8(l/16) .. +7 (low nibbles: sub-block 2g, high: 2g + 1).
+//   Q8_0: per block j of the chunk, its f16 scale and quant bytes 8(l/16) .. +7.
+template <int RT>
+struct Q4kChunk {
+    uint4 hd[RT];
+    uint2 qv[RT][4];
+};
+template <int RT>
+struct Q80Chunk {
+    uint32_t sc[RT][4];  // the 8 scales, two per word
+    uint2 qv[RT][8];
+};
+
+// Rows past n (and their tiles) read row n-1 / the last tile: loads stay in bounds and
+// the results are never stored.
+template <int RT, bool TILED>
+__device__ __forceinline__ void load_q4k(Q4kChunk<RT> &W, const uint8_t *__restrict__ w, uint32_t n, uint32_t rt0,
+                                         uint32_t nb, uint32_t cb, uint64_t row_bytes) {
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
-    float *ps = part + (uint64_t)blockIdx.y * m * n;
 #pragma unroll
     for (int i = 0; i < RT; i++) {
-        const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+        if constexpr (TILED) {  // 2304-byte tiles: each load reads 256 (headers) or 512 contiguous bytes
+            const uint32_t ntiles = (n + 15) / 16, t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
+            const uint8_t *tb = w + ((uint64_t)t * nb + cb) * Q4K_TILE;
+            W.hd[i] = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
 #pragma unroll
-        for (int t = 0; t < TT; t++)
+            for (int g = 0; g < 4; g++) W.qv[i][g] = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * g + 8 * l);
+        } else {
+            // the tile's first row (scalar; tiles past n read the last tile) plus the
+            // lane's row within it (clamped to n - 1)
+            const uint32_t rlast = (n - 1) & ~15u, r0 = (rt0 + i) * 16 < rlast ? (rt0 + i) * 16 : rlast;
+            const uint32_t rl = r0 + (l & 15u) < n ? (l & 15u) : n - 1 - r0;
+            const uint8_t *blk = w + (uint64_t)r0 * row_bytes + (uint64_t)cb * Q4K_BYTES;
+            const uint32_t lo = rl * (uint32_t)row_bytes;
+            W.hd[i] = *reinterpret_cast<const uint4 *>(blk + lo);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t tok = t * 16 + 4 * kg + r;
-                if (row < n && tok < m) ps[(uint64_t)tok * n + row] = acc[i][t][r];
-            }
+            for (int g = 0; g < 4; g++) W.qv[i][g] = *reinterpret_cast<const uint2 *>(blk + lo + 16 + 32 * g + 8 * kg);
+        }
     }
 }
 
-// The finishing launch of a wide split-k product (one plain product: no residual, no
-// epilogue).  Workgroup (c, t) covers rows 64c .. 64c+63 and tokens 16t .. 16t+15:
-// thread (token threadIdx.x / 16, quad threadIdx.x % 16) adds rows 4 quad .. 4 quad + 3
-// of the S slices in slice order, with the loads of SUM_MAXS slices in flight at once.
-// V4: rows in float4 (n % 4 == 0 and a 16-byte aligned output).
-constexpr uint32_t SUM_ROWS = 64, SUM_MAXS = 16;
-// Launches of at least this many workgroups (about four rounds of the resident ones)
-// finish in k_mm_sum: there every workgroup's wait for its arrival would be paid in
-// each round.  Smaller ones finish in the kernel, where the last workgroups' reads of
-// the partial sums overlap other columns' products (a separate finishing launch cost
-// those 5-6 us per product on the draft's shapes).
-constexpr uint64_t WIDE_MIN_WGS = 4096;
-template <bool V4>
-__global__ __launch_bounds__(256) void k_mm_sum(const float *__restrict__ part, float *__restrict__ out, uint32_t m,
-                                                uint32_t n, uint32_t S) {
-    const uint32_t tl = threadIdx.x >> 4, qd = threadIdx.x & 15u;
-    const uint32_t tok = 16 * blockIdx.y + tl, row0 = blockIdx.x * SUM_ROWS + 4 * qd;
-    const uint64_t mn = (uint64_t)m * n;
-    const uint32_t tc = tok < m ? tok : m - 1;  // branch-free loads: rows and tokens past the end are clamped
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t q0 = 0; q0 < S; q0 += SUM_MAXS) {
-        float4 pv[SUM_MAXS];
+// Raw Q8_0 blocks are 2-byte aligned: the quant bytes of a lane are one 8-byte load
+// at 2-byte alignment (gfx950 global loads need no natural alignment).
+struct __attribute__((packed, aligned(2))) U32x2a2 {
+    uint32_t x, y;
+};
+
+template <int RT, bool TILED>
+__device__ __forceinline__ void load_q80(Q80Chunk<RT> &W, const uint8_t *__restrict__ w, uint32_t n, uint32_t rt0,
+                                         uint32_t nb, uint32_t cb, uint64_t row_bytes) {
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
 #pragma unroll
-        for (uint32_t g = 0; g < SUM_MAXS; g++) {
-            const uint32_t q = q0 + g < S ? q0 + g : S - 1;
-            const float *src = part + q * mn + (uint64_t)tc * n;
-            if constexpr (V4) {
-                pv[g] = *reinterpret_cast<const float4 *>(src + (row0 < n ? row0 : n - 4));
-            } else {
-                float e4[4];
+    for (int i = 0; i < RT; i++) {
+        if constexpr (TILED) {  // 4352-byte tiles: a row's 8 scales in one 16-byte load, 512 contiguous bytes per quant load
+            const uint32_t ntiles = (n + 15) / 16, t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
+            const uint8_t *tb = w + ((uint64_t)t * nb + cb) * Q80_TILE;
+            const uint4 s = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
+            W.sc[i][0] = s.x;
+            W.sc[i][1] = s.y;
+            W.sc[i][2] = s.z;
+            W.sc[i][3] = s.w;
 #pragma unroll
-                for (int e = 0; e < 4; e++) e4[e] = src[row0 + e < n ? row0 + e : n - 1];
-                pv[g] = make_float4(e4[0], e4[1], e4[2], e4[3]);
+            for (int j = 0; j < 8; j++) W.qv[i][j] = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * j + 8 * l);
+        } else {
+            const uint32_t rlast = (n - 1) & ~15u, r0 = (rt0 + i) * 16 < rlast ? (rt0 + i) * 16 : rlast;
+            const uint32_t rl = r0 + (l & 15u) < n ? (l & 15u) : n - 1 - r0;
+            const uint8_t *blk = w + (uint64_t)r0 * row_bytes + (uint64_t)cb * 8 * Q80_BYTES;
+            const uint32_t lo = rl * (uint32_t)row_bytes;
+            uint32_t d[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                d[j] = *reinterpret_cast<const uint16_t *>(blk + lo + j * Q80_BYTES);
+                const U32x2a2 v = *reinterpret_cast<const U32x2a2 *>(blk + lo + j * Q80_BYTES + 2 + 8 * kg);
+                W.qv[i][j] = make_uint2(v.x, v.y);
             }
+#pragma unroll
+            for (int h = 0; h < 4; h++) W.sc[i][h] = d[2 * h] | (d[2 * h + 1] << 16);
         }
-#pragma unroll
-        for (uint32_t g = 0; g < SUM_MAXS; g++)
-            if (q0 + g < S) {
-                v[0] += pv[g].x;
-                v[1] += pv[g].y;
-                v[2] += pv[g].z;
-                v[3] += pv[g].w;
-            }
-    }
-    if (tok >= m) return;
-    const uint64_t o = (uint64_t)tok * n + row0;
-    if (V4 && row0 < n) {
-        *reinterpret_cast<float4 *>(out + o) = make_float4(v[0], v[1], v[2], v[3]);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (row0 + e < n) out[o + e] = v[e];
     }
 }
 
-// Q4_K.  Wavefront w owns row tiles (4*blockIdx.x + w)*RT .. +RT-1; each activation
-// fragment read from LDS serves all RT tiles.  Order of work: the activation loads,
-// every weight load of the slice (branch-free: rows past n and blocks past k read
-// row n-1 / the last block and are never used), the fragment build while the
-// weights are in flight, then the products.
-template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM, bool WIDE = false>
-__global__ __launch_bounds__(256) void k_q4k_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
-                                                uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
-    MM_JOB_SELECT;
-    constexpr int SB = 8 * CH;
-    __shared__ uint4 lf[TT * SB * PARTS * 64];
-    __shared__ float lx[TT * SB * 16];
-    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
-    const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
-    const uint32_t nb = k / QK_K, b0 = blockIdx.y * CH;
-    Frags<TT, PARTS, CH, FUSE> fr;
-    fr.load(x, up, m, k, 8 * b0);
-    uint4 hd[RT][CH];
-    uint2 qv[RT][CH][4];
-    if (jobs.tiled) {  // 2304-byte tiles: each load is 512 (quants) or 256 (headers) contiguous bytes
-        const uint32_t ntiles = (n + 15) / 16;
+// One fragment record per token tile into registers and from there into LDS.  Thread
+// t copies words t, t + 256, t + 512, t + 768 and 1024 + t % 64 (the last 64 words are
+// read and written by all four wavefronts, with the same values): every load and store
+// is unconditional, so the compiler keeps the loads where they are issued.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <int TT>
+struct RecCopy {
+    u32x4 v[TT][5];
+    __device__ __forceinline__ static uint32_t word(int i) {
+        return i < 4 ? threadIdx.x + 256 * i : 1024 + (threadIdx.x & 63u);
+    }
+    __device__ __forceinline__ void load(const uint4 *fr, uint32_t nb, uint32_t c) {
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const uint32_t t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
+        for (int t = 0; t < TT; t++) {
+            const u32x4 *src = reinterpret_cast<const u32x4 *>(fr + ((uint64_t)t * nb + c) * FR_U4);
 #pragma unroll
-            for (int cb = 0; cb < CH; cb++) {
-                const uint8_t *tb = w + ((uint64_t)t * nb + (b0 + cb < nb ? b0 + cb : nb - 1)) * Q4K_TILE;
-                hd[i][cb] = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
-#pragma unroll
-                for (int g = 0; g < 4; g++) qv[i][cb][g] = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * g + 8 * l);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const uint32_t row = (rt0 + i) * 16 + (l & 15u);
-            const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
-#pragma unroll
-            for (int cb = 0; cb < CH; cb++) {
-                const uint8_t *blk = wr + (uint64_t)(b0 + cb < nb ? b0 + cb : nb - 1) * Q4K_BYTES;
-                hd[i][cb] = *reinterpret_cast<const uint4 *>(blk);
-#pragma unroll
-                for (int g = 0; g < 4; g++) qv[i][cb][g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kg);
-            }
+            for (int i = 0; i < 5; i++) v[t][i] = src[word(i)];
         }
     }
-    asm volatile("" ::: "memory");  // keep the weight loads issued ahead of the fragment build
-    fr.store(lf, lx, m, k, 8 * b0);
-    __syncthreads();
-    float acc[RT][TT][4];
-#pragma unroll
-    for (int i = 0; i < RT; i++)
+    __device__ __forceinline__ void store(uint4 *lds) const {
+        u32x4 *d = reinterpret_cast<u32x4 *>(lds);
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
+            for (int i = 0; i < 5; i++) d[t * FR_U4 + word(i)] = v[t][i];
+    }
+};
+static_assert(FR_U4 == 1088, "RecCopy covers 1024 + 64 words");
+
+// The chunk's min / bias terms and token scales: tmp += X (16x4) * coef (4x16) for
+// sub-blocks kg and kg + 4, then acc += tmp * 2^-e per token.
+template <int TT, int RT>
+__device__ __forceinline__ void chunk_close(const uint4 *lds, f32x4 (&tmp)[RT][TT], const float (&cm)[RT][2],
+                                            float (&acc)[RT][TT][4]) {
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
 #pragma unroll
-    for (int cb = 0; cb < CH; cb++) {
-        if (b0 + cb >= nb) continue;  // uniform: past the end of k
-        // code terms a_j D_j per sub-block on the VALU; the super-block's min terms
-        // -(a_j + dmin m_j) X_j as two f32 matrix products (k = the 8 sub-blocks)
-        // accumulated into acc: A = X[token][sub-block], B = coefficient[sub-block][row]
-        float sa[RT][8], cmin[RT][2];
+    for (int t = 0; t < TT; t++) {
+        const float2 xv = reinterpret_cast<const float2 *>(lds + t * FR_U4 + FR_X)[l];
+        const float4 sv = reinterpret_cast<const float4 *>(lds + t * FR_U4 + FR_S)[kg];
 #pragma unroll
         for (int i = 0; i < RT; i++) {
-            const float d16 = 16.0f * ref_half(hd[i][cb].x & 0xFFFFu), dmin = ref_half(hd[i][cb].x >> 16);
-            q4k_scales_a(hd[i][cb].y, hd[i][cb].w, d16, sa[i]);
-            q4k_min_coef(hd[i][cb].y, hd[i][cb].z, hd[i][cb].w, d16, dmin, kg, cmin[i][0], cmin[i][1]);
+            f32x4 C = tmp[i][t];
+            C = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, cm[i][0], C, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, cm[i][1], C, 0, 0, 0);
+            acc[i][t][0] = __builtin_fmaf(C[0], sv.x, acc[i][t][0]);
+            acc[i][t][1] = __builtin_fmaf(C[1], sv.y, acc[i][t][1]);
+            acc[i][t][2] = __builtin_fmaf(C[2], sv.z, acc[i][t][2]);
+            acc[i][t][3] = __builtin_fmaf(C[3], sv.w, acc[i][t][3]);
         }
+    }
+}
+
+// The products of two sub-blocks (j0, j0 + 1) for every tile and token tile, each over
+// both parts of A, and their scaled sum into tmp (started when `add` is false).  With
+// one tile and one token tile both sub-blocks' products are issued before the scale
+// multiplications (two independent chains); otherwise one sub-block at a time, whose
+// RT * TT chains already overlap (and keep the register count down).
+template <int TT, int RT>
+__device__ __forceinline__ void mma_pair(const f16x8 (&A)[TT][2][2], const f16x8 (&B)[RT][2], const float (&a)[RT][8],
+                                         int j0, bool add, f32x4 (&tmp)[RT][TT]) {
+    constexpr int G = RT * TT == 1 ? 2 : 1;  // sub-blocks per group of products
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            bf16x8 blo[RT], bhi[RT];
+    for (int u0 = 0; u0 < 2; u0 += G) {
+        f32x4 D[RT][G][TT];
 #pragma unroll
-            for (int i = 0; i < RT; i++) q4_codes(qv[i][cb][g].x, qv[i][cb][g].y, blo[i], bhi[i]);
+        for (int i = 0; i < RT; i++)
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const uint32_t j = 2 * g + u, jj = cb * 8 + j;
-                bf16x8 A[TT][PARTS];
+            for (int v = 0; v < G; v++)
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+                    D[i][v][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][u0 + v][0], B[i][u0 + v],
+                                                                        (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int v = 0; v < G; v++)
+#pragma unroll
+                for (int t = 0; t < TT; t++)
+                    D[i][v][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[t][u0 + v][1], B[i][u0 + v], D[i][v][t], 0,
+                                                                        0, 0);
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int v = 0; v < G; v++)
 #pragma unroll
                 for (int t = 0; t < TT; t++)
 #pragma unroll
-                    for (int p = 0; p < PARTS; p++)
-                        A[t][p] = __builtin_bit_cast(bf16x8, lf[((t * SB + jj) * PARTS + p) * 64 + l]);
-#pragma unroll
-                for (int i = 0; i < RT; i++) {
-                    const float a = sa[i][j];
-#pragma unroll
-                    for (int t = 0; t < TT; t++) {
-                        f32x4 D = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int p = 0; p < PARTS; p++)
-                            D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t][p], u ? bhi[i] : blo[i], D, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; r++) acc[i][t][r] = __builtin_fmaf(a, D[r], acc[i][t][r]);
+                    for (int r = 0; r < 4; r++) {
+                        const float aj = a[i][j0 + u0 + v];
+                        tmp[i][t][r] = add || u0 + v > 0 ? __builtin_fmaf(aj, D[i][v][t][r], tmp[i][t][r])
+                                                         : aj * D[i][v][t][r];
                     }
-                }
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-            const float x_lo = lx[(t * SB + cb * 8 + kg) * 16 + (l & 15u)];
-            const float x_hi = lx[(t * SB + cb * 8 + kg + 4) * 16 + (l & 15u)];
-#pragma unroll
-            for (int i = 0; i < RT; i++) {
-                f32x4 C = {acc[i][t][0], acc[i][t][1], acc[i][t][2], acc[i][t][3]};
-                C = __builtin_amdgcn_mfma_f32_16x16x4f32(x_lo, cmin[i][0], C, 0, 0, 0);
-                C = __builtin_amdgcn_mfma_f32_16x16x4f32(x_hi, cmin[i][1], C, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[i][t][r] = C[r];
-            }
-        }
     }
-    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
-    static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lf), "the head exchange fits in the fragment LDS");
-    if constexpr (WIDE) {  // the slices' sums are added by k_mm_sum
-        store_slice<TT, RT>(acc, part, rt0, m, n);
-        return;
-    }
-    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
-                              jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
 
-// Q8_0: a chunk is 8 blocks of 34 bytes (2-byte aligned).  Raw rows are staged through
-// LDS with 16-byte loads where they fit (see STAGE), else read as 16-bit words.
-template <int TT, int PARTS, int CH, int RT, bool FUSE, bool GLU, bool NORM, bool WIDE = false>
-__global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, const float *__restrict__ up, MmJobs jobs,
-                                                uint32_t *cnt, uint32_t m, uint32_t k, uint64_t row_bytes) {
-    MM_JOB_SELECT;
-    constexpr int SB = 8 * CH;
-    __shared__ uint4 lf[TT * SB * PARTS * 64];
-    __shared__ float lx[TT * SB * 16];
-    const uint32_t l = threadIdx.x & 63u, wave = threadIdx.x >> 6, kg = l >> 4;
-    const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
-    const uint32_t nsb = k / 32, sb0 = blockIdx.y * SB;
-    // raw rows can be staged through the fragment LDS when the wavefronts' rows fit (not
-    // for a gate/up pair, whose halves read different weights: the staging's barrier
-    // must be reached by the whole workgroup on one condition)
-    constexpr bool STAGE = !GLU && 64u * RT * SB * Q80_BYTES <= sizeof(lf);
-    Frags<TT, PARTS, CH, FUSE> fr;
-    fr.load(x, up, m, k, sb0);
-    uint32_t dq[RT][SB], v0[RT][SB], v1[RT][SB];
-    if (jobs.tiled) {  // 4352-byte tiles: one 16-byte load for a row's 8 scales, 512 contiguous bytes per quant load
-        const uint32_t ntiles = (n + 15) / 16, nc = k / 256;
+// One Q4_K chunk: per tile the header's scales a_j = 2^24 d sc_j (2^20 for the high
+// nibbles' sub-blocks) and the min coefficients -dmin m_j of sub-blocks kg, kg + 4.
+// Per 64-element group g, every (tile, sub-block, token tile) product is issued before
+// the scale multiplications that use them, so the matrix products overlap.
+template <int TT, int RT>
+__device__ __forceinline__ void q4k_chunk(const uint4 *lds, const Q4kChunk<RT> &W, float (&acc)[RT][TT][4]) {
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
+    float a[RT][8], cm[RT][2];
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const uint32_t t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
-#pragma unroll
-            for (int cc = 0; cc < CH; cc++) {
-                const uint32_t c = blockIdx.y * CH + cc;
-                const uint8_t *tb = w + ((uint64_t)t * nc + (c < nc ? c : nc - 1)) * Q80_TILE;
-                const uint4 sc = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
-                const uint32_t sw[4] = {sc.x, sc.y, sc.z, sc.w};
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    const uint2 q = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * jj + 8 * l);
-                    dq[i][8 * cc + jj] = (sw[jj >> 1] >> (16 * (jj & 1))) & 0xFFFFu;
-                    v0[i][8 * cc + jj] = q.x;
-                    v1[i][8 * cc + jj] = q.y;
-                }
-            }
-        }
-    } else if (STAGE && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 && row_bytes % 16 == 0) {  // uniform
-        // Raw rows staged through the fragment LDS (free until the fragments are built):
-        // each wavefront reads its 16 RT rows' SB*34 bytes of the slice with 16-byte loads
-        // (RP pieces per row), then every lane picks its blocks' scale and quants out of
-        // LDS as 16-bit words.  Pieces past the end of a row re-read its last piece.
-        constexpr uint32_t RP = SB * Q80_BYTES / 16, NP = 16 * RT * RP, NL = (NP + 63) / 64;
-        uint4 *st = lf + wave * NP;
-        const uint64_t c0 = (uint64_t)sb0 * Q80_BYTES;
-        uint4 pc[NL];
-#pragma unroll
-        for (uint32_t i = 0; i < NL; i++) {
-            const uint32_t e = l + 64 * i < NP ? l + 64 * i : NP - 1;
-            const uint32_t r = e / RP, row = rt0 * 16 + r;
-            const uint64_t o = c0 + 16 * (e % RP);
-            pc[i] = *reinterpret_cast<const uint4 *>(w + (uint64_t)(row < n ? row : n - 1) * row_bytes +
-                                                     (o + 16 <= row_bytes ? o : row_bytes - 16));
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < NL; i++)
-            if (l + 64 * i < NP) st[l + 64 * i] = pc[i];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const uint16_t *sw = reinterpret_cast<const uint16_t *>(st);
-#pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const uint16_t *sr = sw + (i * 16 + (l & 15u)) * RP * 8;
-#pragma unroll
-            for (int j = 0; j < SB; j++) {
-                const uint16_t *blk = sr + j * (Q80_BYTES / 2);
-                const uint16_t *q = blk + 1 + 4 * kg;
-                dq[i][j] = blk[0];
-                v0[i][j] = q[0] | ((uint32_t)q[1] << 16);
-                v1[i][j] = q[2] | ((uint32_t)q[3] << 16);
-            }
-        }
-        __syncthreads();  // every wavefront has its weights: the LDS is free for the fragments
-    } else {
-#pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const uint32_t row = (rt0 + i) * 16 + (l & 15u);
-            const uint8_t *wr = w + (uint64_t)(row < n ? row : n - 1) * row_bytes;
-#pragma unroll
-            for (int j = 0; j < SB; j++) {
-                const uint16_t *blk =
-                    reinterpret_cast<const uint16_t *>(wr + (uint64_t)(sb0 + j < nsb ? sb0 + j : nsb - 1) * Q80_BYTES);
-                const uint16_t *q = blk + 1 + 4 * kg;
-                dq[i][j] = blk[0];
-                v0[i][j] = q[0] | ((uint32_t)q[1] << 16);
-                v1[i][j] = q[2] | ((uint32_t)q[3] << 16);
-            }
-        }
+    for (int i = 0; i < RT; i++) {
+        const float d = ref_half_hw(W.hd[i].x & 0xFFFFu), dmin = ref_half_hw(W.hd[i].x >> 16);
+        const uint32_t s0 = W.hd[i].y, s1 = W.hd[i].z, s2 = W.hd[i].w;
+        const uint32_t sl = s0 & 0x3F3F3F3Fu, sh = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const float d24 = d * 16777216.0f, d20 = d * 1048576.0f;
+        a[i][0] = d24 * ubyte_f<0>(sl);
+        a[i][1] = d20 * ubyte_f<1>(sl);
+        a[i][2] = d24 * ubyte_f<2>(sl);
+        a[i][3] = d20 * ubyte_f<3>(sl);
+        a[i][4] = d24 * ubyte_f<0>(sh);
+        a[i][5] = d20 * ubyte_f<1>(sh);
+        a[i][6] = d24 * ubyte_f<2>(sh);
+        a[i][7] = d20 * ubyte_f<3>(sh);
+        const uint32_t sh8 = 8 * kg;
+        const uint32_t m_lo = (s1 >> sh8) & 63u;
+        const uint32_t m_hi = ((s2 >> (sh8 + 4)) & 15u) | (((s1 >> (sh8 + 6)) & 3u) << 4);
+        cm[i][0] = -dmin * (float)m_lo;
+        cm[i][1] = -dmin * (float)m_hi;
     }
-    asm volatile("" ::: "memory");  // keep the weight loads issued ahead of the fragment build
-    fr.store(lf, lx, m, k, sb0);
-    __syncthreads();
+    f32x4 tmp[RT][TT];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        f16x8 A[TT][2][2];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    A[t][u][p] = __builtin_bit_cast(f16x8, lds[t * FR_U4 + ((2 * g + u) * 2 + p) * 64 + l]);
+        f16x8 B[RT][2];
+#pragma unroll
+        for (int i = 0; i < RT; i++) {
+            const uint32_t v0 = W.qv[i][g].x, v1 = W.qv[i][g].y, u0 = v0 >> 8, u1 = v1 >> 8;
+            B[i][0] = as_f16x8(v0 & LO4, u0 & LO4, v1 & LO4, u1 & LO4);
+            B[i][1] = as_f16x8(v0 & HI4, u0 & HI4, v1 & HI4, u1 & HI4);
+        }
+        mma_pair<TT, RT>(A, B, a, 2 * g, g > 0, tmp);
+    }
+    chunk_close<TT, RT>(lds, tmp, cm, acc);
+}
+
+// One Q8_0 chunk: a_j = 2^24 d_j, bias coefficients -128 d_j of blocks kg, kg + 4.
+// Per pair of blocks, the products are issued before the scale multiplications.
+template <int TT, int RT>
+__device__ __forceinline__ void q80_chunk(const uint4 *lds, const Q80Chunk<RT> &W, float (&acc)[RT][TT][4]) {
+    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
+    float a[RT][8], cm[RT][2];
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[i][j] = 16777216.0f * ref_half_hw((W.sc[i][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+        // blocks kg and kg + 4: words kg / 2 and kg / 2 + 2, half kg % 2
+        const uint32_t wl = kg < 2 ? W.sc[i][0] : W.sc[i][1], wh = kg < 2 ? W.sc[i][2] : W.sc[i][3];
+        const uint32_t sh = 16 * (kg & 1u);
+        cm[i][0] = -128.0f * ref_half_hw((wl >> sh) & 0xFFFFu);
+        cm[i][1] = -128.0f * ref_half_hw((wh >> sh) & 0xFFFFu);
+    }
+    f32x4 tmp[RT][TT];
+#pragma unroll
+    for (int jp = 0; jp < 4; jp++) {
+        f16x8 A[TT][2][2];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    A[t][u][p] = __builtin_bit_cast(f16x8, lds[t * FR_U4 + ((2 * jp + u) * 2 + p) * 64 + l]);
+        f16x8 B[RT][2];
+#pragma unroll
+        for (int i = 0; i < RT; i++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t v0 = W.qv[i][2 * jp + u].x ^ 0x80808080u, v1 = W.qv[i][2 * jp + u].y ^ 0x80808080u;
+                B[i][u] = as_f16x8(v0 & LO8, (v0 >> 8) & LO8, v1 & LO8, (v1 >> 8) & LO8);
+            }
+        mma_pair<TT, RT>(A, B, a, 2 * jp, jp > 0, tmp);
+    }
+    chunk_close<TT, RT>(lds, tmp, cm, acc);
+}
+
+// The small-M product.  Wavefront w owns row tiles (4*bx + w)*RT .. +RT-1 (GLU: gate
+// rows in wavefronts 0-1, up rows in 2-3) over chunks blockIdx.y*ch .. +ch-1 of k.
+// Software pipeline, per chunk c: the record of chunk c (loaded into registers during
+// chunk c-1) is stored to LDS buffer c%2 and the workgroup meets at a barrier; then the
+// record of chunk c+1 and the weights of chunk c+2 (a ring of three chunks in
+// registers) are issued, and chunk c is multiplied.  The loads of one chunk are used
+// only by the next iteration, so nothing moves them next to their use.
+template <bool Q4, int TT, int RT, bool GLU, bool NORM, bool TILED>
+__global__ __launch_bounds__(256) void k_mm_mf(const uint4 *fr, MmJobs jobs, uint32_t *cnt, uint32_t m, uint32_t k,
+                                               uint64_t row_bytes, uint32_t ch) {
+    MM_JOB_SELECT;
+    __shared__ uint4 lrec[2][TT * FR_U4];
+    // uniform over the wavefront: row-tile addresses are scalar
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
+    const uint32_t nb = k / QK_K, c0 = blockIdx.y * ch, nch = nb - c0 < ch ? nb - c0 : ch;
+    using Chunk = typename std::conditional<Q4, Q4kChunk<RT>, Q80Chunk<RT>>::type;
+    Chunk Wc[3];
+    // chunk ci of the slice; past the slice the last chunk again (loads stay in bounds,
+    // never multiplied)
+    auto load_w = [&](Chunk &Wd, uint32_t ci) {
+        const uint32_t c = c0 + (ci < nch ? ci : nch - 1);
+        if constexpr (Q4) load_q4k<RT, TILED>(Wd, w, n, rt0, nb, c, row_bytes);
+        else load_q80<RT, TILED>(Wd, w, n, rt0, nb, c, row_bytes);
+    };
     float acc[RT][TT][4];
 #pragma unroll
     for (int i = 0; i < RT; i++)
@@ -806,44 +772,39 @@ __global__ __launch_bounds__(256) void k_q80_mm(const void *__restrict__ x, cons
         for (int t = 0; t < TT; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
+    RecCopy<TT> rc;
+    rc.load(fr, nb, c0);
+    load_w(Wc[0], 0);
+    load_w(Wc[1], 1);
+    // chunk 0 ahead of the loop, so the loop is entered in the state it repeats
+    rc.store(lrec[0]);
+    __syncthreads();
+    rc.load(fr, nb, c0 + (1 < nch ? 1 : 0));
+    __builtin_amdgcn_sched_barrier(0);  // issue order: the record, then the weights
+    load_w(Wc[2], 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (Q4) q4k_chunk<TT, RT>(lrec[0], Wc[0], acc);
+    else q80_chunk<TT, RT>(lrec[0], Wc[0], acc);
+    // three chunks per iteration, so the ring's registers are named at compile time
+    // (chunk c in Wc[c % 3]: ci = 1 mod 3)
+    for (uint32_t ci = 1; ci < nch; ci += 3) {
 #pragma unroll
-    for (int j = 0; j < SB; j++) {
-        if (sb0 + j >= nsb) continue;  // uniform: past the end of k
-        bf16x8 A[TT][PARTS];
-        float4 X[TT];
-#pragma unroll
-        for (int t = 0; t < TT; t++) {
-#pragma unroll
-            for (int p = 0; p < PARTS; p++)
-                A[t][p] = __builtin_bit_cast(bf16x8, lf[((t * SB + j) * PARTS + p) * 64 + l]);
-            X[t] = *reinterpret_cast<const float4 *>(lx + (t * SB + j) * 16 + 4 * kg);
-        }
-#pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const float d = ref_half(dq[i][j]);
-            uint32_t a0, a1, a2, a3;
-            q8_codes(v0[i][j], a0, a1);
-            q8_codes(v1[i][j], a2, a3);
-            const bf16x8 B = as_bf16x8(a0, a1, a2, a3);
-#pragma unroll
-            for (int t = 0; t < TT; t++) {
-                f32x4 D = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int p = 0; p < PARTS; p++) D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[t][p], B, D, 0, 0, 0);
-                acc[i][t][0] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].x, D[0]), acc[i][t][0]);
-                acc[i][t][1] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].y, D[1]), acc[i][t][1]);
-                acc[i][t][2] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].z, D[2]), acc[i][t][2]);
-                acc[i][t][3] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, X[t].w, D[3]), acc[i][t][3]);
-            }
+        for (int h = 0; h < 3; h++) {
+            const uint32_t c = ci + h;
+            if (c >= nch) break;  // uniform
+            rc.store(lrec[c & 1u]);
+            __syncthreads();
+            rc.load(fr, nb, c0 + (c + 1 < nch ? c + 1 : nch - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(Wc[h], c + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (Q4) q4k_chunk<TT, RT>(lrec[c & 1u], Wc[(h + 1) % 3], acc);
+            else q80_chunk<TT, RT>(lrec[c & 1u], Wc[(h + 1) % 3], acc);
         }
     }
-    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lf), "GLU exchange fits in the fragment LDS");
-    static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lf), "the head exchange fits in the fragment LDS");
-    if constexpr (WIDE) {  // the slices' sums are added by k_mm_sum
-        store_slice<TT, RT>(acc, part, rt0, m, n);
-        return;
-    }
-    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lf), jobs, k,
+    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lrec), "GLU exchange fits in the record LDS");
+    static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lrec), "the head exchange fits in the record LDS");
+    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(&lrec[0][0]), jobs, k,
                               jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
 }
 
@@ -903,79 +864,84 @@ __global__ __launch_bounds__(256) void k_generic_batch(const void *__restrict__ 
     }
 }
 
-// Launch shape: CH chunks per slice (the slice's fragments fill LDS: 48 KB for f32
-// activations), one slice per workgroup column, RT row tiles per wavefront: the
-// most that still gives 256 workgroups (n is the jobs' total rows).
+// Launch shape: RT 16-row tiles per wavefront, `ch` chunks of 256 elements per k
+// slice, `slices` = ceil(nb / ch) workgroup rows.  Automatic choice: RT = 2 (RT = 1
+// when that gives fewer than 256 workgroup columns... see mm_shape), and slices so
+// that columns x slices is about MM_TARGET_PER_CU workgroups per compute unit.
 struct MmShape {
-    uint32_t ch, slices, tiles, rt;
+    uint32_t ch, slices, rt;
 };
 
 std::atomic<uint32_t> g_mm_ch{0}, g_mm_rt{0};  // launch-shape overrides (0 = automatic)
+constexpr uint32_t MM_TARGET_PER_CU = 2;
 
-MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m) {
-    const uint32_t tiles = (m + 15) / 16 > 2 ? 2 : (m + 15) / 16;  // per launch; larger m runs in pairs of tiles
-    uint32_t ch = dtype == LG_Q4_K ? (tiles == 1 ? 2 : 1) : 1;
-    // chunks of 8 sub-blocks per slice: 1, 2 or (one token tile only) 4
-    const uint32_t och = g_mm_ch.load(std::memory_order_relaxed), ort = g_mm_rt.load(std::memory_order_relaxed);
-    if (och) ch = och >= 4 && tiles == 1 ? 4 : och >= 2 ? 2 : 1;
-    if (dtype != LG_Q4_K && ch > 2) ch = 2;
-    const uint32_t chunks = (k + 255) / 256, slices = (chunks + ch - 1) / ch;
-    // the most rows per wavefront that still give about three workgroups per CU per
-    // token tile (fewer, larger workgroups measured slower on every shape tried);
-    // four (two waves per SIMD) only when two already give twelve per CU
-    uint32_t rt = (n + 127) / 128 * slices >= 3072 * tiles ? 4 : 2;
-    while (rt > 1 && (n + 64 * rt - 1) / (64 * rt) * slices < 768 * tiles) rt /= 2;
+// n: rows per workgroup column's job span (the jobs' total rows; a gate/up pair's n);
+// rows_per_wave_tile: 16.  glu: both products in every column (32 RT rows each).
+MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool qk) {
+    const uint32_t nb = k / QK_K;
+    const uint32_t cus = (uint32_t)device_cus(), target = MM_TARGET_PER_CU * cus;
+    const uint32_t per = glu ? 32u : 64u;  // rows per column and row tile per wavefront
+    uint32_t rt = 2;
+    if ((n + per * 2 - 1) / (per * 2) < cus / 4) rt = 1;
+    const uint32_t ort = g_mm_rt.load(std::memory_order_relaxed);
     if (ort) rt = ort >= 4 ? 4 : ort >= 2 ? 2 : 1;
-    while (rt * ch > (dtype == LG_Q4_K ? 8u : 4u)) rt /= 2;  // register budget
-    return {ch, slices, tiles, rt};
+    if (dtype != LG_Q4_K && rt > 2) rt = 2;  // register budget of the Q8_0 chunk
+    if (m > 16 && rt > 2) rt = 2;
+    if (qk) rt = 2;  // whole heads of 128 rows per column
+    const uint32_t cols = (n + per * rt - 1) / (per * rt);
+    uint32_t slices = (target + cols / 2) / cols;
+    slices = slices < 1 ? 1 : (slices > nb ? nb : slices);
+    uint32_t ch = nb ? (nb + slices - 1) / slices : 1;
+    const uint32_t och = g_mm_ch.load(std::memory_order_relaxed);
+    if (och) ch = och < nb ? och : (nb ? nb : 1);
+    ch = ch ? ch : 1;
+    return {ch, nb ? (nb + ch - 1) / ch : 1, rt};
 }
 
-template <int TT, int PARTS, int CH, bool FUSE, bool GLU, bool NORM, bool WIDE>
-void launch_rt(int dtype, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt,
-               uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
-#define LG_MM(K, R) \
-    hipLaunchKernelGGL((K<TT, PARTS, CH, R, FUSE, GLU, NORM, WIDE>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb)
-    // mm_shape keeps rt * ch within each kernel's register budget
-    if (dtype == LG_Q4_K) {
-        if constexpr (4 * CH <= 8)
-            if (rt == 4) {
-                LG_MM(k_q4k_mm, 4);
-                return;
-            }
-        if constexpr (2 * CH <= 8)
-            if (rt == 2) {
-                LG_MM(k_q4k_mm, 2);
-                return;
-            }
-        LG_MM(k_q4k_mm, 1);
-    } else {
-        if constexpr (4 * CH <= 4)
-            if (rt == 4) {
-                LG_MM(k_q80_mm, 4);
-                return;
-            }
-        if constexpr (2 * CH <= 4)
-            if (rt == 2) {
-                LG_MM(k_q80_mm, 2);
-                return;
-            }
-        if constexpr (CH <= 2) LG_MM(k_q80_mm, 1);
+template <bool Q4, int TT, bool GLU, bool NORM, bool TILED>
+void launch_rt(uint32_t rt, dim3 grid, const uint4 *fr, const MmJobs &jobs, uint32_t *cnt, uint32_t m, uint32_t k,
+               uint64_t rb, uint32_t ch, hipStream_t s) {
+#define LG_MM(R) \
+    hipLaunchKernelGGL((k_mm_mf<Q4, TT, R, GLU, NORM, TILED>), grid, dim3(256), 0, s, fr, jobs, cnt, m, k, rb, ch)
+    if constexpr (Q4 && TT == 1)
+        if (rt == 4) {
+            LG_MM(4);
+            return;
+        }
+    if (rt == 2) {
+        LG_MM(2);
+        return;
     }
+    LG_MM(1);
 #undef LG_MM
 }
 
-template <int PARTS, bool FUSE, bool GLU = false, bool NORM = false, bool WIDE = false>
-int launch_mm(int dtype, const MmShape &sh, uint32_t groups, const void *x, const float *up, const MmJobs &jobs,
-              uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
+template <bool Q4, bool GLU, bool NORM>
+void launch_tt(uint32_t tt, bool tiled, uint32_t rt, dim3 grid, const uint4 *fr, const MmJobs &jobs, uint32_t *cnt,
+               uint32_t m, uint32_t k, uint64_t rb, uint32_t ch, hipStream_t s) {
+    if (tt == 2) {
+        if (tiled) launch_rt<Q4, 2, GLU, NORM, true>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
+        else launch_rt<Q4, 2, GLU, NORM, false>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
+    } else {
+        if (tiled) launch_rt<Q4, 1, GLU, NORM, true>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
+        else launch_rt<Q4, 1, GLU, NORM, false>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
+    }
+}
+
+int launch_mm(int dtype, bool tiled, bool glu, bool norm, uint32_t tt, const MmShape &sh, uint32_t groups,
+              const uint4 *fr, const MmJobs &jobs, uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
     const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
-    if (sh.tiles == 1) {
-        if (sh.ch == 4) launch_rt<1, PARTS, 4, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else if (sh.ch == 2) launch_rt<1, PARTS, 2, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<1, PARTS, 1, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+    if (dtype == LG_Q4_K) {
+        if (glu && norm) launch_tt<true, true, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
+        else if (glu) launch_tt<true, true, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
+        else if (norm) launch_tt<true, false, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
+        else launch_tt<true, false, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
     } else {
-        if (sh.ch == 2) launch_rt<2, PARTS, 2, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
-        else launch_rt<2, PARTS, 1, FUSE, GLU, NORM, WIDE>(dtype, sh.rt, grid, x, up, jobs, cnt, m, k, rb, s);
+        if (glu && norm) launch_tt<false, true, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
+        else if (glu) launch_tt<false, true, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
+        else if (norm) launch_tt<false, false, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
+        else launch_tt<false, false, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
     }
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
 }
@@ -984,37 +950,56 @@ uint64_t align256(uint64_t b) { return (b + 255) & ~(uint64_t)255; }
 
 // Workspace layout: the arrival counters at a fixed place (offset 0, one per
 // workgroup column, CNT_MAX of them) so that every call finds them zero, then the
-// partial sums, job after job.
+// partial sums, job after job, then the fragment records of every token tile.
 constexpr uint64_t CNT_BYTES = PROJ_WS_COUNTERS;
 constexpr uint32_t CNT_MAX = CNT_BYTES / 4;
+
+// The shape of the launch over the token tiles 16 t0 .. (pairs of tiles; ml rows).
+MmShape launch_shape(int w_dtype, uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t ml, bool glu, bool qk) {
+    uint64_t ntot = 0;
+    for (uint32_t j = 0; j < jobs; j++) ntot += n[j];
+    return mm_shape(w_dtype, k, glu ? n[0] : (uint32_t)ntot, ml, glu, qk);
+}
 
 }  // namespace
 
 namespace lg {
 
-uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype) {
+// The workspace of one call: counters, partial sums of the largest tile pair, records.
+static uint64_t multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype, bool glu,
+                               bool qk) {
     if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
     if (w_dtype == LG_Q8_0_T16) w_dtype = LG_Q8_0;
-    if (w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) return 0;
-    uint64_t ntot = 0;
-    for (uint32_t j = 0; j < jobs; j++) ntot += n[j];
+    if ((w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) || k % QK_K || m == 0) return 0;
     const uint32_t ml = m < 32 ? m : 32;
-    const MmShape sh = mm_shape(w_dtype, k, (uint32_t)ntot, ml);
-    if (sh.slices <= 1) return 0;
+    const MmShape sh = launch_shape(w_dtype, k, n, jobs, ml, glu, qk);
     uint64_t b = CNT_BYTES;
-    for (uint32_t j = 0; j < jobs; j++) b += align256((uint64_t)sh.slices * ml * n[j] * 4);
+    if (sh.slices > 1)
+        for (uint32_t j = 0; j < jobs; j++) b += align256((uint64_t)sh.slices * ml * n[j] * 4);
+    return b + (uint64_t)((m + 15) / 16) * (k / QK_K) * FR_BYTES;
+}
+
+uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype) {
+    // the largest of the plain, gate/up (two jobs of equal n) and QK-normed shapes
+    uint64_t b = multi_ws_bytes(k, n, jobs, m, w_dtype, false, false);
+    const uint64_t q = multi_ws_bytes(k, n, jobs, m, w_dtype, false, true);
+    b = q > b ? q : b;
+    if (jobs == 2 && n[0] == n[1]) {
+        const uint64_t g = multi_ws_bytes(k, n, jobs, m, w_dtype, true, false);
+        b = g > b ? g : b;
+    }
     return b;
 }
 
 uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype) {
     (void)x_dtype;
-    return proj_batch_multi_ws_bytes(k, &n, 1, m, w_dtype);
+    return multi_ws_bytes(k, &n, 1, m, w_dtype, false, false);
 }
 
 uint32_t proj_batch_norm_cols(int w_dtype, uint32_t k, uint32_t n, uint32_t m) {
     if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
     if (w_dtype == LG_Q8_0_T16) w_dtype = LG_Q8_0;
-    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32);
+    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32, false, false);
     return (n + 64 * sh.rt - 1) / (64 * sh.rt);
 }
 
@@ -1024,7 +1009,7 @@ bool proj_batch_mfma_ok(int w_dtype, uint32_t k, const void *w) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
     if (w_dtype == LG_Q4_K_T16 || w_dtype == LG_Q8_0_T16) return k && k % QK_K == 0 && (a & 15u) == 0;
     if (w_dtype == LG_Q4_K) return k && k % QK_K == 0 && (a & 15u) == 0;
-    if (w_dtype == LG_Q8_0) return k && k % QK8_0 == 0 && (a & 1u) == 0;
+    if (w_dtype == LG_Q8_0) return k && k % QK_K == 0 && (a & 1u) == 0;
     return false;
 }
 
@@ -1090,14 +1075,13 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     if (ntot == 0) return LG_OK;
     if (norm) LG_EXTENT(rs->ss, (uint64_t)(m - rs->tok0) * rs->cols * 4, name);
     if (tiled) w_dtype = w_dtype == LG_Q4_K_T16 ? LG_Q4_K : LG_Q8_0;  // the same kernels, reading tiles
-    const uint32_t blk = w_dtype == LG_Q4_K ? QK_K : QK8_0;
-    bool fast = k && w_dtype != LG_F32 && k % blk == 0 && k % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+    bool fast = k && w_dtype != LG_F32 && k % QK_K == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                 (!up || (reinterpret_cast<uintptr_t>(up) & 15u) == 0);
     for (uint32_t j = 0; j < njobs; j++)
         fast = fast && (w_dtype != LG_Q4_K || (reinterpret_cast<uintptr_t>(jb[j].w) & 15u) == 0) &&
                (reinterpret_cast<uintptr_t>(jb[j].w) & 1u) == 0;
     LG_REQUIRE(fast || !(norm || epi || qkn), "%s: a folded RMSNorm or QK-norm needs the matrix-core path (k a "
-               "multiple of the block, aligned operands)", name);
+               "multiple of 256, aligned operands)", name);
     if (!fast) {
         for (uint32_t j = 0; j < njobs; j++) {
             if (jb[j].n == 0) continue;
@@ -1108,31 +1092,40 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         if (glu) LG_TRY(lg_dispatch_activation(jb[0].c, jb[1].c, jb[0].c, m * jb[0].n, s));
         return LG_OK;
     }
-    const uint64_t need = proj_batch_multi_ws_bytes(k, nv, njobs, m, w_dtype);
+    const uint64_t need = multi_ws_bytes(k, nv, njobs, m, w_dtype, glu, qkn);
     void *ws = ws_given;
-    if (need) {
-        if (ws) {
-            LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small", name, (unsigned long long)ws_bytes);
-        } else {
-            LG_TRY(stream_workspace(s, need, &ws));
-        }
+    if (ws) {
+        LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small (%llu needed)", name,
+                   (unsigned long long)ws_bytes, (unsigned long long)need);
+    } else {
+        LG_TRY(stream_workspace(s, need, &ws));
     }
-    const uint32_t tiles = (m + 15) / 16;
-    const uint64_t xsz = x_dtype == LG_F32 ? 4 : 2;
+    const uint32_t tiles = (m + 15) / 16, nb = k / QK_K;
+    // every token tile's fragment records, after the largest tile pair's partial sums
+    const MmShape sh0 = launch_shape(w_dtype, k, nv, njobs, m < 32 ? m : 32, glu, qkn);
+    uint64_t poff = CNT_BYTES;
+    if (sh0.slices > 1)
+        for (uint32_t j = 0; j < njobs; j++) poff += align256((uint64_t)sh0.slices * (m < 32 ? m : 32) * nv[j] * 4);
+    uint4 *fr = reinterpret_cast<uint4 *>(static_cast<uint8_t *>(ws) + poff);
+    {
+        const dim3 pg(nb, tiles * 4);
+        if (x_dtype == LG_BF16) hipLaunchKernelGGL((k_mm_prep<1, false>), pg, dim3(256), 0, s, x, nullptr, fr, m, k);
+        else if (up) hipLaunchKernelGGL((k_mm_prep<0, true>), pg, dim3(256), 0, s, x, up, fr, m, k);
+        else hipLaunchKernelGGL((k_mm_prep<0, false>), pg, dim3(256), 0, s, x, nullptr, fr, m, k);
+        LG_TRY(after_launch(name, s));
+    }
     for (uint32_t t0 = 0; t0 < tiles; t0 += 2) {  // pairs of 16-token tiles
-        const uint32_t ml = m - 16 * t0 < 32 ? m - 16 * t0 : 32;
-        MmShape sh = mm_shape(w_dtype, k, (uint32_t)ntot, ml);
-        if (qkn) sh.rt = 2;  // within every budget: mm_shape keeps ch <= 4 (Q4_K) and <= 2 (Q8_0)
+        const uint32_t ml = m - 16 * t0 < 32 ? m - 16 * t0 : 32, tt = (ml + 15) / 16;
+        const MmShape sh = launch_shape(w_dtype, k, nv, njobs, ml, glu, qkn);
         uint32_t *cnt = static_cast<uint32_t *>(ws);
-        uint8_t *pb = ws ? static_cast<uint8_t *>(ws) + CNT_BYTES : nullptr;
-        if (sh.slices > 1) LG_REQUIRE(ws, "%s: no workspace for %u slices", name, sh.slices);
+        uint8_t *pb = static_cast<uint8_t *>(ws) + CNT_BYTES;
         MmJobs jobs{};
         uint32_t groups = 0;
         for (uint32_t j = 0; j < njobs; j++) {
             const uint64_t off = (uint64_t)16 * t0 * jb[j].n;
             jobs.j[j] = {static_cast<const uint8_t *>(jb[j].w), jb[j].c + off, jb[j].res ? jb[j].res + off : nullptr,
                          reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups, jb[j].qkw};
-            if (pb) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
+            if (sh.slices > 1) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
             groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
         }
         if (glu) {  // both products in every workgroup column
@@ -1153,31 +1146,9 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
             jobs.rs_cols = rs->cols;
             jobs.rs_eps = rs->eps;
         }
-        // one plain product split over k in many rounds of workgroups: the slices only
-        // store their partial sums and k_mm_sum adds them
-        const bool wide = njobs == 1 && !qkn && !glu && !up && !pnorm && !jb[0].res && !jb[0].ss && sh.slices > 1 &&
-                          (uint64_t)groups * sh.slices >= WIDE_MIN_WGS;
         LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
-        const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
-        const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
-        if (wide && x_dtype == LG_BF16)
-            LG_TRY((launch_mm<1, false, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        else if (wide) LG_TRY((launch_mm<3, false, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        else if (x_dtype == LG_BF16) LG_TRY((launch_mm<1, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        else if (up) LG_TRY((launch_mm<3, true>(w_dtype, sh, groups, xt, ut, jobs, cnt, ml, k, s)));
-        else if (glu && pnorm) LG_TRY((launch_mm<3, false, true, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        else if (glu) LG_TRY((launch_mm<3, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        else if (pnorm) LG_TRY((launch_mm<3, false, false, true>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        else LG_TRY((launch_mm<3, false>(w_dtype, sh, groups, xt, nullptr, jobs, cnt, ml, k, s)));
-        if (wide) {
-            const MmJob &j0 = jobs.j[0];
-            const dim3 sg((j0.n + SUM_ROWS - 1) / SUM_ROWS, (ml + 15) / 16);
-            if (j0.n % 4 == 0 && (reinterpret_cast<uintptr_t>(j0.out) & 15u) == 0)
-                hipLaunchKernelGGL(k_mm_sum<true>, sg, dim3(256), 0, s, j0.part, j0.out, ml, j0.n, sh.slices);
-            else
-                hipLaunchKernelGGL(k_mm_sum<false>, sg, dim3(256), 0, s, j0.part, j0.out, ml, j0.n, sh.slices);
-            LG_TRY(after_launch(name, s));
-        }
+        LG_TRY(launch_mm(w_dtype, tiled, glu, pnorm, tt, sh, groups, fr + (uint64_t)t0 * nb * FR_U4, jobs, cnt, ml, k,
+                         s));
     }
     return LG_OK;
 }
@@ -1348,7 +1319,7 @@ extern "C" int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, c
     clear_error();
     const char *name = "lg_dispatch_proj_quant_batch_static";
     if (n == 0 || m == 0) return LG_OK;
-    const uint64_t need = lg::proj_batch_ws_bytes(k, n, m < 32 ? m : 32, x_dtype, w_dtype);
+    const uint64_t need = lg::proj_batch_ws_bytes(k, n, m, x_dtype, w_dtype);
     LG_REQUIRE(need <= STATIC_SCRATCH_BYTES,
                "%s: k=%u n=%u m=%u needs %llu bytes of scratch, more than the %llu this entry point has", name, k, n,
                m, (unsigned long long)need, (unsigned long long)STATIC_SCRATCH_BYTES);
@@ -1357,6 +1328,11 @@ extern "C" int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, c
     void *ws = nullptr;
     LG_TRY(static_scratch(dev, (hipStream_t)stream, false, &ws));
     return lg::proj_batch(x, x_dtype, w, c, k, n, m, w_dtype, ws, STATIC_SCRATCH_BYTES, (hipStream_t)stream);
+}
+
+extern "C" uint64_t lg_proj_quant_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int w_dtype) {
+    if (n == 0 || m == 0 || m > 64) return 0;
+    return lg::proj_batch_ws_bytes(k, n, m, LG_F32, w_dtype);
 }
 
 extern "C" int lg_dispatch_silu_gate_up_batch(const float *x, const void *w_gate, const void *w_up, float *h,

@@ -30,6 +30,7 @@ F32, F16, Q8_0, Q4_K, BF16 = 0, 1, 8, 12, 30
 Q8_0_T16, Q4_K_T16 = 1008, 1012  # Q8_0 / Q4_K repacked into 16-row tiles by repack_tiled (not GGUF types)
 TILED = {Q4_K: Q4_K_T16, Q8_0: Q8_0_T16}
 OK, EINVAL, EHIP, ENOMEM, EUNSUPPORTED, EIO, ENODEV, ENOTFOUND = range(8)
+STATIC_SCRATCH_BYTES = (16 << 20) + 65536  # the allocation-free product's device array
 
 # C-ABI symbols declared in include/laguna_hip.h, with ctypes signatures.
 _vp, _u32, _u64, _i, _f = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
@@ -58,6 +59,7 @@ SIGNATURES = {
     "lg_dispatch_silu_mul_proj_quant": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _i, _vp]),
     "lg_dispatch_proj_quant_batch": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_proj_quant_batch_static": (_i, [_vp, _i, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
+    "lg_proj_quant_batch_ws_bytes": (_u64, [_u32, _u32, _u32, _i]),
     "lg_dispatch_silu_gate_up_batch": (_i, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "lg_dispatch_argmax": (_i, [_vp, _u32, _u32, _u64, _vp, _vp]),
     "lg_tiled_bytes": (_u64, [_i, _u32, _u32]),
@@ -107,6 +109,7 @@ SIGNATURES = {
     # ceiling kernels for measurement (no counterpart in the reference)
     "lg_bench_empty": (_i, [_u32, _vp]),
     "lg_bench_read": (_i, [_vp, _u64, _vp]),
+    "lg_bench_read_shape": (_i, [_vp, _u64, _u32, _u32, _u32, _u32, _vp]),
 }
 
 
