@@ -1,21 +1,20 @@
 // Small-M products (block verify, m <= 64 activation rows): lg_dispatch_proj_quant_batch.
 // Replaces kernels/matmul.comp (never dispatched by the reference) with f16 MFMA
-// tiles on gfx950 (v_mfma_f32_16x16x32_f16: D[16x16] += A[16x32] * B[32x16]), in two
-// launches per call.
+// tiles on gfx950 (v_mfma_f32_16x16x32_f16: D[16x16] += A[16x32] * B[32x16]).
 //
-//   k_mm_prep builds the A operands once per call, for every 16-token tile and
-//       256-element chunk of k (a "fragment record"): each token's chunk is scaled by
-//       a power of two 2^e that puts its largest magnitude in [2^14, 2^15), and every
+//   A = activations, converted by each workgroup into a "fragment record" per 16-token
+//       tile and 256-element chunk of k, in LDS: each token's chunk is scaled by a
+//       power of two 2^e that puts its largest magnitude in [2^14, 2^15), and every
 //       scaled value v is split into two f16 parts, hi = f16(v) and lo = f16(v - hi)
 //       (22 significant bits, down to the f16 subnormal step 2^-24 of the scaled
 //       chunk), laid out as the MFMA's lane fragments; with them the sums X of each
 //       32-element sub-block of the scaled values, and 2^-e.
-//   k_q4k_mf / k_q80_mf stream the weights: B = weight codes of 16 output rows x 32 k
-//       built in registers from the raw blocks as f16 subnormals (gfx950's MFMA keeps
-//       f16 denormals), so the code of a nibble is the nibble itself:
+//   B = weight codes of 16 output rows x 32 k, built in registers from the raw blocks
+//       as f16 subnormals (gfx950's MFMA keeps f16 denormals), so the code of a nibble
+//       is the nibble itself:
 //         Q4_K  low nibble q -> q 2^-24 (one and per pair), high nibble -> 16 q 2^-24;
 //         Q8_0  int8 q -> (q + 128) 2^-24 (xor, and per pair).
-//       Per sub-block j of output row i (D_j = sum_k A_k B_k, over both parts):
+//   Per sub-block j of output row i (D_j = sum_k A_k B_k, over both parts):
 //         Q4_K  sum x w = 2^24 d sc_j D_j (2^20 for high nibbles) - dmin m_j X_j
 //         Q8_0  sum x w = 2^24 d_j D_j - 128 d_j X_j
 //       the X terms as f32 matrix products (k = the chunk's 8 sub-blocks), and the
@@ -29,10 +28,10 @@
 //
 // Work split: workgroup (blockIdx.x, blockIdx.y) = 64*RT output rows (RT 16-row
 // tiles per wavefront, four wavefronts) x slice blockIdx.y of k: `ch` chunks walked
-// in order, the next chunk's weights and fragment record in flight while the
-// current one is multiplied (the record double-buffered in LDS, one barrier per
-// chunk).  With one slice the workgroup writes the result; otherwise each writes
-// its slice's partial sums and the last workgroup of a row group to finish (a
+// in order, the next chunk's activations and the weights two chunks ahead in flight
+// while the current one is multiplied (the record double-buffered in LDS, one
+// barrier per chunk).  With one slice the workgroup writes the result; otherwise each
+// writes its slice's partial sums and the last workgroup of a row group to finish (a
 // per-row-group arrival counter, reset by that workgroup) adds the slices in slice
 // order: the result does not depend on which workgroup finishes last.
 #include <mutex>
@@ -64,14 +63,13 @@ __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, ui
     return __builtin_bit_cast(f16x8, make_uint4(a, b, c, d));
 }
 
-// Fragment record of one (16-token tile, 256-element chunk), FR_U4 16-byte words:
+// Fragment record of one (16-token tile, 256-element chunk) in LDS, FR_U4 16-byte words:
 //   [0, 1024)     word (j*2 + p)*64 + l: part p (0 = hi, 1 = lo) of sub-block j's A
 //                 operand, lane l: token l%16, elements 32j + 8(l/16) + {0,2,1,3,4,6,5,7}
 //   [1024, 1056)  float2 per lane l: (X[l%16][l/16], X[l%16][l/16 + 4]), X the sums of
 //                 the scaled values over each sub-block
 //   [1056, 1060)  the 16 tokens' 2^-e
-constexpr uint32_t FR_X = 1024, FR_S = 1056, FR_U4 = 1088;
-constexpr uint32_t FR_BYTES = FR_U4 * 16;
+constexpr uint32_t FR_X = 1024, FR_S = 1056, FR_U4 = 1060;
 
 // 2^-24 scaled codes: Q4_K nibbles in place (low nibbles of bytes 0 and 2 / 1 and 3
 // of a dword: `& LO4`, high nibbles `& HI4`), Q8_0 bytes biased to unsigned.
@@ -93,7 +91,7 @@ constexpr uint32_t LO4 = 0x000F000Fu, HI4 = 0x00F000F0u, LO8 = 0x00FF00FFu;
 //    The workgroup that finishes a column computes the scales, with the slices'
 //    partial sums in flight.
 constexpr int MM_JOBS = 4;
-constexpr uint32_t MM_SS_LOADS = 4;  // partial sums a consuming lane loads (per-token capacity 4 * 16 / TT)
+constexpr uint32_t MM_SS_LOADS = 8;  // partial sums a consuming lane loads (per-token capacity 8 * 16 / TT)
 struct MmJob {
     const uint8_t *w;
     float *out;
@@ -134,93 +132,20 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return g * (1.0f / (1.0f + expf(-g))) * u;
 }
 
-// ---- fragment records (k_mm_prep)
-//
-// Workgroup (c, tq) builds chunk c of the records of tokens 4 tq .. 4 tq + 3: wavefront
-// w takes token 4 tq + w (tokens past m are zero), lane q its elements 4q .. 4q + 3 of
-// the chunk, which are half of k-group (q % 8) / 2 of sub-block q / 8.  The chunk's
-// largest magnitude meets in a wavefront reduction, each sub-block's sum in DPP steps
-// over its 8 lanes.  XT: 0 = f32 activations, 1 = bf16; FUSE: the activations are
-// silu(x) * up (f32).
-__device__ __forceinline__ float wave_max(float v) {
+// ---- fragment records
+
+// Maximum over each 16-lane row: DPP xor 1, xor 2 (quad_perm), then row_ror 4 and 8.
+__device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));   // quad_perm 1,0,3,2
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));   // quad_perm 2,3,0,1
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false)));  // row_ror 4
     v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false)));  // row_ror 8
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return v;
 }
 
 __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     const _Float16 ha = (_Float16)a, hb = (_Float16)b;
     return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
-}
-
-template <int XT, bool FUSE>
-__global__ __launch_bounds__(256) void k_mm_prep(const void *__restrict__ x, const float *__restrict__ up,
-                                                 uint4 *__restrict__ fr, uint32_t m, uint32_t k) {
-    const uint32_t c = blockIdx.x, nb = k / QK_K;
-    const uint32_t w = threadIdx.x >> 6, q = threadIdx.x & 63u, t = blockIdx.y * 4 + w, tok = t & 15u;
-    const bool live = t < m;
-    const uint64_t e0 = (uint64_t)(live ? t : m - 1) * k + (uint64_t)QK_K * c + 4 * q;
-    float v[4];
-    if constexpr (XT == 1) {
-        const uint2 h = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(x) + e0);
-        v[0] = bf16_to_f32(h.x & 0xFFFFu);
-        v[1] = __uint_as_float(h.x & 0xFFFF0000u);
-        v[2] = bf16_to_f32(h.y & 0xFFFFu);
-        v[3] = __uint_as_float(h.y & 0xFFFF0000u);
-    } else {
-        const float4 f = *reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e0);
-        v[0] = f.x;
-        v[1] = f.y;
-        v[2] = f.z;
-        v[3] = f.w;
-        if constexpr (FUSE) {  // kernels/activation.comp:21-28
-            const float4 u = *reinterpret_cast<const float4 *>(up + e0);
-            v[0] = silu_mul(v[0], u.x);
-            v[1] = silu_mul(v[1], u.y);
-            v[2] = silu_mul(v[2], u.z);
-            v[3] = silu_mul(v[3], u.w);
-        }
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        v[i] = live ? v[i] : 0.0f;
-        amax = fmaxf(amax, fabsf(v[i]));
-    }
-    amax = wave_max(amax);
-    // 2^e puts the chunk's largest magnitude in [2^14, 2^15); a zero or non-finite
-    // chunk keeps e = 0 (non-finite values then reach the products as f16 inf / NaN)
-    int e = 0;
-    if (amax > 0.0f && amax <= 3.4028234664e38f) {
-        e = 15 - __builtin_amdgcn_frexp_expf(amax);
-        e = e < -126 ? -126 : (e > 126 ? 126 : e);
-    }
-    float hi[4], lo[4], s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float wv = __builtin_ldexpf(v[i], e);
-        hi[i] = (float)(_Float16)wv;
-        lo[i] = wv - hi[i];  // exact: hi is the f16 nearest wv
-        s += wv;
-    }
-    // the sub-block's sum over its 8 lanes: quads, then the half-row mirror (lane i and
-    // 7 - i of each 8), the same float in all 8
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x141, 0xF, 0xF, false));
-    uint4 *rec = fr + ((uint64_t)(t >> 4) * nb + c) * FR_U4;
-    const uint32_t j = q >> 3, kg = (q & 7u) >> 1, half = q & 1u, lane = kg * 16 + tok;
-    uint2 *wa = reinterpret_cast<uint2 *>(rec + (j * 2) * 64 + lane) + half;
-    wa[0] = make_uint2(pk_f16(hi[0], hi[2]), pk_f16(hi[1], hi[3]));
-    wa[128] = make_uint2(pk_f16(lo[0], lo[2]), pk_f16(lo[1], lo[3]));  // part 1: 64 words on
-    float *rf = reinterpret_cast<float *>(rec);
-    if ((q & 7u) == 0) rf[4 * FR_X + ((j & 3u) * 16 + tok) * 2 + (j >> 2)] = s;
-    if (q == 0) rf[4 * FR_S + tok] = __builtin_ldexpf(1.0f, -e);
 }
 
 // NORM: token threadIdx.x / LT of the launch (LT = 16 / TT lanes per token) takes its
@@ -554,34 +479,105 @@ __device__ __forceinline__ void load_q80(Q80Chunk<RT> &W, const uint8_t *__restr
     }
 }
 
-// One fragment record per token tile into registers and from there into LDS.  Thread
-// t copies words t, t + 256, t + 512, t + 768 and 1024 + t % 64 (the last 64 words are
-// read and written by all four wavefronts, with the same values): every load and store
-// is unconditional, so the compiler keeps the loads where they are issued.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-template <int TT>
-struct RecCopy {
-    u32x4 v[TT][5];
-    __device__ __forceinline__ static uint32_t word(int i) {
-        return i < 4 ? threadIdx.x + 256 * i : 1024 + (threadIdx.x & 63u);
-    }
-    __device__ __forceinline__ void load(const uint4 *fr, uint32_t nb, uint32_t c) {
+// The fragment record of one chunk for TT token tiles, built by the workgroup from the
+// activations: thread (token threadIdx.x / 16, q = threadIdx.x % 16) loads elements
+// 16 q .. 16 q + 15 of the chunk (half of sub-block q / 2, k-groups 2 (q % 2) and
+// 2 (q % 2) + 1) of each token tile, during the previous chunk's products, and stores
+// their record words to LDS: the token's chunk maximum meets in DPP steps over its
+// 16-lane row, and 2^e, the two f16 parts and the sub-block sums X follow as in
+// the record layout.  XM: 0 = f32 activations, 1 = bf16, 2 = f32 silu(x) * up.
+// Tokens past m are zero.
+template <int TT, int XM>
+struct RecBuild {
+    float v[TT][16];
+    float u[XM == 2 ? TT : 1][16];
+    __device__ __forceinline__ void load(const void *x, const float *up, uint32_t m, uint32_t k, uint32_t c) {
+        const uint32_t tok = threadIdx.x >> 4, q = threadIdx.x & 15u;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            const u32x4 *src = reinterpret_cast<const u32x4 *>(fr + ((uint64_t)t * nb + c) * FR_U4);
+            const uint32_t tr = t * 16 + tok;
+            const uint64_t e0 = (uint64_t)(tr < m ? tr : m - 1) * k + (uint64_t)QK_K * c + 16 * q;
+            if constexpr (XM == 1) {
+                const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + e0);
+                const uint4 h0 = p[0], h1 = p[1];
+                const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
 #pragma unroll
-            for (int i = 0; i < 5; i++) v[t][i] = src[word(i)];
+                for (int i = 0; i < 8; i++) {
+                    v[t][2 * i] = bf16_to_f32(hw[i] & 0xFFFFu);
+                    v[t][2 * i + 1] = __uint_as_float(hw[i] & 0xFFFF0000u);
+                }
+            } else {
+                const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 f = p[i];
+                    v[t][4 * i] = f.x;
+                    v[t][4 * i + 1] = f.y;
+                    v[t][4 * i + 2] = f.z;
+                    v[t][4 * i + 3] = f.w;
+                }
+                if constexpr (XM == 2) {
+                    const float4 *pu = reinterpret_cast<const float4 *>(up + e0);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float4 f = pu[i];
+                        u[t][4 * i] = f.x;
+                        u[t][4 * i + 1] = f.y;
+                        u[t][4 * i + 2] = f.z;
+                        u[t][4 * i + 3] = f.w;
+                    }
+                }
+            }
         }
     }
-    __device__ __forceinline__ void store(uint4 *lds) const {
-        u32x4 *d = reinterpret_cast<u32x4 *>(lds);
+    __device__ __forceinline__ void store(uint4 *lds, uint32_t m) const {
+        const uint32_t tok = threadIdx.x >> 4, q = threadIdx.x & 15u, j = q >> 1;
 #pragma unroll
-        for (int t = 0; t < TT; t++)
+        for (int t = 0; t < TT; t++) {
+            const bool live = t * 16 + tok < m;
+            float w[16], amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 5; i++) d[t * FR_U4 + word(i)] = v[t][i];
+            for (int i = 0; i < 16; i++) {
+                float a = v[t][i];
+                if constexpr (XM == 2) a = silu_mul(a, u[t][i]);  // kernels/activation.comp:21-28
+                w[i] = live ? a : 0.0f;
+                amax = fmaxf(amax, fabsf(w[i]));
+            }
+            amax = row16_max(amax);
+            // 2^e puts the chunk's largest magnitude in [2^14, 2^15); a zero or non-finite
+            // chunk keeps e = 0 (non-finite values then reach the products as f16 inf / NaN)
+            int e = 0;
+            if (amax > 0.0f && amax <= 3.4028234664e38f) {
+                e = 15 - __builtin_amdgcn_frexp_expf(amax);
+                e = e < -126 ? -126 : (e > 126 ? 126 : e);
+            }
+            float hi[16], lo[16], sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float sv = __builtin_ldexpf(w[i], e);
+                hi[i] = (float)(_Float16)sv;
+                lo[i] = sv - hi[i];  // exact: hi is the f16 nearest sv
+                sum += sv;
+            }
+            // the sub-block's sum: this thread's 16 and its neighbour's (q ^ 1), the same
+            // float in both (addition is commutative)
+            sum += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+            uint4 *rec = lds + t * FR_U4;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t lane = ((q & 1u) * 2 + h) * 16 + tok;
+                const float *a = hi + 8 * h, *b = lo + 8 * h;
+                rec[(j * 2 + 0) * 64 + lane] = make_uint4(pk_f16(a[0], a[2]), pk_f16(a[1], a[3]), pk_f16(a[4], a[6]),
+                                                          pk_f16(a[5], a[7]));
+                rec[(j * 2 + 1) * 64 + lane] = make_uint4(pk_f16(b[0], b[2]), pk_f16(b[1], b[3]), pk_f16(b[4], b[6]),
+                                                          pk_f16(b[5], b[7]));
+            }
+            float *rf = reinterpret_cast<float *>(rec);
+            if ((q & 1u) == 0) rf[4 * FR_X + ((j & 3u) * 16 + tok) * 2 + (j >> 2)] = sum;
+            if (q == 0) rf[4 * FR_S + tok] = __builtin_ldexpf(1.0f, -e);
+        }
     }
 };
-static_assert(FR_U4 == 1088, "RecCopy covers 1024 + 64 words");
 
 // The chunk's min / bias terms and token scales: tmp += X (16x4) * coef (4x16) for
 // sub-blocks kg and kg + 4, then acc += tmp * 2^-e per token.
@@ -741,15 +737,15 @@ __device__ __forceinline__ void q80_chunk(const uint4 *lds, const Q80Chunk<RT> &
 }
 
 // The small-M product.  Wavefront w owns row tiles (4*bx + w)*RT .. +RT-1 (GLU: gate
-// rows in wavefronts 0-1, up rows in 2-3) over chunks blockIdx.y*ch .. +ch-1 of k.
-// Software pipeline, per chunk c: the record of chunk c (loaded into registers during
-// chunk c-1) is stored to LDS buffer c%2 and the workgroup meets at a barrier; then the
-// record of chunk c+1 and the weights of chunk c+2 (a ring of three chunks in
-// registers) are issued, and chunk c is multiplied.  The loads of one chunk are used
-// only by the next iteration, so nothing moves them next to their use.
-template <bool Q4, int TT, int RT, bool GLU, bool NORM, bool TILED>
-__global__ __launch_bounds__(256) void k_mm_mf(const uint4 *fr, MmJobs jobs, uint32_t *cnt, uint32_t m, uint32_t k,
-                                               uint64_t row_bytes, uint32_t ch) {
+// rows in wavefronts 0-1, up rows in 2-3) over chunks blockIdx.y*ch .. +ch-1 of k;
+// x (and up) hold the launch's token tiles.  Software pipeline, per chunk c: the
+// record of chunk c, built from the activations loaded during chunk c-1, is stored to
+// LDS buffer c%2 and the workgroup meets at a barrier; then the activations of chunk
+// c+1 and the weights of chunk c+2 (a ring of three chunks in registers) are issued,
+// and chunk c is multiplied.
+template <bool Q4, int TT, int RT, bool GLU, bool NORM, bool TILED, int XM>
+__global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, MmJobs jobs, uint32_t *cnt, uint32_t m,
+                                               uint32_t k, uint64_t row_bytes, uint32_t ch) {
     MM_JOB_SELECT;
     __shared__ uint4 lrec[2][TT * FR_U4];
     // uniform over the wavefront: row-tile addresses are scalar
@@ -772,15 +768,15 @@ __global__ __launch_bounds__(256) void k_mm_mf(const uint4 *fr, MmJobs jobs, uin
         for (int t = 0; t < TT; t++)
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[i][t][r] = 0.0f;
-    RecCopy<TT> rc;
-    rc.load(fr, nb, c0);
+    RecBuild<TT, XM> rb;
+    rb.load(x, up, m, k, c0);
     load_w(Wc[0], 0);
     load_w(Wc[1], 1);
     // chunk 0 ahead of the loop, so the loop is entered in the state it repeats
-    rc.store(lrec[0]);
+    rb.store(lrec[0], m);
     __syncthreads();
-    rc.load(fr, nb, c0 + (1 < nch ? 1 : 0));
-    __builtin_amdgcn_sched_barrier(0);  // issue order: the record, then the weights
+    rb.load(x, up, m, k, c0 + (1 < nch ? 1 : 0));
+    __builtin_amdgcn_sched_barrier(0);  // issue order: the activations, then the weights
     load_w(Wc[2], 2);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (Q4) q4k_chunk<TT, RT>(lrec[0], Wc[0], acc);
@@ -792,9 +788,9 @@ __global__ __launch_bounds__(256) void k_mm_mf(const uint4 *fr, MmJobs jobs, uin
         for (int h = 0; h < 3; h++) {
             const uint32_t c = ci + h;
             if (c >= nch) break;  // uniform
-            rc.store(lrec[c & 1u]);
+            rb.store(lrec[c & 1u], m);
             __syncthreads();
-            rc.load(fr, nb, c0 + (c + 1 < nch ? c + 1 : nch - 1));
+            rb.load(x, up, m, k, c0 + (c + 1 < nch ? c + 1 : nch - 1));
             __builtin_amdgcn_sched_barrier(0);
             load_w(Wc[h], c + 2);
             __builtin_amdgcn_sched_barrier(0);
@@ -877,7 +873,9 @@ constexpr uint32_t MM_TARGET_PER_CU = 2;
 
 // n: rows per workgroup column's job span (the jobs' total rows; a gate/up pair's n);
 // rows_per_wave_tile: 16.  glu: both products in every column (32 RT rows each).
-MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool qk) {
+// epi: the job writes a folded norm's per-column sums of squares, whose consumers read
+// at most proj_batch_rs_cols_max partial sums per token: at most 64 columns.
+MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool qk, bool epi = false) {
     const uint32_t nb = k / QK_K;
     const uint32_t cus = (uint32_t)device_cus(), target = MM_TARGET_PER_CU * cus;
     const uint32_t per = glu ? 32u : 64u;  // rows per column and row tile per wavefront
@@ -888,6 +886,7 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool q
     if (dtype != LG_Q4_K && rt > 2) rt = 2;  // register budget of the Q8_0 chunk
     if (m > 16 && rt > 2) rt = 2;
     if (qk) rt = 2;  // whole heads of 128 rows per column
+    while (epi && rt < 2 && (n + per * rt - 1) / (per * rt) > 64) rt *= 2;
     const uint32_t cols = (n + per * rt - 1) / (per * rt);
     uint32_t slices = (target + cols / 2) / cols;
     slices = slices < 1 ? 1 : (slices > nb ? nb : slices);
@@ -898,11 +897,12 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool q
     return {ch, nb ? (nb + ch - 1) / ch : 1, rt};
 }
 
-template <bool Q4, int TT, bool GLU, bool NORM, bool TILED>
-void launch_rt(uint32_t rt, dim3 grid, const uint4 *fr, const MmJobs &jobs, uint32_t *cnt, uint32_t m, uint32_t k,
-               uint64_t rb, uint32_t ch, hipStream_t s) {
-#define LG_MM(R) \
-    hipLaunchKernelGGL((k_mm_mf<Q4, TT, R, GLU, NORM, TILED>), grid, dim3(256), 0, s, fr, jobs, cnt, m, k, rb, ch)
+template <bool Q4, int TT, bool GLU, bool NORM, bool TILED, int XM>
+void launch_rt(uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt, uint32_t m,
+               uint32_t k, uint64_t rb, uint32_t ch, hipStream_t s) {
+#define LG_MM(R)                                                                                                  \
+    hipLaunchKernelGGL((k_mm_mf<Q4, TT, R, GLU, NORM, TILED, XM>), grid, dim3(256), 0, s, x, up, jobs, cnt, m, k, rb, \
+                       ch)
     if constexpr (Q4 && TT == 1)
         if (rt == 4) {
             LG_MM(4);
@@ -916,33 +916,37 @@ void launch_rt(uint32_t rt, dim3 grid, const uint4 *fr, const MmJobs &jobs, uint
 #undef LG_MM
 }
 
-template <bool Q4, bool GLU, bool NORM>
-void launch_tt(uint32_t tt, bool tiled, uint32_t rt, dim3 grid, const uint4 *fr, const MmJobs &jobs, uint32_t *cnt,
-               uint32_t m, uint32_t k, uint64_t rb, uint32_t ch, hipStream_t s) {
+// XM (activation kind) other than plain f32 only for plain products (no pair, no norm)
+template <bool Q4, bool GLU, bool NORM, int XM>
+void launch_tt(uint32_t tt, bool tiled, uint32_t rt, dim3 grid, const void *x, const float *up, const MmJobs &jobs,
+               uint32_t *cnt, uint32_t m, uint32_t k, uint64_t rb, uint32_t ch, hipStream_t s) {
     if (tt == 2) {
-        if (tiled) launch_rt<Q4, 2, GLU, NORM, true>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
-        else launch_rt<Q4, 2, GLU, NORM, false>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
+        if (tiled) launch_rt<Q4, 2, GLU, NORM, true, XM>(rt, grid, x, up, jobs, cnt, m, k, rb, ch, s);
+        else launch_rt<Q4, 2, GLU, NORM, false, XM>(rt, grid, x, up, jobs, cnt, m, k, rb, ch, s);
     } else {
-        if (tiled) launch_rt<Q4, 1, GLU, NORM, true>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
-        else launch_rt<Q4, 1, GLU, NORM, false>(rt, grid, fr, jobs, cnt, m, k, rb, ch, s);
+        if (tiled) launch_rt<Q4, 1, GLU, NORM, true, XM>(rt, grid, x, up, jobs, cnt, m, k, rb, ch, s);
+        else launch_rt<Q4, 1, GLU, NORM, false, XM>(rt, grid, x, up, jobs, cnt, m, k, rb, ch, s);
     }
 }
 
-int launch_mm(int dtype, bool tiled, bool glu, bool norm, uint32_t tt, const MmShape &sh, uint32_t groups,
-              const uint4 *fr, const MmJobs &jobs, uint32_t *cnt, uint32_t m, uint32_t k, hipStream_t s) {
+template <bool Q4>
+void launch_q(int xm, bool tiled, bool glu, bool norm, uint32_t tt, const MmShape &sh, dim3 grid, const void *x,
+              const float *up, const MmJobs &jobs, uint32_t *cnt, uint32_t m, uint32_t k, uint64_t rb, hipStream_t s) {
+    if (xm == 1) launch_tt<Q4, false, false, 1>(tt, tiled, sh.rt, grid, x, up, jobs, cnt, m, k, rb, sh.ch, s);
+    else if (xm == 2) launch_tt<Q4, false, false, 2>(tt, tiled, sh.rt, grid, x, up, jobs, cnt, m, k, rb, sh.ch, s);
+    else if (glu && norm) launch_tt<Q4, true, true, 0>(tt, tiled, sh.rt, grid, x, up, jobs, cnt, m, k, rb, sh.ch, s);
+    else if (glu) launch_tt<Q4, true, false, 0>(tt, tiled, sh.rt, grid, x, up, jobs, cnt, m, k, rb, sh.ch, s);
+    else if (norm) launch_tt<Q4, false, true, 0>(tt, tiled, sh.rt, grid, x, up, jobs, cnt, m, k, rb, sh.ch, s);
+    else launch_tt<Q4, false, false, 0>(tt, tiled, sh.rt, grid, x, up, jobs, cnt, m, k, rb, sh.ch, s);
+}
+
+int launch_mm(int dtype, int xm, bool tiled, bool glu, bool norm, uint32_t tt, const MmShape &sh, uint32_t groups,
+              const void *x, const float *up, const MmJobs &jobs, uint32_t *cnt, uint32_t m, uint32_t k,
+              hipStream_t s) {
     const dim3 grid(groups, sh.slices);
     const uint64_t rb = dtype == LG_Q4_K ? (uint64_t)k / QK_K * Q4K_BYTES : (uint64_t)k / QK8_0 * Q80_BYTES;
-    if (dtype == LG_Q4_K) {
-        if (glu && norm) launch_tt<true, true, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-        else if (glu) launch_tt<true, true, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-        else if (norm) launch_tt<true, false, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-        else launch_tt<true, false, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-    } else {
-        if (glu && norm) launch_tt<false, true, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-        else if (glu) launch_tt<false, true, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-        else if (norm) launch_tt<false, false, true>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-        else launch_tt<false, false, false>(tt, tiled, sh.rt, grid, fr, jobs, cnt, m, k, rb, sh.ch, s);
-    }
+    if (dtype == LG_Q4_K) launch_q<true>(xm, tiled, glu, norm, tt, sh, grid, x, up, jobs, cnt, m, k, rb, s);
+    else launch_q<false>(xm, tiled, glu, norm, tt, sh, grid, x, up, jobs, cnt, m, k, rb, s);
     return after_launch(dtype == LG_Q4_K ? "proj_q4k_mm" : "proj_q8_0_mm", s);
 }
 
@@ -955,10 +959,11 @@ constexpr uint64_t CNT_BYTES = PROJ_WS_COUNTERS;
 constexpr uint32_t CNT_MAX = CNT_BYTES / 4;
 
 // The shape of the launch over the token tiles 16 t0 .. (pairs of tiles; ml rows).
-MmShape launch_shape(int w_dtype, uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t ml, bool glu, bool qk) {
+MmShape launch_shape(int w_dtype, uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t ml, bool glu, bool qk,
+                     bool epi) {
     uint64_t ntot = 0;
     for (uint32_t j = 0; j < jobs; j++) ntot += n[j];
-    return mm_shape(w_dtype, k, glu ? n[0] : (uint32_t)ntot, ml, glu, qk);
+    return mm_shape(w_dtype, k, glu ? n[0] : (uint32_t)ntot, ml, glu, qk, epi);
 }
 
 }  // namespace
@@ -967,25 +972,28 @@ namespace lg {
 
 // The workspace of one call: counters, partial sums of the largest tile pair, records.
 static uint64_t multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype, bool glu,
-                               bool qk) {
+                               bool qk, bool epi) {
     if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
     if (w_dtype == LG_Q8_0_T16) w_dtype = LG_Q8_0;
     if ((w_dtype != LG_Q4_K && w_dtype != LG_Q8_0) || k % QK_K || m == 0) return 0;
     const uint32_t ml = m < 32 ? m : 32;
-    const MmShape sh = launch_shape(w_dtype, k, n, jobs, ml, glu, qk);
+    const MmShape sh = launch_shape(w_dtype, k, n, jobs, ml, glu, qk, epi);
     uint64_t b = CNT_BYTES;
     if (sh.slices > 1)
         for (uint32_t j = 0; j < jobs; j++) b += align256((uint64_t)sh.slices * ml * n[j] * 4);
-    return b + (uint64_t)((m + 15) / 16) * (k / QK_K) * FR_BYTES;
+    return b;
 }
 
 uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uint32_t m, int w_dtype) {
-    // the largest of the plain, gate/up (two jobs of equal n) and QK-normed shapes
-    uint64_t b = multi_ws_bytes(k, n, jobs, m, w_dtype, false, false);
-    const uint64_t q = multi_ws_bytes(k, n, jobs, m, w_dtype, false, true);
+    // the largest of the plain, norm-producing, gate/up (two jobs of equal n) and
+    // QK-normed shapes
+    uint64_t b = multi_ws_bytes(k, n, jobs, m, w_dtype, false, false, false);
+    const uint64_t q = multi_ws_bytes(k, n, jobs, m, w_dtype, false, true, false);
     b = q > b ? q : b;
+    const uint64_t e = multi_ws_bytes(k, n, jobs, m, w_dtype, false, false, true);
+    b = e > b ? e : b;
     if (jobs == 2 && n[0] == n[1]) {
-        const uint64_t g = multi_ws_bytes(k, n, jobs, m, w_dtype, true, false);
+        const uint64_t g = multi_ws_bytes(k, n, jobs, m, w_dtype, true, false, false);
         b = g > b ? g : b;
     }
     return b;
@@ -993,13 +1001,15 @@ uint64_t proj_batch_multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs,
 
 uint64_t proj_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int x_dtype, int w_dtype) {
     (void)x_dtype;
-    return multi_ws_bytes(k, &n, 1, m, w_dtype, false, false);
+    const uint64_t a = multi_ws_bytes(k, &n, 1, m, w_dtype, false, false, false);
+    const uint64_t e = multi_ws_bytes(k, &n, 1, m, w_dtype, false, false, true);
+    return a > e ? a : e;
 }
 
 uint32_t proj_batch_norm_cols(int w_dtype, uint32_t k, uint32_t n, uint32_t m) {
     if (w_dtype == LG_Q4_K_T16) w_dtype = LG_Q4_K;
     if (w_dtype == LG_Q8_0_T16) w_dtype = LG_Q8_0;
-    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32, false, false);
+    const MmShape sh = mm_shape(w_dtype, k, n, m < 32 ? m : 32, false, false, true);
     return (n + 64 * sh.rt - 1) / (64 * sh.rt);
 }
 
@@ -1092,7 +1102,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         if (glu) LG_TRY(lg_dispatch_activation(jb[0].c, jb[1].c, jb[0].c, m * jb[0].n, s));
         return LG_OK;
     }
-    const uint64_t need = multi_ws_bytes(k, nv, njobs, m, w_dtype, glu, qkn);
+    const uint64_t need = multi_ws_bytes(k, nv, njobs, m, w_dtype, glu, qkn, epi);
     void *ws = ws_given;
     if (ws) {
         LG_REQUIRE(ws_bytes >= need, "%s: workspace of %llu bytes too small (%llu needed)", name,
@@ -1100,23 +1110,12 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
     } else {
         LG_TRY(stream_workspace(s, need, &ws));
     }
-    const uint32_t tiles = (m + 15) / 16, nb = k / QK_K;
-    // every token tile's fragment records, after the largest tile pair's partial sums
-    const MmShape sh0 = launch_shape(w_dtype, k, nv, njobs, m < 32 ? m : 32, glu, qkn);
-    uint64_t poff = CNT_BYTES;
-    if (sh0.slices > 1)
-        for (uint32_t j = 0; j < njobs; j++) poff += align256((uint64_t)sh0.slices * (m < 32 ? m : 32) * nv[j] * 4);
-    uint4 *fr = reinterpret_cast<uint4 *>(static_cast<uint8_t *>(ws) + poff);
-    {
-        const dim3 pg(nb, tiles * 4);
-        if (x_dtype == LG_BF16) hipLaunchKernelGGL((k_mm_prep<1, false>), pg, dim3(256), 0, s, x, nullptr, fr, m, k);
-        else if (up) hipLaunchKernelGGL((k_mm_prep<0, true>), pg, dim3(256), 0, s, x, up, fr, m, k);
-        else hipLaunchKernelGGL((k_mm_prep<0, false>), pg, dim3(256), 0, s, x, nullptr, fr, m, k);
-        LG_TRY(after_launch(name, s));
-    }
+    const uint32_t tiles = (m + 15) / 16;
+    const uint64_t xsz = x_dtype == LG_F32 ? 4 : 2;
+    const int xm = x_dtype == LG_BF16 ? 1 : (up ? 2 : 0);
     for (uint32_t t0 = 0; t0 < tiles; t0 += 2) {  // pairs of 16-token tiles
         const uint32_t ml = m - 16 * t0 < 32 ? m - 16 * t0 : 32, tt = (ml + 15) / 16;
-        const MmShape sh = launch_shape(w_dtype, k, nv, njobs, ml, glu, qkn);
+        const MmShape sh = launch_shape(w_dtype, k, nv, njobs, ml, glu, qkn, epi);
         uint32_t *cnt = static_cast<uint32_t *>(ws);
         uint8_t *pb = static_cast<uint8_t *>(ws) + CNT_BYTES;
         MmJobs jobs{};
@@ -1147,8 +1146,9 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
             jobs.rs_eps = rs->eps;
         }
         LG_REQUIRE(groups <= CNT_MAX, "%s: %u workgroup columns exceed %u", name, groups, CNT_MAX);
-        LG_TRY(launch_mm(w_dtype, tiled, glu, pnorm, tt, sh, groups, fr + (uint64_t)t0 * nb * FR_U4, jobs, cnt, ml, k,
-                         s));
+        const void *xt = static_cast<const uint8_t *>(x) + (uint64_t)16 * t0 * k * xsz;
+        const float *ut = up ? up + (uint64_t)16 * t0 * k : nullptr;
+        LG_TRY(launch_mm(w_dtype, xm, tiled, glu, pnorm, tt, sh, groups, xt, ut, jobs, cnt, ml, k, s));
     }
     return LG_OK;
 }

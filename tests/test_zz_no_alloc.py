@@ -38,13 +38,17 @@ def test_static_scratch_equals_workspace_entry_point(ctx):
 
 
 def test_static_scratch_rejects_oversize(ctx):
-    # k = 262144 at m = 64: four token tiles x 1024 chunks of fragment records (about
-    # 71 MB), past the 16 MiB scratch
-    k, n, m = 262144, 16, 64
-    need = lh.lib().lg_proj_quant_batch_ws_bytes(k, n, m, lh.Q8_0)
-    assert need > lh.STATIC_SCRATCH_BYTES
-    st = lh.lib().lg_dispatch_proj_quant_batch_static(None, lh.F32, None, None, k, n, m, lh.Q8_0, None)
-    assert st == lh.EINVAL and b"scratch" in lh.lib().lg_last_error()
+    # one 256-element chunk per k slice (a launch-shape override) at m = 32: 16 slices of
+    # 32 x 14336 partial sums (about 29 MB), past the 16 MiB scratch
+    k, n, m = 4096, 14336, 32
+    lh.check(lh.lib().lg_set_batch_shape(1, 0))
+    try:
+        need = lh.lib().lg_proj_quant_batch_ws_bytes(k, n, m, lh.Q4_K)
+        assert need > lh.STATIC_SCRATCH_BYTES
+        st = lh.lib().lg_dispatch_proj_quant_batch_static(None, lh.F32, None, None, k, n, m, lh.Q4_K, None)
+        assert st == lh.EINVAL and b"scratch" in lh.lib().lg_last_error()
+    finally:
+        lh.check(lh.lib().lg_set_batch_shape(0, 0))
 
 
 def test_static_scratch_several_tile_pairs(ctx):
@@ -64,30 +68,36 @@ def test_static_scratch_several_tile_pairs(ctx):
 
 
 def test_static_scratch_limit(ctx):
-    # the largest k (n = 64, m = 16) whose workspace fits the scratch runs and equals the
-    # workspace entry point; the next multiple of 256 is refused
-    n, m = 64, 16
+    # with one chunk per k slice (a launch-shape override), the largest k (n = 1024,
+    # m = 32) whose partial sums fit the scratch runs and equals the workspace entry
+    # point; the next multiple of 256 is refused
+    n, m = 1024, 32
     L = lh.lib()
-    k = 256
-    while L.lg_proj_quant_batch_ws_bytes(k + 256, n, m, lh.Q4_K) <= lh.STATIC_SCRATCH_BYTES:
-        k += 256
-    print(f"static scratch limit: k={k} fits, k={k + 256} does not", flush=True)
-    raw = synth.q4k_weight(0x5EED0023, k + 256, n)
-    x = synth.normal(0x5EED0024, m * (k + 256))
-    wb = lh.upload_bytes(ctx, raw)
-    xb = lh.upload_f32(ctx, x)
-    cb = lh.GpuBuffer(ctx, 4 * m * n)
-    st = L.lg_dispatch_proj_quant_batch_static(xb.ptr, lh.F32, wb.ptr, cb.ptr, k + 256, n, m, lh.Q4_K, ctx.stream)
-    assert st == lh.EINVAL and b"scratch" in L.lg_last_error()
-    cb.free()
-    raw = synth.q4k_weight(0x5EED0023, k, n)
-    wb.free()
-    wb = lh.upload_bytes(ctx, raw)
-    xs = x[: m * k]
-    xb.free()
-    xb = lh.upload_f32(ctx, xs)
-    want = run(ctx, "lg_dispatch_proj_quant_batch", xb, lh.F32, wb, k, n, m, lh.Q4_K)
-    got = run(ctx, "lg_dispatch_proj_quant_batch_static", xb, lh.F32, wb, k, n, m, lh.Q4_K)
+    lh.check(L.lg_set_batch_shape(1, 0))
+    try:
+        k = 256
+        while L.lg_proj_quant_batch_ws_bytes(k + 256, n, m, lh.Q4_K) <= lh.STATIC_SCRATCH_BYTES:
+            k += 256
+        print(f"static scratch limit: k={k} fits, k={k + 256} does not", flush=True)
+        raw = synth.q4k_weight(0x5EED0023, k + 256, n)
+        x = synth.normal(0x5EED0024, m * (k + 256))
+        wb = lh.upload_bytes(ctx, raw)
+        xb = lh.upload_f32(ctx, x)
+        cb = lh.GpuBuffer(ctx, 4 * m * n)
+        st = L.lg_dispatch_proj_quant_batch_static(xb.ptr, lh.F32, wb.ptr, cb.ptr, k + 256, n, m, lh.Q4_K,
+                                                   ctx.stream)
+        assert st == lh.EINVAL and b"scratch" in L.lg_last_error()
+        cb.free()
+        raw = synth.q4k_weight(0x5EED0023, k, n)
+        wb.free()
+        wb = lh.upload_bytes(ctx, raw)
+        xs = x[: m * k]
+        xb.free()
+        xb = lh.upload_f32(ctx, xs)
+        want = run(ctx, "lg_dispatch_proj_quant_batch", xb, lh.F32, wb, k, n, m, lh.Q4_K)
+        got = run(ctx, "lg_dispatch_proj_quant_batch_static", xb, lh.F32, wb, k, n, m, lh.Q4_K)
+    finally:
+        lh.check(L.lg_set_batch_shape(0, 0))
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     y64, a = orc.proj_quant_f64(xs.reshape(m, k), raw, lh.Q4_K, k, n)
     parity(got, y64, a)
