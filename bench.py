@@ -261,11 +261,12 @@ class DFlashBlock(Workload):
 
     graph_mode = False  # the forward is itself a graph (or its eager launches)
 
-    def __init__(self, m=16, ctx_len=2048, seed=0x5EED000A, graph=True):
-        self.m, self.ctx_len, self.seed, self.as_graph = m, ctx_len, seed, graph
+    def __init__(self, m=16, ctx_len=2048, seed=0x5EED000A, graph=True, tiled=True):
+        self.m, self.ctx_len, self.seed, self.as_graph, self.tiled = m, ctx_len, seed, graph, tiled
         self.cfg = lh.DFlashConfig()
         self.name = (f"DFlash 6-layer block forward, {m} tokens over {ctx_len}-position f32 KV "
-                     f"({'HIP graph' if graph else 'eager'})")
+                     f"({'HIP graph' if graph else 'eager'}, "
+                     f"{'16-row tiles' if tiled else 'raw GGUF blocks'})")
 
     def setup(self, ctx, stream=None):
         cfg, m = self.cfg, self.m
@@ -276,7 +277,7 @@ class DFlashBlock(Workload):
         wbytes += sum(nbytes(L[n]) for L in layers for n in lh.DFLASH_NORMS + lh.DFLASH_PROJ)
         kvbytes = sum(nbytes(a) for a in kc + vc)
         self.bytes_per_call = wbytes + kvbytes + feat.nbytes + tok.nbytes + 4 * m * cfg.n_embd
-        self.model = lh.DFlashModel(ctx, cfg, W, layers)
+        self.model = lh.DFlashModel(ctx, cfg, W, layers, tiled=self.tiled)
         self.model.set_context(kc, vc)
         del W, layers, kc, vc
         self.fb, self.tb = lh.upload_f32(ctx, feat), lh.upload_f32(ctx, tok)
@@ -464,6 +465,8 @@ WORKLOADS = {
     "lm_head_verify_m16": lambda: VerifyBlock(4096, 151936, 0x5EED000B),
     "dflash_block": lambda: DFlashBlock(),
     "dflash_block_eager": lambda: DFlashBlock(graph=False),
+    # the same forward over the raw GGUF blocks as uploaded (no repack at load)
+    "dflash_block_raw": lambda: DFlashBlock(graph=False, tiled=False),
     "target_token": lambda: TargetToken(),
     "ceil_empty": lambda: Empty(256),
     "ceil_read_17.8MB": lambda: Read(17858560),
@@ -472,7 +475,7 @@ WORKLOADS = {
 }
 EXTRA = ["q8_0_m1", "q4k_down_silu", "q4k_m1_k14336", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
          "q8_0_m16_f32", "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16",
-         "dflash_block", "dflash_block_eager", "target_token", "ceil_empty"]
+         "dflash_block", "dflash_block_eager", "dflash_block_raw", "target_token", "ceil_empty"]
 
 
 def time_workload(ctx, hip, wl, steps, warmup, launches=None):
