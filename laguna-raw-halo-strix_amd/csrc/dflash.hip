@@ -333,20 +333,21 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(QkJob a, QkJob b, const fl
 // (k1, v1) row p - n0 (the reference's K/V sequence without the host copy).  Query qi
 // of kv head h is (row t = qi / G, q head h*G + qi % G), at position qpos0 + t.
 
-constexpr uint32_t AHD = 128;       // head dim of the matrix-core path
-constexpr uint32_t ACH = 64;        // positions per chunk (workgroup)
-constexpr uint32_t AQ = 64;         // queries per kv head handled by one workgroup
+constexpr uint32_t AHD = 128;  // head dim of the matrix-core path
+constexpr uint32_t ACH = 64;   // positions per chunk of the few-query kernels (k_attn_decode, k_attn_token)
+constexpr uint32_t AQ = 64;    // queries per kv head handled by one workgroup
+constexpr uint32_t AMT = 5;    // most 16-position tiles per chunk of k_attn_chunk
 constexpr uint32_t KSTR = AHD + 8;  // bf16 row stride of the K tile (padding against bank conflicts)
-constexpr uint32_t VSTR = ACH + 8;  // bf16 row stride of the transposed V tile
-constexpr uint32_t PSTR = ACH + 8;  // bf16 row stride of P
 constexpr int NP = 3;               // bf16 parts per f32 operand
 
 // f32 operands enter the matrix cores as three bf16 parts x = x0 + x1 + x2, each the
 // nearest bf16 of what the previous parts leave: together all 24 significant bits.
+// MT position tiles: K rows, and V^T columns in whole 32-position steps of P V.
+template <int MT>
 struct __attribute__((aligned(16))) AttnLds {
-    uint16_t k[NP][ACH * KSTR];
-    uint16_t v[NP][AHD * VSTR];  // transposed: [dim][position]
-    uint16_t p[NP][AQ * PSTR];
+    static constexpr uint32_t KR = 16 * MT, VC = 32 * ((MT + 1) / 2), VSTR = VC + 8;
+    uint16_t k[NP][KR * KSTR];
+    uint16_t v[NP][AHD * VSTR];  // V^T: [dim][position, in P V operand order]
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -372,66 +373,82 @@ __device__ __forceinline__ bf16x8 ld_frag(const uint16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(p));
 }
 
+// d[t] += a[t] b for N tiles over the six part products that reach f32 precision
+// (|a_i b_j| <= 2^-9(i+j) |a b|; the three dropped ones are below 2^-26), smallest
+// first; each product is issued for every tile before the next (independent
+// accumulators back to back).
+template <int N>
+__device__ __forceinline__ void mfma6_n(const bf16x8 (*a)[NP], const bf16x8 *b, f32x4 *d) {
+    constexpr int ia[6] = {1, 2, 0, 1, 0, 0}, ib[6] = {1, 0, 2, 0, 1, 0};
+#pragma unroll
+    for (int j = 0; j < 6; j++)
+#pragma unroll
+        for (int t = 0; t < N; t++) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][ia[j]], b[ib[j]], d[t], 0, 0, 0);
+}
 
-// D += A B over the six part products that reach f32 precision (|a_i b_j| <= 2^-9(i+j)
-// |a b|; the three dropped ones are below 2^-26), smallest first.
-__device__ __forceinline__ f32x4 mfma6(const bf16x8 *a, const bf16x8 *b, f32x4 d) {
-    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[1], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[0], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[2], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[0], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[1], d, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[0], d, 0, 0, 0);
-    return d;
+// Max over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows), in every lane.
+__device__ __forceinline__ float rows4_max(float v) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// Chunks of k_attn_chunk: the sequence's ceil(S / 16) position tiles split into nch
+// runs of consecutive tiles, chunk c taking tiles [c nt / nch, (c + 1) nt / nch).
+__host__ __device__ inline uint32_t attn_tile0(uint32_t c, uint32_t nt, uint32_t nch) {
+    return (uint32_t)((uint64_t)c * nt / nch);
 }
 
 // Partials per (kv head, chunk, query): O (unnormalised, AHD floats), max, sum.
-// Wavefront w owns queries 16w..16w+15 (A operands in registers), all 64 positions
-// of the chunk (K tile in LDS) and all 128 output dims (V tile in LDS).
+// Wavefront w owns queries 16w .. 16w + 15 and computes, over the chunk's (at most
+// MT) position tiles,
+//   S^T = K Q^T     A = K rows from LDS, B = the wave's query rows (registers);
+//   P = exp(S - max) per query: a lane holds 4 positions x MT tiles of one query, so
+//                   its max and sum take two lane swaps;
+//   O^T = V^T P^T   A = V^T from LDS, B = P^T straight from the S^T registers: the
+//                   eight k values of lane l are positions 4(l/16) + {0..3} of two
+//                   consecutive tiles, and V^T's columns are stored in that order.
+// All MT tiles are computed (zero K and V past the chunk's own): the chunks of one
+// launch take MT - 1 or MT tiles, and the longest sets the launch's time.
+// O^T lands as 4 consecutive dims of one query per lane: one 16-byte store each.
+template <int MT>
 __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q, const float *__restrict__ k0,
                                                     const float *__restrict__ v0, uint32_t n0,
                                                     const float *__restrict__ k1, const float *__restrict__ v1,
                                                     uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv,
                                                     uint32_t qpos0, int causal, float scale, uint32_t nch,
                                                     float *__restrict__ part_o, float *__restrict__ part_ml) {
-    __shared__ AttnLds L;
+    using Lds = AttnLds<MT>;
+    constexpr uint32_t VSTR = Lds::VSTR, NKS = Lds::VC / 32, VQ = Lds::VC / 4;  // V position quads
+    constexpr uint32_t KB = 4 * MT * 32, VB = VQ * 32;                          // 4x4 blocks of K, of V
+    constexpr int KR = (KB + 255) / 256, VR = (VB + 255) / 256;
+    __shared__ Lds L;
     const uint32_t h = blockIdx.y, c = blockIdx.x;
     const uint32_t G = n_q / n_kv, nq = rows * G;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t l16 = lane & 15u, kg = lane >> 4;
     const uint32_t kvld = n_kv * AHD, qld = n_q * AHD;
-
-    // K and V of the chunk's 64 positions as bf16 parts.  A thread takes blocks of 4
-    // positions x 4 dims (two rounds): K rows and the transposed V rows go to LDS 4
-    // values (8 bytes) at a time.  Every load of both rounds is issued first.  K
-    // blocks run along the dims (a wavefront writes two whole K rows); V blocks run
-    // along the positions, so that the 16 lanes writing one V^T row write 128
-    // contiguous bytes (along the dims, lanes 576 bytes apart share banks 8 ways).
-    constexpr int KVR = (ACH / 4) * (AHD / 4) / 256;
-    float4 kq[KVR][4], vq[KVR][4];
-    auto kblk = [&](uint32_t e, uint32_t &pq, uint32_t &d) { pq = e / (AHD / 4), d = 4 * (e % (AHD / 4)); };
-    auto vblk = [&](uint32_t e, uint32_t &pq, uint32_t &d) { pq = e % (ACH / 4), d = 4 * (e / (ACH / 4)); };
-#pragma unroll
-    for (int rd = 0; rd < KVR; rd++) {
-        const uint32_t e = tid + 256u * rd;
-        uint32_t pk, dk;
-        kblk(e, pk, dk);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {  // branch-free: positions past S read position S-1 (zeroed below)
-            const uint32_t p = c * ACH + 4 * pk + i, pc = p < S ? p : S - 1;
-            const bool s0 = pc < n0;
-            kq[rd][i] = *reinterpret_cast<const float4 *>((s0 ? k0 : k1) + (uint64_t)(s0 ? pc : pc - n0) * kvld +
-                                                          h * AHD + dk);
-        }
-    }
-    // this lane's query row (A operand fragments for the 4 k-steps), then the V rows:
-    // every load is in flight together, and loads complete in issue order, so the
-    // K split waits only for K and Q, and V arrives under the scores and softmax
+    const uint32_t nt = (S + 15) / 16, tb = attn_tile0(c, nt, nch), ntl = attn_tile0(c + 1, nt, nch) - tb;
+    const uint32_t P0 = 16 * tb;                                      // first position of the chunk
+    const uint32_t pend = P0 + 16 * ntl < S ? P0 + 16 * ntl : S;      // past its last live position
+    // K and V in blocks of 4 positions x 4 dims per thread: K blocks run along the
+    // dims (two whole K rows per wavefront), V blocks along the positions (the lanes
+    // writing one V^T row write 64 contiguous bytes).  Positions at or past `pend`
+    // re-read the chunk's last live row (no further HBM traffic) and enter LDS as
+    // zeros.  The queries and K first; V's loads are issued after the K split, so that
+    // they do not delay K and the queries (every CU streams its K and V at once) and
+    // arrive under the scores.
+    auto kv_at = [&](const float *a0, const float *a1, uint32_t p, uint32_t d) {
+        const uint32_t pc = p < pend ? p : pend - 1;
+        return *reinterpret_cast<const float4 *>(
+            (pc < n0 ? a0 + (uint64_t)pc * kvld : a1 + (uint64_t)(pc - n0) * kvld) + h * AHD + d);
+    };
     const uint32_t qr = 16 * wave + l16;
-    const bool qlive = qr < nq;  // branch-free: query rows past nq read row 0, zeroed
+    const bool qlive = qr < nq;
     float4 qx[AHD / 32][2];
     {
-        const uint32_t t = qlive ? qr / G : 0, hq = qlive ? h * G + qr % G : h * G;
+        const uint32_t t = qlive ? qr / G : 0, hq = qlive ? h * G + qr % G : h * G;  // dead rows read row 0, zeroed
         const float *qp = q + (uint64_t)t * qld + hq * AHD + 8 * kg;
 #pragma unroll
         for (int ks = 0; ks < (int)(AHD / 32); ks++) {
@@ -439,44 +456,41 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
             qx[ks][1] = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
         }
     }
+    float4 kq[KR][4], vq[VR][4];
 #pragma unroll
-    for (int rd = 0; rd < KVR; rd++) {
-        const uint32_t e = tid + 256u * rd;
-        uint32_t pv, dv;
-        vblk(e, pv, dv);
+    for (int rd = 0; rd < KR; rd++) {
+        const uint32_t e = tid + 256u * rd, pk = e / 32, dk = 4 * (e % 32);
+        if (KB % 256 && e >= KB) break;  // uniform over the wavefront
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t pw = c * ACH + 4 * pv + i, pwc = pw < S ? pw : S - 1;
-            const bool sv = pwc < n0;
-            vq[rd][i] = *reinterpret_cast<const float4 *>((sv ? v0 : v1) + (uint64_t)(sv ? pwc : pwc - n0) * kvld +
-                                                          h * AHD + dv);
-        }
+        for (int i = 0; i < 4; i++) kq[rd][i] = kv_at(k0, k1, P0 + 4 * pk + i, dk);
     }
 #pragma unroll
-    for (int rd = 0; rd < KVR; rd++) {
-        const uint32_t e = tid + 256u * rd;
-        uint32_t pk, dk;
-        kblk(e, pk, dk);
-        float fk[4][4];  // [position][dim]
+    for (int rd = 0; rd < KR; rd++) {
+        const uint32_t e = tid + 256u * rd, pk = e / 32, dk = 4 * (e % 32);
+        if (KB % 256 && e >= KB) break;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool okk = c * ACH + 4 * pk + i < S;
+        for (int i = 0; i < 4; i++) {  // K: position P0 + 4pk + i, dims dk..dk+3
+            const bool ok = P0 + 4 * pk + i < pend;
             const float4 kv = kq[rd][i];
-            fk[i][0] = okk ? kv.x : 0.f, fk[i][1] = okk ? kv.y : 0.f, fk[i][2] = okk ? kv.z : 0.f;
-            fk[i][3] = okk ? kv.w : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {  // K: position 4pk+i, dims dk..dk+3
             uint32_t a[2], b[2], cc[2];
-            split3x2(fk[i][0], fk[i][1], a[0], b[0], cc[0]);
-            split3x2(fk[i][2], fk[i][3], a[1], b[1], cc[1]);
+            split3x2(ok ? kv.x : 0.f, ok ? kv.y : 0.f, a[0], b[0], cc[0]);
+            split3x2(ok ? kv.z : 0.f, ok ? kv.w : 0.f, a[1], b[1], cc[1]);
             const uint32_t o = (4 * pk + i) * KSTR + dk;
             *reinterpret_cast<uint2 *>(L.k[0] + o) = make_uint2(a[0], a[1]);
             *reinterpret_cast<uint2 *>(L.k[1] + o) = make_uint2(b[0], b[1]);
             *reinterpret_cast<uint2 *>(L.k[2] + o) = make_uint2(cc[0], cc[1]);
         }
     }
-    bf16x8 qa[AHD / 32][NP];
+    // V, now that K is in LDS: its loads stream under the scores
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rd = 0; rd < VR; rd++) {
+        const uint32_t e = tid + 256u * rd, pv = e % VQ, dv = 4 * (e / VQ);
+        if (VB % 256 && e >= VB) break;  // uniform over the wavefront
+#pragma unroll
+        for (int i = 0; i < 4; i++) vq[rd][i] = kv_at(v0, v1, P0 + 4 * pv + i, dv);
+    }
+    bf16x8 qb[AHD / 32][NP];
 #pragma unroll
     for (int ks = 0; ks < (int)(AHD / 32); ks++) {
         const float4 x0 = qx[ks][0], x1 = qx[ks][1];
@@ -487,120 +501,114 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q,
         for (int i = 0; i < 4; i++) split3x2(f[2 * i], f[2 * i + 1], wp[0][i], wp[1][i], wp[2][i]);
 #pragma unroll
         for (int pp = 0; pp < NP; pp++)
-            qa[ks][pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
+            qb[ks][pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
     }
     __syncthreads();
 
-    // S = Q K^T for query rows 16*wave .. +15 and the 4 position tiles
-    f32x4 Sd[4];
+    // S^T for the chunk's tiles: lane holds S[query qr][position P0 + 16pt + 4kg + r] in Sd[pt][r]
+    f32x4 Sd[MT];
 #pragma unroll
-    for (int pt = 0; pt < 4; pt++) Sd[pt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int pt = 0; pt < MT; pt++) Sd[pt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < (int)(AHD / 32); ks++) {
+        bf16x8 ka[MT][NP];
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++) {
+        for (int pt = 0; pt < MT; pt++) {
             const uint32_t ko = (16 * pt + l16) * KSTR + 32 * ks + 8 * kg;
-            const bf16x8 kb[NP] = {ld_frag(L.k[0] + ko), ld_frag(L.k[1] + ko), ld_frag(L.k[2] + ko)};
-            Sd[pt] = mfma6(qa[ks], kb, Sd[pt]);
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) ka[pt][pp] = ld_frag(L.k[pp] + ko);
         }
+        mfma6_n<MT>(ka, qb[ks], Sd);
     }
-    // scale, mask, row max / sum; lane holds rows 16w + 4kg + r, columns 16pt + l16
-    float mrow[4], lrow[4];
+    // scale, mask, the query's max and sum over the chunk
+    const uint32_t qpos = qpos0 + (qlive ? qr / G : 0);
+    float m = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t qi = 16 * wave + 4 * kg + r;
-        const uint32_t qpos = qi < nq ? qpos0 + qi / G : 0;
-        float m = -INFINITY;
+    for (int pt = 0; pt < MT; pt++)
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++) {
-            const uint32_t p = c * ACH + 16 * pt + l16;
-            const bool ok = qi < nq && p < S && (!causal || p <= qpos);
+        for (int r = 0; r < 4; r++) {
+            const uint32_t p = P0 + 16 * pt + 4 * kg + r;
+            const bool ok = qlive && p < pend && (!causal || p <= qpos);
             const float sv = ok ? Sd[pt][r] * scale : -INFINITY;
             Sd[pt][r] = sv;
             m = fmaxf(m, sv);
         }
+    m = rows4_max(m);
+    const float mu = m == -INFINITY ? 0.0f : m;  // a fully masked query has P = 0
+    float l = 0.0f;
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
-        const float mu = m == -INFINITY ? 0.0f : m;  // a fully masked row has P = 0
-        float l = 0.0f;
+    for (int pt = 0; pt < MT; pt++)
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++) {
+        for (int r = 0; r < 4; r++) {
             const float pv = expf(Sd[pt][r] - mu);
             Sd[pt][r] = pv;
             l += pv;
         }
+    l = lane_add_x32(lane_add_x16(l));
+    // V^T to LDS, now that the scores are done: block (positions 4pv..4pv+3, dims
+    // dv..dv+3); position 32b + 16hh + 4g + j of the chunk goes to column 32b + 8g + 4hh + j
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o);
-        mrow[r] = m, lrow[r] = l;
-    }
-    // P to LDS (rows of this wave only) as bf16 parts in A-operand order
-#pragma unroll
-    for (int pt = 0; pt < 4; pt++)
-#pragma unroll
-        for (int r = 0; r < 4; r += 2) {  // rows r and r+1 converted together
-            const uint32_t idx = (16 * wave + 4 * kg + r) * PSTR + 16 * pt + l16;
-            uint32_t w[NP];
-            split3x2(Sd[pt][r], Sd[pt][r + 1], w[0], w[1], w[2]);
-#pragma unroll
-            for (int pp = 0; pp < NP; pp++) {
-                L.p[pp][idx] = (uint16_t)w[pp];
-                L.p[pp][idx + PSTR] = (uint16_t)(w[pp] >> 16);
-            }
-        }
-    // V^T to LDS (dim dv+j, positions 4pv..4pv+3), now that the scores are done
-#pragma unroll
-    for (int rd = 0; rd < KVR; rd++) {
-        const uint32_t e = tid + 256u * rd;
-        uint32_t pv, dv;
-        vblk(e, pv, dv);
-        float fv[4][4];  // [position][dim]
+    for (int rd = 0; rd < VR; rd++) {
+        const uint32_t e = tid + 256u * rd, pv = e % VQ, dv = 4 * (e / VQ);
+        if (VB % 256 && e >= VB) break;
+        const uint32_t col = 32 * (pv / 8) + 8 * (pv % 4) + 4 * ((pv / 4) % 2);
+        float fv[4][4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const bool okv = c * ACH + 4 * pv + i < S;
+            const bool ok = P0 + 4 * pv + i < pend;
             const float4 vv = vq[rd][i];
-            fv[i][0] = okv ? vv.x : 0.f, fv[i][1] = okv ? vv.y : 0.f, fv[i][2] = okv ? vv.z : 0.f;
-            fv[i][3] = okv ? vv.w : 0.f;
+            fv[i][0] = ok ? vv.x : 0.f, fv[i][1] = ok ? vv.y : 0.f, fv[i][2] = ok ? vv.z : 0.f;
+            fv[i][3] = ok ? vv.w : 0.f;
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             uint32_t a[2], b[2], cc[2];
             split3x2(fv[0][j], fv[1][j], a[0], b[0], cc[0]);
             split3x2(fv[2][j], fv[3][j], a[1], b[1], cc[1]);
-            const uint32_t o = (dv + j) * VSTR + 4 * pv;
+            const uint32_t o = (dv + j) * VSTR + col;
             *reinterpret_cast<uint2 *>(L.v[0] + o) = make_uint2(a[0], a[1]);
             *reinterpret_cast<uint2 *>(L.v[1] + o) = make_uint2(b[0], b[1]);
             *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
         }
     }
-    __syncthreads();  // V^T and every wave's P rows are in LDS
+    __syncthreads();  // V^T in LDS
 
-    // O = P V for this wave's 16 query rows and the 8 dimension tiles
+    // O^T = V^T P^T over the chunk's 32-position steps and the 8 dimension tiles (two halves)
     f32x4 Od[8];
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) Od[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < (int)(ACH / 32); ks++) {
-        const uint32_t po = (16 * wave + l16) * PSTR + 32 * ks + 8 * kg;
-        const bf16x8 pa[NP] = {ld_frag(L.p[0] + po), ld_frag(L.p[1] + po), ld_frag(L.p[2] + po)};
+    for (int ks = 0; ks < (int)NKS; ks++) {
+        uint32_t wp[NP][4];
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-            const uint32_t vo = (16 * dt + l16) * VSTR + 32 * ks + 8 * kg;
-            const bf16x8 vb[NP] = {ld_frag(L.v[0] + vo), ld_frag(L.v[1] + vo), ld_frag(L.v[2] + vo)};
-            Od[dt] = mfma6(pa, vb, Od[dt]);
+        for (int i = 0; i < 2; i++) {
+            const f32x4 sv = 2 * ks + i < MT ? Sd[2 * ks + i < MT ? 2 * ks + i : 0] : (f32x4){0.f, 0.f, 0.f, 0.f};
+            split3x2(sv[0], sv[1], wp[0][2 * i], wp[1][2 * i], wp[2][2 * i]);
+            split3x2(sv[2], sv[3], wp[0][2 * i + 1], wp[1][2 * i + 1], wp[2][2 * i + 1]);
+        }
+        bf16x8 pb[NP];
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++)
+            pb[pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            bf16x8 va[4][NP];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t vo = (16 * (4 * half + t) + l16) * VSTR + 32 * ks + 8 * kg;
+#pragma unroll
+                for (int pp = 0; pp < NP; pp++) va[t][pp] = ld_frag(L.v[pp] + vo);
+            }
+            mfma6_n<4>(va, pb, Od + 4 * half);
         }
     }
-    // partials: O[q][d], (m, l)[q]
-    const uint64_t pbase = ((uint64_t)h * nch + c) * AQ;
+    // partials: O[q][d] (lane: dims 16dt + 4kg .. +3 of query qr), (m, l)[q]
+    if (!qlive) return;
+    const uint64_t pq = ((uint64_t)h * nch + c) * AQ + qr;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t qi = 16 * wave + 4 * kg + r;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) part_o[(pbase + qi) * AHD + 16 * dt + l16] = Od[dt][r];
-        if (l16 == 0) {
-            part_ml[2 * (pbase + qi)] = mrow[r];
-            part_ml[2 * (pbase + qi) + 1] = lrow[r];
-        }
-    }
+    for (int dt = 0; dt < 8; dt++)
+        __builtin_nontemporal_store(Od[dt], reinterpret_cast<f32x4 *>(part_o + pq * AHD + 16 * dt + 4 * kg));
+    if (kg == 0) __builtin_nontemporal_store((f32x2_t){m, l}, reinterpret_cast<f32x2_t *>(part_ml + 2 * pq));
 }
 
 __device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g : logf(1.0f + expf(g)); }  // src/dflash.rs:957
@@ -855,20 +863,21 @@ __global__ __launch_bounds__(256) void k_attn_token(TokAttn t) {
     }
 }
 
-// The block's own positions (the `tail`, at most ATAIL, after the n0 context
-// positions that the chunk kernel covers) are attended here, in f32: wave w takes
-// tail positions 16w .. 16w+15 and forms a partial like a chunk's.
+// With the few-query chunk kernels, the block's own positions (the `tail`, at most
+// ATAIL, after the n0 context positions that those chunks cover) are attended here,
+// in f32: wave w takes tail positions 16w .. 16w+15 and forms a partial like a chunk's.
 constexpr uint32_t ATAIL = 64;
 
 // out[t][hq][d] = sum_c e^(m_c - M) O_c[d] / sum_c e^(m_c - M) l_c.  One workgroup per
-// query: wave w takes the w-th quarter of the chunks (their partials loaded CB at a
-// time, all in flight together), then its part of the tail; the quarters meet in
-// LDS, added in wave order.  With `gate` ([rows][n_q]), the result of head hq of
+// query: wave w takes its part of the tail, then its share of the chunks (their
+// partials loaded CB at a time, all in flight together), merged into one partial
+// relative to the wave's own max; the four meet in LDS, each scaled to the overall
+// max, added in wave order.  With `gate` ([rows][n_q]), the result of head hq of
 // row t is then multiplied by softplus(gate[t][hq]) (gmode 1: the draft forward's
 // attention gate, src/dflash.rs:956-959; gmode 2: kernels/gate_attn.comp:27, the
 // target's, log(1 + exp(g)) with no threshold).  With gj.units > 0 the gate is
 // computed here instead (the draft's Q4_K gate, unit t * n_q + hq), by wave 3,
-// which has no share of the tail while the tail fits waves 0-2.
+// which then has no share of the chunks, nor of the tail while it fits waves 0-2.
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part_o,
                                                       const float *__restrict__ part_ml, float *__restrict__ out,
                                                       uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t nch,
@@ -876,7 +885,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
                                                       const float *__restrict__ k1, const float *__restrict__ v1,
                                                       uint32_t T, uint32_t n0, uint32_t qpos0, int causal,
                                                       float scale, int gmode, GateJob gj) {
-    constexpr uint32_t CB = 8, TW = ATAIL / 4;
+    constexpr uint32_t CB = 12, TW = ATAIL / 4;
     __shared__ float sm[4], sl[4], so[4][AHD], sg;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t gq = blockIdx.x;  // over n_kv * AQ
@@ -884,7 +893,9 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     const uint32_t h = gq / AQ, qi = gq % AQ;
     if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup
     const uint64_t q0 = (uint64_t)h * nch * AQ + qi;  // partial index of chunk c: q0 + c * AQ
-    const uint32_t per = (nch + 3) / 4, cb0 = wave * per, cb1 = cb0 + per < nch ? cb0 + per : nch;
+    // the chunks over waves 0-3, or 0-2 when wave 3 computes the gate
+    const uint32_t nw = gj.units ? 3 : 4, per = (nch + nw - 1) / nw;
+    const uint32_t cb0 = wave < nw ? wave * per : nch, cb1 = cb0 + per < nch ? cb0 + per : nch;
     if (gj.units && wave == 3) {  // uniform over the wave
         const float gv = gate_value(gj, (qi / G) * n_q + h * G + qi % G, lane);
         if (lane == 0) sg = gv;
@@ -923,51 +934,51 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
             }
         }
     }
-    float M = tm;
-    for (uint32_t c0 = cb0; c0 < cb1; c0 += CB) {
-        float mc[CB];
-#pragma unroll
-        for (uint32_t b = 0; b < CB; b++) mc[b] = c0 + b < cb1 ? part_ml[2 * (q0 + (c0 + b) * AQ)] : -INFINITY;
-#pragma unroll
-        for (uint32_t b = 0; b < CB; b++) M = fmaxf(M, mc[b]);
-    }
-    if (lane == 0) sm[wave] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
-    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    // This wave's chunks, CB at a time with every load in flight, merged into the
+    // wave's (M, L, o0, o1) after its tail partial: what is merged so far is rescaled
+    // to the batch's max (exactly 1 when the max does not move).
+    float M = tm, L = tl, o0 = t0, o1 = t1;
     for (uint32_t c0 = cb0; c0 < cb1; c0 += CB) {
         float mc[CB], lc[CB], a0[CB], a1[CB];
 #pragma unroll
         for (uint32_t b = 0; b < CB; b++) {
             const uint32_t c = c0 + b < cb1 ? c0 + b : cb1 - 1;
             const uint64_t pq = q0 + (uint64_t)c * AQ;
-            mc[b] = c0 + b < cb1 ? part_ml[2 * pq] : -INFINITY;
-            lc[b] = part_ml[2 * pq + 1];
+            const float2 ml = *reinterpret_cast<const float2 *>(part_ml + 2 * pq);
+            mc[b] = c0 + b < cb1 ? ml.x : -INFINITY;
+            lc[b] = ml.y;
             a0[b] = part_o[pq * AHD + lane];
             a1[b] = part_o[pq * AHD + 64 + lane];
         }
+        float mn = M;
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) mn = fmaxf(mn, mc[b]);
+        const float f = M == -INFINITY ? 0.0f : expf(M - mn);
+        L *= f, o0 *= f, o1 *= f;
 #pragma unroll
         for (uint32_t b = 0; b < CB; b++) {  // chunk order
-            const float wgt = mc[b] == -INFINITY ? 0.0f : expf(mc[b] - M);
+            const float wgt = mc[b] == -INFINITY ? 0.0f : expf(mc[b] - mn);
             L = __builtin_fmaf(wgt, lc[b], L);
             o0 = __builtin_fmaf(wgt, a0[b], o0);
             o1 = __builtin_fmaf(wgt, a1[b], o1);
         }
+        M = mn;
     }
-    if (tm != -INFINITY) {  // the tail after the chunks
-        const float wgt = expf(tm - M);
-        L = __builtin_fmaf(wgt, tl, L);
-        o0 = __builtin_fmaf(wgt, t0, o0);
-        o1 = __builtin_fmaf(wgt, t1, o1);
-    }
-    if (lane == 0) sl[wave] = L;
+    if (lane == 0) sm[wave] = M, sl[wave] = L;
     so[wave][lane] = o0;
     so[wave][64 + lane] = o1;
     __syncthreads();
     if (wave != 0) return;
-    L = ((sl[0] + sl[1]) + sl[2]) + sl[3];
-    o0 = ((so[0][lane] + so[1][lane]) + so[2][lane]) + so[3][lane];
-    o1 = ((so[0][64 + lane] + so[1][64 + lane]) + so[2][64 + lane]) + so[3][64 + lane];
+    // the four waves in wave order, each scaled to the overall max
+    const float Mx = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+    L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float f = sm[w] == -INFINITY ? 0.0f : expf(sm[w] - Mx);
+        L = __builtin_fmaf(f, sl[w], L);
+        o0 = __builtin_fmaf(f, so[w][lane], o0);
+        o1 = __builtin_fmaf(f, so[w][64 + lane], o1);
+    }
     const uint32_t t = qi / G, hq = h * G + qi % G;
     float *o = out + (uint64_t)t * n_q * AHD + hq * AHD;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
@@ -1100,6 +1111,14 @@ int run_qk_norm_rope(const QkJob &a, const QkJob &b, const float *freq, uint32_t
 
 bool aligned16_ptr(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Chunks per kv head of k_attn_chunk over S positions: four 16-position tiles each,
+// or, when that would not fit one round of workgroups (one per CU) and at most AMT
+// tiles each would, one chunk per CU.  Never more than ceil(S / 64).
+uint32_t attn_chunks(uint32_t S, uint32_t n_kv) {
+    const uint32_t nt = (S + 15) / 16, n4 = (nt + 3) / 4, cap = (uint32_t)device_cus() / n_kv;
+    return n4 > cap && cap && (nt + cap - 1) / cap <= AMT ? cap : n4;
+}
+
 size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
     const uint32_t nch = (S + ACH - 1) / ACH;
     return (size_t)n_kv * nch * AQ * (AHD + 2);
@@ -1113,21 +1132,33 @@ int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0,
                   const GateJob *gj = nullptr) {
     const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
     const uint32_t G = n_q / n_kv;
-    if (part && hd == AHD && rows * G <= AQ) {
-        // The chunks cover the context; a short run of positions after it (the
-        // block's own keys in k1) is attended by the combine, so that the chunk
-        // grid does not spill a few workgroups into a second round.
-        const uint32_t T = k1 && S > n0 && S - n0 <= ATAIL ? S - n0 : 0;
-        const uint32_t Sc = T ? n0 : S, nch = (Sc + ACH - 1) / ACH;
+    const bool al = aligned16_ptr(q) && aligned16_ptr(k0) && aligned16_ptr(v0) &&
+                    (!k1 || (aligned16_ptr(k1) && aligned16_ptr(v1)));
+    if (part && hd == AHD && rows * G <= AQ && al) {
+        uint32_t T = 0, Sc = S, nch;
+        if (rows * G <= ADQ) {
+            // The chunks cover the context; a short run of positions after it (the
+            // block's own keys in k1) is attended by the combine, so that the chunk
+            // grid does not spill a few workgroups into a second round.
+            T = k1 && S > n0 && S - n0 <= ATAIL ? S - n0 : 0;
+            Sc = T ? n0 : S;
+            nch = (Sc + ACH - 1) / ACH;
+        } else {
+            nch = attn_chunks(S, n_kv);  // every position, up to AMT tiles per chunk
+        }
         float *part_ml = part + (size_t)n_kv * nch * AQ * AHD;
-        if (nch && rows * G <= ADQ && aligned16_ptr(q) && aligned16_ptr(k0) && aligned16_ptr(v0) &&
-            (!k1 || (aligned16_ptr(k1) && aligned16_ptr(v1)))) {
+        if (nch && rows * G <= ADQ) {
             hipLaunchKernelGGL(k_attn_decode, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, Sc,
                                rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
             LG_TRY(after_launch("attn_decode", s));
         } else if (nch) {
-            hipLaunchKernelGGL(k_attn_chunk, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, Sc,
-                               rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
+            const uint32_t nt = (S + 15) / 16;
+            if ((nt + nch - 1) / nch > 4)
+                hipLaunchKernelGGL(k_attn_chunk<5>, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S,
+                                   rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
+            else
+                hipLaunchKernelGGL(k_attn_chunk<4>, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S,
+                                   rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
             LG_TRY(after_launch("attn_chunk", s));
         }
         hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, part, part_ml, out, rows, n_q,

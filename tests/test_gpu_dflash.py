@@ -91,9 +91,10 @@ def test_qk_norm_rope(ctx, n_heads, hd, rows, pos):
 
 ATTN_CASES = [
     # n_q, n_kv, hd, rows, seq_len, q_pos, causal      (hd 128 with rows*G <= 64: matrix cores)
-    (32, 8, 128, 16, 2080, 2064, 1),   # the draft block: 2048 context + 16 injected + 16 tokens
-    (32, 8, 128, 16, 2070, 2054, 1),   # 32-position chunks (more than one 64-chunk per CU), ragged
-    (32, 8, 128, 9, 4100, 0, 0),       # 32-position chunks, non-causal, ragged
+    (32, 8, 128, 16, 2080, 2064, 1),   # the draft block: 2048 context + 16 injected + 16 tokens (4-5 tiles a chunk)
+    (32, 8, 128, 16, 2070, 2054, 1),   # 4-5 tiles a chunk, the last tile ragged
+    (32, 8, 128, 16, 2560, 2540, 1),   # 5 tiles in every chunk
+    (32, 8, 128, 9, 4100, 0, 0),       # more chunks than CUs: 4 tiles a chunk, non-causal, ragged
     (32, 8, 128, 1, 2, 1, 1),          # the reference's one-token sequence
     (32, 8, 128, 16, 63, 40, 1),
     (32, 8, 128, 16, 64, 10, 1),       # early rows see nothing past q_pos + r
