@@ -450,6 +450,7 @@ HEAD_KERNEL = "k_q4k_m1_dig"
 WORKLOADS = {
     "q4k_m1": lambda: MatvecM1(lh.Q4_K, 4096, 14336, 0x5EED0003, kernel=HEAD_KERNEL),
     "q8_0_m1": lambda: MatvecM1(lh.Q8_0, 4096, 4096, 0x5EED0001, kernel="k_q80_m1_dig"),
+    "q4k_m1_4096": lambda: MatvecM1(lh.Q4_K, 4096, 4096, 0x5EED000F, kernel=HEAD_KERNEL),
     "q4k_down_silu": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, fused=True, kernel="k_q4k_m1_wide"),
     "q4k_m1_k14336": lambda: MatvecM1(lh.Q4_K, 14336, 4096, 0x5EED0005, kernel="k_q4k_m1_wide"),
     "q4k_m1_k20480": lambda: MatvecM1(lh.Q4_K, 20480, 4096, 0x5EED000C, kernel="k_q4k_m1"),
@@ -473,7 +474,7 @@ WORKLOADS = {
     "ceil_read_33.1MB": lambda: Read(33103872),
     "ceil_read_350MB": lambda: Read(350684672),
 }
-EXTRA = ["q8_0_m1", "q4k_down_silu", "q4k_m1_k14336", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
+EXTRA = ["q8_0_m1", "q4k_m1_4096", "q4k_down_silu", "q4k_m1_k14336", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
          "q8_0_m16_f32", "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16",
          "dflash_block", "dflash_block_eager", "dflash_block_raw", "target_token", "ceil_empty"]
 

@@ -850,9 +850,10 @@ __device__ __forceinline__ void dig_load_x(const float *__restrict__ x, uint32_t
 
 // After a barrier that follows dg.bad = 0; flags dg.bad when some live group cannot be
 // scaled (non-finite, >= 2^21, nonzero below 2^-60).  A barrier must follow before
-// dig_read.
+// dig_read.  Threads past the first 256 (workgroups of eight wavefronts) convert nothing.
 __device__ __forceinline__ void dig_convert(const float4 (&xv)[4], uint32_t k, DigLds &dg) {
     const uint32_t tid = threadIdx.x;
+    if (tid >= 256) return;  // uniform over the wavefront
     float v[16];
 #pragma unroll
     for (int j = 0; j < 4; j++) v[4 * j] = xv[j].x, v[4 * j + 1] = xv[j].y, v[4 * j + 2] = xv[j].z, v[4 * j + 3] = xv[j].w;
@@ -953,7 +954,7 @@ template <int TEAMS, int R, bool IN, int NJ = 1, bool GLU = false>
 __device__ __forceinline__ void q4k_m1_dig_body(const float *__restrict__ x, const uint8_t *__restrict__ w,
                                                 float *__restrict__ y, uint32_t k, uint32_t n, uint64_t row_bytes,
                                                 const DigIn &in) {
-    static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
+    static_assert(TEAMS == 4 || (TEAMS == 8 && !IN), "the first 256 threads convert 16 of the 4096 elements each");
     static_assert(!GLU || (IN && NJ == 2 && R == 2), "GLU pairs the two rows of a wave");
     __shared__ __attribute__((aligned(16))) DigLds dg;
     __shared__ float ssq[IN ? TEAMS : 1];
@@ -1743,10 +1744,22 @@ template <bool FUSE>
 int launch_q4k(const float *x, const float *up, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
     const uint32_t P = k / 64;
     if (P <= 64 && !FUSE) {
+        const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed), cus = (uint32_t)device_cus();
+        if (n <= 16 * cus) {
+            // at most two rows per wavefront: one 8-wavefront workgroup per CU (half the
+            // conversions of x), the wave's two rows in flight from the start.  Measured
+            // on 4096 -> 4096: 4.60 against 5.14 us for the layout below.
+            constexpr int TEAMS = 8, R = 1;
+            uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
+            const uint32_t cap = gc ? gc : cus;
+            grid = grid < cap ? grid : cap;
+            hipLaunchKernelGGL((k_q4k_m1_dig<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
+                               (uint64_t)k / QK_K * Q4K_BYTES);
+            return after_launch("proj_q4k_m1", s);
+        }
         constexpr int TEAMS = 4, R = 2;
         uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
-        const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed);
-        const uint32_t cap = gc ? gc : 512;  // two workgroups per CU: measured best for 14336 rows
+        const uint32_t cap = gc ? gc : 2 * cus;  // two workgroups per CU: measured best for 14336 rows
         grid = grid < cap ? grid : cap;
         hipLaunchKernelGGL((k_q4k_m1_dig<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
                            (uint64_t)k / QK_K * Q4K_BYTES);

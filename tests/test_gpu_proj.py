@@ -37,6 +37,7 @@ def run_proj(ctx, dtype, raw, x, k, n, expert_offset=None):
     (lh.Q4_K, 4096, 14336, 0x5EED0003),   # gate/up projection, headline shape
     (lh.Q4_K, 14336, 4096, 0x5EED0005),   # down projection
     (lh.Q4_K, 12288, 4096, 0x5EED000B),   # encoder fc (3 x 4096 in)
+    (lh.Q4_K, 4096, 4096, 0x5EED000F),    # attn_q: one 8-wavefront workgroup per CU, two rows a wave
     (lh.Q4_K, 4096, 1024, 0x5EED000C),    # attn_k / attn_v
     (lh.Q4_K, 4096, 32, 0x5EED000D),      # attn_gate
     (lh.Q8_0, 4096, 4096, 0x5EED0001),    # o_proj
