@@ -1205,7 +1205,7 @@ template <int TEAMS, int R>
 __global__ __launch_bounds__(TEAMS * 64) void k_q80_m1_dig(const float *__restrict__ x, const uint8_t *__restrict__ w,
                                                             float *__restrict__ y, uint32_t k, uint32_t n,
                                                             uint64_t row_bytes) {
-    static_assert(TEAMS * 64 * 16 == 4096, "one thread converts 16 of the 4096 elements");
+    static_assert(TEAMS == 4 || TEAMS == 8, "the first 256 threads convert 16 of the 4096 elements each");
     constexpr int NL = (int)Q8_LOADS;
     __shared__ __attribute__((aligned(16))) DigLds dg;
     __shared__ __attribute__((aligned(16))) lg_u32x4 stage_all[TEAMS][64 * NL];
@@ -1796,10 +1796,22 @@ int launch_q80_t(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_
 int launch_q80(const float *x, const uint8_t *w, float *y, uint32_t k, uint32_t n, hipStream_t s) {
     const uint32_t P = k / 64;
     if (P <= 64) {
+        const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed), cus = (uint32_t)device_cus();
+        if (n <= 16 * cus) {
+            // as for Q4_K: one 8-wavefront workgroup per CU, at most two rows a wave.
+            // Measured on 4096 -> 4096: 5.10 against 5.53 us (and 6.27 with both rows
+            // of a wave loaded at once)
+            constexpr int TEAMS = 8, R = 1;
+            uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
+            const uint32_t cap = gc ? gc : cus;
+            grid = grid < cap ? grid : cap;
+            hipLaunchKernelGGL((k_q80_m1_dig<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
+                               (uint64_t)k / QK8_0 * Q80_BYTES);
+            return after_launch("proj_q8_0_m1", s);
+        }
         constexpr int TEAMS = 4, R = 2;
         uint32_t grid = (n + TEAMS * R - 1) / (TEAMS * R);
-        const uint32_t gc = g_grid_cap.load(std::memory_order_relaxed);
-        const uint32_t cap = gc ? gc : 256;  // one per CU: measured best for 4096 rows (5.62 us, 512: 5.73)
+        const uint32_t cap = gc ? gc : cus;  // one per CU: measured best for 4096 rows (5.62 us, 512: 5.73)
         grid = grid < cap ? grid : cap;
         hipLaunchKernelGGL((k_q80_m1_dig<TEAMS, R>), dim3(grid), dim3(TEAMS * 64), 0, s, x, w, y, k, n,
                            (uint64_t)k / QK8_0 * Q80_BYTES);
