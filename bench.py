@@ -261,7 +261,7 @@ class DFlashBlock(Workload):
 
     graph_mode = False  # the forward is itself a graph (or its eager launches)
 
-    def __init__(self, m=16, ctx_len=2048, seed=0x5EED000A, graph=True, tiled=True):
+    def __init__(self, m=16, ctx_len=2048, seed=0x5EED000A, graph=False, tiled=True):
         self.m, self.ctx_len, self.seed, self.as_graph, self.tiled = m, ctx_len, seed, graph, tiled
         self.cfg = lh.DFlashConfig()
         self.name = (f"DFlash 6-layer block forward, {m} tokens over {ctx_len}-position f32 KV "
@@ -464,8 +464,8 @@ WORKLOADS = {
     "q4k_lm_head_m1": lambda: MatvecM1(lh.Q4_K, 4096, 151936, 0x5EED000B, kernel=HEAD_KERNEL),
     "q4k_lm_head_m16": lambda: BatchM16(lh.Q4_K, 4096, 151936, lh.F32, 0x5EED000B, kernel="k_q4k_mm"),
     "lm_head_verify_m16": lambda: VerifyBlock(4096, 151936, 0x5EED000B),
-    "dflash_block": lambda: DFlashBlock(),
-    "dflash_block_eager": lambda: DFlashBlock(graph=False),
+    "dflash_block": lambda: DFlashBlock(graph=False),
+    "dflash_block_graph": lambda: DFlashBlock(graph=True),
     # the same forward over the raw GGUF blocks as uploaded (no repack at load)
     "dflash_block_raw": lambda: DFlashBlock(graph=False, tiled=False),
     "target_token": lambda: TargetToken(),
@@ -476,7 +476,7 @@ WORKLOADS = {
 }
 EXTRA = ["q8_0_m1", "q4k_m1_4096", "q4k_down_silu", "q4k_m1_k14336", "q4k_m1_k20480", "q4k_m16_bf16", "q4k_m16_f32", "q4k_m16_f32_tiled",
          "q8_0_m16_f32", "q8_0_m16_f32_tiled", "q4k_lm_head_m1", "q4k_lm_head_m16", "lm_head_verify_m16",
-         "dflash_block", "dflash_block_eager", "dflash_block_raw", "target_token", "ceil_empty"]
+         "dflash_block", "dflash_block_graph", "dflash_block_raw", "target_token", "ceil_empty"]
 
 
 def time_workload(ctx, hip, wl, steps, warmup, launches=None):
