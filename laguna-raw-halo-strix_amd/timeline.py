@@ -1,0 +1,200 @@
+"""Per-wavefront phase timestamps of the small-M product and the draft attention kernels.
+
+Measurement only: this builds an instrumented copy of the library in which lane 0 of
+every wavefront writes the real-time clock (s_memrealtime, 100 MHz) at the phase
+boundaries listed in STAMPS, plus the hardware CU it runs on, into a device array; then
+it runs a bench.py workload and prints, per stamp, percentiles over the wavefronts of the
+last call (ns from the first wavefront's start), and how the workgroups spread over CUs.
+The shipped library is not touched; the instrumented one is built into _timeline/
+(each wavefront's lane 0 stores its stamps with ordinary vector stores).
+
+    python timeline.py build
+    python timeline.py run WORKLOAD [mm|attn]
+
+`mm` reads the last k_mm_mf launch of the workload, `attn` the last attention chunk and
+combine launches (the draft block's last layer).
+"""
+import argparse
+import collections
+import ctypes
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT = os.path.join(HERE, "_timeline")
+LIB = os.path.join(OUT, "liblaguna_hip_timeline.so")
+HIPCC = "/opt/rocm/bin/hipcc"
+SLOTS, WAVES = 40, 6553  # stamps per wavefront, wavefronts recorded
+
+HEADER = r'''
+__device__ unsigned long long lg_tl_%(f)s[%(n)d];
+extern "C" int lg_timeline_read_%(f)s(void *host, unsigned long long bytes) {
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(lg_tl_%(f)s), bytes) == hipSuccess ? 0 : 1;
+}
+extern "C" int lg_timeline_clear_%(f)s() {
+    static unsigned long long z[%(n)d];
+    return hipMemcpyToSymbol(HIP_SYMBOL(lg_tl_%(f)s), z, sizeof(z)) == hipSuccess ? 0 : 1;
+}
+#define LG_WID() (((blockIdx.y * gridDim.x) + blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6))
+#define TS(k) do { const unsigned long long t_ = __builtin_amdgcn_s_memrealtime(); \
+    if ((threadIdx.x & 63u) == 0 && LG_WID() < %(w)du) lg_tl_%(f)s[LG_WID() * %(s)d + (k)] = t_; } while (0)
+#define TSID() do { unsigned hw_, xc_; asm volatile("s_getreg_b32 %%0, hwreg(HW_REG_HW_ID)" : "=s"(hw_)); \
+    asm volatile("s_getreg_b32 %%0, hwreg(HW_REG_XCC_ID)" : "=s"(xc_)); \
+    if ((threadIdx.x & 63u) == 0 && LG_WID() < %(w)du) \
+        lg_tl_%(f)s[LG_WID() * %(s)d + %(s)d - 1] = ((unsigned long long)xc_ << 32) | hw_; } while (0)
+'''
+
+# (file, kernel signature start, [(mode, marker, text)]): text goes after / before the
+# first occurrence of marker past the kernel's start.
+STAMPS = {
+    "proj_batch.hip": ("void k_mm_mf(", [
+        ("after", "uint32_t k, uint64_t row_bytes, uint32_t ch) {", "\n    TS(0); TSID();"),
+        ("after", "    rb.store(lrec[0], m);\n    __syncthreads();", "\n    TS(1);"),
+        ("after", "            rb.store(lrec[c & 1u], m);\n            __syncthreads();",
+         "\n            if (c < 34) TS(1 + c);"),
+        ("before", "    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lrec)", "    TS(36);\n"),
+        ("after", "jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);", "\n    TS(38);"),
+    ]),
+    "dflash.hip": ("void k_attn_chunk(", [
+        ("after", "    __shared__ Lds L;", "\n    TS(0); TSID();"),
+        ("before", "    // V, now that K is in LDS", "    TS(1);\n"),
+        ("before", "    // S^T for the chunk", "    TS(2);\n"),
+        ("before", "    // V^T to LDS, now that", "    TS(3);\n"),
+        ("before", "    // O^T = V^T P^T over", "    TS(4);\n"),
+        ("before", "    // partials: O[q][d] (lane", "    TS(5);\n"),
+        ("after", "reinterpret_cast<f32x2_t *>(part_ml + 2 * pq));", "\n    TS(6);"),
+    ]),
+    "dflash.hip#combine": ("void k_attn_combine(", [
+        ("after", "if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup", "\n    TS(20);"),
+        ("before", "    float M = tm, L = tl, o0 = t0, o1 = t1;", "    TS(21);\n"),
+        ("before", "    if (lane == 0) sm[wave] = M, sl[wave] = L;", "    TS(22);\n"),
+        ("before", "    const float Mx = fmaxf", "    TS(23);\n"),
+        ("before", "    const float inv = L > 0.0f ? 1.0f / L : 0.0f;", "    TS(24);\n"),
+    ]),
+}
+
+PHASES = {
+    "mm": [(0, "start"), (1, "chunk 0's activations in LDS"), (2, "chunk 1 in LDS"), (3, "chunk 2 in LDS"),
+           (4, "chunk 3 in LDS"), (36, "products done"), (38, "split-k finish done")],
+    "attn": [(0, "chunk: start"), (1, "K split to LDS"), (2, "queries split, barrier"), (3, "scores + softmax"),
+             (4, "V split to LDS, barrier"), (5, "P V"), (6, "partials stored"), (20, "combine: start"),
+             (21, "tail / gate"), (22, "chunk partials merged"), (23, "waves met in LDS"), (24, "result")],
+}
+
+
+def instrument(src, sig, edits):
+    s = src
+    k0 = s.index(sig)
+    for mode, marker, text in edits:
+        j = s.index(marker, k0)
+        j = j + len(marker) if mode == "after" else j
+        s = s[:j] + text + s[j:]
+    return s
+
+
+def build():
+    os.makedirs(OUT, exist_ok=True)
+    csrc = os.path.join(HERE, "csrc")
+    flags = ["-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature",
+             "-Xclang", "-packed-fp32-ops", "-I" + os.path.join(HERE, "..", "include"), "-I" + csrc]
+    extra = {"proj_batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+             "proj_m1.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
+    objs = []
+    for f in ["runtime.cpp", "gguf.cpp", "dequant.hip", "proj_m1.hip", "proj_batch.hip", "dflash.hip", "verify.hip",
+              "ceiling.hip", "target.hip"]:
+        src = open(os.path.join(csrc, f)).read()
+        if f in ("proj_batch.hip", "dflash.hip"):
+            for key, (sig, edits) in STAMPS.items():
+                if key.split("#")[0] == f:
+                    src = instrument(src, sig, edits)
+            i = src.index("namespace {")
+            tag = "mm" if f == "proj_batch.hip" else "attn"
+            src = src[:i] + HEADER % {"f": tag, "n": SLOTS * WAVES, "w": WAVES, "s": SLOTS} + src[i:]
+        path = os.path.join(OUT, f)
+        open(path, "w").write(src)
+        obj = path + ".o"
+        subprocess.run([HIPCC] + flags + extra.get(f, []) + ["-c", path, "-o", obj], check=True)
+        objs.append(obj)
+    subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-o", LIB] + objs, check=True)
+    print("built", LIB)
+
+
+def run(workload, what):
+    sys.path.insert(0, HERE)
+    sys.path.insert(0, os.path.join(HERE, ".."))
+    import numpy as np
+    import laguna_hip as lh
+    lh.LIB_PATH = LIB
+    import bench
+    L = lh.lib()
+    read = getattr(L, "lg_timeline_read_" + what)
+    read.argtypes = [ctypes.c_void_p, ctypes.c_ulonglong]
+    ctx = lh.VulkanContext(0)
+    wl = bench.WORKLOADS[workload]()
+    st = lh.Stream()
+    if isinstance(wl, bench.DFlashBlock):
+        wl.setup(ctx, st)
+    else:
+        wl.setup(ctx)
+    for i in range(10):
+        wl.step(i, st.ptr)
+    st.sync()
+    lh.check(getattr(L, "lg_timeline_clear_" + what)())
+    ctx.sync()
+    for i in range(3):  # stamps of the last call survive
+        wl.step(100 + i, st.ptr)
+    st.sync()
+    buf = np.zeros(SLOTS * WAVES, np.uint64)
+    lh.check(read(buf.ctypes.data, buf.nbytes))
+    ts = buf.reshape(WAVES, SLOTS)
+    live = (ts[:, 0] > 0) | (ts[:, 20] > 0)
+    n = int(np.nonzero(live)[0].max()) + 1
+    T = ts[:n, :SLOTS - 1].astype(np.int64)
+    starts = [T[:, k][T[:, k] > 0] for k in (0, 20)]
+    t0 = min(v.min() for v in starts if v.size)
+    print(f"{workload} ({what}): {n} wavefronts of the last call; ns from the first wavefront's start")
+    print("| stamp | phase | p10 | p50 | p90 | max |")
+    print("|---|---|---|---|---|---|")
+    for k, name in PHASES[what]:
+        v = T[:, k]
+        v = (v[v > 0] - t0) * 10
+        if v.size:
+            print(f"| {k} | {name} | {int(np.percentile(v, 10))} | {int(np.median(v))} | "
+                  f"{int(np.percentile(v, 90))} | {int(v.max())} |")
+    nw = int(np.nonzero(ts[:, 0] > 0)[0].max()) + 1  # wavefronts of the kernel that records its CU
+    ids = ts[:nw, SLOTS - 1]
+    hw, xcc = ids & 0xFFFFFFFF, ids >> 32
+    # HW_ID: CU_ID bits 8-11, SH_ID bit 12, SE_ID bits 13-15 (gfx9)
+    cu = (xcc << 8) | (((hw >> 13) & 7) << 5) | (((hw >> 12) & 1) << 4) | ((hw >> 8) & 15)
+    wpg = 4
+    wg_cu = cu[0::wpg]
+    rel = np.where(T[:nw] > 0, (T[:nw] - t0) * 10, -1)
+    end_k = 38 if what == "mm" else 6
+    ends = rel[:, end_k].reshape(-1, wpg).max(axis=1)
+    cnt = collections.Counter(wg_cu.tolist())
+    hist = collections.Counter(cnt.values())
+    print(f"\nworkgroups {len(wg_cu)} on {len(cnt)} CUs; CUs by workgroups held: {dict(sorted(hist.items()))}")
+    for c in sorted(hist):
+        sel = np.array([cnt[x] == c for x in wg_cu.tolist()])
+        e = ends[sel]
+        e = e[e >= 0]
+        if e.size:
+            print(f"workgroups on CUs holding {c}: {int(sel.sum())}, end p50 {int(np.median(e))} ns, "
+                  f"max {int(e.max())} ns")
+    wl.teardown()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    sub.add_parser("build")
+    r = sub.add_parser("run")
+    r.add_argument("workload")
+    r.add_argument("what", nargs="?", default="mm", choices=["mm", "attn"])
+    a = ap.parse_args()
+    build() if a.cmd == "build" else run(a.workload, a.what)
+
+
+if __name__ == "__main__":
+    main()
