@@ -64,8 +64,11 @@ __device__ __forceinline__ f16x8 as_f16x8(uint32_t a, uint32_t b, uint32_t c, ui
 }
 
 // Fragment record of one (16-token tile, 256-element chunk) in LDS, FR_U4 16-byte words:
-//   [0, 1024)     word (j*2 + p)*64 + l: part p (0 = hi, 1 = lo) of sub-block j's A
-//                 operand, lane l: token l%16, elements 32j + 8(l/16) + {0,2,1,3,4,6,5,7}
+//   [0, 1024)     word (j*2 + p)*64 + (l ^ (2j + l/32)): part p (0 = hi, 1 = lo) of
+//                 sub-block j's A operand, lane l: token l%16, elements
+//                 32j + 8(l/16) + {0,2,1,3,4,6,5,7}.  The XOR spreads over all LDS banks
+//                 the 16 threads of one token that store a word together (thread q of
+//                 the token stores lane slots 16(2(q%2) + h) + token, XOR q)
 //   [1024, 1056)  float2 per lane l: (X[l%16][l/16], X[l%16][l/16 + 4]), X the sums of
 //                 the scaled values over each sub-block
 //   [1056, 1060)  the 16 tokens' 2^-e
@@ -567,10 +570,10 @@ struct RecBuild {
             for (int h = 0; h < 2; h++) {
                 const uint32_t lane = ((q & 1u) * 2 + h) * 16 + tok;
                 const float *a = hi + 8 * h, *b = lo + 8 * h;
-                rec[(j * 2 + 0) * 64 + lane] = make_uint4(pk_f16(a[0], a[2]), pk_f16(a[1], a[3]), pk_f16(a[4], a[6]),
-                                                          pk_f16(a[5], a[7]));
-                rec[(j * 2 + 1) * 64 + lane] = make_uint4(pk_f16(b[0], b[2]), pk_f16(b[1], b[3]), pk_f16(b[4], b[6]),
-                                                          pk_f16(b[5], b[7]));
+                rec[(j * 2 + 0) * 64 + (lane ^ q)] = make_uint4(pk_f16(a[0], a[2]), pk_f16(a[1], a[3]),
+                                                                pk_f16(a[4], a[6]), pk_f16(a[5], a[7]));
+                rec[(j * 2 + 1) * 64 + (lane ^ q)] = make_uint4(pk_f16(b[0], b[2]), pk_f16(b[1], b[3]),
+                                                                pk_f16(b[4], b[6]), pk_f16(b[5], b[7]));
             }
             float *rf = reinterpret_cast<float *>(rec);
             if ((q & 1u) == 0) rf[4 * FR_X + ((j & 3u) * 16 + tok) * 2 + (j >> 2)] = sum;
@@ -683,7 +686,8 @@ __device__ __forceinline__ void q4k_chunk(const uint4 *lds, const Q4kChunk<RT> &
             for (int u = 0; u < 2; u++)
 #pragma unroll
                 for (int p = 0; p < 2; p++)
-                    A[t][u][p] = __builtin_bit_cast(f16x8, lds[t * FR_U4 + ((2 * g + u) * 2 + p) * 64 + l]);
+                    A[t][u][p] = __builtin_bit_cast(
+                        f16x8, lds[t * FR_U4 + ((2 * g + u) * 2 + p) * 64 + (l ^ (2 * (2 * g + u) + (l >> 5)))]);
         f16x8 B[RT][2];
 #pragma unroll
         for (int i = 0; i < RT; i++) {
@@ -722,7 +726,8 @@ __device__ __forceinline__ void q80_chunk(const uint4 *lds, const Q80Chunk<RT> &
             for (int u = 0; u < 2; u++)
 #pragma unroll
                 for (int p = 0; p < 2; p++)
-                    A[t][u][p] = __builtin_bit_cast(f16x8, lds[t * FR_U4 + ((2 * jp + u) * 2 + p) * 64 + l]);
+                    A[t][u][p] = __builtin_bit_cast(
+                        f16x8, lds[t * FR_U4 + ((2 * jp + u) * 2 + p) * 64 + (l ^ (2 * (2 * jp + u) + (l >> 5)))]);
         f16x8 B[RT][2];
 #pragma unroll
         for (int i = 0; i < RT; i++)
