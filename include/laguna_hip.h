@@ -176,8 +176,8 @@ int lg_dispatch_proj_quant_batch(const void *x, int x_dtype, const void *w, floa
 /* lg_dispatch_proj_quant_batch without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments and results, bit for bit; the activation fragment records, partial
- * sums and arrival counters live in a fixed 16 MiB + 64 KiB device array that
+ * arguments and results, bit for bit; the split-k partial sums and arrival
+ * counters live in a fixed 16 MiB + 64 KiB device array that
  * every GPU the library runs on holds until the process ends (set up by lg_init,
  * or by the first call on a device).  Shapes whose workspace
  * (lg_proj_quant_batch_ws_bytes) exceeds it are LG_EINVAL.  Calls on one GPU share
@@ -188,9 +188,9 @@ int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, const void *
 
 /* Device workspace bytes lg_dispatch_proj_quant_batch needs for this shape on the
  * current device (0: the shape takes the element-wise path, which needs none).  No
- * counterpart in the reference.  It is about (m / 16 rounded up) * (k / 256) * 17 KiB
- * of fragment records, plus 64 KiB of arrival counters, plus the split-k partial
- * sums: slices * min(m, 32) * n * 4 bytes when the product splits k over slices.
+ * counterpart in the reference.  It is 64 KiB of arrival counters plus, when the
+ * product splits k over slices, the split-k partial sums: slices * min(m, 32) * n * 4
+ * bytes (slices chosen for about two workgroups per CU).
  * lg_dispatch_proj_quant_batch_static accepts a shape when this is at most
  * 16 MiB + 64 KiB. */
 uint64_t lg_proj_quant_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int w_dtype);
