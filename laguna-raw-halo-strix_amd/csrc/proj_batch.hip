@@ -44,6 +44,8 @@ namespace {
 using namespace lg;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
@@ -146,10 +148,6 @@ __device__ __forceinline__ float row16_max(float v) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
-    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
-    return (uint32_t)__builtin_bit_cast(uint16_t, ha) | ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
-}
 
 // NORM: token threadIdx.x / LT of the launch (LT = 16 / TT lanes per token) takes its
 // partial sums p = sub, sub + LT, ... (branch-free: slots past the columns and tokens
@@ -489,7 +487,8 @@ __device__ __forceinline__ void load_q80(Q80Chunk<RT> &W, const uint8_t *__restr
 // their record words to LDS: the token's chunk maximum meets in DPP steps over its
 // 16-lane row, and 2^e, the two f16 parts and the sub-block sums X follow as in
 // the record layout.  XM: 0 = f32 activations, 1 = bf16, 2 = f32 silu(x) * up.
-// Tokens past m are zero.
+// Tokens past m repeat token m - 1 (each token's record is its own; their results are
+// never stored).
 template <int TT, int XM>
 struct RecBuild {
     float v[TT][16];
@@ -537,13 +536,12 @@ struct RecBuild {
         const uint32_t tok = threadIdx.x >> 4, q = threadIdx.x & 15u, j = q >> 1;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
-            const bool live = t * 16 + tok < m;
             float w[16], amax = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 float a = v[t][i];
                 if constexpr (XM == 2) a = silu_mul(a, u[t][i]);  // kernels/activation.comp:21-28
-                w[i] = live ? a : 0.0f;
+                w[i] = a;
                 amax = fmaxf(amax, fabsf(w[i]));
             }
             amax = row16_max(amax);
@@ -554,13 +552,23 @@ struct RecBuild {
                 e = 15 - __builtin_amdgcn_frexp_expf(amax);
                 e = e < -126 ? -126 : (e > 126 ? 126 : e);
             }
-            float hi[16], lo[16], sum = 0.0f;
+            float sv[16], sum = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                const float sv = __builtin_ldexpf(w[i], e);
-                hi[i] = (float)(_Float16)sv;
-                lo[i] = sv - hi[i];  // exact: hi is the f16 nearest sv
-                sum += sv;
+                sv[i] = __builtin_ldexpf(w[i], e);
+                sum += sv[i];
+            }
+            // the two f16 parts of elements i, i + 2 in one word each (v_cvt_pk_f16_f32,
+            // round to nearest even): hi the nearest f16, lo that of the exact remainder
+            uint32_t hp[8], lp[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int i0 = 8 * (c >> 2) + (c & 1) + 4 * ((c >> 1) & 1), i1 = i0 + 2;
+                const f16x2_t hv = __builtin_convertvector((f32x2_t){sv[i0], sv[i1]}, f16x2_t);
+                const f32x2_t hf = __builtin_convertvector(hv, f32x2_t);
+                const f16x2_t lv = __builtin_convertvector((f32x2_t){sv[i0] - hf.x, sv[i1] - hf.y}, f16x2_t);
+                hp[c] = __builtin_bit_cast(uint32_t, hv);
+                lp[c] = __builtin_bit_cast(uint32_t, lv);
             }
             // the sub-block's sum: this thread's 16 and its neighbour's (q ^ 1), the same
             // float in both (addition is commutative)
@@ -569,11 +577,8 @@ struct RecBuild {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const uint32_t lane = ((q & 1u) * 2 + h) * 16 + tok;
-                const float *a = hi + 8 * h, *b = lo + 8 * h;
-                rec[(j * 2 + 0) * 64 + (lane ^ q)] = make_uint4(pk_f16(a[0], a[2]), pk_f16(a[1], a[3]),
-                                                                pk_f16(a[4], a[6]), pk_f16(a[5], a[7]));
-                rec[(j * 2 + 1) * 64 + (lane ^ q)] = make_uint4(pk_f16(b[0], b[2]), pk_f16(b[1], b[3]),
-                                                                pk_f16(b[4], b[6]), pk_f16(b[5], b[7]));
+                rec[(j * 2 + 0) * 64 + (lane ^ q)] = make_uint4(hp[4 * h], hp[4 * h + 1], hp[4 * h + 2], hp[4 * h + 3]);
+                rec[(j * 2 + 1) * 64 + (lane ^ q)] = make_uint4(lp[4 * h], lp[4 * h + 1], lp[4 * h + 2], lp[4 * h + 3]);
             }
             float *rf = reinterpret_cast<float *>(rec);
             if ((q & 1u) == 0) rf[4 * FR_X + ((j & 3u) * 16 + tok) * 2 + (j >> 2)] = sum;
