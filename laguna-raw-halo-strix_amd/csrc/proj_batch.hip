@@ -565,9 +565,13 @@ struct RecBuild {
             for (int c = 0; c < 8; c++) {
                 const int i0 = 8 * (c >> 2) + (c & 1) + 4 * ((c >> 1) & 1), i1 = i0 + 2;
                 const f16x2_t hv = __builtin_convertvector((f32x2_t){sv[i0], sv[i1]}, f16x2_t);
-                const f32x2_t hf = __builtin_convertvector(hv, f32x2_t);
-                const f16x2_t lv = __builtin_convertvector((f32x2_t){sv[i0] - hf.x, sv[i1] - hf.y}, f16x2_t);
-                hp[c] = __builtin_bit_cast(uint32_t, hv);
+                const uint32_t hw = __builtin_bit_cast(uint32_t, hv);
+                // sv - hi, exact, straight from the packed f16 halves (one v_fma_mix_f32 each)
+                float r0, r1;
+                asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r0) : "v"(hw), "v"(sv[i0]));
+                asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r1) : "v"(hw), "v"(sv[i1]));
+                const f16x2_t lv = __builtin_convertvector((f32x2_t){r0, r1}, f16x2_t);
+                hp[c] = hw;
                 lp[c] = __builtin_bit_cast(uint32_t, lv);
             }
             // the sub-block's sum: this thread's 16 and its neighbour's (q ^ 1), the same
