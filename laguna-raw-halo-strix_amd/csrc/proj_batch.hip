@@ -440,43 +440,93 @@ __device__ __forceinline__ void load_q4k(Q4kChunk<RT> &W, const uint8_t *__restr
     }
 }
 
-// Raw Q8_0 blocks are 2-byte aligned: the quant bytes of a lane are one 8-byte load
-// at 2-byte alignment (gfx950 global loads need no natural alignment).
-struct __attribute__((packed, aligned(2))) U32x2a2 {
-    uint32_t x, y;
-};
-
-template <int RT, bool TILED>
-__device__ __forceinline__ void load_q80(Q80Chunk<RT> &W, const uint8_t *__restrict__ w, uint32_t n, uint32_t rt0,
-                                         uint32_t nb, uint32_t cb, uint64_t row_bytes) {
-    const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
+// Q8_0 over 16-row tiles (4352-byte tiles): a row's 8 scales in one 16-byte load, 512
+// contiguous bytes per quant load.  Tiles past the last read the last tile.
+template <int RT>
+__device__ __forceinline__ void load_q80_tiled(Q80Chunk<RT> &W, const uint8_t *__restrict__ w, uint32_t n,
+                                               uint32_t rt0, uint32_t nb, uint32_t cb) {
+    const uint32_t l = threadIdx.x & 63u;
 #pragma unroll
     for (int i = 0; i < RT; i++) {
-        if constexpr (TILED) {  // 4352-byte tiles: a row's 8 scales in one 16-byte load, 512 contiguous bytes per quant load
-            const uint32_t ntiles = (n + 15) / 16, t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
-            const uint8_t *tb = w + ((uint64_t)t * nb + cb) * Q80_TILE;
-            const uint4 s = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
-            W.sc[i][0] = s.x;
-            W.sc[i][1] = s.y;
-            W.sc[i][2] = s.z;
-            W.sc[i][3] = s.w;
+        const uint32_t ntiles = (n + 15) / 16, t = rt0 + i < ntiles ? rt0 + i : ntiles - 1;
+        const uint8_t *tb = w + ((uint64_t)t * nb + cb) * Q80_TILE;
+        const uint4 s = *reinterpret_cast<const uint4 *>(tb + 16 * (l & 15u));
+        W.sc[i][0] = s.x;
+        W.sc[i][1] = s.y;
+        W.sc[i][2] = s.z;
+        W.sc[i][3] = s.w;
 #pragma unroll
-            for (int j = 0; j < 8; j++) W.qv[i][j] = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * j + 8 * l);
-        } else {
-            const uint32_t rlast = (n - 1) & ~15u, r0 = (rt0 + i) * 16 < rlast ? (rt0 + i) * 16 : rlast;
-            const uint32_t rl = r0 + (l & 15u) < n ? (l & 15u) : n - 1 - r0;
-            const uint8_t *blk = w + (uint64_t)r0 * row_bytes + (uint64_t)cb * 8 * Q80_BYTES;
-            const uint32_t lo = rl * (uint32_t)row_bytes;
-            uint32_t d[8];
+        for (int j = 0; j < 8; j++) W.qv[i][j] = *reinterpret_cast<const uint2 *>(tb + 256 + 512 * j + 8 * l);
+    }
+}
+
+// Raw Q8_0 blocks are only 2-byte aligned, so the raw path loads a chunk's rows whole:
+// a 16-row tile's chunk is 16 rows x 272 bytes (8 blocks of 34), 272 aligned 16-byte
+// pieces (k % 256 == 0 and a 16-byte aligned base keep them aligned), piece e of the
+// tile (row e / 17, bytes 16 (e % 17) ..) in lane e % 64, round e / 64.  Before the
+// chunk's products the wavefront writes them to its own LDS region, where the row's
+// bytes lie as in memory, and each lane reads back its blocks' scales and quants
+// (stage_q80).
+constexpr uint32_t Q80_PIECES = 8 * Q80_BYTES / 16;  // 17 per row and chunk
+template <int RT>
+struct Q80RawChunk {
+    lg_u32x4 v[RT][5];  // a vector type: HIP's uint4 struct keeps arrays of it out of registers
+};
+
+template <int RT>
+__device__ __forceinline__ void load_q80_raw(Q80RawChunk<RT> &W, const uint8_t *__restrict__ w, uint32_t n,
+                                             uint32_t rt0, uint32_t cb, uint64_t row_bytes) {
+    const uint32_t l = threadIdx.x & 63u;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                d[j] = *reinterpret_cast<const uint16_t *>(blk + lo + j * Q80_BYTES);
-                const U32x2a2 v = *reinterpret_cast<const U32x2a2 *>(blk + lo + j * Q80_BYTES + 2 + 8 * kg);
-                W.qv[i][j] = make_uint2(v.x, v.y);
-            }
+    for (int i = 0; i < RT; i++) {
+        const uint32_t rlast = (n - 1) & ~15u, r0 = (rt0 + i) * 16 < rlast ? (rt0 + i) * 16 : rlast;
 #pragma unroll
-            for (int h = 0; h < 4; h++) W.sc[i][h] = d[2 * h] | (d[2 * h + 1] << 16);
+        for (int rd = 0; rd < 5; rd++) {
+            const uint32_t e0 = l + 64u * rd, e = e0 < 16 * Q80_PIECES ? e0 : 16 * Q80_PIECES - 1;  // past: a repeat
+            const uint32_t rr = e / Q80_PIECES, row = r0 + rr < n ? r0 + rr : n - 1;
+            W.v[i][rd] = *reinterpret_cast<const lg_u32x4 *>(w + (uint64_t)row * row_bytes +
+                                                             (uint64_t)cb * 8 * Q80_BYTES + 16 * (e % Q80_PIECES));
         }
+    }
+}
+
+// The raw pieces through the wavefront's LDS region (RT x 4352 bytes) into the lane's
+// scales and quants, as load_q80_tiled reads them from 16-row tiles.
+template <int RT>
+__device__ __forceinline__ void stage_q80(const Q80RawChunk<RT> &R, Q80Chunk<RT> &W, lg_u32x4 *st) {
+    const uint32_t l = threadIdx.x & 63u, rr = l & 15u, kg = l >> 4;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the previous chunk's reads are done
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int rd = 0; rd < 5; rd++) {
+            const uint32_t e0 = l + 64u * rd, e = e0 < 16 * Q80_PIECES ? e0 : 16 * Q80_PIECES - 1;
+            st[i * 16 * Q80_PIECES + e] = R.v[i][rd];  // lanes past the tile rewrite the last piece
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint8_t *row = reinterpret_cast<const uint8_t *>(st + i * 16 * Q80_PIECES) + rr * 8 * Q80_BYTES;
+        uint32_t d[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint8_t *b = row + j * Q80_BYTES;  // 4-byte aligned for even j, 2-byte for odd j
+            d[j] = *reinterpret_cast<const uint16_t *>(b);
+            if (j % 2 == 0) {  // quants at b + 2 + 8 kg: three aligned dwords from b + 8 kg
+                const uint32_t *p = reinterpret_cast<const uint32_t *>(b + 8 * kg);
+                const uint32_t a0 = p[0], a1 = p[1], a2 = p[2];
+                W.qv[i][j] = make_uint2(__builtin_amdgcn_alignbit(a1, a0, 16), __builtin_amdgcn_alignbit(a2, a1, 16));
+            } else {
+                const uint32_t *p = reinterpret_cast<const uint32_t *>(b + 2 + 8 * kg);
+                W.qv[i][j] = make_uint2(p[0], p[1]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 4; h++) W.sc[i][h] = d[2 * h] | (d[2 * h + 1] << 16);
     }
 }
 
@@ -766,14 +816,18 @@ __global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, M
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
     const uint32_t nb = k / QK_K, c0 = blockIdx.y * ch, nch = nb - c0 < ch ? nb - c0 : ch;
-    using Chunk = typename std::conditional<Q4, Q4kChunk<RT>, Q80Chunk<RT>>::type;
+    constexpr bool RAW8 = !Q4 && !TILED;  // raw Q8_0: rows through a per-wavefront LDS region
+    using Chunk = typename std::conditional<Q4, Q4kChunk<RT>,
+                                            typename std::conditional<RAW8, Q80RawChunk<RT>, Q80Chunk<RT>>::type>::type;
+    __shared__ lg_u32x4 lstage[RAW8 ? 4 * RT * 16 * Q80_PIECES : 1];
     Chunk Wc[3];
     // chunk ci of the slice; past the slice the last chunk again (loads stay in bounds,
     // never multiplied)
     auto load_w = [&](Chunk &Wd, uint32_t ci) {
         const uint32_t c = c0 + (ci < nch ? ci : nch - 1);
         if constexpr (Q4) load_q4k<RT, TILED>(Wd, w, n, rt0, nb, c, row_bytes);
-        else load_q80<RT, TILED>(Wd, w, n, rt0, nb, c, row_bytes);
+        else if constexpr (RAW8) load_q80_raw<RT>(Wd, w, n, rt0, c, row_bytes);
+        else load_q80_tiled<RT>(Wd, w, n, rt0, nb, c);
     };
     float acc[RT][TT][4];
 #pragma unroll
@@ -793,8 +847,18 @@ __global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, M
     __builtin_amdgcn_sched_barrier(0);  // issue order: the activations, then the weights
     load_w(Wc[2], 2);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (Q4) q4k_chunk<TT, RT>(lrec[0], Wc[0], acc);
-    else q80_chunk<TT, RT>(lrec[0], Wc[0], acc);
+    auto chunk = [&](const uint4 *rec, const Chunk &Wk) {
+        if constexpr (Q4) {
+            q4k_chunk<TT, RT>(rec, Wk, acc);
+        } else if constexpr (RAW8) {
+            Q80Chunk<RT> Ws;
+            stage_q80<RT>(Wk, Ws, lstage + wave * RT * 16 * Q80_PIECES);
+            q80_chunk<TT, RT>(rec, Ws, acc);
+        } else {
+            q80_chunk<TT, RT>(rec, Wk, acc);
+        }
+    };
+    chunk(lrec[0], Wc[0]);
     // three chunks per iteration, so the ring's registers are named at compile time
     // (chunk c in Wc[c % 3]: ci = 1 mod 3)
     for (uint32_t ci = 1; ci < nch; ci += 3) {
@@ -808,8 +872,7 @@ __global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, M
             __builtin_amdgcn_sched_barrier(0);
             load_w(Wc[h], c + 2);
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (Q4) q4k_chunk<TT, RT>(lrec[c & 1u], Wc[(h + 1) % 3], acc);
-            else q80_chunk<TT, RT>(lrec[c & 1u], Wc[(h + 1) % 3], acc);
+            chunk(lrec[c & 1u], Wc[(h + 1) % 3]);
         }
     }
     static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lrec), "GLU exchange fits in the record LDS");
@@ -1033,7 +1096,7 @@ bool proj_batch_mfma_ok(int w_dtype, uint32_t k, const void *w) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(w);
     if (w_dtype == LG_Q4_K_T16 || w_dtype == LG_Q8_0_T16) return k && k % QK_K == 0 && (a & 15u) == 0;
     if (w_dtype == LG_Q4_K) return k && k % QK_K == 0 && (a & 15u) == 0;
-    if (w_dtype == LG_Q8_0) return k && k % QK_K == 0 && (a & 1u) == 0;
+    if (w_dtype == LG_Q8_0) return k && k % QK_K == 0 && (a & 15u) == 0;  // rows staged with 16-byte loads
     return false;
 }
 
