@@ -530,6 +530,58 @@ __device__ __forceinline__ void stage_q80(const Q80RawChunk<RT> &R, Q80Chunk<RT>
     }
 }
 
+// Raw Q4_K rows the same way: a tile's chunk is 16 rows x 144 bytes (one super-block
+// each), 144 aligned 16-byte pieces (piece e: row e / 9, bytes 16 (e % 9) ..), staged
+// through the wavefront's LDS region, from which each lane reads its row's header and
+// its 8-byte quant pieces as load_q4k reads them in place.
+constexpr uint32_t Q4K_PIECES = Q4K_BYTES / 16;  // 9 per row and chunk
+template <int RT>
+struct Q4kRawChunk {
+    lg_u32x4 v[RT][3];
+};
+
+template <int RT>
+__device__ __forceinline__ void load_q4k_raw(Q4kRawChunk<RT> &W, const uint8_t *__restrict__ w, uint32_t n,
+                                             uint32_t rt0, uint32_t cb, uint64_t row_bytes) {
+    const uint32_t l = threadIdx.x & 63u;
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint32_t rlast = (n - 1) & ~15u, r0 = (rt0 + i) * 16 < rlast ? (rt0 + i) * 16 : rlast;
+#pragma unroll
+        for (int rd = 0; rd < 3; rd++) {
+            const uint32_t e0 = l + 64u * rd, e = e0 < 16 * Q4K_PIECES ? e0 : 16 * Q4K_PIECES - 1;  // past: a repeat
+            const uint32_t rr = e / Q4K_PIECES, row = r0 + rr < n ? r0 + rr : n - 1;
+            W.v[i][rd] = *reinterpret_cast<const lg_u32x4 *>(w + (uint64_t)row * row_bytes + (uint64_t)cb * Q4K_BYTES +
+                                                             16 * (e % Q4K_PIECES));
+        }
+    }
+}
+
+template <int RT>
+__device__ __forceinline__ void stage_q4k(const Q4kRawChunk<RT> &R, Q4kChunk<RT> &W, lg_u32x4 *st) {
+    const uint32_t l = threadIdx.x & 63u, rr = l & 15u, kg = l >> 4;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the previous chunk's reads are done
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < RT; i++)
+#pragma unroll
+        for (int rd = 0; rd < 3; rd++) {
+            const uint32_t e0 = l + 64u * rd, e = e0 < 16 * Q4K_PIECES ? e0 : 16 * Q4K_PIECES - 1;
+            st[i * 16 * Q4K_PIECES + e] = R.v[i][rd];  // lanes past the tile rewrite the last piece
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        const uint8_t *blk = reinterpret_cast<const uint8_t *>(st + i * 16 * Q4K_PIECES) + rr * Q4K_BYTES;
+        W.hd[i] = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+        for (int g = 0; g < 4; g++) W.qv[i][g] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * g + 8 * kg);
+    }
+}
+
 // The fragment record of one chunk for TT token tiles, built by the workgroup from the
 // activations: thread (token threadIdx.x / 16, q = threadIdx.x % 16) loads elements
 // 16 q .. 16 q + 15 of the chunk (half of sub-block q / 2, k-groups 2 (q % 2) and
@@ -816,16 +868,20 @@ __global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, M
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
     const uint32_t nb = k / QK_K, c0 = blockIdx.y * ch, nch = nb - c0 < ch ? nb - c0 : ch;
-    constexpr bool RAW8 = !Q4 && !TILED;  // raw Q8_0: rows through a per-wavefront LDS region
-    using Chunk = typename std::conditional<Q4, Q4kChunk<RT>,
-                                            typename std::conditional<RAW8, Q80RawChunk<RT>, Q80Chunk<RT>>::type>::type;
-    __shared__ lg_u32x4 lstage[RAW8 ? 4 * RT * 16 * Q80_PIECES : 1];
+    // raw blocks: rows through a per-wavefront LDS region
+    constexpr bool RAW8 = !Q4 && !TILED, RAW4 = Q4 && !TILED;
+    constexpr uint32_t SPW = RT * 16 * (RAW8 ? Q80_PIECES : Q4K_PIECES);  // staged pieces per wavefront
+    using Chunk = typename std::conditional<
+        Q4, typename std::conditional<RAW4, Q4kRawChunk<RT>, Q4kChunk<RT>>::type,
+        typename std::conditional<RAW8, Q80RawChunk<RT>, Q80Chunk<RT>>::type>::type;
+    __shared__ lg_u32x4 lstage[TILED ? 1 : 4 * SPW];
     Chunk Wc[3];
     // chunk ci of the slice; past the slice the last chunk again (loads stay in bounds,
     // never multiplied)
     auto load_w = [&](Chunk &Wd, uint32_t ci) {
         const uint32_t c = c0 + (ci < nch ? ci : nch - 1);
-        if constexpr (Q4) load_q4k<RT, TILED>(Wd, w, n, rt0, nb, c, row_bytes);
+        if constexpr (RAW4) load_q4k_raw<RT>(Wd, w, n, rt0, c, row_bytes);
+        else if constexpr (Q4) load_q4k<RT, TILED>(Wd, w, n, rt0, nb, c, row_bytes);
         else if constexpr (RAW8) load_q80_raw<RT>(Wd, w, n, rt0, c, row_bytes);
         else load_q80_tiled<RT>(Wd, w, n, rt0, nb, c);
     };
@@ -848,11 +904,15 @@ __global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, M
     load_w(Wc[2], 2);
     __builtin_amdgcn_sched_barrier(0);
     auto chunk = [&](const uint4 *rec, const Chunk &Wk) {
-        if constexpr (Q4) {
+        if constexpr (RAW4) {
+            Q4kChunk<RT> Ws;
+            stage_q4k<RT>(Wk, Ws, lstage + wave * SPW);
+            q4k_chunk<TT, RT>(rec, Ws, acc);
+        } else if constexpr (Q4) {
             q4k_chunk<TT, RT>(rec, Wk, acc);
         } else if constexpr (RAW8) {
             Q80Chunk<RT> Ws;
-            stage_q80<RT>(Wk, Ws, lstage + wave * RT * 16 * Q80_PIECES);
+            stage_q80<RT>(Wk, Ws, lstage + wave * SPW);
             q80_chunk<TT, RT>(rec, Ws, acc);
         } else {
             q80_chunk<TT, RT>(rec, Wk, acc);
