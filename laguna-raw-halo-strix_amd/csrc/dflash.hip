@@ -336,55 +336,6 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(QkJob a, QkJob b, const fl
 constexpr uint32_t AHD = 128;  // head dim of the matrix-core path
 constexpr uint32_t ACH = 64;   // positions per chunk of the few-query kernels (k_attn_decode, k_attn_token)
 constexpr uint32_t AQ = 64;    // queries per kv head handled by one workgroup
-constexpr uint32_t AMT = 5;    // most 16-position tiles per chunk of k_attn_chunk
-constexpr uint32_t KSTR = AHD + 8;  // bf16 row stride of the K tile (padding against bank conflicts)
-constexpr int NP = 3;               // bf16 parts per f32 operand
-
-// f32 operands enter the matrix cores as three bf16 parts x = x0 + x1 + x2, each the
-// nearest bf16 of what the previous parts leave: together all 24 significant bits.
-// MT position tiles: K rows, and V^T columns in whole 32-position steps of P V.
-template <int MT>
-struct __attribute__((aligned(16))) AttnLds {
-    static constexpr uint32_t KR = 16 * MT, VC = 32 * ((MT + 1) / 2), VSTR = VC + 8;
-    uint16_t k[NP][KR * KSTR];
-    uint16_t v[NP][AHD * VSTR];  // V^T: [dim][position, in P V operand order]
-};
-
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-// Two f32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32): a low, b high.
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
-}
-
-// The three parts of the pair (a, b), each packed (a low, b high).
-__device__ __forceinline__ void split3x2(float a, float b, uint32_t &w0, uint32_t &w1, uint32_t &w2) {
-    w0 = pk_bf16(a, b);
-    a -= __uint_as_float(w0 << 16);  // exact
-    b -= __uint_as_float(w0 & 0xFFFF0000u);
-    w1 = pk_bf16(a, b);
-    a -= __uint_as_float(w1 << 16);
-    b -= __uint_as_float(w1 & 0xFFFF0000u);
-    w2 = pk_bf16(a, b);
-}
-
-__device__ __forceinline__ bf16x8 ld_frag(const uint16_t *p) {
-    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(p));
-}
-
-// d[t] += a[t] b for N tiles over the six part products that reach f32 precision
-// (|a_i b_j| <= 2^-9(i+j) |a b|; the three dropped ones are below 2^-26), smallest
-// first; each product is issued for every tile before the next (independent
-// accumulators back to back).
-template <int N>
-__device__ __forceinline__ void mfma6_n(const bf16x8 (*a)[NP], const bf16x8 *b, f32x4 *d) {
-    constexpr int ia[6] = {1, 2, 0, 1, 0, 0}, ib[6] = {1, 0, 2, 0, 1, 0};
-#pragma unroll
-    for (int j = 0; j < 6; j++)
-#pragma unroll
-        for (int t = 0; t < N; t++) d[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[t][ia[j]], b[ib[j]], d[t], 0, 0, 0);
-}
 
 // Max over the lanes l, l ^ 16, l ^ 32, l ^ 48 (the four 16-lane rows), in every lane.
 __device__ __forceinline__ float rows4_max(float v) {
@@ -394,226 +345,18 @@ __device__ __forceinline__ float rows4_max(float v) {
     return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
-// Chunks of k_attn_chunk: the sequence's ceil(S / 16) position tiles split into nch
+// Chunks of k_attn_split: the sequence's ceil(S / 16) position tiles split into nch
 // runs of consecutive tiles, chunk c taking tiles [c nt / nch, (c + 1) nt / nch).
+// floor(c nt / nch) in 32-bit steps (c <= nch < 2^16): c floor(nt / nch) + floor(c (nt mod
+// nch) / nch) -- a 64-bit division by a runtime value is a long software loop on the GPU.
 __host__ __device__ inline uint32_t attn_tile0(uint32_t c, uint32_t nt, uint32_t nch) {
-    return (uint32_t)((uint64_t)c * nt / nch);
-}
-
-// Partials per (kv head, chunk, query): O (unnormalised, AHD floats), max, sum.
-// Wavefront w owns queries 16w .. 16w + 15 and computes, over the chunk's (at most
-// MT) position tiles,
-//   S^T = K Q^T     A = K rows from LDS, B = the wave's query rows (registers);
-//   P = exp(S - max) per query: a lane holds 4 positions x MT tiles of one query, so
-//                   its max and sum take two lane swaps;
-//   O^T = V^T P^T   A = V^T from LDS, B = P^T straight from the S^T registers: the
-//                   eight k values of lane l are positions 4(l/16) + {0..3} of two
-//                   consecutive tiles, and V^T's columns are stored in that order.
-// All MT tiles are computed (zero K and V past the chunk's own): the chunks of one
-// launch take MT - 1 or MT tiles, and the longest sets the launch's time.
-// O^T lands as 4 consecutive dims of one query per lane: one 16-byte store each.
-template <int MT>
-__global__ __launch_bounds__(256) void k_attn_chunk(const float *__restrict__ q, const float *__restrict__ k0,
-                                                    const float *__restrict__ v0, uint32_t n0,
-                                                    const float *__restrict__ k1, const float *__restrict__ v1,
-                                                    uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv,
-                                                    uint32_t qpos0, int causal, float scale, uint32_t nch,
-                                                    float *__restrict__ part_o, float *__restrict__ part_ml) {
-    using Lds = AttnLds<MT>;
-    constexpr uint32_t VSTR = Lds::VSTR, NKS = Lds::VC / 32, VQ = Lds::VC / 4;  // V position quads
-    constexpr uint32_t KB = 4 * MT * 32, VB = VQ * 32;                          // 4x4 blocks of K, of V
-    constexpr int KR = (KB + 255) / 256, VR = (VB + 255) / 256;
-    __shared__ Lds L;
-    const uint32_t h = blockIdx.y, c = blockIdx.x;
-    const uint32_t G = n_q / n_kv, nq = rows * G;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t l16 = lane & 15u, kg = lane >> 4;
-    const uint32_t kvld = n_kv * AHD, qld = n_q * AHD;
-    const uint32_t nt = (S + 15) / 16, tb = attn_tile0(c, nt, nch), ntl = attn_tile0(c + 1, nt, nch) - tb;
-    const uint32_t P0 = 16 * tb;                                      // first position of the chunk
-    const uint32_t pend = P0 + 16 * ntl < S ? P0 + 16 * ntl : S;      // past its last live position
-    // K and V in blocks of 4 positions x 4 dims per thread: K blocks run along the
-    // dims (two whole K rows per wavefront), V blocks along the positions (the lanes
-    // writing one V^T row write 64 contiguous bytes).  Positions at or past `pend`
-    // re-read the chunk's last live row (no further HBM traffic) and enter LDS as
-    // zeros.  The queries and K first; V's loads are issued after the K split, so that
-    // they do not delay K and the queries (every CU streams its K and V at once) and
-    // arrive under the scores.
-    auto kv_at = [&](const float *a0, const float *a1, uint32_t p, uint32_t d) {
-        const uint32_t pc = p < pend ? p : pend - 1;
-        return *reinterpret_cast<const float4 *>(
-            (pc < n0 ? a0 + (uint64_t)pc * kvld : a1 + (uint64_t)(pc - n0) * kvld) + h * AHD + d);
-    };
-    const uint32_t qr = 16 * wave + l16;
-    const bool qlive = qr < nq;
-    float4 qx[AHD / 32][2];
-    {
-        const uint32_t t = qlive ? qr / G : 0, hq = qlive ? h * G + qr % G : h * G;  // dead rows read row 0, zeroed
-        const float *qp = q + (uint64_t)t * qld + hq * AHD + 8 * kg;
-#pragma unroll
-        for (int ks = 0; ks < (int)(AHD / 32); ks++) {
-            qx[ks][0] = *reinterpret_cast<const float4 *>(qp + 32 * ks);
-            qx[ks][1] = *reinterpret_cast<const float4 *>(qp + 32 * ks + 4);
-        }
-    }
-    float4 kq[KR][4], vq[VR][4];
-#pragma unroll
-    for (int rd = 0; rd < KR; rd++) {
-        const uint32_t e = tid + 256u * rd, pk = e / 32, dk = 4 * (e % 32);
-        if (KB % 256 && e >= KB) break;  // uniform over the wavefront
-#pragma unroll
-        for (int i = 0; i < 4; i++) kq[rd][i] = kv_at(k0, k1, P0 + 4 * pk + i, dk);
-    }
-#pragma unroll
-    for (int rd = 0; rd < KR; rd++) {
-        const uint32_t e = tid + 256u * rd, pk = e / 32, dk = 4 * (e % 32);
-        if (KB % 256 && e >= KB) break;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {  // K: position P0 + 4pk + i, dims dk..dk+3
-            const bool ok = P0 + 4 * pk + i < pend;
-            const float4 kv = kq[rd][i];
-            uint32_t a[2], b[2], cc[2];
-            split3x2(ok ? kv.x : 0.f, ok ? kv.y : 0.f, a[0], b[0], cc[0]);
-            split3x2(ok ? kv.z : 0.f, ok ? kv.w : 0.f, a[1], b[1], cc[1]);
-            const uint32_t o = (4 * pk + i) * KSTR + dk;
-            *reinterpret_cast<uint2 *>(L.k[0] + o) = make_uint2(a[0], a[1]);
-            *reinterpret_cast<uint2 *>(L.k[1] + o) = make_uint2(b[0], b[1]);
-            *reinterpret_cast<uint2 *>(L.k[2] + o) = make_uint2(cc[0], cc[1]);
-        }
-    }
-    // V, now that K is in LDS: its loads stream under the scores
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int rd = 0; rd < VR; rd++) {
-        const uint32_t e = tid + 256u * rd, pv = e % VQ, dv = 4 * (e / VQ);
-        if (VB % 256 && e >= VB) break;  // uniform over the wavefront
-#pragma unroll
-        for (int i = 0; i < 4; i++) vq[rd][i] = kv_at(v0, v1, P0 + 4 * pv + i, dv);
-    }
-    bf16x8 qb[AHD / 32][NP];
-#pragma unroll
-    for (int ks = 0; ks < (int)(AHD / 32); ks++) {
-        const float4 x0 = qx[ks][0], x1 = qx[ks][1];
-        const float f[8] = {qlive ? x0.x : 0.f, qlive ? x0.y : 0.f, qlive ? x0.z : 0.f, qlive ? x0.w : 0.f,
-                            qlive ? x1.x : 0.f, qlive ? x1.y : 0.f, qlive ? x1.z : 0.f, qlive ? x1.w : 0.f};
-        uint32_t wp[NP][4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) split3x2(f[2 * i], f[2 * i + 1], wp[0][i], wp[1][i], wp[2][i]);
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++)
-            qb[ks][pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
-    }
-    __syncthreads();
-
-    // S^T for the chunk's tiles: lane holds S[query qr][position P0 + 16pt + 4kg + r] in Sd[pt][r]
-    f32x4 Sd[MT];
-#pragma unroll
-    for (int pt = 0; pt < MT; pt++) Sd[pt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < (int)(AHD / 32); ks++) {
-        bf16x8 ka[MT][NP];
-#pragma unroll
-        for (int pt = 0; pt < MT; pt++) {
-            const uint32_t ko = (16 * pt + l16) * KSTR + 32 * ks + 8 * kg;
-#pragma unroll
-            for (int pp = 0; pp < NP; pp++) ka[pt][pp] = ld_frag(L.k[pp] + ko);
-        }
-        mfma6_n<MT>(ka, qb[ks], Sd);
-    }
-    // scale, mask, the query's max and sum over the chunk
-    const uint32_t qpos = qpos0 + (qlive ? qr / G : 0);
-    float m = -INFINITY;
-#pragma unroll
-    for (int pt = 0; pt < MT; pt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t p = P0 + 16 * pt + 4 * kg + r;
-            const bool ok = qlive && p < pend && (!causal || p <= qpos);
-            const float sv = ok ? Sd[pt][r] * scale : -INFINITY;
-            Sd[pt][r] = sv;
-            m = fmaxf(m, sv);
-        }
-    m = rows4_max(m);
-    const float mu = m == -INFINITY ? 0.0f : m;  // a fully masked query has P = 0
-    float l = 0.0f;
-#pragma unroll
-    for (int pt = 0; pt < MT; pt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float pv = expf(Sd[pt][r] - mu);
-            Sd[pt][r] = pv;
-            l += pv;
-        }
-    l = lane_add_x32(lane_add_x16(l));
-    // V^T to LDS, now that the scores are done: block (positions 4pv..4pv+3, dims
-    // dv..dv+3); position 32b + 16hh + 4g + j of the chunk goes to column 32b + 8g + 4hh + j
-#pragma unroll
-    for (int rd = 0; rd < VR; rd++) {
-        const uint32_t e = tid + 256u * rd, pv = e % VQ, dv = 4 * (e / VQ);
-        if (VB % 256 && e >= VB) break;
-        const uint32_t col = 32 * (pv / 8) + 8 * (pv % 4) + 4 * ((pv / 4) % 2);
-        float fv[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool ok = P0 + 4 * pv + i < pend;
-            const float4 vv = vq[rd][i];
-            fv[i][0] = ok ? vv.x : 0.f, fv[i][1] = ok ? vv.y : 0.f, fv[i][2] = ok ? vv.z : 0.f;
-            fv[i][3] = ok ? vv.w : 0.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            uint32_t a[2], b[2], cc[2];
-            split3x2(fv[0][j], fv[1][j], a[0], b[0], cc[0]);
-            split3x2(fv[2][j], fv[3][j], a[1], b[1], cc[1]);
-            const uint32_t o = (dv + j) * VSTR + col;
-            *reinterpret_cast<uint2 *>(L.v[0] + o) = make_uint2(a[0], a[1]);
-            *reinterpret_cast<uint2 *>(L.v[1] + o) = make_uint2(b[0], b[1]);
-            *reinterpret_cast<uint2 *>(L.v[2] + o) = make_uint2(cc[0], cc[1]);
-        }
-    }
-    __syncthreads();  // V^T in LDS
-
-    // O^T = V^T P^T over the chunk's 32-position steps and the 8 dimension tiles (two halves)
-    f32x4 Od[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++) Od[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < (int)NKS; ks++) {
-        uint32_t wp[NP][4];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const f32x4 sv = 2 * ks + i < MT ? Sd[2 * ks + i < MT ? 2 * ks + i : 0] : (f32x4){0.f, 0.f, 0.f, 0.f};
-            split3x2(sv[0], sv[1], wp[0][2 * i], wp[1][2 * i], wp[2][2 * i]);
-            split3x2(sv[2], sv[3], wp[0][2 * i + 1], wp[1][2 * i + 1], wp[2][2 * i + 1]);
-        }
-        bf16x8 pb[NP];
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++)
-            pb[pp] = __builtin_bit_cast(bf16x8, make_uint4(wp[pp][0], wp[pp][1], wp[pp][2], wp[pp][3]));
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-            bf16x8 va[4][NP];
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const uint32_t vo = (16 * (4 * half + t) + l16) * VSTR + 32 * ks + 8 * kg;
-#pragma unroll
-                for (int pp = 0; pp < NP; pp++) va[t][pp] = ld_frag(L.v[pp] + vo);
-            }
-            mfma6_n<4>(va, pb, Od + 4 * half);
-        }
-    }
-    // partials: O[q][d] (lane: dims 16dt + 4kg .. +3 of query qr), (m, l)[q]
-    if (!qlive) return;
-    const uint64_t pq = ((uint64_t)h * nch + c) * AQ + qr;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-        __builtin_nontemporal_store(Od[dt], reinterpret_cast<f32x4 *>(part_o + pq * AHD + 16 * dt + 4 * kg));
-    if (kg == 0) __builtin_nontemporal_store((f32x2_t){m, l}, reinterpret_cast<f32x2_t *>(part_ml + 2 * pq));
+    const uint32_t q = nt / nch, r = nt - q * nch;
+    return c * q + c * r / nch;
 }
 
 __device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g : logf(1.0f + expf(g)); }  // src/dflash.rs:957
 
-// The chunk partials of k_attn_chunk for a few queries (rows * G <= ADQ: one token's
+// The chunk partials for a few queries (rows * G <= ADQ: one token's
 // query heads), straight from memory in f32: no bf16 parts, no LDS tiles.  One
 // workgroup per (64-position chunk, kv head); wave w takes positions 16w .. 16w+15.
 //   scores: lane (p, quarter) dots the 32 dims 32 quarter .. of K row p with every
@@ -621,8 +364,8 @@ __device__ __forceinline__ float softplus_gate(float g) { return g > 20.0f ? g :
 //   softmax: wave w takes queries w, w + 4 over the chunk's 64 scores;
 //   P V: each wave adds its 16 positions for every query (lane = dims 2l, 2l+1), and
 //        the four waves' sums meet in LDS in wave order.
-// Every K and V load of the chunk is issued at the start.  Partials as k_attn_chunk
-// writes them (unnormalised O, and the chunk's max and sum of each query).
+// Every K and V load of the chunk is issued at the start.  Partials per (kv head,
+// chunk, query): the unnormalised O (AHD floats), and the chunk's max and sum.
 constexpr uint32_t ADQ = 8;
 
 __global__ __launch_bounds__(256) void k_attn_decode(const float *__restrict__ q, const float *__restrict__ k0,
@@ -730,7 +473,7 @@ struct TokAttn {
     float *k;                  // [S][n_kv][128]: rows below S-1 normed and roped, row S-1 as projected
     const float *v;            // [S][n_kv][128]
     uint32_t S, n_q, n_kv, nch;
-    float *part_o, *part_ml;   // per (kv head, chunk, query): as k_attn_chunk writes them
+    float *part_o, *part_ml;   // per (kv head, chunk, query): as k_attn_decode writes them
 };
 
 // A head (128 floats, lane d: dims d and d + 64) normed with weights (w0, w1) and
@@ -993,6 +736,283 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
     }
 }
 
+// Many queries (rows * G > ADQ), one launch.  Workgroup (kv head h, query group qg,
+// chunk c) takes queries 16 qg .. 16 qg + 15 of kv head h (query qi: row qi / G, q head
+// h G + qi % G) over chunk c of the sequence's 16-position tiles, its wavefront w the
+// tiles tb + w, tb + w + 4, ...  K and V stream from memory straight into f32 matrix
+// products (v_mfma_f32_16x16x4_f32), whose k index runs over dims / positions in the
+// order the lanes load them:
+//   S^T = K Q^T   A = K: lane (position l16, kg) holds dims 16b + 4kg .. +3 of its row
+//                 in one float4 for the four k steps of block b; B = Q^T likewise;
+//   P = exp(S - running max) per query (lane l16's query, four positions per lane);
+//   O^T += V^T P^T  A = V^T: lane (l16, kg) loads dims 64hh + 4 l16 .. +3 of position
+//                 4kg + s, and component cc feeds output tile 4hh + cc (dim 64hh + 4i
+//                 + cc of its row i); B = P^T, the lane's own probabilities.
+// No LDS for K and V, no bf16 parts: every product is an f32 fma.  The four wavefronts
+// meet in LDS (one partial per workgroup), the partial goes to the workspace, and the
+// last workgroup of the (h, qg) group to arrive merges the chunks in chunk order,
+// applies the gate and writes the result.  Workgroups sharing (h, c) sit on one XCD
+// (workgroup ids 8 apart) so that their K and V reads meet in its L2.
+constexpr uint32_t AQG = 16;  // queries per workgroup of k_attn_split
+
+// 16- and 8-byte loads and stores coherent across the device (sc1: every XCD's L2
+// sees them), for the partials that one workgroup writes and another merges.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), 0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ float4 dev_ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ float2 dev_ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ void dev_st4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void dev_st2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, byte_off, 0, CPOL_SC1);
+}
+
+struct SplitAttn {
+    const float *q, *k0, *v0, *k1, *v1;
+    uint32_t n0, S, rows, n_q, n_kv, qpos0, ngq, nch;
+    int causal, gmode;
+    float scale;
+    float *part_o, *part_ml, *gbuf;  // [group][chunk][16][128], [group][chunk][16][2], [group][16]
+    uint32_t *cnt;                   // one arrival counter per group, zero between calls
+    float *out;
+    const float *gate;
+    GateJob gj;
+};
+
+__device__ __forceinline__ float f4c(const float4 &v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
+
+__global__ __launch_bounds__(256) void k_attn_split(SplitAttn a) {
+    constexpr uint32_t OST = AHD + 4;  // LDS row stride of a wavefront's O
+    __shared__ __attribute__((aligned(16))) float so[4][AQG][OST];
+    __shared__ float sm[4][AQG], sl[4][AQG];
+    __shared__ uint32_t last;
+    const uint32_t id = blockIdx.x, slot = id / 8;
+    const uint32_t qg = slot % a.ngq, r = (slot / a.ngq) * 8 + id % 8;
+    if (r >= a.n_kv * a.nch) return;  // uniform over the workgroup
+    const uint32_t h = r / a.nch, c = r % a.nch, grp = h * a.ngq + qg;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, l16 = lane & 15u, kg = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t G = a.n_q / a.n_kv, nq = a.rows * G, kvld = a.n_kv * AHD;
+    // the group's gate units, spread over wavefronts 2-3 of its workgroups (wavefront 0
+    // takes a chunk's extra tile, when it has one)
+    auto gate_units = [&]() {
+        if (a.gj.units && wave >= 2)
+            for (uint32_t j = c + a.nch * (wave - 2); j < AQG; j += 2 * a.nch) {
+                const uint32_t qj = AQG * qg + j;
+                if (qj >= nq) break;  // uniform over the wavefront
+                const float gv = gate_value(a.gj, (qj / G) * a.n_q + h * G + qj % G, lane);
+                if (lane == 0)
+                    __hip_atomic_store(a.gbuf + grp * AQG + j, gv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+    };
+    // the lane's query: dims 16b + 4kg .. +3 in qf[b] (a dead query column reads the
+    // group's first query; its scores are masked)
+    const uint32_t qi = AQG * qg + l16;
+    const bool qlive = qi < nq;
+    const uint32_t qc = qlive ? qi : AQG * qg, qt = qc / G, qpos = a.qpos0 + qt;
+    float4 qf[8];
+    {
+        const float *qp = a.q + (uint64_t)qt * a.n_q * AHD + (h * G + qc % G) * AHD + 4 * kg;
+#pragma unroll
+        for (int b = 0; b < 8; b++) qf[b] = *reinterpret_cast<const float4 *>(qp + 16 * b);
+    }
+    const uint32_t nt = (a.S + 15) / 16, tb = attn_tile0(c, nt, a.nch), te = attn_tile0(c + 1, nt, a.nch);
+    const uint32_t nmine = te > tb + wave ? (te - tb - wave + 3) / 4 : 0;
+    const uint32_t tlast = tb + wave + 4 * (nmine ? nmine - 1 : 0);  // the wavefront's last tile
+    // position p's row of K or V (positions past S read row S - 1, masked)
+    auto kvrow = [&](const float *b0, const float *b1, uint32_t p) {
+        const uint32_t pc = p < a.S ? p : a.S - 1;
+        return (pc < a.n0 ? b0 + (uint64_t)pc * kvld : b1 + (uint64_t)(pc - a.n0) * kvld) + h * AHD;
+    };
+    auto load_k = [&](float4 (&kr)[8], uint32_t tile) {
+        const float *kp = kvrow(a.k0, a.k1, 16 * tile + l16) + 4 * kg;
+#pragma unroll
+        for (int b = 0; b < 8; b++) kr[b] = *reinterpret_cast<const float4 *>(kp + 16 * b);
+    };
+    auto load_v = [&](float4 (&vr)[8], uint32_t tile) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const float *vp = kvrow(a.v0, a.v1, 16 * tile + 4 * kg + s) + 4 * l16;
+            vr[2 * s] = *reinterpret_cast<const float4 *>(vp);
+            vr[2 * s + 1] = *reinterpret_cast<const float4 *>(vp + 64);
+        }
+    };
+    f32x4 Od[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) Od[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, lsum = 0.0f;  // running max (base-2 units) and sum of the lane's query
+    const float sl2 = a.scale * 1.44269504088896341f;
+    // One tile: S^T from kr, then kr refilled with tile `next` (two tiles ahead), the
+    // softmax, P V from vr, then vr refilled with tile `next`.  Every load is
+    // unconditional (past the wavefront's last tile: the last tile again), so that
+    // each product waits for its own operands only.
+    auto tile_step = [&](float4 (&kr)[8], float4 (&vr)[8], uint32_t tile, uint32_t next) {
+        f32x4 sc[4];  // four independent chains over the blocks b, b + 4 (b mod 4)
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < 8; b++)
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                sc[b & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(kr[b], s), f4c(qf[b], s), sc[b & 3], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_k(kr, next);
+        __builtin_amdgcn_sched_barrier(0);
+        // scores in base-2 units: s log2(e) / sqrt(d), so that P = 2^(s - max)
+        float sv[4], tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t p = 16 * tile + 4 * kg + i;
+            const bool ok = qlive && p < a.S && (!a.causal || p <= qpos);
+            sv[i] = ok ? ((sc[0][i] + sc[1][i]) + (sc[2][i] + sc[3][i])) * sl2 : -INFINITY;
+            tmax = fmaxf(tmax, sv[i]);
+        }
+        tmax = rows4_max(tmax);
+        const float mn = fmaxf(m, tmax), mu = mn == -INFINITY ? 0.0f : mn;
+        if (__builtin_amdgcn_ballot_w64(mn != m)) {  // some query's max moved: rescale (2^-inf = 0)
+            const float f = __builtin_amdgcn_exp2f(m - mu);
+            lsum *= f;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) Od[dt] *= f;
+        }
+        m = mn;
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            pv[i] = __builtin_amdgcn_exp2f(sv[i] - mu);
+            lsum += pv[i];
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++)
+                    Od[4 * hh + cc] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(vr[2 * s + hh], cc), pv[s], Od[4 * hh + cc], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(vr, next);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // the wavefront's tiles, two sets of K and V registers in turn: each tile's loads
+    // are issued two tiles ahead
+    if (nmine) {
+        float4 ka[8], va[8], kb[8], vb[8];
+        const uint32_t t0 = tb + wave;
+        auto tile_at = [&](uint32_t i) { return i < nmine ? t0 + 4 * i : tlast; };
+        load_k(ka, t0);
+        load_v(va, t0);
+        load_k(kb, tile_at(1));
+        load_v(vb, tile_at(1));
+        __builtin_amdgcn_sched_barrier(0);
+        gate_units();  // its loads after the first tiles'
+        for (uint32_t i = 0; i < nmine; i += 2) {
+            tile_step(ka, va, t0 + 4 * i, tile_at(i + 2));
+            if (i + 1 >= nmine) break;
+            tile_step(kb, vb, t0 + 4 * i + 4, tile_at(i + 3));
+        }
+    } else {
+        gate_units();
+    }
+    lsum = lane_add_x32(lane_add_x16(lsum));
+    // the wavefronts' partials meet in LDS: lane (query l16, kg) holds dims
+    // 64hh + 16kg + 4i + cc in Od[4hh + cc][i]
+    if (kg == 0) sm[wave][l16] = m, sl[wave][l16] = lsum;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            *reinterpret_cast<float4 *>(&so[wave][l16][64 * hh + 16 * kg + 4 * i]) =
+                make_float4(Od[4 * hh][i], Od[4 * hh + 1][i], Od[4 * hh + 2][i], Od[4 * hh + 3][i]);
+    __syncthreads();
+    // thread (query mq, dims md .. md + 7): the workgroup's partial, waves in order
+    const uint32_t mq = tid >> 4, md = 8 * (tid & 15u);
+    float M = fmaxf(fmaxf(sm[0][mq], sm[1][mq]), fmaxf(sm[2][mq], sm[3][mq])), L = 0.0f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float f = sm[w][mq] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sm[w][mq] - M);
+        L = __builtin_fmaf(f, sl[w][mq], L);
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = __builtin_fmaf(f, so[w][mq][md + e], o[e]);
+    }
+    // the group's partials: byte offsets within part_o (< 2^31: the workspace bound)
+    const __amdgpu_buffer_rsrc_t ro = dev_rsrc(a.part_o + (uint64_t)grp * a.nch * AQG * AHD),
+                                 rm = dev_rsrc(a.part_ml + (uint64_t)grp * a.nch * AQG * 2);
+    {
+        const uint32_t pi = c * AQG + mq;
+        dev_st4(ro, 4 * (pi * AHD + md), make_float4(o[0], o[1], o[2], o[3]));
+        dev_st4(ro, 4 * (pi * AHD + md + 4), make_float4(o[4], o[5], o[6], o[7]));
+        if ((tid & 15u) == 0) dev_st2(rm, 8 * pi, make_float2(M, L));
+    }
+    // the last workgroup of the group to arrive merges its chunks, in chunk order
+    if (!arrive_last(a.cnt + grp, a.nch, &last)) return;
+    constexpr uint32_t CB = 8;
+    M = -INFINITY, L = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = 0.0f;
+    for (uint32_t c0 = 0; c0 < a.nch; c0 += CB) {
+        float mc[CB], lc[CB];
+        float4 oc[CB][2];
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) {
+            const uint32_t pi = (c0 + b < a.nch ? c0 + b : a.nch - 1) * AQG + mq;
+            const float2 ml = dev_ld2(rm, 8 * pi);
+            oc[b][0] = dev_ld4(ro, 4 * (pi * AHD + md));
+            oc[b][1] = dev_ld4(ro, 4 * (pi * AHD + md + 4));
+            mc[b] = c0 + b < a.nch ? ml.x : -INFINITY;
+            lc[b] = ml.y;
+        }
+        float mn = M;
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) mn = fmaxf(mn, mc[b]);
+        const float f = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+        L *= f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] *= f;
+#pragma unroll
+        for (uint32_t b = 0; b < CB; b++) {  // chunk order
+            const float w = mc[b] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc[b] - mn);
+            L = __builtin_fmaf(w, lc[b], L);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                o[e] = __builtin_fmaf(w, f4c(oc[b][0], e), o[e]);
+                o[4 + e] = __builtin_fmaf(w, f4c(oc[b][1], e), o[4 + e]);
+            }
+        }
+        M = mn;
+    }
+    const uint32_t qo = AQG * qg + mq;
+    if (qo >= nq) return;
+    const uint32_t t = qo / G, hq = h * G + qo % G;
+    float sc = L > 0.0f ? 1.0f / L : 0.0f;
+    if (a.gate || a.gj.units) {
+        const float gv = a.gj.units
+                             ? __hip_atomic_load(a.gbuf + grp * AQG + mq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : a.gate[(uint64_t)t * a.n_q + hq];
+        const float g = a.gmode == 2 ? logf(1.0f + expf(gv)) : softplus_gate(gv);
+        float *op = a.out + (uint64_t)t * a.n_q * AHD + hq * AHD + md;
+        *reinterpret_cast<float4 *>(op) =
+            make_float4((o[0] * sc) * g, (o[1] * sc) * g, (o[2] * sc) * g, (o[3] * sc) * g);
+        *reinterpret_cast<float4 *>(op + 4) =
+            make_float4((o[4] * sc) * g, (o[5] * sc) * g, (o[6] * sc) * g, (o[7] * sc) * g);
+    } else {
+        float *op = a.out + (uint64_t)t * a.n_q * AHD + hq * AHD + md;
+        *reinterpret_cast<float4 *>(op) = make_float4(o[0] * sc, o[1] * sc, o[2] * sc, o[3] * sc);
+        *reinterpret_cast<float4 *>(op + 4) = make_float4(o[4] * sc, o[5] * sc, o[6] * sc, o[7] * sc);
+    }
+}
+
 // Any head_dim <= 256: one wavefront per (row, q head), online softmax as mha_attn.comp.
 __global__ __launch_bounds__(256) void k_attn_simple(const float *__restrict__ q, const float *__restrict__ k0,
                                                      const float *__restrict__ v0, uint32_t n0,
@@ -1111,55 +1131,65 @@ int run_qk_norm_rope(const QkJob &a, const QkJob &b, const float *freq, uint32_t
 
 bool aligned16_ptr(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Chunks per kv head of k_attn_chunk over S positions: four 16-position tiles each,
-// or, when that would not fit one round of workgroups (one per CU) and at most AMT
-// tiles each would, one chunk per CU.  Never more than ceil(S / 64).
-uint32_t attn_chunks(uint32_t S, uint32_t n_kv) {
-    const uint32_t nt = (S + 15) / 16, n4 = (nt + 3) / 4, cap = (uint32_t)device_cus() / n_kv;
-    return n4 > cap && cap && (nt + cap - 1) / cap <= AMT ? cap : n4;
+// Chunks per (kv head, query group) of k_attn_split: about one workgroup per CU over
+// the `groups` groups, each chunk at least four tiles (one per wavefront) when S allows.
+uint32_t attn_split_chunks(uint32_t S, uint32_t groups) {
+    const uint32_t nt = (S + 15) / 16, per = (uint32_t)device_cus() / groups, cap = (nt + 3) / 4;
+    const uint32_t nch = per < cap ? per : cap;
+    return nch ? nch : 1;
 }
+
+// The attention workspace: arrival counters first (k_attn_split's, one per query group,
+// zero between calls), then the partials of whichever kernel runs.
+uint32_t attn_cnt_floats(uint32_t n_kv) { return (4 * n_kv + 63) / 64 * 64; }
 
 size_t attn_partial_floats(uint32_t S, uint32_t n_kv) {
-    const uint32_t nch = (S + ACH - 1) / ACH;
-    return (size_t)n_kv * nch * AQ * (AHD + 2);
+    const uint32_t nch = (S + ACH - 1) / ACH, cus = (uint32_t)device_cus();
+    const size_t decode = (size_t)n_kv * nch * AQ * (AHD + 2);
+    // k_attn_split: groups <= 4 n_kv (at most AQ queries per kv head), groups * chunks <= max(CUs, groups)
+    const size_t gc = cus > 4 * n_kv ? cus : 4 * n_kv;
+    const size_t split = gc * AQG * (AHD + 2) + (size_t)4 * n_kv * AQG;
+    return attn_cnt_floats(n_kv) + (decode > split ? decode : split);
 }
 
-// `part` holds attn_partial_floats(S, n_kv) floats when the matrix-core path applies.
-// With `gate` ([rows][n_q]) each head's result is multiplied by softplus of its gate.
+// `part` holds attn_partial_floats(S, n_kv) floats when the matrix-core path applies,
+// zeroed before its first use; `cnt` (when given) replaces its counters.  With `gate`
+// ([rows][n_q]) each head's result is multiplied by softplus of its gate.
 int run_attention(const float *q, const float *k0, const float *v0, uint32_t n0, const float *k1, const float *v1,
                   uint32_t S, uint32_t rows, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t qpos0, int causal,
                   float *out, float *part, hipStream_t s, const float *gate = nullptr, int gmode = 1,
-                  const GateJob *gj = nullptr) {
+                  const GateJob *gj = nullptr, uint32_t *cnt = nullptr) {
     const float scale = 1.0f / sqrtf((float)hd);  // src/dflash.rs:1173
     const uint32_t G = n_q / n_kv;
     const bool al = aligned16_ptr(q) && aligned16_ptr(k0) && aligned16_ptr(v0) &&
                     (!k1 || (aligned16_ptr(k1) && aligned16_ptr(v1)));
-    if (part && hd == AHD && rows * G <= AQ && al) {
-        uint32_t T = 0, Sc = S, nch;
-        if (rows * G <= ADQ) {
-            // The chunks cover the context; a short run of positions after it (the
-            // block's own keys in k1) is attended by the combine, so that the chunk
-            // grid does not spill a few workgroups into a second round.
-            T = k1 && S > n0 && S - n0 <= ATAIL ? S - n0 : 0;
-            Sc = T ? n0 : S;
-            nch = (Sc + ACH - 1) / ACH;
-        } else {
-            nch = attn_chunks(S, n_kv);  // every position, up to AMT tiles per chunk
-        }
+    if (part && hd == AHD && rows * G <= AQ && al && rows * G > ADQ) {
+        const uint32_t ngq = (rows * G + AQG - 1) / AQG, groups = n_kv * ngq, nch = attn_split_chunks(S, groups);
+        SplitAttn a{};
+        a.q = q, a.k0 = k0, a.v0 = v0, a.k1 = k1, a.v1 = v1;
+        a.n0 = n0, a.S = S, a.rows = rows, a.n_q = n_q, a.n_kv = n_kv, a.qpos0 = qpos0, a.ngq = ngq, a.nch = nch;
+        a.causal = causal, a.gmode = gmode, a.scale = scale;
+        a.part_o = part + attn_cnt_floats(n_kv);
+        a.part_ml = a.part_o + (size_t)groups * nch * AQG * AHD;
+        a.gbuf = a.part_ml + (size_t)groups * nch * AQG * 2;
+        a.cnt = cnt ? cnt : reinterpret_cast<uint32_t *>(part);
+        a.out = out, a.gate = gate, a.gj = gj ? *gj : GateJob{};
+        const uint32_t R = n_kv * nch;
+        hipLaunchKernelGGL(k_attn_split, dim3((R + 7) / 8 * 8 * ngq), dim3(256), 0, s, a);
+        return after_launch("attn_split", s);
+    }
+    if (part && hd == AHD && rows * G <= ADQ && al) {
+        // Few queries: the chunks cover the context; a short run of positions after it
+        // (the block's own keys in k1) is attended by the combine, so that the chunk
+        // grid does not spill a few workgroups into a second round.
+        part += attn_cnt_floats(n_kv);
+        const uint32_t T = k1 && S > n0 && S - n0 <= ATAIL ? S - n0 : 0, Sc = T ? n0 : S;
+        const uint32_t nch = (Sc + ACH - 1) / ACH;
         float *part_ml = part + (size_t)n_kv * nch * AQ * AHD;
-        if (nch && rows * G <= ADQ) {
+        if (nch) {
             hipLaunchKernelGGL(k_attn_decode, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, Sc,
                                rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
             LG_TRY(after_launch("attn_decode", s));
-        } else if (nch) {
-            const uint32_t nt = (S + 15) / 16;
-            if ((nt + nch - 1) / nch > 4)
-                hipLaunchKernelGGL(k_attn_chunk<5>, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S,
-                                   rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
-            else
-                hipLaunchKernelGGL(k_attn_chunk<4>, dim3(nch, n_kv), dim3(256), 0, s, q, k0, v0, n0, k1, v1, S,
-                                   rows, n_q, n_kv, qpos0, causal, scale, nch, part, part_ml);
-            LG_TRY(after_launch("attn_chunk", s));
         }
         hipLaunchKernelGGL(k_attn_combine, dim3(n_kv * AQ), dim3(256), 0, s, part, part_ml, out, rows, n_q,
                            n_kv, nch, gate, q, k1, v1, T, n0, qpos0, causal, scale, gmode, gj ? *gj : GateJob{});
@@ -1436,7 +1466,7 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
         // causal attention over [context; injected; tokens] (src/dflash.rs:945-954), each head
         // scaled by softplus of its gate (src/dflash.rs:956-959)
         LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m, 1,
-                             W.att, W.part, s, gate));
+                             W.att, W.part, s, gate, 1, nullptr, static_cast<uint32_t *>(W.pws)));
         LG_TRY(proj(W, W.att, L.attn_output, L.attn_output_type, x, QD, E, m, s, x));  // x += o_proj
         // SwiGLU FFN (src/dflash.rs:962-968)
         LG_TRY(run_rmsnorm(x, L.ffn_norm, W.h, E, m, 1, E, hp.rms_eps, s));
@@ -1528,7 +1558,7 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
             gj = {ny, static_cast<const uint8_t *>(L.attn_gate), W.gate + (uint64_t)m * H, H, E, m * H, (m * H + 3) / 4,
                   W.ssa, cols_a, eps};
             LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m,
-                                 1, W.att, W.part, s, nullptr, 1, &gj));
+                                 1, W.att, W.part, s, nullptr, 1, &gj, static_cast<uint32_t *>(W.pws)));
         } else {
             if (kvq && L.attn_gate_type == LG_Q4_K) {
                 const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
@@ -1562,7 +1592,7 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
                                     qk_job(q, L.attn_q_norm, q, H, ctx_len + m, m), W.freq, HD, hp.rope_dim,
                                     hp.qk_eps, s, gj));
             LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m,
-                                 1, W.att, W.part, s, gate));
+                                 1, W.att, W.part, s, gate, 1, nullptr, static_cast<uint32_t *>(W.pws)));
         }
         // x += o_proj, writing x ffn_norm and the sums of x^2 for the FFN norm (src/dflash.rs:960-962)
         const uint32_t cols_b = proj_batch_norm_cols(L.attn_output_type, QD, E, m);
@@ -1663,7 +1693,7 @@ int glue_attention_token(const float *q, const float *qn_w, const float *kn_w, c
     t.q = q, t.qn_w = qn_w, t.kn_w = kn_w, t.freq = freq, t.rope = rope_dim ? 1u : 0u, t.pos = pos, t.eps = eps;
     t.scale = 1.0f / sqrtf((float)head_dim);  // src/dflash.rs:1173
     t.k = k, t.v = v, t.S = seq_len, t.n_q = n_q, t.n_kv = n_kv, t.nch = (seq_len + ACH - 1) / ACH;
-    t.part_o = part;
+    t.part_o = part + attn_cnt_floats(n_kv);
     t.part_ml = part + (size_t)n_kv * t.nch * AQ * AHD;
     hipLaunchKernelGGL(k_attn_token, dim3(t.nch, n_kv), dim3(256), 0, s, t);
     LG_TRY(after_launch("attention_token", s));

@@ -11,8 +11,8 @@ The shipped library is not touched; the instrumented one is built into _timeline
     python timeline.py build
     python timeline.py run WORKLOAD [mm|attn]
 
-`mm` reads the last k_mm_mf launch of the workload, `attn` the last attention chunk and
-combine launches (the draft block's last layer).
+`mm` reads the last k_mm_mf launch of the workload, `attn` the last k_attn_split launch
+(the draft block's last layer), or the last combine launch of the few-query path.
 """
 import argparse
 import collections
@@ -56,14 +56,15 @@ STAMPS = {
         ("before", "    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lrec)", "    TS(36);\n"),
         ("after", "jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);", "\n    TS(38);"),
     ]),
-    "dflash.hip": ("void k_attn_chunk(", [
-        ("after", "    __shared__ Lds L;", "\n    TS(0); TSID();"),
-        ("before", "    // V, now that K is in LDS", "    TS(1);\n"),
-        ("before", "    // S^T for the chunk", "    TS(2);\n"),
-        ("before", "    // V^T to LDS, now that", "    TS(3);\n"),
-        ("before", "    // O^T = V^T P^T over", "    TS(4);\n"),
-        ("before", "    // partials: O[q][d] (lane", "    TS(5);\n"),
-        ("after", "reinterpret_cast<f32x2_t *>(part_ml + 2 * pq));", "\n    TS(6);"),
+    "dflash.hip": ("void k_attn_split(", [
+        ("after", "grp = h * a.ngq + qg;", "\n    TS(0); TSID();"),
+        ("before", "    const uint32_t nt = (a.S + 15) / 16, tb = attn_tile0(c, nt, a.nch)", "    TS(1);\n"),
+        ("before", "        for (uint32_t i = 0; i < nmine; i += 2) {", "        TS(2);\n"),
+        ("before", "    lsum = lane_add_x32(lane_add_x16(lsum));", "    TS(3);\n"),
+        ("before", "    // thread (query mq, dims md .. md + 7): the workgroup's partial", "    TS(4);\n"),
+        ("before", "    // the last workgroup of the group to arrive merges", "    TS(5);\n"),
+        ("after", "if (!arrive_last(a.cnt + grp, a.nch, &last)) return;", "\n    TS(6);"),
+        ("before", "    const uint32_t qo = AQG * qg + mq;", "    TS(7);\n"),
     ]),
     "dflash.hip#combine": ("void k_attn_combine(", [
         ("after", "if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup", "\n    TS(20);"),
@@ -77,9 +78,10 @@ STAMPS = {
 PHASES = {
     "mm": [(0, "start"), (1, "chunk 0's activations in LDS"), (2, "chunk 1 in LDS"), (3, "chunk 2 in LDS"),
            (4, "chunk 3 in LDS"), (36, "products done"), (38, "split-k finish done")],
-    "attn": [(0, "chunk: start"), (1, "K split to LDS"), (2, "queries split, barrier"), (3, "scores + softmax"),
-             (4, "V split to LDS, barrier"), (5, "P V"), (6, "partials stored"), (20, "combine: start"),
-             (21, "tail / gate"), (22, "chunk partials merged"), (23, "waves met in LDS"), (24, "result")],
+    "attn": [(0, "start"), (1, "queries issued"), (2, "first tile issued, gate units done"),
+             (3, "tiles done"), (4, "wavefronts met in LDS"), (5, "partial stored"), (6, "last to arrive"),
+             (7, "chunks merged"), (20, "combine: start"), (21, "tail / gate"), (22, "chunk partials merged"),
+             (23, "waves met in LDS"), (24, "result")],
 }
 
 
@@ -170,8 +172,11 @@ def run(workload, what):
     wpg = 4
     wg_cu = cu[0::wpg]
     rel = np.where(T[:nw] > 0, (T[:nw] - t0) * 10, -1)
-    end_k = 38 if what == "mm" else 6
+    end_k = 38 if what == "mm" else 5
     ends = rel[:, end_k].reshape(-1, wpg).max(axis=1)
+    wg_xcc = xcc[0::wpg]
+    rr = int((wg_xcc == (np.arange(len(wg_xcc)) % 8)).sum())
+    print(f"workgroups on XCD (workgroup id mod 8): {rr} of {len(wg_xcc)}")
     cnt = collections.Counter(wg_cu.tolist())
     hist = collections.Counter(cnt.values())
     print(f"\nworkgroups {len(wg_cu)} on {len(cnt)} CUs; CUs by workgroups held: {dict(sorted(hist.items()))}")

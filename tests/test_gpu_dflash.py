@@ -3,8 +3,8 @@
 Tolerances (all relative to the largest magnitude of the f64 result, ||y-yhat||_inf
 / ||yhat||_inf, written per test):
 * norms, RoPE, gates: f32 arithmetic, 1e-5 (measured 1e-7);
-* attention on matrix cores: q, k, p and v enter as three bf16 parts each (all 24
-  bits) with the six significant part products, 1e-5 (measured 8e-7);
+* attention on matrix cores: f32 products of q, k, p and v (v_mfma_f32_16x16x4_f32)
+  with base-2 exponentials of the scaled scores, 1e-5;
 * the block forward on weights of trained magnitude (N(0, 0.02) quantized): 3e-6
   (measured 1.4e-7 .. 2.3e-7);
 * the block forward on GGUF-random Q4_K blocks, whose large common-mode weight
