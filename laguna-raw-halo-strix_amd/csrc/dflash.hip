@@ -1363,6 +1363,13 @@ int check_model(const lg_dflash_model *md, uint32_t m, const char *name, bool wi
 }
 
 // c = W x, or c = res + W x
+// A job over the forward's 2m rows [injected; tokens] whose result is read for the
+// token rows only (the queries, the attention gate).
+BatchJob tok_rows(BatchJob b, uint32_t m) {
+    b.row0 = m;
+    return b;
+}
+
 int proj(const FwdLayout &W, const float *x, const void *w, int type, float *c, uint32_t k, uint32_t n, uint32_t m,
          hipStream_t s, const float *res = nullptr) {
     return proj_batch(x, LG_F32, w, c, k, n, m, type, W.pws, W.pws_bytes, s, res);
@@ -1443,14 +1450,15 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
             // K, V, Q in one launch; the gate (H rows) is computed with the QK norms
             // below, which keeps the grouped launch's workgroups to whole rounds
             const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                    {L.attn_q, W.q, nullptr, QD}};
+                                    tok_rows({L.attn_q, W.q, nullptr, QD}, m)};
             LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
             q = W.q + (uint64_t)m * QD;
             gate = W.gate + (uint64_t)m * H;
             gj = {nx, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4};
         } else if (kvq && L.attn_k_type == L.attn_gate_type) {
             const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                    {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
+                                    tok_rows({L.attn_q, W.q, nullptr, QD}, m),
+                                    tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
             LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
             q = W.q + (uint64_t)m * QD;
             gate = W.gate + (uint64_t)m * H;
@@ -1548,7 +1556,7 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
         const bool kvq = L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type;
         if (qkf && kvq && L.attn_gate_type == LG_Q4_K) {
             BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                              {L.attn_q, W.q, nullptr, QD}};
+                              tok_rows({L.attn_q, W.q, nullptr, QD}, m)};
             jb[0].qkw = L.attn_k_norm;
             jb[2].qkw = L.attn_q_norm;
             const QkRope qk{W.rope, hp.qk_eps};
@@ -1562,7 +1570,7 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
         } else {
             if (kvq && L.attn_gate_type == LG_Q4_K) {
                 const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                        {L.attn_q, W.q, nullptr, QD}};
+                                        tok_rows({L.attn_q, W.q, nullptr, QD}, m)};
                 LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
                                         false, &ra));
                 q = W.q + (uint64_t)m * QD;
@@ -1571,7 +1579,8 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
                       W.ssa, cols_a, eps};
             } else if (kvq && L.attn_k_type == L.attn_gate_type) {
                 const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                        {L.attn_q, W.q, nullptr, QD}, {L.attn_gate, W.gate, nullptr, H}};
+                                        tok_rows({L.attn_q, W.q, nullptr, QD}, m),
+                                        tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
                 LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
                                         false, &ra));
                 q = W.q + (uint64_t)m * QD;

@@ -152,6 +152,7 @@ struct BatchJob {
     const float *yw = nullptr;
     float *ss = nullptr;
     const float *qkw = nullptr;
+    uint32_t row0 = 0;  // rows of c below row0 are not needed (left unwritten or zero, in steps of 16)
 };
 struct RowScale {
     const float *ss = nullptr;

@@ -107,6 +107,7 @@ struct MmJob {
     float *ss;
     uint32_t n, g0;
     const float *qkw;  // QK-norm weights (heads of 128 rows, RT = 2), or null
+    uint32_t tlo;      // 1: only the second token tile of a two-tile launch is needed
 };
 struct MmJobs {
     MmJob j[MM_JOBS];
@@ -121,11 +122,12 @@ struct MmJobs {
 // GLU launches pair two products of n rows each (gate: job 0, up: job 1): every
 // workgroup column covers the same 32*RT rows of both, wavefronts 0-1 the gate
 // rows and 2-3 the up rows, and writes only silu(gate) * up, to job 0's output.
-#define MM_JOB_SELECT                                                                     \
+#define MM_JOB_INDEX                                                                      \
     uint32_t J_ = 0;                                                                      \
     if constexpr (GLU) J_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 7);             \
     else _Pragma("unroll") for (int j_ = 1; j_ < MM_JOBS; j_++) if ((uint32_t)j_ < jobs.count && \
-                                                              blockIdx.x >= jobs.j[j_].g0) J_ = j_; \
+                                                              blockIdx.x >= jobs.j[j_].g0) J_ = j_
+#define MM_JOB_FIELDS                                                                     \
     const uint8_t *w = jobs.j[J_].w;                                                      \
     float *out = jobs.j[J_].out;                                                          \
     const float *res = jobs.j[J_].res;                                                    \
@@ -859,22 +861,30 @@ __device__ __forceinline__ void q80_chunk(const uint4 *lds, const Q80Chunk<RT> &
 // LDS buffer c%2 and the workgroup meets at a barrier; then the activations of chunk
 // c+1 and the weights of chunk c+2 (a ring of three chunks in registers) are issued,
 // and chunk c is multiplied.
+// Staged pieces per wavefront of the raw-block paths.
+template <bool Q4, int RT>
+constexpr uint32_t mm_spw() {
+    return RT * 16 * (Q4 ? Q4K_PIECES : Q80_PIECES);
+}
+
+// The product of job J_ over TT token tiles; lrec holds two records of TT tiles,
+// lstage (raw blocks) 4 mm_spw<Q4, RT>() pieces.
 template <bool Q4, int TT, int RT, bool GLU, bool NORM, bool TILED, int XM>
-__global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, MmJobs jobs, uint32_t *cnt, uint32_t m,
-                                               uint32_t k, uint64_t row_bytes, uint32_t ch) {
-    MM_JOB_SELECT;
-    __shared__ uint4 lrec[2][TT * FR_U4];
+__device__ __forceinline__ void mm_body(const void *x, const float *up, const MmJobs &jobs, uint32_t J_, uint32_t *cnt,
+                                        uint32_t m, uint32_t k, uint64_t row_bytes, uint32_t ch, uint4 *lrec_base,
+                                        lg_u32x4 *lstage) {
+    MM_JOB_FIELDS;
+    uint4 (*lrec)[TT * FR_U4] = reinterpret_cast<uint4 (*)[TT * FR_U4]>(lrec_base);
     // uniform over the wavefront: row-tile addresses are scalar
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t rt0 = (GLU ? bx * 2 + (wave & 1u) : bx * 4 + wave) * RT;
     const uint32_t nb = k / QK_K, c0 = blockIdx.y * ch, nch = nb - c0 < ch ? nb - c0 : ch;
     // raw blocks: rows through a per-wavefront LDS region
     constexpr bool RAW8 = !Q4 && !TILED, RAW4 = Q4 && !TILED;
-    constexpr uint32_t SPW = RT * 16 * (RAW8 ? Q80_PIECES : Q4K_PIECES);  // staged pieces per wavefront
+    constexpr uint32_t SPW = mm_spw<Q4, RT>();
     using Chunk = typename std::conditional<
         Q4, typename std::conditional<RAW4, Q4kRawChunk<RT>, Q4kChunk<RT>>::type,
         typename std::conditional<RAW8, Q80RawChunk<RT>, Q80Chunk<RT>>::type>::type;
-    __shared__ lg_u32x4 lstage[TILED ? 1 : 4 * SPW];
     Chunk Wc[3];
     // chunk ci of the slice; past the slice the last chunk again (loads stay in bounds,
     // never multiplied)
@@ -935,10 +945,40 @@ __global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, M
             chunk(lrec[c & 1u], Wc[(h + 1) % 3]);
         }
     }
-    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lrec), "GLU exchange fits in the record LDS");
-    static_assert(RT != 2 || 8 * TT * 256 * 4 <= sizeof(lrec), "the head exchange fits in the record LDS");
-    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(&lrec[0][0]), jobs, k,
+    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= 2 * TT * FR_U4 * 16, "GLU exchange fits in the record LDS");
+    static_assert(RT != 2 || 8 * TT * 256 * 4 <= 2 * TT * FR_U4 * 16, "the head exchange fits in the record LDS");
+    finish<TT, RT, GLU, NORM>(acc, out, res, part, cnt, rt0, m, n, reinterpret_cast<float *>(lrec_base), jobs, k,
                               jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);
+}
+
+template <bool Q4, int TT, int RT, bool GLU, bool NORM, bool TILED, int XM>
+__global__ __launch_bounds__(256) void k_mm_mf(const void *x, const float *up, MmJobs jobs, uint32_t *cnt, uint32_t m,
+                                               uint32_t k, uint64_t row_bytes, uint32_t ch) {
+    MM_JOB_INDEX;
+    __shared__ uint4 lrec[2 * TT * FR_U4];
+    __shared__ lg_u32x4 lstage[TILED ? 1 : 4 * mm_spw<Q4, RT>()];
+    if constexpr (TT == 2 && !GLU && XM == 0) {
+        if (jobs.j[J_].tlo) {  // uniform: this job takes token rows 16 .. m - 1 only (one tile)
+            // a launch of that one job, held as job 0 (static indices: no private copy)
+            MmJobs j1;
+            j1.j[0] = jobs.j[J_];
+            j1.j[0].out += (uint64_t)16 * j1.j[0].n;
+            if (j1.j[0].res) j1.j[0].res += (uint64_t)16 * j1.j[0].n;
+            j1.count = 1;
+            j1.tiled = jobs.tiled;
+            j1.rs_cols = jobs.rs_cols;
+            j1.rs_eps = jobs.rs_eps;
+            // the folded norm's rows, relative to the tile
+            j1.rs_ss = jobs.rs_ss + (uint64_t)(jobs.rs_tok0 < 16 ? 16 - jobs.rs_tok0 : 0) * jobs.rs_cols;
+            j1.rs_tok0 = jobs.rs_tok0 > 16 ? jobs.rs_tok0 - 16 : 0;
+            j1.rope = jobs.rope ? jobs.rope + 16 * 128 : nullptr;
+            j1.qk_eps = jobs.qk_eps;
+            mm_body<Q4, 1, RT, GLU, NORM, TILED, XM>(static_cast<const float *>(x) + (uint64_t)16 * k, up, j1, 0u, cnt,
+                                                     m - 16, k, row_bytes, ch, lrec, lstage);
+            return;
+        }
+    }
+    mm_body<Q4, TT, RT, GLU, NORM, TILED, XM>(x, up, jobs, J_, cnt, m, k, row_bytes, ch, lrec, lstage);
 }
 
 // Fallback for shapes outside the MFMA path (f32 weights, k not a multiple of the
@@ -1259,8 +1299,10 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
         uint32_t groups = 0;
         for (uint32_t j = 0; j < njobs; j++) {
             const uint64_t off = (uint64_t)16 * t0 * jb[j].n;
+            // a job whose rows below 16 t0 + 16 are not needed skips the pair's first tile
+            const uint32_t tlo = tt == 2 && !glu && xm == 0 && !jb[j].ss && jb[j].row0 >= 16 * t0 + 16 ? 1u : 0u;
             jobs.j[j] = {static_cast<const uint8_t *>(jb[j].w), jb[j].c + off, jb[j].res ? jb[j].res + off : nullptr,
-                         reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups, jb[j].qkw};
+                         reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups, jb[j].qkw, tlo};
             if (sh.slices > 1) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
             groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
         }
