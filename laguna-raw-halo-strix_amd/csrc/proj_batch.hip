@@ -1065,7 +1065,11 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool q
     if (qk) rt = 2;  // whole heads of 128 rows per column
     while (epi && rt < 2 && (n + per * rt - 1) / (per * rt) > 64) rt *= 2;
     const uint32_t cols = (n + per * rt - 1) / (per * rt);
-    uint32_t slices = (target + cols / 2) / cols;
+    // two token tiles of two row tiles take every register of a SIMD (one workgroup per
+    // CU): about 9/8 workgroups per CU instead (the 32-row K/V/Q launch of the draft
+    // block: 610 against 624 us per block forward with 2 per CU, 614 with 3/4 per CU)
+    const uint32_t tgt = m > 16 && rt == 2 ? cus * 9 / 8 : target;
+    uint32_t slices = (tgt + cols / 2) / cols;
     slices = slices < 1 ? 1 : (slices > nb ? nb : slices);
     uint32_t ch = nb ? (nb + slices - 1) / slices : 1;
     const uint32_t och = g_mm_ch.load(std::memory_order_relaxed);
