@@ -11,7 +11,7 @@ The shipped library is not touched; the instrumented one is built into _timeline
     python timeline.py build
     python timeline.py run WORKLOAD [mm|attn]
 
-`mm` reads the last k_mm_mf launch of the workload, `attn` the last k_attn_split launch
+`mm` reads the last small-M product launch (k_mm_mf) of the workload, `attn` the last k_attn_split launch
 (the draft block's last layer), or the last combine launch of the few-query path.
 """
 import argparse
@@ -48,12 +48,12 @@ extern "C" int lg_timeline_clear_%(f)s() {
 # (file, kernel signature start, [(mode, marker, text)]): text goes after / before the
 # first occurrence of marker past the kernel's start.
 STAMPS = {
-    "proj_batch.hip": ("void k_mm_mf(", [
-        ("after", "uint32_t k, uint64_t row_bytes, uint32_t ch) {", "\n    TS(0); TSID();"),
+    "proj_batch.hip": ("void mm_body(", [
+        ("after", "lg_u32x4 *lstage) {", "\n    TS(0); TSID();"),
         ("after", "    rb.store(lrec[0], m);\n    __syncthreads();", "\n    TS(1);"),
         ("after", "            rb.store(lrec[c & 1u], m);\n            __syncthreads();",
          "\n            if (c < 34) TS(1 + c);"),
-        ("before", "    static_assert(!GLU || 2 * RT * TT * 256 * 4 <= sizeof(lrec)", "    TS(36);\n"),
+        ("before", "    static_assert(!GLU || 2 * RT * TT * 256 * 4", "    TS(36);\n"),
         ("after", "jobs.j[J_].y, jobs.j[J_].yw, jobs.j[J_].ss, bx, jobs.j[J_].qkw);", "\n    TS(38);"),
     ]),
     "dflash.hip": ("void k_attn_split(", [
@@ -160,7 +160,7 @@ def run(workload, what):
     print("|---|---|---|---|---|---|")
     for k, name in PHASES[what]:
         v = T[:, k]
-        v = (v[v > 0] - t0) * 10
+        v = (v[v >= t0] - t0) * 10  # stamps of the last launch only (others are left from earlier ones)
         if v.size:
             print(f"| {k} | {name} | {int(np.percentile(v, 10))} | {int(np.median(v))} | "
                   f"{int(np.percentile(v, 90))} | {int(v.max())} |")
