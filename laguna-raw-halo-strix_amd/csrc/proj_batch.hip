@@ -1058,6 +1058,10 @@ MmShape mm_shape(int dtype, uint32_t k, uint32_t n, uint32_t m, bool glu, bool q
     const uint32_t per = glu ? 32u : 64u;  // rows per column and row tile per wavefront
     uint32_t rt = 2;
     if ((n + per * 2 - 1) / (per * 2) < cus / 4) rt = 1;
+    // a gate/up pair with at least one RT = 1 column per CU: no k split, so no partial
+    // sums and no finishing workgroup (the draft's 14336-row pair: 448 columns of whole
+    // k against 224 x 2 slices, 610.2 -> 604.9 us per block forward)
+    if (glu && m <= 16 && (n + per - 1) / per >= cus) rt = 1;
     const uint32_t ort = g_mm_rt.load(std::memory_order_relaxed);
     if (ort) rt = ort >= 4 ? 4 : ort >= 2 ? 2 : 1;
     if (dtype != LG_Q4_K && rt > 2) rt = 2;  // register budget of the Q8_0 chunk
