@@ -36,7 +36,9 @@
  *     not run at the same time as direct calls on that stream.  A draft-forward
  *     graph (lg_dflash_graph_create) owns its workspace.  lg_stream_destroy
  *     releases a stream's workspaces; a stream destroyed without it leaves them
- *     to the next stream that gets the same handle.
+ *     to the next stream that gets the same handle.  hipStreamPerThread gets
+ *     one workspace per host thread.  One stream is driven from one host thread
+ *     at a time (a workspace that grows is freed under calls racing on it).
  *   - Registries inside the library are locked; the launch-shape hooks of
  *     laguna_hip_tuning.h are atomic.
  */

@@ -1312,6 +1312,12 @@ int upload_table(uint64_t (&tag)[2], const lg_dflash_hparams &hp, const FwdLayou
     uint32_t bb = 0;
     std::memcpy(&bb, &hp.rope_base, 4);
     if (tag[0] == hp.rope_dim && tag[1] == bb) return LG_OK;
+    {  // a new table is a host copy and a synchronise, which a capturing stream cannot take
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        LG_HIP_TRY(hipStreamIsCapturing(s, &cs));
+        LG_REQUIRE(cs == hipStreamCaptureStatusNone, "the RoPE table of this model must be uploaded while the stream "
+                   "is being captured; make the same call once before capturing");
+    }
     const std::vector<float> f = rope_table(hp);
     LG_HIP_TRY(hipMemcpyAsync(L.freq, f.data(), f.size() * 4, hipMemcpyHostToDevice, s));
     LG_HIP_TRY(hipStreamSynchronize(s));  // f is released on return

@@ -5,6 +5,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <vector>
 
@@ -80,7 +81,13 @@ int after_launch(const char *what, hipStream_t s) {
 // ---- library-owned device buffers, one per (purpose, device, stream)
 
 static std::mutex g_sb_mu;
-static std::map<std::tuple<int, int, uintptr_t>, StreamBuf> g_sb;
+// (purpose, device, stream handle, host thread): the thread is part of the key only for
+// hipStreamPerThread, one handle that names a different stream in each host thread
+static std::map<std::tuple<int, int, uintptr_t, size_t>, StreamBuf> g_sb;
+
+static size_t stream_thread(hipStream_t s) {
+    return s == hipStreamPerThread ? std::hash<std::thread::id>{}(std::this_thread::get_id()) : 0;
+}
 static std::vector<void *> g_retired;  // buffers a captured graph may still use: never freed
 
 BufLease::~BufLease() { delete static_cast<std::unique_lock<std::mutex> *>(lock); }
@@ -93,7 +100,7 @@ int stream_buffer(int purpose, hipStream_t s, uint64_t need, BufLease &lease, co
     const bool capturing = cs != hipStreamCaptureStatusNone;
     auto *lk = new std::unique_lock<std::mutex>(g_sb_mu);
     lease.lock = lk;
-    StreamBuf &b = g_sb[std::make_tuple(purpose, dev, reinterpret_cast<uintptr_t>(s))];
+    StreamBuf &b = g_sb[std::make_tuple(purpose, dev, reinterpret_cast<uintptr_t>(s), stream_thread(s))];
     if (b.bytes < need) {
         if (capturing)
             return fail(LG_EINVAL,
@@ -130,7 +137,7 @@ static int release_stream_buffers(hipStream_t s) {
     std::lock_guard<std::mutex> lk(g_sb_mu);
     bool synced = false;
     for (auto it = g_sb.begin(); it != g_sb.end();) {
-        if (std::get<2>(it->first) != reinterpret_cast<uintptr_t>(s)) {
+        if (std::get<2>(it->first) != reinterpret_cast<uintptr_t>(s) || std::get<3>(it->first) != stream_thread(s)) {
             ++it;
             continue;
         }

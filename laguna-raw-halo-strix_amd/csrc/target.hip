@@ -67,6 +67,12 @@ int upload_tables(uint64_t (&tag)[2], const lg_target_hparams &hp, const TgtLayo
     const float base = base_or(hp.rope_base, 500000.0f), base_swa = base_or(hp.rope_base_swa, 10000.0f);
     const uint64_t t0 = table_tag(hp.rope_dim, base), t1 = table_tag(hp.swa ? hp.rope_dim_swa : 0, base_swa);
     if (tag[0] == t0 && tag[1] == t1) return LG_OK;
+    {  // a new table is a host copy and a synchronise, which a capturing stream cannot take
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        LG_HIP_TRY(hipStreamIsCapturing(s, &cs));
+        LG_REQUIRE(cs == hipStreamCaptureStatusNone, "the RoPE table of this model must be uploaded while the stream "
+                   "is being captured; make the same call once before capturing");
+    }
     float f[2 * TABLE_FLOATS] = {0.0f};
     glue_rope_table(hp.rope_dim, base, f);
     if (hp.swa) glue_rope_table(hp.rope_dim_swa, base_swa, f + TABLE_FLOATS);
