@@ -1447,13 +1447,21 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
         LG_TRY(run_rmsnorm(W.xe, L.attn_norm, W.nxe, E, 2 * m, 1, E, hp.rms_eps, s));
         // K, V of [injected; tokens] at positions ctx_len .. ctx_len + 2m - 1 (src/dflash.rs:924-941),
         // Q and the attention gate of the tokens (src/dflash.rs:942-944).  With one weight
-        // type the four share a launch over all 2m rows (Q and the gate of the injected
-        // rows are computed and not used: the weights are read once either way).
+        // type the four share a launch over all 2m rows (Q and the gate over the token
+        // rows' tile only, where the rows split into 16-row tiles: BatchJob::row0).
         float *q = W.q, *gate = W.gate;
         GateJob gj{};
         const bool kvq = L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type;
-        if (kvq && L.attn_gate_type == LG_Q4_K && E % QK_K == 0 && (reinterpret_cast<uintptr_t>(L.attn_gate) & 15u) == 0) {
-            // K, V, Q in one launch; the gate (H rows) is computed with the QK norms
+        if (kvq && L.attn_k_type == L.attn_gate_type) {
+            const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                    tok_rows({L.attn_q, W.q, nullptr, QD}, m),
+                                    tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
+            LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
+            q = W.q + (uint64_t)m * QD;
+            gate = W.gate + (uint64_t)m * H;
+        } else if (kvq && L.attn_gate_type == LG_Q4_K && E % QK_K == 0 &&
+                   (reinterpret_cast<uintptr_t>(L.attn_gate) & 15u) == 0) {
+            // K, V, Q in one launch; the raw gate (H rows) is computed with the QK norms
             // below, which keeps the grouped launch's workgroups to whole rounds
             const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
                                     tok_rows({L.attn_q, W.q, nullptr, QD}, m)};
@@ -1461,13 +1469,6 @@ int forward(const lg_dflash_model *md, const FwdLayout &W, const float *features
             q = W.q + (uint64_t)m * QD;
             gate = W.gate + (uint64_t)m * H;
             gj = {nx, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4};
-        } else if (kvq && L.attn_k_type == L.attn_gate_type) {
-            const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                    tok_rows({L.attn_q, W.q, nullptr, QD}, m),
-                                    tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
-            LG_TRY(proj_batch_multi(W.nxe, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s));
-            q = W.q + (uint64_t)m * QD;
-            gate = W.gate + (uint64_t)m * H;
         } else {
             LG_TRY(proj(W, W.nxe, L.attn_k, L.attn_k_type, W.kk, E, KVD, 2 * m, s));
             LG_TRY(proj(W, W.nxe, L.attn_v, L.attn_v_type, W.vv, E, KVD, 2 * m, s));
@@ -1560,7 +1561,21 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
         float *q = W.q, *gate = W.gate;
         GateJob gj{};
         const bool kvq = L.attn_k_type == L.attn_v_type && L.attn_k_type == L.attn_q_type;
-        if (qkf && kvq && L.attn_gate_type == LG_Q4_K) {
+        if (qkf && kvq && L.attn_gate_type == L.attn_k_type) {
+            // the gate as a fourth job of the K/V/Q launch (token rows, no QK-norm)
+            BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                              tok_rows({L.attn_q, W.q, nullptr, QD}, m),
+                              tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
+            jb[0].qkw = L.attn_k_norm;
+            jb[2].qkw = L.attn_q_norm;
+            const QkRope qk{W.rope, hp.qk_eps};
+            LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s, false,
+                                    &ra, &qk));
+            q = W.q + (uint64_t)m * QD;
+            gate = W.gate + (uint64_t)m * H;
+            LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m,
+                                 1, W.att, W.part, s, gate, 1, nullptr, static_cast<uint32_t *>(W.pws)));
+        } else if (qkf && kvq && L.attn_gate_type == LG_Q4_K) {
             BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
                               tok_rows({L.attn_q, W.q, nullptr, QD}, m)};
             jb[0].qkw = L.attn_k_norm;
@@ -1574,7 +1589,15 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
             LG_TRY(run_attention(q, L.k_ctx, L.v_ctx, ctx_len, W.kk, W.vv, ctx_len + 2 * m, m, H, KV, HD, ctx_len + m,
                                  1, W.att, W.part, s, nullptr, 1, &gj, static_cast<uint32_t *>(W.pws)));
         } else {
-            if (kvq && L.attn_gate_type == LG_Q4_K) {
+            if (kvq && L.attn_k_type == L.attn_gate_type) {
+                const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
+                                        tok_rows({L.attn_q, W.q, nullptr, QD}, m),
+                                        tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
+                LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
+                                        false, &ra));
+                q = W.q + (uint64_t)m * QD;
+                gate = W.gate + (uint64_t)m * H;
+            } else if (kvq && L.attn_gate_type == LG_Q4_K) {
                 const BatchJob jb[3] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
                                         tok_rows({L.attn_q, W.q, nullptr, QD}, m)};
                 LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 3, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
@@ -1583,14 +1606,6 @@ int forward_folded(const lg_dflash_model *md, const FwdLayout &W, const float *f
                 gate = W.gate + (uint64_t)m * H;
                 gj = {ny, static_cast<const uint8_t *>(L.attn_gate), gate, H, E, m * H, (m * H + 3) / 4,
                       W.ssa, cols_a, eps};
-            } else if (kvq && L.attn_k_type == L.attn_gate_type) {
-                const BatchJob jb[4] = {{L.attn_k, W.kk, nullptr, KVD}, {L.attn_v, W.vv, nullptr, KVD},
-                                        tok_rows({L.attn_q, W.q, nullptr, QD}, m),
-                                        tok_rows({L.attn_gate, W.gate, nullptr, H}, m)};
-                LG_TRY(proj_batch_multi(Y, LG_F32, nullptr, jb, 4, E, 2 * m, L.attn_k_type, W.pws, W.pws_bytes, s,
-                                        false, &ra));
-                q = W.q + (uint64_t)m * QD;
-                gate = W.gate + (uint64_t)m * H;
             } else {
                 const BatchJob k1{L.attn_k, W.kk, nullptr, KVD}, v1{L.attn_v, W.vv, nullptr, KVD};
                 const BatchJob q1{L.attn_q, W.q, nullptr, QD}, g1{L.attn_gate, W.gate, nullptr, H};

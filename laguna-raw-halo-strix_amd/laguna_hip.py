@@ -475,9 +475,9 @@ class DFlashModel:
         shapes = {"attn_q": (E, QD), "attn_k": (E, KVD), "attn_v": (E, KVD), "attn_gate": (E, cfg.n_heads),
                   "attn_output": (QD, E), "ffn_gate": (E, cfg.n_ff), "ffn_up": (E, cfg.n_ff), "ffn_down": (cfg.n_ff, E)}
 
-        def proj_w(a, dtype, k, n, tile=True):
+        def proj_w(a, dtype, k, n):
             b = up(a)
-            if not tiled or not tile or int(dtype) not in TILED or k % 256:
+            if not tiled or int(dtype) not in TILED or k % 256:
                 return b, int(dtype)
             t = repack_tiled(ctx, b, int(dtype), k, n)
             self._bufs.append(t)
@@ -496,9 +496,7 @@ class DFlashModel:
             for n in DFLASH_NORMS:
                 setattr(d, n, up(L[n], np.float32).ptr)
             for n in DFLASH_PROJ:
-                # the attention gate (n_heads rows) stays raw: the forward computes it
-                # with the QK norms, one wavefront per (token, head)
-                b, t = proj_w(L[n], L[n + "_dtype"], *shapes[n], tile=n != "attn_gate")
+                b, t = proj_w(L[n], L[n + "_dtype"], *shapes[n])
                 setattr(d, n, b.ptr)
                 setattr(d, n + "_type", t)
         self._desc = _Model()
