@@ -207,8 +207,9 @@ uint64_t lg_proj_quant_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int w_
  *     piece p][row r] (row r's bytes 32g+8p .. 32g+8p+7 at 256 + 512g + 128p + 8r).
  *   LG_Q8_0_T16 tile (4352 bytes, blocks 8c..8c+7): the 16 rows' 8 f16 scales
  *     (row r, block j at 16r + 2j), then the quants as [block j][8-byte piece p]
- *     [row r] (row r's quants 8p .. 8p+7 of block j at 256 + 512j + 128p + 8r).
- * The repack is a byte permutation, and the products over tiled weights
+ *     [row r] (row r's quants 8p .. 8p+7 of block j at 256 + 512j + 128p + 8r),
+ *     each biased to unsigned (q XOR 0x80, as the products take them).
+ * The repack is a byte permutation (and that bias), and the products over tiled weights
  * (lg_dispatch_proj_quant_batch, lg_dispatch_silu_gate_up_batch, the draft
  * forward) equal those over the raw blocks bit for bit; a workgroup then reads
  * whole tiles instead of short pieces of rows that lie a row apart.  dtype

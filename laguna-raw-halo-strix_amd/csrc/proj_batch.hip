@@ -815,7 +815,7 @@ __device__ __forceinline__ void q4k_chunk(const uint4 *lds, const Q4kChunk<RT> &
 
 // One Q8_0 chunk: a_j = 2^24 d_j, bias coefficients -128 d_j of blocks kg, kg + 4.
 // Per pair of blocks, the products are issued before the scale multiplications.
-template <int TT, int RT>
+template <int TT, int RT, bool BIASED>
 __device__ __forceinline__ void q80_chunk(const uint4 *lds, const Q80Chunk<RT> &W, float (&acc)[RT][TT][4]) {
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
     float a[RT][8], cm[RT][2];
@@ -846,7 +846,9 @@ __device__ __forceinline__ void q80_chunk(const uint4 *lds, const Q80Chunk<RT> &
         for (int i = 0; i < RT; i++)
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t v0 = W.qv[i][2 * jp + u].x ^ 0x80808080u, v1 = W.qv[i][2 * jp + u].y ^ 0x80808080u;
+                // BIASED (tiles): the quants are stored as q + 128 already
+                const uint32_t bias = BIASED ? 0u : 0x80808080u;
+                const uint32_t v0 = W.qv[i][2 * jp + u].x ^ bias, v1 = W.qv[i][2 * jp + u].y ^ bias;
                 B[i][u] = as_f16x8(v0 & LO8, (v0 >> 8) & LO8, v1 & LO8, (v1 >> 8) & LO8);
             }
         mma_pair<TT, RT>(A, B, a, 2 * jp, jp > 0, tmp);
@@ -923,9 +925,9 @@ __device__ __forceinline__ void mm_body(const void *x, const float *up, const Mm
         } else if constexpr (RAW8) {
             Q80Chunk<RT> Ws;
             stage_q80<RT>(Wk, Ws, lstage + wave * SPW);
-            q80_chunk<TT, RT>(rec, Ws, acc);
+            q80_chunk<TT, RT, false>(rec, Ws, acc);
         } else {
-            q80_chunk<TT, RT>(rec, Wk, acc);
+            q80_chunk<TT, RT, TILED>(rec, Wk, acc);
         }
     };
     chunk(lrec[0], Wc[0]);
@@ -1400,7 +1402,9 @@ __global__ __launch_bounds__(256) void k_repack_q80_t16(const uint8_t *__restric
         const bool live = row < n;
         const uint16_t *src = reinterpret_cast<const uint16_t *>(w + (uint64_t)(live ? row : n - 1) * rowb +
                                                                  (uint64_t)(8 * c + j) * Q80_BYTES + 2 + 8 * q);
-        const uint2 v = make_uint2(src[0] | ((uint32_t)src[1] << 16), src[2] | ((uint32_t)src[3] << 16));
+        // quants biased to unsigned (q + 128 = q XOR 0x80), as the products take them
+        const uint2 v = make_uint2((src[0] | ((uint32_t)src[1] << 16)) ^ 0x80808080u,
+                                   (src[2] | ((uint32_t)src[3] << 16)) ^ 0x80808080u);
         *reinterpret_cast<uint2 *>(tile + 256 + 8 * p) = live ? v : make_uint2(0u, 0u);
     }
     if (threadIdx.x < 128) {

@@ -196,10 +196,12 @@ def tile_q4k(raw, k, n):
 
 def tile_q80(raw, k, n):
     """The LG_Q8_0_T16 layout restated in numpy: tile (t, c) = the 16 rows' 8 f16
-    scales (row-major), then quants [block j][piece p][row r]."""
+    scales (row-major), then quants [block j][piece p][row r], biased to unsigned
+    (q + 128 = q XOR 0x80); rows past n are zero bytes."""
     nc, nt = k // 256, -(-n // 16)
     blocks = np.zeros((nt * 16, nc, 8, 34), np.uint8)
     blocks[:n] = np.frombuffer(np.ascontiguousarray(raw).tobytes(), np.uint8).reshape(n, nc, 8, 34)
+    blocks[:n, :, :, 2:] ^= 0x80
     blocks = blocks.reshape(nt, 16, nc, 8, 34).transpose(0, 2, 1, 3, 4)  # [t][c][r][j][34]
     sc = blocks[..., :2].reshape(nt, nc, 256)
     q = blocks[..., 2:].reshape(nt, nc, 16, 8, 4, 8).transpose(0, 1, 3, 4, 2, 5).reshape(nt, nc, 4096)
