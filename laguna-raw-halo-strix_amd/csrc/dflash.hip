@@ -30,8 +30,60 @@ namespace {
 using namespace lg;
 
 
-typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// f16 parts of f32 values: hi = x rounded to f16 (nearest even), lo = x - hi rounded
+// to f16.  hi + lo holds x to about 22 bits while 2^-3 <= |x| < 65504 (below that lo
+// is subnormal: absolute error at most 2^-25).  x - hi is one v_fma_mix_f32 (hi's half
+// as an f16 operand of an f32 fma, exact), which the compiler forms from fma(hi, neg1,
+// x) only while it cannot fold neg1 = -1 into a subtraction: callers pass -1.0f from
+// neg_one().
+__device__ __forceinline__ float neg_one() {
+    float v = -1.0f;
+    asm("" : "+s"(v));  // no instruction: hides the constant from the optimizer
+    return v;
+}
+__device__ __forceinline__ void f16_parts2(float a, float b, float neg1, uint32_t &hi, uint32_t &lo) {
+    const f16x2 h = __builtin_convertvector((f32x2){a, b}, f16x2);
+    const f32x2 d = {__builtin_fmaf((float)h[0], neg1, a), __builtin_fmaf((float)h[1], neg1, b)};
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, f16x2));
+}
+__device__ __forceinline__ void f16_parts8(const float4 &a, const float4 &b, float neg1, f16x8 &hi, f16x8 &lo) {
+    uint4 h, l;
+    f16_parts2(a.x, a.y, neg1, h.x, l.x);
+    f16_parts2(a.z, a.w, neg1, h.y, l.y);
+    f16_parts2(b.x, b.y, neg1, h.z, l.z);
+    f16_parts2(b.z, b.w, neg1, h.w, l.w);
+    hi = __builtin_bit_cast(f16x8, h);
+    lo = __builtin_bit_cast(f16x8, l);
+}
+__device__ __forceinline__ void f16_parts4(float a, float b, float c, float d, float neg1, f16x4 &hi,
+                                           f16x4 &lo) {
+    uint2 h, l;
+    f16_parts2(a, b, neg1, h.x, l.x);
+    f16_parts2(c, d, neg1, h.y, l.y);
+    hi = __builtin_bit_cast(f16x4, h);
+    lo = __builtin_bit_cast(f16x4, l);
+}
+// max(acc, |x|) over the eight values of a and b: v_max3_f32 with |x| operands (as
+// asm, since fmaxf would first quiet every operand; a NaN operand may give NaN, and
+// callers treat a NaN maximum as out of range)
+__device__ __forceinline__ float absmax3(float acc, float a, float b) {
+    float d;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(d) : "v"(acc), "v"(a), "v"(b));
+    return d;
+}
+__device__ __forceinline__ float absmax8(float acc, const float4 &a, const float4 &b) {
+    acc = absmax3(acc, a.x, a.y);
+    acc = absmax3(acc, a.z, a.w);
+    acc = absmax3(acc, b.x, b.y);
+    return absmax3(acc, b.z, b.w);
+}
 
 
 // Sum over the threads of a workgroup of THREADS; every thread receives it.
@@ -739,16 +791,22 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
 // Many queries (rows * G > ADQ), one launch.  Workgroup (kv head h, query group qg,
 // chunk c) takes queries 16 qg .. 16 qg + 15 of kv head h (query qi: row qi / G, q head
 // h G + qi % G) over chunk c of the sequence's 16-position tiles, its wavefront w the
-// tiles tb + w, tb + w + 4, ...  K and V stream from memory straight into f32 matrix
-// products (v_mfma_f32_16x16x4_f32), whose k index runs over dims / positions in the
-// order the lanes load them:
+// tiles tb + w, tb + w + 4, ...  K and V stream from memory straight into matrix
+// products, whose k index runs over dims / positions in the order the lanes load them:
 //   S^T = K Q^T   A = K: lane (position l16, kg) holds dims 16b + 4kg .. +3 of its row
-//                 in one float4 for the four k steps of block b; B = Q^T likewise;
+//                 in one float4 (kr[b]); B = Q^T likewise;
 //   P = exp(S - running max) per query (lane l16's query, four positions per lane);
 //   O^T += V^T P^T  A = V^T: lane (l16, kg) loads dims 64hh + 4 l16 .. +3 of position
 //                 4kg + s, and component cc feeds output tile 4hh + cc (dim 64hh + 4i
 //                 + cc of its row i); B = P^T, the lane's own probabilities.
-// No LDS for K and V, no bf16 parts: every product is an f32 fma.  The four wavefronts
+// Each product is three f16 matrix products over the operands' f16 parts, hi hi + hi lo
+// + lo hi (f16_parts2: every f16 product is exact in f32, and the dropped lo lo is below
+// 2^-21 of hi hi): S on v_mfma_f32_16x16x32_f16 (blocks 2j, 2j + 1 of kr form the eight
+// halves of k step j), P V on v_mfma_f32_16x16x16f16 (halves s = 0..3: positions 4kg +
+// s).  A tile whose K or V (or a query) has a magnitude f16 cannot hold, or whose V is
+// all below 2^-4 (where lo's subnormal floor would show), takes that product in f32 on
+// v_mfma_f32_16x16x4f32 instead (k steps over the same lanes' values).  No LDS for K
+// and V.  The four wavefronts
 // meet in LDS (one partial per workgroup), the partial goes to the workspace, and the
 // last workgroup of the (h, qg) group to arrive merges the chunks in chunk order,
 // applies the gate and writes the result.  Workgroups sharing (h, c) sit on one XCD
@@ -815,16 +873,28 @@ __global__ __launch_bounds__(256) void k_attn_split(SplitAttn a) {
             }
     };
     // the lane's query: dims 16b + 4kg .. +3 in qf[b] (a dead query column reads the
-    // group's first query; its scores are masked)
+    // group's first query; its scores are masked).  Once the first tiles' loads are
+    // issued it is held as f16 parts (k step j: blocks 2j, 2j + 1), used while every
+    // query of the wavefront lies in f16's range; the f32 products read it again.
     const uint32_t qi = AQG * qg + l16;
     const bool qlive = qi < nq;
     const uint32_t qc = qlive ? qi : AQG * qg, qt = qc / G, qpos = a.qpos0 + qt;
+    const float *qp = a.q + (uint64_t)qt * a.n_q * AHD + (h * G + qc % G) * AHD + 4 * kg;
     float4 qf[8];
-    {
-        const float *qp = a.q + (uint64_t)qt * a.n_q * AHD + (h * G + qc % G) * AHD + 4 * kg;
 #pragma unroll
-        for (int b = 0; b < 8; b++) qf[b] = *reinterpret_cast<const float4 *>(qp + 16 * b);
-    }
+    for (int b = 0; b < 8; b++) qf[b] = *reinterpret_cast<const float4 *>(qp + 16 * b);
+    const float neg1 = neg_one();
+    f16x8 qh[4], ql[4];
+    bool q16 = true;
+    auto split_q = [&]() {
+        float qmx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            f16_parts8(qf[2 * j], qf[2 * j + 1], neg1, qh[j], ql[j]);
+            qmx = absmax8(qmx, qf[2 * j], qf[2 * j + 1]);
+        }
+        q16 = !__builtin_amdgcn_ballot_w64(!(qmx < 65504.0f));
+    };
     const uint32_t nt = (a.S + 15) / 16, tb = attn_tile0(c, nt, a.nch), te = attn_tile0(c + 1, nt, a.nch);
     const uint32_t nmine = te > tb + wave ? (te - tb - wave + 3) / 4 : 0;
     const uint32_t tlast = tb + wave + 4 * (nmine ? nmine - 1 : 0);  // the wavefront's last tile
@@ -856,14 +926,30 @@ __global__ __launch_bounds__(256) void k_attn_split(SplitAttn a) {
     // unconditional (past the wavefront's last tile: the last tile again), so that
     // each product waits for its own operands only.
     auto tile_step = [&](float4 (&kr)[8], float4 (&vr)[8], uint32_t tile, uint32_t next) {
-        f32x4 sc[4];  // four independent chains over the blocks b, b + 4 (b mod 4)
+        f32x4 sc[4];  // four independent chains
 #pragma unroll
         for (int j = 0; j < 4; j++) sc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        float kmx = 0.0f;
 #pragma unroll
-        for (int b = 0; b < 8; b++)
+        for (int b = 0; b < 8; b += 2) kmx = absmax8(kmx, kr[b], kr[b + 1]);
+        if (q16 && !__builtin_amdgcn_ballot_w64(!(kmx < 65504.0f))) {
 #pragma unroll
-            for (int s = 0; s < 4; s++)
-                sc[b & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(kr[b], s), f4c(qf[b], s), sc[b & 3], 0, 0, 0);
+            for (int j = 0; j < 4; j++) {  // chain j: k step j, the small products first
+                f16x8 kh, kl;
+                f16_parts8(kr[2 * j], kr[2 * j + 1], neg1, kh, kl);
+                sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[j], sc[j], 0, 0, 0);
+                sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[j], sc[j], 0, 0, 0);
+                sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[j], sc[j], 0, 0, 0);
+            }
+        } else {  // chain b mod 4: blocks b, b + 4
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const float4 qb = *reinterpret_cast<const float4 *>(qp + 16 * b);
+#pragma unroll
+                for (int s = 0; s < 4; s++)
+                    sc[b & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(kr[b], s), f4c(qb, s), sc[b & 3], 0, 0, 0);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
         load_k(kr, next);
         __builtin_amdgcn_sched_barrier(0);
@@ -891,14 +977,34 @@ __global__ __launch_bounds__(256) void k_attn_split(SplitAttn a) {
             pv[i] = __builtin_amdgcn_exp2f(sv[i] - mu);
             lsum += pv[i];
         }
+        float vmx = 0.0f;
 #pragma unroll
-        for (int s = 0; s < 4; s++)
+        for (int b = 0; b < 8; b += 2) vmx = absmax8(vmx, vr[b], vr[b + 1]);
+        if (!__builtin_amdgcn_ballot_w64(!(vmx < 65504.0f)) && __builtin_amdgcn_ballot_w64(vmx >= 0.0625f)) {
+            f16x4 ph, pl;
+            f16_parts4(pv[0], pv[1], pv[2], pv[3], neg1, ph, pl);
 #pragma unroll
             for (int hh = 0; hh < 2; hh++)
 #pragma unroll
-                for (int cc = 0; cc < 4; cc++)
-                    Od[4 * hh + cc] =
-                        __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(vr[2 * s + hh], cc), pv[s], Od[4 * hh + cc], 0, 0, 0);
+                for (int cc = 0; cc < 4; cc++) {
+                    f16x4 vh, vl;
+                    f16_parts4(f4c(vr[hh], cc), f4c(vr[2 + hh], cc), f4c(vr[4 + hh], cc), f4c(vr[6 + hh], cc),
+                               neg1, vh, vl);
+                    f32x4 &o = Od[4 * hh + cc];
+                    o = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph, o, 0, 0, 0);
+                    o = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl, o, 0, 0, 0);
+                    o = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph, o, 0, 0, 0);
+                }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                    for (int cc = 0; cc < 4; cc++)
+                        Od[4 * hh + cc] = __builtin_amdgcn_mfma_f32_16x16x4f32(f4c(vr[2 * s + hh], cc), pv[s],
+                                                                              Od[4 * hh + cc], 0, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
         load_v(vr, next);
         __builtin_amdgcn_sched_barrier(0);
@@ -914,6 +1020,7 @@ __global__ __launch_bounds__(256) void k_attn_split(SplitAttn a) {
         load_k(kb, tile_at(1));
         load_v(vb, tile_at(1));
         __builtin_amdgcn_sched_barrier(0);
+        split_q();
         gate_units();  // its loads after the first tiles'
         for (uint32_t i = 0; i < nmine; i += 2) {
             tile_step(ka, va, t0 + 4 * i, tile_at(i + 2));

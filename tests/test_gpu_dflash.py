@@ -129,6 +129,35 @@ def test_mha_attn(ctx, n_q, n_kv, hd, rows, S, q_pos, causal):
     check("mha_attn", ob.read_f32(q.size).reshape(rows, -1), want, TOL_ATTN)
 
 
+# The many-query kernel multiplies f16 parts of its operands; a tile whose values f16
+# cannot hold takes f32 products.  Each case plants a value that the f16 parts would
+# turn into inf (times a zero operand: NaN) or, for a V of small magnitude, into an
+# error far above the tolerance.
+@pytest.mark.parametrize("case", ["k_wide", "q_wide", "v_wide", "v_small"])
+def test_mha_attn_f16_range(ctx, case):
+    n_q, n_kv, hd, rows, S, q_pos = 32, 8, 128, 16, 300, 280
+    print(f"mha_attn f16 range: {case}", flush=True)
+    q = synth.normal(0x5EED020B, rows * n_q * hd).reshape(rows, n_q, hd)
+    K = synth.normal(0x5EED020C, S * n_kv * hd).reshape(S, n_kv, hd)
+    V = synth.normal(0x5EED020D, S * n_kv * hd).reshape(S, n_kv, hd)
+    if case == "k_wide":  # dim 5 of every query is zero
+        q[:, :, 5] = 0.0
+        K[37, 2, 5] = 7.0e4
+    elif case == "q_wide":  # dim 9 of every key is zero
+        K[:, :, 9] = 0.0
+        q[3, 9, 9] = 7.0e4
+    elif case == "v_wide":  # position 299 is past every row's causal limit (p = 0)
+        V[299, 1, 17] = 7.0e4
+    else:
+        V *= np.float32(2.0 ** -12)
+    q, K, V = q.reshape(rows, -1), K.reshape(S, -1), V.reshape(S, -1)
+    qb, kb, vb, ob = (lh.upload_f32(ctx, q), lh.upload_f32(ctx, K), lh.upload_f32(ctx, V),
+                      lh.GpuBuffer(ctx, q.nbytes))
+    lh.dispatch_mha_attn_seq(ctx, qb, kb, vb, ob, n_q, n_kv, hd, S, q_pos, rows=rows, causal=1)
+    want = dfo.attention(q, K, V, q_pos + np.arange(rows), n_q, n_kv, hd, causal=True)
+    check("mha_attn " + case, ob.read_f32(q.size).reshape(rows, -1), want, TOL_ATTN)
+
+
 def test_gates_and_add(ctx):
     rows, H, hd = 16, 32, 128
     print("gate_mul / softplus_gate_mul / add", flush=True)
