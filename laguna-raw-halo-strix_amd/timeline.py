@@ -61,11 +61,6 @@ STAMPS = {
         ("before", "    const uint32_t nt = (a.S + 15) / 16, tb = attn_tile0(c, nt, a.nch)", "    TS(1);\n"),
         ("before", "        for (uint32_t i = 0; i < nmine; i += 2) {", "        TS(2);\n"),
         ("before", "    lsum = lane_add_x32(lane_add_x16(lsum));", "    TS(3);\n"),
-        ("before", "    auto tile_step = [&]", "    uint32_t tl_i = 0;\n"),
-        ("after", "        load_k(kr, next);\n        __builtin_amdgcn_sched_barrier(0);",
-         "\n        if (tl_i < 6) TS(8 + 2 * tl_i);"),
-        ("after", "        load_v(vr, next);\n        __builtin_amdgcn_sched_barrier(0);",
-         "\n        if (tl_i < 6) TS(9 + 2 * tl_i);\n        tl_i++;"),
         ("before", "    // thread (query mq, dims md .. md + ", "    TS(4);\n"),
         ("before", "    // the last workgroup of the group to arrive merges", "    TS(5);\n"),
         ("after", "if (!arrive_last(a.cnt + grp, a.nch, &last)) return;", "\n    TS(6);"),
@@ -84,9 +79,6 @@ PHASES = {
     "mm": [(0, "start"), (1, "chunk 0's activations in LDS"), (2, "chunk 1 in LDS"), (3, "chunk 2 in LDS"),
            (4, "chunk 3 in LDS"), (36, "products done"), (38, "split-k finish done")],
     "attn": [(0, "start"), (1, "queries issued"), (2, "first tile issued, gate units done"),
-             (8, "tile 0: S done, K refill issued"), (9, "tile 0: P V done, V refill issued"),
-             (10, "tile 1: S"), (11, "tile 1: P V"), (12, "tile 2: S"), (13, "tile 2: P V"),
-             (14, "tile 3: S"), (15, "tile 3: P V"), (16, "tile 4: S"), (17, "tile 4: P V"),
              (3, "tiles done"), (4, "wavefronts met in LDS"), (5, "partial stored"), (6, "last to arrive"),
              (7, "chunks merged"), (20, "combine: start"), (21, "tail / gate"), (22, "chunk partials merged"),
              (23, "waves met in LDS"), (24, "result")],
