@@ -8,8 +8,12 @@ last call (ns from the first wavefront's start), and how the workgroups spread o
 The shipped library is not touched; the instrumented one is built into _timeline/
 (each wavefront's lane 0 stores its stamps with ordinary vector stores).
 
-    python timeline.py build
+    python timeline.py build [--tiles]
     python timeline.py run WORKLOAD [mm|attn]
+
+`--tiles` adds stamps inside the attention's tile loop (after each tile's scores and
+after its P V, each with the next tile's loads issued); they slow that kernel by about
+a quarter, so its other phases read best from a build without them.
 
 `mm` reads the last small-M product launch (k_mm_mf) of the workload, `attn` the last k_attn_split launch
 (the draft block's last layer), or the last combine launch of the few-query path.
@@ -75,10 +79,23 @@ STAMPS = {
     ]),
 }
 
+# the attention's per-tile stamps (build --tiles): slot 8 + 2i after tile i's scores and
+# K loads, 9 + 2i after its P V and V loads
+TILE_STAMPS = [
+    ("before", "    auto tile_step = [&]", "    uint32_t tl_i = 0;\n"),
+    ("after", "        load_k(kr, next);\n        __builtin_amdgcn_sched_barrier(0);",
+     "\n        if (tl_i < 6) TS(8 + 2 * tl_i);"),
+    ("after", "        load_v(vr, next);\n        __builtin_amdgcn_sched_barrier(0);",
+     "\n        if (tl_i < 6) TS(9 + 2 * tl_i);\n        tl_i++;"),
+]
+
 PHASES = {
     "mm": [(0, "start"), (1, "chunk 0's activations in LDS"), (2, "chunk 1 in LDS"), (3, "chunk 2 in LDS"),
            (4, "chunk 3 in LDS"), (36, "products done"), (38, "split-k finish done")],
     "attn": [(0, "start"), (1, "queries issued"), (2, "first tile issued, gate units done"),
+             (8, "tile 0: scores, K refill issued"), (9, "tile 0: P V, V refill issued"),
+             (10, "tile 1: scores"), (11, "tile 1: P V"), (12, "tile 2: scores"), (13, "tile 2: P V"),
+             (14, "tile 3: scores"), (15, "tile 3: P V"), (16, "tile 4: scores"), (17, "tile 4: P V"),
              (3, "tiles done"), (4, "wavefronts met in LDS"), (5, "partial stored"), (6, "last to arrive"),
              (7, "chunks merged"), (20, "combine: start"), (21, "tail / gate"), (22, "chunk partials merged"),
              (23, "waves met in LDS"), (24, "result")],
@@ -95,7 +112,7 @@ def instrument(src, sig, edits):
     return s
 
 
-def build():
+def build(tiles=False):
     os.makedirs(OUT, exist_ok=True)
     csrc = os.path.join(HERE, "csrc")
     flags = ["-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature",
@@ -109,7 +126,7 @@ def build():
         if f in ("proj_batch.hip", "dflash.hip"):
             for key, (sig, edits) in STAMPS.items():
                 if key.split("#")[0] == f:
-                    src = instrument(src, sig, edits)
+                    src = instrument(src, sig, edits + (TILE_STAMPS if tiles and key == "dflash.hip" else []))
             i = src.index("namespace {")
             tag = "mm" if f == "proj_batch.hip" else "attn"
             src = src[:i] + HEADER % {"f": tag, "n": SLOTS * WAVES, "w": WAVES, "s": SLOTS} + src[i:]
@@ -193,12 +210,13 @@ def run(workload, what):
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
-    sub.add_parser("build")
+    b = sub.add_parser("build")
+    b.add_argument("--tiles", action="store_true")
     r = sub.add_parser("run")
     r.add_argument("workload")
     r.add_argument("what", nargs="?", default="mm", choices=["mm", "attn"])
     a = ap.parse_args()
-    build() if a.cmd == "build" else run(a.workload, a.what)
+    build(a.tiles) if a.cmd == "build" else run(a.workload, a.what)
 
 
 if __name__ == "__main__":
