@@ -813,27 +813,6 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
 // (workgroup ids 8 apart) so that their K and V reads meet in its L2.
 constexpr uint32_t AQG = 16;  // queries per workgroup of k_attn_split
 
-// 16- and 8-byte loads and stores coherent across the device (sc1: every XCD's L2
-// sees them), for the partials that one workgroup writes and another merges.
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-constexpr int CPOL_SC1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), 0, 0x7FFFFFFF, 0x00020000);
-}
-__device__ __forceinline__ float4 dev_ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SC1));
-}
-__device__ __forceinline__ float2 dev_ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL_SC1));
-}
-__device__ __forceinline__ void dev_st4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, CPOL_SC1);
-}
-__device__ __forceinline__ void dev_st2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float2 v) {
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, byte_off, 0, CPOL_SC1);
-}
-
 struct SplitAttn {
     const float *q, *k0, *v0, *k1, *v1;
     uint32_t n0, S, rows, n_q, n_kv, qpos0, ngq, nch;

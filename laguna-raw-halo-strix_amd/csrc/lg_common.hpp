@@ -91,11 +91,33 @@ int stream_buffer(int purpose, hipStream_t s, uint64_t need, BufLease &lease, co
 // zero.
 int stream_workspace(hipStream_t s, uint64_t need, void **out);
 
+// 16- and 8-byte loads and stores coherent across the device (sc1: written through to,
+// and read from, the device's coherence point), for partial results that one
+// workgroup writes and another reads back; buffer offsets in bytes, below 2^31.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const float *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), 0, 0x7FFFFFFF, 0x00020000);
+}
+__device__ __forceinline__ float4 dev_ld4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ float2 dev_ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ void dev_st4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void dev_st2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, byte_off, 0, CPOL_SC1);
+}
+
 // Split-k arrival, called by every thread of a (one-dimensional) workgroup after it
-// has stored its partial results with device-coherent atomic stores (relaxed, agent
-// scope: written through to the device's coherence point).  True in every thread of
-// the last workgroup to arrive at *cnt (of `total`), which resets the counter; that
-// workgroup reads the partial results back with device-coherent atomic loads.  Each
+// has stored its partial results with device-coherent stores (dev_st4, or relaxed
+// agent-scope atomics: written through to the device's coherence point).  True in
+// every thread of the last workgroup to arrive at *cnt (of `total`), which resets the
+// counter; that workgroup reads the partial results back with device-coherent loads.  Each
 // wave waits for its own stores to complete (vmcnt 0, in an asm statement with a
 // memory clobber, so the compiler keeps every store before it) before the barrier
 // that precedes the arrival, so every partial result is at the coherence point

@@ -251,22 +251,19 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
                                        uint32_t bx, const float *qkw) {
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4;
     const uint32_t S = gridDim.y, s = blockIdx.y;
-    const uint64_t mn = (uint64_t)m * n;
+    // split k: the column's partials, [slice][wavefront][RT][TT][lane] float4 (the lane's
+    // four tokens of one row), each wavefront's as it holds them, in device-coherent
+    // 16-byte stores and loads (mm_part_floats)
+    constexpr uint32_t WB = RT * TT * 256;  // floats of one wavefront's partial
+    const uint32_t pw = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t rp = dev_rsrc(part + (uint64_t)bx * S * 4 * WB);
+    auto poff = [&](uint32_t q, int i, int t) { return 4u * ((q * 4 + pw) * WB + (i * TT + t) * 256 + 4 * l); };
     if (S > 1) {
-        float *ps = part + s * mn;
 #pragma unroll
-        for (int i = 0; i < RT; i++) {
-            const uint32_t row = (rt0 + i) * 16 + (l & 15u);
+        for (int i = 0; i < RT; i++)
 #pragma unroll
             for (int t = 0; t < TT; t++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint32_t tok = t * 16 + 4 * kg + r;
-                    if (row < n && tok < m)
-                        __hip_atomic_store(ps + (uint64_t)tok * n + row, acc[i][t][r], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
-        }
+                dev_st4(rp, poff(s, i, t), make_float4(acc[i][t][0], acc[i][t][1], acc[i][t][2], acc[i][t][3]));
         // the last workgroup of the column to arrive adds the slices
         __shared__ uint32_t last;
         if (!arrive_last(&cnt[blockIdx.x], S, &last)) return;
@@ -286,23 +283,14 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
 #pragma unroll
             for (int r = 0; r < 4; r++) v[i][t][r] = S > 1 ? 0.0f : acc[i][t][r];
     for (uint32_t q0 = 0; q0 < (S > 1 ? S : 0u); q0 += G) {
-        float pv[G][RT][TT][4];
+        float4 pv[G][RT][TT];
 #pragma unroll
         for (uint32_t g = 0; g < G; g++) {
             const uint32_t q = q0 + g < S ? q0 + g : S - 1;
 #pragma unroll
-            for (int i = 0; i < RT; i++) {
-                const uint32_t row = (rt0 + i) * 16 + (l & 15u);
-                const uint32_t rowc = row < n ? row : n - 1;
+            for (int i = 0; i < RT; i++)
 #pragma unroll
-                for (int t = 0; t < TT; t++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const uint32_t tok = t * 16 + 4 * kg + r;
-                        pv[g][i][t][r] = __hip_atomic_load(part + q * mn + (uint64_t)(tok < m ? tok : m - 1) * n + rowc,
-                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-            }
+                for (int t = 0; t < TT; t++) pv[g][i][t] = dev_ld4(rp, poff(q, i, t));
         }
 #pragma unroll
         for (uint32_t g = 0; g < G; g++)
@@ -310,8 +298,12 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
             for (int i = 0; i < RT; i++)
 #pragma unroll
                 for (int t = 0; t < TT; t++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) v[i][t][r] += q0 + g < S ? pv[g][i][t][r] : 0.0f;
+                    if (q0 + g < S) {
+                        v[i][t][0] += pv[g][i][t].x;
+                        v[i][t][1] += pv[g][i][t].y;
+                        v[i][t][2] += pv[g][i][t].z;
+                        v[i][t][3] += pv[g][i][t].w;
+                    }
     }
     if constexpr (NORM) {
         __shared__ float rsl[TT * 16];
@@ -1153,6 +1145,14 @@ MmShape launch_shape(int w_dtype, uint32_t k, const uint32_t *n, uint32_t jobs, 
     return mm_shape(w_dtype, k, glu ? n[0] : (uint32_t)ntot, ml, glu, qk, epi);
 }
 
+// Floats of one job's split-k partials (finish): per workgroup column and slice, four
+// wavefronts' RT x TT tiles of 256 values (columns of 64 RT rows, or 32 RT for a gate/up
+// pair, whose two jobs share the columns).
+uint64_t mm_part_floats(uint32_t n, uint32_t ml, uint32_t rt, uint32_t slices, bool glu) {
+    const uint32_t per = (glu ? 32u : 64u) * rt, cols = (n + per - 1) / per, tt = (ml + 15) / 16;
+    return (uint64_t)slices * cols * 4 * rt * tt * 256;
+}
+
 }  // namespace
 
 namespace lg {
@@ -1167,7 +1167,7 @@ static uint64_t multi_ws_bytes(uint32_t k, const uint32_t *n, uint32_t jobs, uin
     const MmShape sh = launch_shape(w_dtype, k, n, jobs, ml, glu, qk, epi);
     uint64_t b = CNT_BYTES;
     if (sh.slices > 1)
-        for (uint32_t j = 0; j < jobs; j++) b += align256((uint64_t)sh.slices * ml * n[j] * 4);
+        for (uint32_t j = 0; j < jobs; j++) b += align256(mm_part_floats(n[j], ml, sh.rt, sh.slices, glu) * 4);
     return b;
 }
 
@@ -1313,7 +1313,7 @@ int proj_batch_multi(const void *x, int x_dtype, const float *up, const BatchJob
             const uint32_t tlo = tt == 2 && !glu && xm == 0 && !jb[j].ss && jb[j].row0 >= 16 * t0 + 16 ? 1u : 0u;
             jobs.j[j] = {static_cast<const uint8_t *>(jb[j].w), jb[j].c + off, jb[j].res ? jb[j].res + off : nullptr,
                          reinterpret_cast<float *>(pb), jb[j].y, jb[j].yw, jb[j].ss, jb[j].n, groups, jb[j].qkw, tlo};
-            if (sh.slices > 1) pb += align256((uint64_t)sh.slices * ml * jb[j].n * 4);
+            if (sh.slices > 1) pb += align256(mm_part_floats(jb[j].n, ml, sh.rt, sh.slices, glu) * 4);
             groups += (jb[j].n + 64 * sh.rt - 1) / (64 * sh.rt);
         }
         if (glu) {  // both products in every workgroup column

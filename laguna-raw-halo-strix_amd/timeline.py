@@ -8,8 +8,12 @@ last call (ns from the first wavefront's start), and how the workgroups spread o
 The shipped library is not touched; the instrumented one is built into _timeline/
 (each wavefront's lane 0 stores its stamps with ordinary vector stores).
 
-    python timeline.py build [--tiles]
+    python timeline.py build [--tiles] [--mm-if CONDITION]
     python timeline.py run WORKLOAD [mm|attn]
+
+`--mm-if` keeps the small-M product's stamps to the instances whose template parameters
+satisfy CONDITION (C++ over Q4, TT, RT, GLU, NORM, TILED, XM; e.g. "NORM && !GLU", the draft's
+K/V/Q launch), so that `run ... mm` reads that launch rather than the workload's last product.
 
 `--tiles` adds stamps inside the attention's tile loop (after each tile's scores and
 after its P V, each with the next tile's loads issued); they slow that kernel by about
@@ -41,12 +45,13 @@ extern "C" int lg_timeline_clear_%(f)s() {
     return hipMemcpyToSymbol(HIP_SYMBOL(lg_tl_%(f)s), z, sizeof(z)) == hipSuccess ? 0 : 1;
 }
 #define LG_WID() (((blockIdx.y * gridDim.x) + blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6))
-#define TS(k) do { const unsigned long long t_ = __builtin_amdgcn_s_memrealtime(); \
-    if ((threadIdx.x & 63u) == 0 && LG_WID() < %(w)du) lg_tl_%(f)s[LG_WID() * %(s)d + (k)] = t_; } while (0)
-#define TSID() do { unsigned hw_, xc_; asm volatile("s_getreg_b32 %%0, hwreg(HW_REG_HW_ID)" : "=s"(hw_)); \
+#define TS(k) do { if constexpr (%(cond)s) { const unsigned long long t_ = __builtin_amdgcn_s_memrealtime(); \
+    if ((threadIdx.x & 63u) == 0 && LG_WID() < %(w)du) lg_tl_%(f)s[LG_WID() * %(s)d + (k)] = t_; } } while (0)
+#define TSID() do { if constexpr (%(cond)s) { unsigned hw_, xc_; \
+    asm volatile("s_getreg_b32 %%0, hwreg(HW_REG_HW_ID)" : "=s"(hw_)); \
     asm volatile("s_getreg_b32 %%0, hwreg(HW_REG_XCC_ID)" : "=s"(xc_)); \
     if ((threadIdx.x & 63u) == 0 && LG_WID() < %(w)du) \
-        lg_tl_%(f)s[LG_WID() * %(s)d + %(s)d - 1] = ((unsigned long long)xc_ << 32) | hw_; } while (0)
+        lg_tl_%(f)s[LG_WID() * %(s)d + %(s)d - 1] = ((unsigned long long)xc_ << 32) | hw_; } } while (0)
 '''
 
 # (file, kernel signature start, [(mode, marker, text)]): text goes after / before the
@@ -112,7 +117,7 @@ def instrument(src, sig, edits):
     return s
 
 
-def build(tiles=False):
+def build(tiles=False, mm_if="true"):
     os.makedirs(OUT, exist_ok=True)
     csrc = os.path.join(HERE, "csrc")
     flags = ["-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature",
@@ -129,7 +134,8 @@ def build(tiles=False):
                     src = instrument(src, sig, edits + (TILE_STAMPS if tiles and key == "dflash.hip" else []))
             i = src.index("namespace {")
             tag = "mm" if f == "proj_batch.hip" else "attn"
-            src = src[:i] + HEADER % {"f": tag, "n": SLOTS * WAVES, "w": WAVES, "s": SLOTS} + src[i:]
+            cond = mm_if if tag == "mm" else "true"
+            src = src[:i] + HEADER % {"f": tag, "n": SLOTS * WAVES, "w": WAVES, "s": SLOTS, "cond": cond} + src[i:]
         path = os.path.join(OUT, f)
         open(path, "w").write(src)
         obj = path + ".o"
@@ -139,7 +145,7 @@ def build(tiles=False):
     print("built", LIB)
 
 
-def run(workload, what):
+def run(workload, what, dump=None):
     sys.path.insert(0, HERE)
     sys.path.insert(0, os.path.join(HERE, ".."))
     import numpy as np
@@ -167,6 +173,8 @@ def run(workload, what):
     buf = np.zeros(SLOTS * WAVES, np.uint64)
     lh.check(read(buf.ctypes.data, buf.nbytes))
     ts = buf.reshape(WAVES, SLOTS)
+    if dump:
+        np.save(dump, ts)
     live = (ts[:, 0] > 0) | (ts[:, 20] > 0)
     n = int(np.nonzero(live)[0].max()) + 1
     T = ts[:n, :SLOTS - 1].astype(np.int64)
@@ -212,11 +220,13 @@ def main():
     sub = ap.add_subparsers(dest="cmd", required=True)
     b = sub.add_parser("build")
     b.add_argument("--tiles", action="store_true")
+    b.add_argument("--mm-if", default="true")
     r = sub.add_parser("run")
     r.add_argument("workload")
     r.add_argument("what", nargs="?", default="mm", choices=["mm", "attn"])
+    r.add_argument("--dump", help="also save the raw stamps (wavefronts x slots, .npy)")
     a = ap.parse_args()
-    build(a.tiles) if a.cmd == "build" else run(a.workload, a.what)
+    build(a.tiles, a.mm_if) if a.cmd == "build" else run(a.workload, a.what, a.dump)
 
 
 if __name__ == "__main__":
