@@ -203,9 +203,22 @@ __device__ __forceinline__ void qk_head(float (&v)[2][TT][4], const float *__res
                                         const float *__restrict__ rope, float eps, uint32_t m, float *xch) {
     __shared__ float ssq[4][TT * 16];
     const uint32_t l = threadIdx.x & 63u, kg = l >> 4, wave = threadIdx.x >> 6;
-    float wd[2];
+    // the norm weights and every rotation angle first: their loads overlap the exchanges
+    float wd[2], rc[TT][4][2], rs[TT][4][2];
 #pragma unroll
     for (int i = 0; i < 2; i++) wd[i] = w[32 * wave + 16 * i + (l & 15u)];
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t tok = t * 16 + 4 * kg + r, tc = tok < m ? tok : m - 1;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t dm = 32 * (wave & 1u) + 16 * i + (l & 15u);
+                rc[t][r][i] = rope[(uint64_t)tc * 128 + dm];
+                rs[t][r][i] = rope[(uint64_t)tc * 128 + 64 + dm];
+            }
+        }
     __syncthreads();  // every wavefront is past its products: xch (the fragment LDS) is free
 #pragma unroll
     for (int t = 0; t < TT; t++)
@@ -232,16 +245,13 @@ __device__ __forceinline__ void qk_head(float (&v)[2][TT][4], const float *__res
 #pragma unroll
     for (int t = 0; t < TT; t++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t tok = t * 16 + 4 * kg + r, tc = tok < m ? tok : m - 1;
+        for (int r = 0; r < 4; r++)
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const float p = xch[(((wave ^ 2u) * 2 + i) * TT + t) * 256 + r * 64 + l];
-                const uint32_t dm = 32 * (wave & 1u) + 16 * i + (l & 15u);
-                const float c = rope[(uint64_t)tc * 128 + dm], sn = rope[(uint64_t)tc * 128 + 64 + dm];
+                const float c = rc[t][r][i], sn = rs[t][r][i];
                 v[i][t][r] = wave < 2 ? v[i][t][r] * c - p * sn : v[i][t][r] * c + p * sn;
             }
-        }
 }
 
 template <int TT, int RT, bool GLU, bool NORM>
@@ -274,7 +284,7 @@ __device__ __forceinline__ void finish(const float (&acc)[RT][TT][4], float *out
     if constexpr (NORM) ss_load<TT>(ssv, jobs, m);
     // Slices are added in slice order (the sum does not depend on arrival order);
     // the loads of G slices for all RT row tiles are in flight together.
-    constexpr uint32_t G = RT * TT >= 16 ? 1u : 16u / (RT * TT);
+    constexpr uint32_t G = RT * TT >= 4 ? 32u / (RT * TT) : 8u;
     float v[RT][TT][4];
 #pragma unroll
     for (int i = 0; i < RT; i++)
