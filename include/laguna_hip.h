@@ -191,8 +191,9 @@ int lg_dispatch_proj_quant_batch_static(const void *x, int x_dtype, const void *
 /* Device workspace bytes lg_dispatch_proj_quant_batch needs for this shape on the
  * current device (0: the shape takes the element-wise path, which needs none).  No
  * counterpart in the reference.  It is 64 KiB of arrival counters plus, when the
- * product splits k over slices, the split-k partial sums: slices * min(m, 32) * n * 4
- * bytes (slices chosen for about two workgroups per CU).
+ * product splits k over slices, the split-k partial sums: slices * n' * 16 * tiles * 4
+ * bytes, n' = n rounded up to whole workgroup columns (64 or 128 rows) and tiles =
+ * ceil(min(m, 32) / 16) (slices chosen for about two workgroups per CU).
  * lg_dispatch_proj_quant_batch_static accepts a shape when this is at most
  * 16 MiB + 64 KiB. */
 uint64_t lg_proj_quant_batch_ws_bytes(uint32_t k, uint32_t n, uint32_t m, int w_dtype);
