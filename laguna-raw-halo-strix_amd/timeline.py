@@ -20,7 +20,8 @@ after its P V, each with the next tile's loads issued); they slow that kernel by
 a quarter, so its other phases read best from a build without them.
 
 `mm` reads the last small-M product launch (k_mm_mf) of the workload, `attn` the last k_attn_split launch
-(the draft block's last layer), or the last combine launch of the few-query path.
+(the draft block's last layer), or the last combine launch of the few-query path, `m1` the last launch of
+the M = 1 integer-dot Q4_K kernel (k_q4k_m1_dig and its norm-fused forms).
 """
 import argparse
 import collections
@@ -75,6 +76,15 @@ STAMPS = {
         ("after", "if (!arrive_last(a.cnt + grp, a.nch, &last)) return;", "\n    TS(6);"),
         ("before", "    const uint32_t qo = AQG * qg + mq;", "    TS(7);\n"),
     ]),
+    "proj_m1.hip": ("void q4k_m1_dig_body(", [
+        ("after", "    const uint32_t stride = gridDim.x * TEAMS * R;\n", "    TS(0); TSID();\n"),
+        ("after", "    dig_convert(xv, k, dg);\n    __syncthreads();", "\n    TS(1);"),
+        ("after", "    dig_read(dg, p, D, X0, X1, F);", "\n    TS(2);"),
+        ("before", "    auto reduce = [&](int b, uint32_t rr) {", "    uint32_t tl_n = 0;\n"),
+        ("after", "            float v = dotrow(hd[b][r], qa[b][r], qb[b][r]);",
+         "\n            if (r == 0) { if (tl_n < 30) TS(3 + tl_n); tl_n++; }"),
+        ("after", "        r0 = r2;\n    }", "\n    TS(38);"),
+    ]),
     "dflash.hip#combine": ("void k_attn_combine(", [
         ("after", "if (h >= n_kv || qi >= rows * G) return;  // uniform over the workgroup", "\n    TS(20);"),
         ("before", "    float M = tm, L = tl, o0 = t0, o1 = t1;", "    TS(21);\n"),
@@ -97,6 +107,8 @@ TILE_STAMPS = [
 PHASES = {
     "mm": [(0, "start"), (1, "chunk 0's activations in LDS"), (2, "chunk 1 in LDS"), (3, "chunk 2 in LDS"),
            (4, "chunk 3 in LDS"), (36, "products done"), (38, "split-k finish done")],
+    "m1": [(0, "start"), (1, "x converted (after the barrier)"), (2, "digits in registers"),
+           (3, "first rows reduced"), (4, "second rows"), (5, "third rows"), (6, "fourth rows"), (38, "done")],
     "attn": [(0, "start"), (1, "queries issued"), (2, "first tile issued, gate units done"),
              (8, "tile 0: scores, K refill issued"), (9, "tile 0: P V, V refill issued"),
              (10, "tile 1: scores"), (11, "tile 1: P V"), (12, "tile 2: scores"), (13, "tile 2: P V"),
@@ -128,12 +140,12 @@ def build(tiles=False, mm_if="true"):
     for f in ["runtime.cpp", "gguf.cpp", "dequant.hip", "proj_m1.hip", "proj_batch.hip", "dflash.hip", "verify.hip",
               "ceiling.hip", "target.hip"]:
         src = open(os.path.join(csrc, f)).read()
-        if f in ("proj_batch.hip", "dflash.hip"):
+        if f in ("proj_batch.hip", "dflash.hip", "proj_m1.hip"):
             for key, (sig, edits) in STAMPS.items():
                 if key.split("#")[0] == f:
                     src = instrument(src, sig, edits + (TILE_STAMPS if tiles and key == "dflash.hip" else []))
             i = src.index("namespace {")
-            tag = "mm" if f == "proj_batch.hip" else "attn"
+            tag = {"proj_batch.hip": "mm", "dflash.hip": "attn", "proj_m1.hip": "m1"}[f]
             cond = mm_if if tag == "mm" else "true"
             src = src[:i] + HEADER % {"f": tag, "n": SLOTS * WAVES, "w": WAVES, "s": SLOTS, "cond": cond} + src[i:]
         path = os.path.join(OUT, f)
@@ -197,7 +209,7 @@ def run(workload, what, dump=None):
     wpg = 4
     wg_cu = cu[0::wpg]
     rel = np.where(T[:nw] > 0, (T[:nw] - t0) * 10, -1)
-    end_k = 38 if what == "mm" else 5
+    end_k = 5 if what == "attn" else 38
     ends = rel[:, end_k].reshape(-1, wpg).max(axis=1)
     wg_xcc = xcc[0::wpg]
     rr = int((wg_xcc == (np.arange(len(wg_xcc)) % 8)).sum())
@@ -223,7 +235,7 @@ def main():
     b.add_argument("--mm-if", default="true")
     r = sub.add_parser("run")
     r.add_argument("workload")
-    r.add_argument("what", nargs="?", default="mm", choices=["mm", "attn"])
+    r.add_argument("what", nargs="?", default="mm", choices=["mm", "attn", "m1"])
     r.add_argument("--dump", help="also save the raw stamps (wavefronts x slots, .npy)")
     a = ap.parse_args()
     build(a.tiles, a.mm_if) if a.cmd == "build" else run(a.workload, a.what, a.dump)
