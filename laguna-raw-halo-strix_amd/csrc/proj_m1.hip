@@ -846,8 +846,12 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void k_q4k_m1_mfma(const float *__re
 // quarter t%4; threads past k/16 read element 0 and fill table entries that only idle
 // lanes read) into the LDS table dg_tab (per group: digit planes 0, 1, 2 x 16 dwords)
 // and dg_xf (per group: the sums of elements 0-31 and 32-63, and 2^-sh).
+// Group p's 48 digit dwords start at dword 52 p: lane p's 16-byte reads of its group
+// then fall on distinct banks over each 16 lanes (at 48 p, every fourth lane shares
+// banks: 16-way conflicts on the read back).
+constexpr uint32_t DIG_STRIDE = 52;
 struct DigLds {
-    uint32_t tab[64 * 48];
+    uint32_t tab[64 * DIG_STRIDE];
     float xf[64 * 4];
     uint32_t bad;
 };
@@ -882,7 +886,7 @@ __device__ __forceinline__ void dig_convert(const float4 (&xv)[4], uint32_t k, D
     uint32_t U[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) U[j] = __float_as_uint(__builtin_fmaf(v[j], scale, 12582912.0f)) - 0x4ABF7F80u;
-    uint32_t *dgp = dg.tab + (tid >> 2) * 48 + 4 * (tid & 3u);
+    uint32_t *dgp = dg.tab + (tid >> 2) * DIG_STRIDE + 4 * (tid & 3u);
 #pragma unroll
     for (int q = 0; q < 4; q++) {  // elements 4q .. 4q+3 of this thread's 16: one dword per digit plane
         const uint32_t lo01 = __builtin_amdgcn_perm(U[4 * q + 1], U[4 * q], 0x05010400u);
@@ -906,7 +910,7 @@ __device__ __forceinline__ void dig_convert(const float4 (&xv)[4], uint32_t k, D
 // Group p's 48 digit dwords and its X0, X1, 2^-sh into registers.
 __device__ __forceinline__ void dig_read(const DigLds &dg, uint32_t p, uint32_t (&D)[48], float &X0, float &X1,
                                          float &F) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(dg.tab + p * 48);
+    const uint4 *src = reinterpret_cast<const uint4 *>(dg.tab + p * DIG_STRIDE);
 #pragma unroll
     for (int i = 0; i < 12; i++) {
         const uint4 u = src[i];
