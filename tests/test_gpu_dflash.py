@@ -3,13 +3,14 @@
 Tolerances (all relative to the largest magnitude of the f64 result, ||y-yhat||_inf
 / ||yhat||_inf, written per test):
 * norms, RoPE, gates: f32 arithmetic, 1e-5 (measured 1e-7);
-* attention on matrix cores: f32 products of q, k, p and v (v_mfma_f32_16x16x4_f32)
-  with base-2 exponentials of the scaled scores, 1e-5;
+* attention on matrix cores: products over f16 parts of q, k, p and v (hi hi + hi lo
+  + lo hi, each f16 product exact in f32; f32 products for tiles out of f16's range)
+  with base-2 exponentials of the scaled scores, 1e-5 (measured 1e-7 .. 7e-7);
 * the block forward on weights of trained magnitude (N(0, 0.02) quantized): 3e-6
   (measured 1.4e-7 .. 2.3e-7);
 * the block forward on GGUF-random Q4_K blocks, whose large common-mode weight
-  drives the hidden state far from trained-model ranges: about ten times each
-  case's measured error (4e-7 .. 8e-5, written per case), 1e-4 for the full draft
+  drives the hidden state far from trained-model ranges: three to seven times each
+  case's measured error (2e-6 .. 1e-4, written per case), 1e-4 for the full draft
   (measured 3.7e-5).  The m = 32 case has token rows in steep regions --
   attention gates near -20, FFN values of 1e3-1e4 -- where one-ulp changes
   inside exp move the output by 1e-3 (an all-f32 numpy evaluation of the same
@@ -202,9 +203,10 @@ def test_encode(ctx):
 
 
 # (config, m, context, tolerance): the measured error of each case, on GGUF-random
-# blocks, is 2.4e-6, 3.3e-6, 8.4e-5, 2.7e-5, 6.0e-4 and 4.1e-7
+# blocks, is 4.5e-6, 9.3e-6, 3.9e-5, 1.0e-4, 8.9e-4 and 1.8e-6 (earlier kernels'
+# rounding orders gave 2.4e-6, 3.3e-6, 8.4e-5, 2.7e-5, 6.0e-4 and 4.1e-7)
 @pytest.mark.parametrize("cfg,m,ctx_len,tol", [(SMALL, 1, 0, 3e-5), (SMALL, 7, 0, 3e-5),
-                                               (SMALL, 16, 100, 8e-4), (SMALL, 16, 64, 3e-4),
+                                               (SMALL, 16, 100, 2e-4), (SMALL, 16, 64, 3e-4),
                                                (SMALL, 32, 70, TOL_FWD_STEEP), (SMALL64, 5, 33, 1e-5)])
 def test_forward_block_small(ctx, cfg, m, ctx_len, tol):
     print(f"forward_block n_embd={cfg.n_embd} hd={cfg.head_dim} m={m} ctx={ctx_len}", flush=True)
@@ -263,7 +265,7 @@ def test_graph_replays_match_eager(ctx):
     stream.destroy()
 
 
-@pytest.mark.parametrize("cfg,m,ctx_len,tol", [(SMALL, 1, 0, 3e-5), (SMALL, 16, 100, 8e-4),
+@pytest.mark.parametrize("cfg,m,ctx_len,tol", [(SMALL, 1, 0, 3e-5), (SMALL, 16, 100, 2e-4),
                                                (SMALL, 32, 70, TOL_FWD_STEEP), (SMALL64, 5, 33, 1e-5)])
 def test_forward_folded_norms_and_separate_norms(ctx, cfg, m, ctx_len, tol):
     # The attention and FFN RMSNorms folded into the projections (the default: the
