@@ -134,7 +134,8 @@ def build(tiles=False, mm_if="true"):
     csrc = os.path.join(HERE, "csrc")
     flags = ["-x", "hip", "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Xclang", "-target-feature",
              "-Xclang", "-packed-fp32-ops", "-I" + os.path.join(HERE, "..", "include"), "-I" + csrc]
-    extra = {"proj_batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "dflash.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    ilp = ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-sched-strategy=max-ilp"]
+    extra = {"proj_batch.hip": ilp, "dflash.hip": ilp,
              "proj_m1.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"]}
     objs = []
     for f in ["runtime.cpp", "gguf.cpp", "dequant.hip", "proj_m1.hip", "proj_batch.hip", "dflash.hip", "verify.hip",
