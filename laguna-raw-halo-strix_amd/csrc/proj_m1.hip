@@ -134,16 +134,23 @@ __device__ __forceinline__ float h_hi(uint32_t v) { return (float)__builtin_bit_
 // Team sums of the RPW row partials and their stores.  TW == 1: DPP/swizzle only.
 // TW > 1: every wave's wavefront sums go to LDS, one barrier, wave 0 of the team
 // adds the TW partials of each row.  Every wave of the workgroup calls this once.
-template <int TW, int TEAMS, int RPW>
+// A row sum that is not finite is replaced by redo(row), the wavefront's element-by-element
+// sum in the reference's terms: the vector kernels' split into S and X turns an inf among
+// the activations into inf - inf (NaN) where the reference's loop gives inf.  Each sum is
+// taken from one lane (TW == 1) or read from LDS by every lane, so that branch is uniform.
+template <int TW, int TEAMS, int RPW, class Redo>
 __device__ __forceinline__ void team_store(float (&acc)[RPW], uint32_t row0, uint32_t n, float *__restrict__ y,
-                                           float *red, uint32_t team, uint32_t lane, uint32_t wt) {
+                                           float *red, uint32_t team, uint32_t lane, uint32_t wt, const Redo &redo) {
 #pragma unroll
     for (int r = 0; r < RPW; r++) acc[r] = wave_sum(acc[r]);
     if constexpr (TW == 1) {
-        if (lane == 0) {
 #pragma unroll
-            for (int r = 0; r < RPW; r++)
-                if (row0 + r < n) y[row0 + r] = acc[r];
+        for (int r = 0; r < RPW; r++) {
+            float s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(acc[r])));  // lane 0's sum
+            if (row0 + r < n) {
+                if (!__builtin_isfinite(s)) s = redo(row0 + r);
+                if (lane == 0) y[row0 + r] = s;
+            }
         }
     } else {
         float *buf = red + team * (RPW * TW);
@@ -152,11 +159,16 @@ __device__ __forceinline__ void team_store(float (&acc)[RPW], uint32_t row0, uin
             for (int r = 0; r < RPW; r++) buf[r * TW + wt] = acc[r];
         }
         __syncthreads();
-        if (wt == 0 && lane < (uint32_t)RPW && row0 + lane < n) {
-            float s = 0.0f;
+        if (wt == 0) {
 #pragma unroll
-            for (int t = 0; t < TW; t++) s += buf[lane * TW + t];
-            y[row0 + lane] = s;
+            for (int r = 0; r < RPW; r++) {
+                if (row0 + r >= n) break;
+                float s = 0.0f;
+#pragma unroll
+                for (int t = 0; t < TW; t++) s += buf[r * TW + t];
+                if (!__builtin_isfinite(s)) s = redo(row0 + r);
+                if (lane == 0) y[row0 + r] = s;
+            }
         }
     }
 }
@@ -182,6 +194,30 @@ __device__ __forceinline__ Q4Lane q4_lane(uint32_t g) {
         }
     }
     return L;
+}
+
+// One element of the weights decoded at the reference's linear index
+// (kernels/proj_q4k.comp:67, proj_q8_0.comp:54).
+__device__ __forceinline__ float q4k_elem(const uint8_t *__restrict__ w, uint64_t lin) {
+    const uint8_t *blk = w + (lin / QK_K) * Q4K_BYTES;
+    const uint32_t e = lin % QK_K, j = e / 32, g = e / 64, wi = e % 64;
+    const float d = ref_half(blk[0] | (blk[1] << 8)), dmin = ref_half(blk[2] | (blk[3] << 8));
+    const uint32_t b0 = blk[4 + j], b4 = blk[8 + (j & 3)], bp = blk[12 + (j & 3)];
+    uint32_t sc, mn;
+    if (j < 4) {
+        sc = b0 & 63u, mn = b4 & 63u;
+    } else {
+        sc = (bp & 15u) | ((blk[4 + j - 4] >> 6) << 4);
+        mn = (bp >> 4) | ((b4 >> 6) << 4);
+    }
+    const uint32_t byte = blk[16 + 32 * g + (wi % 32)];
+    const float q = (float)(wi < 32 ? (byte & 15u) : (byte >> 4));
+    return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), q), __fmul_rn(dmin, (float)mn));
+}
+
+__device__ __forceinline__ float q80_elem(const uint8_t *__restrict__ w, uint64_t lin) {
+    const uint8_t *blk = w + (lin / QK8_0) * Q80_BYTES;
+    return __fmul_rn((float)(int8_t)blk[2 + lin % QK8_0], ref_half(blk[0] | (blk[1] << 8)));
 }
 
 // One lane's contribution to one row: 64 weights of super-block header `hd`
@@ -285,7 +321,15 @@ __global__ __launch_bounds__(TW *TEAMS * 64) void k_q4k_m1(const float *__restri
             acc[r] += active ? v : 0.0f;
         }
     }
-    team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
+    team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt, [&](uint32_t row) {
+        float a = 0.0f;  // kernels/proj_q4k.comp:60-75 (with up: activation.comp:21-28)
+        for (uint32_t j = lane; j < k; j += 64) {
+            float xj = x[j];
+            if constexpr (FUSE) xj = silu_mul(xj, up[j]);
+            a = __builtin_fmaf(xj, q4k_elem(w, (uint64_t)row * k + j), a);
+        }
+        return wave_sum(a);
+    });
 }
 
 // ------------------------------------------------------------------------------------------
@@ -392,34 +436,16 @@ __global__ __launch_bounds__(TW *TEAMS * 64) void k_q80_m1(const float *__restri
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
     }
-    team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt);
+    team_store<TW, TEAMS, RPW>(acc, row0, n, y, red, team, lane, wt, [&](uint32_t row) {
+        float a = 0.0f;  // kernels/proj_q8_0.comp:47-66
+        for (uint32_t j = lane; j < k; j += 64) a = __builtin_fmaf(x[j], q80_elem(w, (uint64_t)row * k + j), a);
+        return wave_sum(a);
+    });
 }
 
 // ------------------------------------------------------------------------------------------
-// Reference-semantics fallback: one wavefront per row, element-wise decode at the
-// reference's linear index (kernels/proj_q4k.comp:67, proj_q8_0.comp:54).
-
-__device__ __forceinline__ float q4k_elem(const uint8_t *__restrict__ w, uint64_t lin) {
-    const uint8_t *blk = w + (lin / QK_K) * Q4K_BYTES;
-    const uint32_t e = lin % QK_K, j = e / 32, g = e / 64, wi = e % 64;
-    const float d = ref_half(blk[0] | (blk[1] << 8)), dmin = ref_half(blk[2] | (blk[3] << 8));
-    const uint32_t b0 = blk[4 + j], b4 = blk[8 + (j & 3)], bp = blk[12 + (j & 3)];
-    uint32_t sc, mn;
-    if (j < 4) {
-        sc = b0 & 63u, mn = b4 & 63u;
-    } else {
-        sc = (bp & 15u) | ((blk[4 + j - 4] >> 6) << 4);
-        mn = (bp >> 4) | ((b4 >> 6) << 4);
-    }
-    const uint32_t byte = blk[16 + 32 * g + (wi % 32)];
-    const float q = (float)(wi < 32 ? (byte & 15u) : (byte >> 4));
-    return __fsub_rn(__fmul_rn(__fmul_rn(d, (float)sc), q), __fmul_rn(dmin, (float)mn));
-}
-
-__device__ __forceinline__ float q80_elem(const uint8_t *__restrict__ w, uint64_t lin) {
-    const uint8_t *blk = w + (lin / QK8_0) * Q80_BYTES;
-    return __fmul_rn((float)(int8_t)blk[2 + lin % QK8_0], ref_half(blk[0] | (blk[1] << 8)));
-}
+// Reference-semantics fallback: one wavefront per row, each element decoded at the
+// reference's linear index (q4k_elem, q80_elem).
 
 template <bool FUSE>
 __global__ __launch_bounds__(256) void k_generic_m1(const float *__restrict__ x, const float *__restrict__ up,

@@ -63,12 +63,15 @@ def assert_same_non_finite(y, y64):
 
 
 @pytest.mark.parametrize("dtype,k,n", [(lh.Q4_K, 4096, 300), (lh.Q4_K, 1024, 37), (lh.Q4_K, 12288, 40),
-                                       (lh.Q8_0, 4096, 300), (lh.Q8_0, 1024, 37)])
+                                       (lh.Q4_K, 20480, 40), (lh.Q8_0, 4096, 300), (lh.Q8_0, 1024, 37),
+                                       (lh.Q8_0, 14336, 40)])
 def test_activations_outside_the_digit_range(ctx, dtype, k, n):
     # Q4_K up to k = 16384 and Q8_0 up to 4096 convert x to byte digits (per
     # 64-element group up to 4096, per super-block beyond); values they cannot scale
     # (non-finite, >= 2^21, nonzero below 2^-60) send the call to the reference's
-    # per-element loop, whose results the f64 accumulation matches.
+    # per-element loop, whose results the f64 accumulation matches.  Beyond those k
+    # (Q4_K 20480, Q8_0 14336) the f32 vector kernels take every finite value as it is
+    # and a lane holding inf or NaN sums its terms element by element.
     raw = weight(dtype, 300 + k, k, n)
     x = synth.normal(301 + k, k)
     for idx, val in [(5, np.inf), (k - 3, -np.inf), (k // 3, np.nan)]:
@@ -209,6 +212,64 @@ def test_fused_silu_other_shapes(ctx, dtype, k, n):
     lh.dispatch_silu_mul_proj_quant(ctx, gb, ub, wb, cb, k, n, dtype)
     y64, a = orc.proj_quant_f64x(orc.silu_mul_f64(gate, up), raw, dtype, k, n)
     parity(cb.read_f32(n), y64, a, TOL)
+
+
+def fused_run(ctx, raw, gate, up, k, n):
+    wb, gb, ub, cb = lh.upload_bytes(ctx, raw), lh.upload_f32(ctx, gate), lh.upload_f32(ctx, up), lh.GpuBuffer(ctx, 4 * n)
+    lh.dispatch_silu_mul_proj_quant(ctx, gb, ub, wb, cb, k, n, lh.Q4_K)
+    return cb.read_f32(n)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+@pytest.mark.parametrize("k,n", [(14336, 4096), (12288, 40), (5120, 33), (16384, 7), (4352, 5)])
+def test_fused_silu_kernel_families(ctx, kind, k, n):
+    # The fused SiLU down projection on the vector kernel (1) and on int8 matrix cores
+    # (2, the automatic choice for k <= 16384), each bit-for-bit repeatable.
+    seed = 7000 + k + n
+    print(f"fused silu family {kind} k={k} n={n}", flush=True)
+    raw = synth.q4k_weight(seed, k, n)
+    gate, up = synth.normal(seed + 1, k), synth.normal(seed + 2, k)
+    lh.check(lh.lib().lg_set_m1_kernel(kind))
+    try:
+        y1 = fused_run(ctx, raw, gate, up, k, n)
+        y2 = fused_run(ctx, raw, gate, up, k, n)
+    finally:
+        lh.check(lh.lib().lg_set_m1_kernel(0))
+    assert np.array_equal(y1, y2)
+    y64, a = orc.proj_quant_f64x(orc.silu_mul_f64(gate, up), raw, orc.Q4_K, k, n)
+    parity(y1, y64, a, TOL)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_fused_silu_outside_digit_range(ctx, kind):
+    # Non-finite silu(gate) * up propagates as in the reference's f32 loop on both
+    # families; tiny activations send the matrix-core kernel's super-blocks (2) to the
+    # per-element loop, while the vector kernel (1) takes them in f32 as they are.  The
+    # matrix-core kernel scales per super-block, so a value 10^6 times its neighbours
+    # costs it up to 2^-22 of that value per element of the super-block: that case is
+    # left to the vector kernel.
+    k, n = 14336, 64
+    raw = synth.q4k_weight(7100, k, n)
+    gate, up = synth.normal(7101, k), synth.normal(7102, k)
+    lh.check(lh.lib().lg_set_m1_kernel(kind))
+    try:
+        for idx, val in [(5, np.inf), (k - 3, -np.inf), (k // 3, np.nan)]:
+            print(f"fused silu family {kind} gate[{idx}]={val}", flush=True)
+            gs = gate.copy()
+            gs[idx] = val
+            y64, _ = orc.proj_quant_f64x(orc.silu_mul_f64(gs, up), raw, orc.Q4_K, k, n)
+            assert_same_non_finite(fused_run(ctx, raw, gs, up, k, n), y64)
+        gh = gate.copy()
+        gh[9000] = 8.0  # silu(8) * 4e5 = 3.2e6 >= 2^21
+        cases = [("tiny", gate, (up * 1e-20).astype(np.float32))]
+        if kind == 1:
+            cases.append(("huge", gh, np.where(np.arange(k) == 9000, np.float32(4e5), up).astype(np.float32)))
+        for name, gs, us in cases:
+            print(f"fused silu family {kind} {name} activations", flush=True)
+            y64, a = orc.proj_quant_f64x(orc.silu_mul_f64(gs, us), raw, orc.Q4_K, k, n)
+            parity(fused_run(ctx, raw, gs, us, k, n), y64, a, TOL)
+    finally:
+        lh.check(lh.lib().lg_set_m1_kernel(0))
 
 
 def test_activation_kernel(ctx):
