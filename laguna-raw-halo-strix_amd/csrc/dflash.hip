@@ -1401,7 +1401,7 @@ int upload_table(uint64_t (&tag)[2], const lg_dflash_hparams &hp, const FwdLayou
     {  // a new table is a host copy and a synchronise, which a capturing stream cannot take
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         LG_HIP_TRY(hipStreamIsCapturing(s, &cs));
-        LG_REQUIRE(cs == hipStreamCaptureStatusNone, "the RoPE table of this model must be uploaded while the stream "
+        LG_REQUIRE(cs == hipStreamCaptureStatusNone, "the RoPE table of this model cannot be uploaded while the stream "
                    "is being captured; make the same call once before capturing");
     }
     const std::vector<float> f = rope_table(hp);

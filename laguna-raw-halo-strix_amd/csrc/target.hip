@@ -70,7 +70,7 @@ int upload_tables(uint64_t (&tag)[2], const lg_target_hparams &hp, const TgtLayo
     {  // a new table is a host copy and a synchronise, which a capturing stream cannot take
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         LG_HIP_TRY(hipStreamIsCapturing(s, &cs));
-        LG_REQUIRE(cs == hipStreamCaptureStatusNone, "the RoPE table of this model must be uploaded while the stream "
+        LG_REQUIRE(cs == hipStreamCaptureStatusNone, "the RoPE table of this model cannot be uploaded while the stream "
                    "is being captured; make the same call once before capturing");
     }
     float f[2 * TABLE_FLOATS] = {0.0f};
