@@ -413,6 +413,94 @@ def dispatch_add(ctx, a, b, out, n):
     check(lib().lg_dispatch_add(_ptr(a), _ptr(b), _ptr(out), n, ctx.stream))
 
 
+MOE_TENSORS = ("ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps", "ffn_gate_shexp", "ffn_up_shexp",
+               "ffn_down_shexp")
+F16_SAFE = np.float32(32768.0)             # src/target.rs:699
+MOE_NORM_MIN = np.float32(6.103515625e-5)  # src/target.rs:666
+
+
+class MoeFfnWeights:
+    """The MoE FFN tensors of a TargetLayer (src/target.rs:181-235): each name of
+    MOE_TENSORS is a (GpuBuffer, dtype) pair of raw blocks (the experts' gate, up and
+    down weights stacked expert after expert), exp_probs_b a GpuBuffer of n_expert f32."""
+
+    def __init__(self, exp_probs_b, **tensors):
+        missing = [t for t in MOE_TENSORS if t not in tensors]
+        if missing:
+            raise LagunaError(EINVAL, f"MoeFfnWeights: missing {missing}")
+        self.exp_probs_b = exp_probs_b
+        for t in MOE_TENSORS:
+            setattr(self, t, tensors[t])
+
+
+def dispatch_moe_ffn(ctx, norm_x, moe, ffn_out, n_embd, n_expert, n_expert_used, n_ff_exp, n_shexp,
+                     expert_weights_norm=False, expert_weights_scale=1.0):
+    """TargetModel::dispatch_moe_ffn (src/target.rs:607-748), driven from the host as
+    there: the router's logits come back to the host, which picks the experts (sigmoid
+    probabilities plus exp_probs_b, a stable descending sort, the first n_expert_used) and
+    their scores, and launches each expert's gate and up projections at the expert's
+    element offset (a u32, as there; Q8_0 and F32 weights ignore it), the activation, the
+    down projection of the hidden rescaled to an L2 norm of 32768 on the host, that
+    scale undone times the score on the host when the score is > 0, and the adds; then
+    the shared expert.  ffn_out receives the sum.  Returns (selected experts, scores)."""
+    if not 0 < n_expert_used <= n_expert:
+        raise LagunaError(EINVAL, f"dispatch_moe_ffn: {n_expert_used} of {n_expert} experts")
+    one = np.float32(1.0)
+    scratch = []
+
+    def buf(n):
+        b = GpuBuffer(ctx, 4 * n)
+        scratch.append(b)
+        return b
+
+    try:
+        scores_buf = buf(n_expert)
+        dispatch_proj_quant(ctx, norm_x, moe.ffn_gate_inp[0], scores_buf, n_embd, n_expert, moe.ffn_gate_inp[1])
+        logits = scores_buf.read_f32(n_expert)
+        probs = (one / (one + np.exp(-logits))).astype(np.float32)
+        sel = (probs + moe.exp_probs_b.read_f32(n_expert)).astype(np.float32)
+        chosen = [int(i) for i in np.argsort(-sel, kind="stable")[:n_expert_used]]
+        scores = probs[chosen].astype(np.float32)
+        if expert_weights_norm:
+            total = np.float32(0.0)
+            for v in scores:  # Iterator::sum, in order
+                total = np.float32(total + v)
+            scores = (scores / max(total, MOE_NORM_MIN)).astype(np.float32)
+        if expert_weights_scale != 0.0 and expert_weights_scale != 1.0:
+            scores = (scores * np.float32(expert_weights_scale)).astype(np.float32)
+
+        moe_out, expert, gate, up, hidden = buf(n_embd), buf(n_embd), buf(n_ff_exp), buf(n_ff_exp), buf(n_ff_exp)
+        moe_out.upload(np.zeros(n_embd, np.float32))
+        for e, sc in zip(chosen, scores):
+            off = (e * n_embd * n_ff_exp) & 0xFFFFFFFF
+            dispatch_proj_quant_expert(ctx, norm_x, moe.ffn_gate_exps[0], gate, n_embd, n_ff_exp,
+                                       moe.ffn_gate_exps[1], off)
+            dispatch_proj_quant_expert(ctx, norm_x, moe.ffn_up_exps[0], up, n_embd, n_ff_exp, moe.ffn_up_exps[1], off)
+            dispatch_activation(ctx, gate, up, hidden, n_ff_exp)
+            h = hidden.read_f32(n_ff_exp)
+            sq = np.add.accumulate(h * h, dtype=np.float32)[-1]  # in order, as Iterator::sum
+            col_l2 = np.float32(min(max(np.float32(np.sqrt(sq)), np.float32(1e-8)), np.float32(1e30)))
+            hidden.upload(((h * F16_SAFE) / col_l2).astype(np.float32))
+            dispatch_proj_quant_expert(ctx, hidden, moe.ffn_down_exps[0], expert, n_ff_exp, n_embd,
+                                       moe.ffn_down_exps[1], off)
+            if sc > 0.0:
+                o = expert.read_f32(n_embd)
+                expert.upload((o * np.float32((col_l2 / F16_SAFE) * sc)).astype(np.float32))
+            dispatch_add(ctx, moe_out, expert, moe_out, n_embd)
+
+        sg, su, sh, so = buf(n_shexp), buf(n_shexp), buf(n_shexp), buf(n_embd)
+        dispatch_proj_quant(ctx, norm_x, moe.ffn_gate_shexp[0], sg, n_embd, n_shexp, moe.ffn_gate_shexp[1])
+        dispatch_proj_quant(ctx, norm_x, moe.ffn_up_shexp[0], su, n_embd, n_shexp, moe.ffn_up_shexp[1])
+        dispatch_activation(ctx, sg, su, sh, n_shexp)
+        dispatch_proj_quant(ctx, sh, moe.ffn_down_shexp[0], so, n_shexp, n_embd, moe.ffn_down_shexp[1])
+        dispatch_add(ctx, moe_out, so, ffn_out, n_embd)
+        return chosen, scores
+    finally:
+        ctx.sync()  # the launches above still read the scratch buffers
+        for b in scratch:
+            b.free()
+
+
 def rope_freq(rope_dim, base=500000.0):
     """The f32 table of src/dflash.rs:898-904: 1 / base^(2i / rope_dim)."""
     i = np.arange(rope_dim // 2, dtype=np.float32)

@@ -12,6 +12,9 @@ The reference's constants: RMSNorm eps 1e-5 (src/target.rs:970), QK-norm eps 1e-
 (:352, :367), SWA layers are those with index % 4 != 0 (:440), attention scale
 1/sqrt(head_dim) (:776).
 
+The MoE FFN of TargetModel::dispatch_moe_ffn (src/target.rs:607-748) is moe_ffn
+below, pinned in tests/test_moe_oracle.py.
+
 Pinning (tests/test_target_oracle.py): closed forms of the composite (zero
 attention output and FFN down weights leave logits = W_out rmsnorm(input) *
 output_norm; one-position attention returns V, so the logits do not depend on the
@@ -134,3 +137,70 @@ def token_embedding(raw, dtype, n_embd, token):
     n = (token + 1) * n_embd
     b = np.ascontiguousarray(raw).view(np.uint8).ravel()  # the tensor's bytes, whatever the array type
     return orc.dequant(b, dtype, n)[token * n_embd:n].astype(np.float32)
+
+
+# ---- MoE FFN (src/target.rs:607-748) ---------------------------------------------------
+
+F16_SAFE = 32768.0             # src/target.rs:699: the expert hidden is scaled to this L2 norm
+MOE_NORM_MIN = 6.103515625e-5  # src/target.rs:666: floor of the selected scores' sum
+MOE_TENSORS = ("ffn_gate_inp", "ffn_gate_exps", "ffn_up_exps", "ffn_down_exps", "ffn_gate_shexp", "ffn_up_shexp",
+               "ffn_down_shexp")
+
+
+def expert_offset(e, n_embd, n_ff_exp):
+    """src/target.rs:684,687: the expert's first element, cast to u32 as there."""
+    return (e * n_embd * n_ff_exp) & 0xFFFFFFFF
+
+
+def proj_expert(x64, raw, dtype, k, n, elem_offset=0):
+    """dispatch_proj_quant_expert in float64: the element offset moves the weights for
+    Q4_K only; Q8_0 and F32 ignore it (src/target.rs:1115-1138).  Returns (y, absdot)."""
+    if dtype == orc.F32:
+        w = np.ascontiguousarray(raw, np.float32).view(np.uint8).ravel()
+    else:
+        w = np.frombuffer(raw, np.uint8) if isinstance(raw, (bytes, bytearray)) else np.asarray(raw, np.uint8)
+        if dtype == orc.Q4_K and elem_offset:
+            assert elem_offset % 256 == 0
+            w = w[elem_offset // 256 * 144:]
+    return orc.proj_quant_f64x(x64, w, dtype, k, n)
+
+
+def moe_ffn(norm_x, w, bias, n_embd, n_expert, n_expert_used, n_ff_exp, n_shexp, expert_weights_norm=False,
+            expert_weights_scale=1.0):
+    """TargetModel::dispatch_moe_ffn (src/target.rs:607-748) in float64.
+
+    w maps each name of MOE_TENSORS to (raw, dtype); bias is exp_probs_b (n_expert f32).
+    Router logits, sigmoid probabilities, selection by probability + bias (a stable
+    descending sort, the first n_expert_used), scores = the selected probabilities,
+    divided by max(their sum, 2^-14) when expert_weights_norm, times expert_weights_scale
+    unless it is 0 or 1.  Each selected expert: h = silu(gate x) * (up x), the down
+    projection of h * 32768 / ||h|| (||h|| clamped to [1e-8, 1e30]), multiplied back by
+    ||h|| / 32768 * score only when score > 0 (the reference adds it unscaled otherwise);
+    then the shared expert's FFN.  Returns (out, absdot, selected, scores), absdot the sum
+    of |term| over every product that reaches out."""
+    x64 = np.asarray(norm_x, np.float32).astype(np.float64)
+    logits, _ = proj_expert(x64, *w["ffn_gate_inp"], n_embd, n_expert)
+    probs = 1.0 / (1.0 + np.exp(-logits))
+    sel = probs + np.asarray(bias, np.float32).astype(np.float64)
+    chosen = [int(i) for i in np.argsort(-sel, kind="stable")[:n_expert_used]]
+    scores = probs[chosen].copy()
+    if expert_weights_norm:
+        scores = scores / max(float(scores.sum()), MOE_NORM_MIN)
+    if expert_weights_scale != 0.0 and expert_weights_scale != 1.0:
+        scores = scores * expert_weights_scale
+    out = np.zeros(n_embd)
+    absdot = np.zeros(n_embd)
+    for e, sc in zip(chosen, scores):
+        off = expert_offset(e, n_embd, n_ff_exp)
+        g, _ = proj_expert(x64, *w["ffn_gate_exps"], n_embd, n_ff_exp, off)
+        u, _ = proj_expert(x64, *w["ffn_up_exps"], n_embd, n_ff_exp, off)
+        h = g / (1.0 + np.exp(-g)) * u
+        col_l2 = min(max(float(np.sqrt(np.sum(h * h))), 1e-8), 1e30)
+        d, a = proj_expert(h * F16_SAFE / col_l2, *w["ffn_down_exps"], n_ff_exp, n_embd, off)
+        f = col_l2 / F16_SAFE * sc if sc > 0.0 else 1.0
+        out += f * d
+        absdot += abs(f) * a
+    g, _ = proj_expert(x64, *w["ffn_gate_shexp"], n_embd, n_shexp)
+    u, _ = proj_expert(x64, *w["ffn_up_shexp"], n_embd, n_shexp)
+    d, a = proj_expert(g / (1.0 + np.exp(-g)) * u, *w["ffn_down_shexp"], n_shexp, n_embd)
+    return out + d, absdot + a, chosen, scores
