@@ -891,7 +891,8 @@ class TargetModel:
         with GGUFReader(gguf_path) as rd:
             md = rd.metadata
             if any("ffn_gate_exps" in t.name for t in rd.tensors):
-                raise LagunaError(EUNSUPPORTED, f"{gguf_path}: MoE layers are not supported")
+                raise LagunaError(EUNSUPPORTED, f"{gguf_path}: MoE layers are not supported by the one-call device "
+                                                "forward (dispatch_moe_ffn runs a MoE FFN from the host)")
             need = {"block_count": md.block_count, "embedding_length": md.embedding_length,
                     "feed_forward_length": md.feed_forward_length, "head_count": md.attention_head_count,
                     "head_count_kv": md.attention_head_count_kv, "key_length": md.attention_key_length}
